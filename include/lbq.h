@@ -1,0 +1,125 @@
+/*
+ * lbq.h -- C ABI of the MI355X quantized-linear library (liblbq.so).
+ *
+ * This is the drop-in boundary for lightbulb's GGUF quantized-linear path.
+ * lightbulb calls QuantizableLinear::Quantized(QMatMul)::forward for every
+ * attention/MLP projection and the LM head
+ * (/root/reference/src/model/quantizable_linear.rs:36-43, 63-69).  A Rust shim
+ * keeps that surface and binds the functions below through `extern "C"`; the
+ * binding is plain pointers, 64-bit sizes and an opaque stream pointer, in
+ * the style of the reference's only FFI precedent
+ * (/root/reference/src/backend/marlin_ffi.rs:84-215), plus status codes.
+ *
+ * Conventions
+ *   - Every function returns 0 (LBQ_OK) or a negative lbq_status, never
+ *     aborts; lbq_last_error() gives a thread-local message for the last
+ *     failure on the calling thread.
+ *   - Pointers named d_* are device pointers (HBM).  `stream` is a
+ *     hipStream_t passed as void* (NULL = the null stream); work is ordered
+ *     on it and the call does not synchronise unless stated.
+ *   - Weights are GGUF blocks in their on-disk byte layout: row-major
+ *     [n][k / block_size] blocks, rows contiguous along k
+ *     (GGUF ne0 = k; /root/reference/src/gguf/parser.rs:180-199).
+ *   - A context owns per-device scratch (quantised activations).  Calls that
+ *     share a context must be ordered on one stream (the reference runs every
+ *     forward on one model thread, src/engine/model_runner.rs:236,383).
+ *     Weight handles are immutable and may be read concurrently.
+ */
+#ifndef LBQ_H
+#define LBQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lbq_ctx lbq_ctx;
+typedef struct lbq_weight lbq_weight;
+
+enum lbq_status {
+    LBQ_OK = 0,
+    LBQ_ERR_INVALID_ARG = -1,      /* null pointer, negative size, misaligned pointer */
+    LBQ_ERR_UNSUPPORTED_TYPE = -2, /* ggml type id not served by this path */
+    LBQ_ERR_SHAPE = -3,            /* k not a multiple of the block size, byte count mismatch */
+    LBQ_ERR_OOM = -4,              /* device allocation failed */
+    LBQ_ERR_HIP = -5,              /* a HIP runtime call failed */
+    LBQ_ERR_LIMIT = -6             /* size beyond a documented maximum */
+};
+
+/* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
+enum lbq_ggml_type {
+    LBQ_TYPE_Q8_0 = 8,
+    LBQ_TYPE_Q4_K = 12,
+    LBQ_TYPE_Q5_K = 13,
+    LBQ_TYPE_Q6_K = 14,
+    LBQ_TYPE_Q8_K = 15 /* activation-only type (vec-dot partner of the k-quants) */
+};
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char *lbq_last_error(void);
+
+/* GgmlDType::block_size / type_size (/root/reference/src/quantization/mod.rs:99-126)
+ * for the five types above; 0 for any other id. */
+int lbq_type_block_size(uint32_t ggml_type);
+int lbq_type_size(uint32_t ggml_type);
+
+/* Open a context on HIP device `device`.  Replaces the device selection at
+ * /root/reference/src/model/parallel_model_manager.rs:239-248. */
+int lbq_init(int device, lbq_ctx **out_ctx);
+int lbq_ctx_destroy(lbq_ctx *ctx);
+
+/* Upload GGUF blocks (host bytes, on-disk layout, unchanged) to the device
+ * and return an immutable weight handle.  Replaces QMatMul::from_qtensor
+ * (called at /root/reference/src/model/custom_attention.rs:195-206,
+ * mlp_wrapper.rs:127-135, custom_transformer.rs:360-363) together with the
+ * upload done by Content::tensor (src/gguf/mod.rs:274-282).
+ * nbytes must equal n * (k / block_size) * type_size. */
+int lbq_weight_create(lbq_ctx *ctx, uint32_t ggml_type, int64_t n, int64_t k, const void *host_blocks,
+                      size_t nbytes, lbq_weight **out_w);
+
+/* As lbq_weight_create, but borrows blocks that are already device resident
+ * (no copy; the caller keeps the memory alive until lbq_weight_destroy). */
+int lbq_weight_wrap_device(lbq_ctx *ctx, uint32_t ggml_type, int64_t n, int64_t k, const void *d_blocks,
+                           size_t nbytes, lbq_weight **out_w);
+
+int lbq_weight_destroy(lbq_weight *w);
+
+/* Shape and type of a weight handle (QTensor::dtype / QTensor::shape). */
+int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_t *k);
+
+/* y[m][n] = x[m][k] . W^T in f32 -- QMatMul::forward (candle-core 0.10.2,
+ * reached through /root/reference/src/model/quantizable_linear.rs:67).
+ * x and y are contiguous f32 device buffers; any leading dims of the
+ * reference's [.., k] tensor are flattened into m.  The activation is
+ * quantised to Q8_K (k-quant weights) or Q8_0 (Q8_0 weights) exactly as the
+ * reference CPU path does, and each output is formed from integer
+ * sub-block dot products.  m == 0 is a no-op. */
+int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
+
+/* Dequantise the whole weight to f32 [n][k] -- QTensor::dequantize (used at
+ * /root/reference/src/model/custom_transformer.rs:323,347 and
+ * custom_transformer_block.rs:229,231).  Bit-exact with the reference. */
+int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream);
+
+/* Dequantise nelem values of raw device blocks -- dequantize_tensor
+ * (/root/reference/src/quantization/mod.rs:158-247), extended to Q5_K/Q6_K/Q8_K.
+ * nelem must be a multiple of the block size. */
+int lbq_dequantize_blocks_f32(uint32_t ggml_type, const void *d_blocks, int64_t nelem, float *d_y, void *stream);
+
+/* Quantise activations x[m][k] to GGUF blocks of `act_type` (LBQ_TYPE_Q8_K:
+ * 292-byte blocks; LBQ_TYPE_Q8_0: 34-byte blocks) -- the activation
+ * quantisation inside QMatMul::forward (candle BlockQ8K::from_float /
+ * BlockQ8_0::from_float).  Exposed so the step can be checked on its own. */
+int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, void *d_out_blocks, void *stream);
+
+/* Quantise f32 weights (nelem values, row-major, rows along k) to GGUF blocks
+ * of `ggml_type` -- quantize_tensor (/root/reference/src/quantization/mod.rs:257-327),
+ * extended to Q5_K/Q6_K.  Runs on the device. */
+int lbq_quantize_weights_f32(uint32_t ggml_type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LBQ_H */

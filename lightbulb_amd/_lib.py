@@ -1,0 +1,75 @@
+"""ctypes binding of liblbq.so (the C ABI declared in include/lbq.h).
+
+The library is the product: there is no fallback.  If ``liblbq.so`` has not
+been built, or cannot be loaded, every entry point raises instead of quietly
+computing something else.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "liblbq.so"
+
+LBQ_OK = 0
+STATUS_NAMES = {
+    -1: "LBQ_ERR_INVALID_ARG",
+    -2: "LBQ_ERR_UNSUPPORTED_TYPE",
+    -3: "LBQ_ERR_SHAPE",
+    -4: "LBQ_ERR_OOM",
+    -5: "LBQ_ERR_HIP",
+    -6: "LBQ_ERR_LIMIT",
+}
+
+# name -> (restype, argtypes); must list every function include/lbq.h declares
+_c = ctypes
+_VP, _I64, _U32, _SZ = _c.c_void_p, _c.c_int64, _c.c_uint32, _c.c_size_t
+SIGNATURES = {
+    "lbq_last_error": (_c.c_char_p, []),
+    "lbq_type_block_size": (_c.c_int, [_U32]),
+    "lbq_type_size": (_c.c_int, [_U32]),
+    "lbq_init": (_c.c_int, [_c.c_int, _c.POINTER(_VP)]),
+    "lbq_ctx_destroy": (_c.c_int, [_VP]),
+    "lbq_weight_create": (_c.c_int, [_VP, _U32, _I64, _I64, _VP, _SZ, _c.POINTER(_VP)]),
+    "lbq_weight_wrap_device": (_c.c_int, [_VP, _U32, _I64, _I64, _VP, _SZ, _c.POINTER(_VP)]),
+    "lbq_weight_destroy": (_c.c_int, [_VP]),
+    "lbq_weight_info": (_c.c_int, [_VP, _c.POINTER(_U32), _c.POINTER(_I64), _c.POINTER(_I64)]),
+    "lbq_qmatmul_f32": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
+    "lbq_dequantize_f32": (_c.c_int, [_VP, _VP, _VP, _VP]),
+    "lbq_dequantize_blocks_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
+    "lbq_quantize_act": (_c.c_int, [_U32, _VP, _I64, _I64, _VP, _VP]),
+    "lbq_quantize_weights_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
+}
+
+
+class LbqError(RuntimeError):
+    """A non-zero status from liblbq, with the library's own message."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP library first "
+                "(python -m lightbulb_amd.build, or __graft_entry__.build())")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != LBQ_OK:
+        msg = lib().lbq_last_error()
+        raise LbqError(status, msg.decode() if msg else "")

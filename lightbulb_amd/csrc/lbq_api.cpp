@@ -1,0 +1,324 @@
+// lbq_api.cpp -- the C ABI (include/lbq.h): argument checking, device scratch,
+// and dispatch between the decode GEMV (m <= 8) and the MFMA GEMM (m > 8).
+//
+// Error behaviour mirrors candle's QMatMul surface as the reference sees it: a
+// failure is returned (candle::Result propagated with `?` through
+// QuantizableLinear::forward, /root/reference/src/model/quantizable_linear.rs:63-69),
+// never an abort.  Here that is a negative status plus a thread-local message.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/lbq.h"
+#include "lbq_device.hpp"
+#include "lbq_internal.hpp"
+
+struct lbq_ctx {
+    int device;
+    std::mutex mu;        // guards scratch growth
+    uint8_t *scratch;     // quantised activations (split layout)
+    size_t scratch_bytes;
+};
+
+struct lbq_weight {
+    lbq_ctx *ctx;
+    int type;
+    int64_t n, k;
+    int64_t row_bytes;
+    size_t nbytes;
+    const uint8_t *d_blocks;
+    bool owned;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int status, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(LBQ_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool weight_type_ok(uint32_t t) {
+    return t == LBQ_TYPE_Q8_0 || t == LBQ_TYPE_Q4_K || t == LBQ_TYPE_Q5_K || t == LBQ_TYPE_Q6_K;
+}
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Split activation layout for m rows of length k quantised to act_type.
+struct ActLayout {
+    size_t q_off, d_off, bs_off, total;
+    int nb;
+};
+
+ActLayout act_layout(int act_type, int64_t m, int64_t k) {
+    ActLayout L;
+    const int bs = act_type == LBQ_TYPE_Q8_K ? 256 : 32;
+    L.nb = (int)(k / bs);
+    L.q_off = 0;
+    L.d_off = align_up((size_t)(m * k), 256);
+    L.bs_off = align_up(L.d_off + (size_t)(m * L.nb) * sizeof(float), 256);
+    L.total = align_up(L.bs_off + (act_type == LBQ_TYPE_Q8_K ? (size_t)(m * (k / 16)) * sizeof(int16_t) : 0), 256);
+    return L;
+}
+
+int ensure_scratch(lbq_ctx *ctx, size_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return LBQ_OK;
+    const size_t want = align_up(bytes > ctx->scratch_bytes * 2 ? bytes : ctx->scratch_bytes * 2, 1 << 20);
+    if (ctx->scratch) {
+        // in-flight kernels on any stream may still read the old buffer
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+        (void)hipFree(ctx->scratch);
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+    }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for activation scratch: %s", want, hipGetErrorString(e));
+    ctx->scratch = static_cast<uint8_t *>(p);
+    ctx->scratch_bytes = want;
+    return LBQ_OK;
+}
+
+int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+    const int bs = lbq_type_block_size(type);
+    if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
+    if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
+    if (k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "k = %lld exceeds the supported maximum", (long long)k);
+    const size_t want = (size_t)n * (size_t)(k / bs) * (size_t)lbq_type_size(type);
+    if (nbytes != want)
+        return fail(LBQ_ERR_SHAPE, "byte count %zu does not match n*(k/%d)*%d = %zu", nbytes, bs, lbq_type_size(type), want);
+    return LBQ_OK;
+}
+
+int make_weight(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const uint8_t *dev, size_t nbytes, bool owned,
+                lbq_weight **out) {
+    lbq_weight *w = new (std::nothrow) lbq_weight;
+    if (!w) return fail(LBQ_ERR_OOM, "host allocation failed");
+    w->ctx = ctx;
+    w->type = (int)type;
+    w->n = n;
+    w->k = k;
+    w->row_bytes = (k / lbq_type_block_size(type)) * lbq_type_size(type);
+    w->nbytes = nbytes;
+    w->d_blocks = dev;
+    w->owned = owned;
+    *out = w;
+    return LBQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *lbq_last_error(void) { return g_err.c_str(); }
+
+int lbq_type_block_size(uint32_t t) {
+    switch (t) {
+    case LBQ_TYPE_Q8_0: return 32;
+    case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K: return 256;
+    default: return 0;
+    }
+}
+
+int lbq_type_size(uint32_t t) {
+    switch (t) {
+    case LBQ_TYPE_Q8_0: return 34;
+    case LBQ_TYPE_Q4_K: return 144;
+    case LBQ_TYPE_Q5_K: return 176;
+    case LBQ_TYPE_Q6_K: return 210;
+    case LBQ_TYPE_Q8_K: return 292;
+    default: return 0;
+    }
+}
+
+int lbq_init(int device, lbq_ctx **out_ctx) {
+    if (!out_ctx) return fail(LBQ_ERR_INVALID_ARG, "out_ctx is null");
+    *out_ctx = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count) return fail(LBQ_ERR_INVALID_ARG, "device %d out of range (%d devices)", device, count);
+    DeviceGuard g(device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq_ctx *c = new (std::nothrow) lbq_ctx;
+    if (!c) return fail(LBQ_ERR_OOM, "host allocation failed");
+    c->device = device;
+    c->scratch = nullptr;
+    c->scratch_bytes = 0;
+    *out_ctx = c;
+    return LBQ_OK;
+}
+
+int lbq_ctx_destroy(lbq_ctx *ctx) {
+    if (!ctx) return LBQ_OK;
+    DeviceGuard g(ctx->device);
+    if (ctx->scratch) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->scratch);
+    }
+    delete ctx;
+    return LBQ_OK;
+}
+
+int lbq_weight_create(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const void *host_blocks, size_t nbytes,
+                      lbq_weight **out_w) {
+    if (!ctx || !host_blocks || !out_w) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_weight_create");
+    *out_w = nullptr;
+    int s = check_weight_args(type, n, k, nbytes);
+    if (s) return s;
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, nbytes);
+    if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for weight blocks: %s", nbytes, hipGetErrorString(e));
+    e = hipMemcpy(d, host_blocks, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "hipMemcpy H2D of weight blocks");
+    }
+    s = make_weight(ctx, type, n, k, static_cast<const uint8_t *>(d), nbytes, true, out_w);
+    if (s) (void)hipFree(d);
+    return s;
+}
+
+int lbq_weight_wrap_device(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const void *d_blocks, size_t nbytes,
+                           lbq_weight **out_w) {
+    if (!ctx || !d_blocks || !out_w) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_weight_wrap_device");
+    *out_w = nullptr;
+    int s = check_weight_args(type, n, k, nbytes);
+    if (s) return s;
+    if (reinterpret_cast<uintptr_t>(d_blocks) & 15u)
+        return fail(LBQ_ERR_INVALID_ARG, "device weight blocks must be 16-byte aligned");
+    return make_weight(ctx, type, n, k, static_cast<const uint8_t *>(d_blocks), nbytes, false, out_w);
+}
+
+int lbq_weight_destroy(lbq_weight *w) {
+    if (!w) return LBQ_OK;
+    if (w->owned) {
+        DeviceGuard g(w->ctx->device);
+        (void)hipFree(const_cast<uint8_t *>(w->d_blocks));
+    }
+    delete w;
+    return LBQ_OK;
+}
+
+int lbq_weight_info(const lbq_weight *w, uint32_t *type, int64_t *n, int64_t *k) {
+    if (!w) return fail(LBQ_ERR_INVALID_ARG, "null weight");
+    if (type) *type = (uint32_t)w->type;
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    return LBQ_OK;
+}
+
+int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream) {
+    if (!ctx || !w) return fail(LBQ_ERR_INVALID_ARG, "null context or weight");
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    if (m == 0) return LBQ_OK;
+    if (!d_x || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null activation or output pointer");
+    if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
+        return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
+    if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    const int act_type = w->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const ActLayout L = act_layout(act_type, m, w->k);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    int s = ensure_scratch(ctx, L.total);
+    if (s) return s;
+    int8_t *xq = reinterpret_cast<int8_t *>(ctx->scratch + L.q_off);
+    float *xd = reinterpret_cast<float *>(ctx->scratch + L.d_off);
+    int16_t *xbs = reinterpret_cast<int16_t *>(ctx->scratch + L.bs_off);
+    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w->k, xq, xd, xbs, nullptr, st);
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    lbq::ActView av{xq, xd, xbs, w->k, L.nb};
+    if (m <= 8) e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
+    else e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, st);
+    if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+    return LBQ_OK;
+}
+
+int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream) {
+    if (!ctx || !w || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_dequantize_f32");
+    if (reinterpret_cast<uintptr_t>(d_y) & 15u) return fail(LBQ_ERR_INVALID_ARG, "output must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = lbq::launch_dequant(w->type, w->d_blocks, w->n * w->k, d_y, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return LBQ_OK;
+}
+
+int lbq_dequantize_blocks_f32(uint32_t type, const void *d_blocks, int64_t nelem, float *d_y, void *stream) {
+    if (!d_blocks || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_dequantize_blocks_f32");
+    if (!weight_type_ok(type) && type != LBQ_TYPE_Q8_K) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
+    const int bs = lbq_type_block_size(type);
+    if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);
+    if ((reinterpret_cast<uintptr_t>(d_blocks) & 3u) || (reinterpret_cast<uintptr_t>(d_y) & 15u))
+        return fail(LBQ_ERR_INVALID_ARG, "blocks must be 4-byte aligned and output 16-byte aligned");
+    if (nelem == 0) return LBQ_OK;
+    hipError_t e = lbq::launch_dequant((int)type, static_cast<const uint8_t *>(d_blocks), nelem, d_y,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return LBQ_OK;
+}
+
+int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, void *d_out_blocks, void *stream) {
+    if (!d_x || !d_out_blocks) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_quantize_act");
+    if (act_type != LBQ_TYPE_Q8_K && act_type != LBQ_TYPE_Q8_0)
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15) or Q8_0 (8)", act_type);
+    const int bs = lbq_type_block_size(act_type);
+    if (m < 0 || k <= 0 || k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a positive multiple of %d", (long long)k, bs);
+    if ((reinterpret_cast<uintptr_t>(d_x) & 3u) || (reinterpret_cast<uintptr_t>(d_out_blocks) & 3u))
+        return fail(LBQ_ERR_INVALID_ARG, "x and the output blocks must be 4-byte aligned");
+    if (m == 0) return LBQ_OK;
+    hipError_t e = lbq::launch_quant_act((int)act_type, d_x, m, k, nullptr, nullptr, nullptr,
+                                         static_cast<uint8_t *>(d_out_blocks), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    return LBQ_OK;
+}
+
+int lbq_quantize_weights_f32(uint32_t type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream) {
+    if (!d_w || !d_out_blocks) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_quantize_weights_f32");
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
+    const int bs = lbq_type_block_size(type);
+    if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);
+    if ((reinterpret_cast<uintptr_t>(d_w) & 3u) || (reinterpret_cast<uintptr_t>(d_out_blocks) & 3u))
+        return fail(LBQ_ERR_INVALID_ARG, "weights and output blocks must be 4-byte aligned");
+    if (nelem == 0) return LBQ_OK;
+    hipError_t e = lbq::launch_quant_weights((int)type, d_w, nelem, static_cast<uint8_t *>(d_out_blocks),
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "weight quantisation launch");
+    return LBQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,33 @@
+// lbq_internal.hpp -- launcher declarations shared between the kernel translation
+// units and the C ABI (lbq_api.cpp).  Host-side only types; no torch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lbq {
+
+enum : int { TYPE_Q8_0 = 8, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15 };
+
+struct ActView;
+
+// Quantise x[m][k] to Q8_K (act_type 15) or Q8_0 (act_type 8).  Writes the split
+// internal layout (xq/xd/xbs) when gguf == nullptr, else GGUF blocks to gguf.
+hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
+                            int16_t *xbs, uint8_t *gguf, hipStream_t st);
+
+// Dequantise nelem values (multiple of the block size) of `type` blocks to f32.
+hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st);
+
+// y[m][n] += nothing: y is overwritten.  Weight rows are row_bytes apart.
+// Requires m <= 8 (decode GEMV) -- the kernels keep one accumulator per row of x.
+hipError_t launch_gemv(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                       int m, float *y, hipStream_t st);
+
+// Batched path (m > 8): dequantise weight tiles into LDS and run them through MFMA.
+hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                       int64_t m, float *y, hipStream_t st);
+
+// f32 weights -> GGUF blocks on the device (ggml reference quantisers).
+hipError_t launch_quant_weights(int type, const float *w, int64_t nelem, uint8_t *out, hipStream_t st);
+
+}  // namespace lbq

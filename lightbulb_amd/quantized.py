@@ -1,0 +1,315 @@
+"""Host-side mirror of the reference's quantized-linear surface, over liblbq.
+
+The reference (Rust) serves every GGUF projection through these types:
+
+* ``GgmlDType``          -- /root/reference/src/quantization/mod.rs:58-147
+* ``QTensor`` / ``QMatMul`` (candle-core 0.10.2, external) -- built at
+  src/model/custom_attention.rs:195-206, mlp_wrapper.rs:127-135 and
+  custom_transformer.rs:360-363; ``forward`` called at custom_attention.rs:265-267,
+  :671, mlp_wrapper.rs:190-195 and custom_transformer.rs:625
+* ``QuantizableLinear``  -- src/model/quantizable_linear.rs:36-70
+* ``dequantize_tensor`` / ``quantize_tensor`` -- src/quantization/mod.rs:158-327
+
+Same names, same argument meaning, same failure cases (raised as exceptions
+where Rust returns ``Err``).  The arithmetic runs in liblbq's HIP kernels on the
+GPU; torch only provides device memory and the current stream.  There is no
+CPU fallback: without the built library or a GPU these raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from enum import IntEnum
+
+import numpy as np
+import torch
+
+from . import _lib
+
+
+class GgmlDType(IntEnum):
+    """GGML quantisation type ids (GGUF ``ggml_type``)."""
+
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
+    Q8_0 = 8
+    Q8_1 = 9
+    Q2K = 10
+    Q3K = 11
+    Q4K = 12
+    Q5K = 13
+    Q6K = 14
+    Q8K = 15
+
+    @classmethod
+    def from_u32(cls, value: int) -> "GgmlDType | None":
+        try:
+            return cls(value)
+        except ValueError:
+            return None
+
+    def block_size(self) -> int:
+        if self in (GgmlDType.F32, GgmlDType.F16):
+            return 1
+        if self in (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q8_1):
+            return 32
+        return 256
+
+    def type_size(self) -> int:
+        return {
+            GgmlDType.F32: 4, GgmlDType.F16: 2, GgmlDType.Q4_0: 18, GgmlDType.Q4_1: 20, GgmlDType.Q5_0: 22,
+            GgmlDType.Q5_1: 24, GgmlDType.Q8_0: 34, GgmlDType.Q8_1: 36, GgmlDType.Q2K: 82, GgmlDType.Q3K: 110,
+            GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292,
+        }[self]
+
+    def type_name(self) -> str:
+        """Human-readable name as the reference prints it (``GgmlDType::name``)."""
+        return {
+            GgmlDType.Q2K: "Q2_K", GgmlDType.Q3K: "Q3_K", GgmlDType.Q4K: "Q4_K", GgmlDType.Q5K: "Q5_K",
+            GgmlDType.Q6K: "Q6_K", GgmlDType.Q8K: "Q8_K",
+        }.get(self, self.name)
+
+
+#: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE
+SERVED = (GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+
+
+# ---------------------------------------------------------------------------
+# contexts: one liblbq context per device, created on first use
+# ---------------------------------------------------------------------------
+_ctx_lock = threading.Lock()
+_ctxs: dict[int, int] = {}
+
+
+def _device_index(device) -> int:
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError(f"the quantized path runs on the GPU; got device {dev}")
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def context(device="cuda") -> int:
+    idx = _device_index(device)
+    with _ctx_lock:
+        if idx not in _ctxs:
+            out = ctypes.c_void_p()
+            _lib.check(_lib.lib().lbq_init(idx, ctypes.byref(out)))
+            _ctxs[idx] = out.value
+        return _ctxs[idx]
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(torch.device(device)).cuda_stream)
+
+
+# ---------------------------------------------------------------------------
+# QTensor: GGUF blocks resident in HBM, in their on-disk layout
+# ---------------------------------------------------------------------------
+class QTensor:
+    """Quantised tensor of shape (n, k): n rows of k/block_size GGUF blocks.
+
+    ``data`` is a flat uint8 device tensor holding the blocks unchanged.  The
+    shape is candle's (n, k) order; a GGUF tensor-info lists it as ne0 = k,
+    ne1 = n (/root/reference/src/gguf/parser.rs:180-199).
+    """
+
+    def __init__(self, data: torch.Tensor, dtype: GgmlDType, shape: tuple[int, int]):
+        dtype = GgmlDType(dtype)
+        n, k = (int(s) for s in shape)
+        if data.dtype != torch.uint8 or data.dim() != 1 or not data.is_contiguous():
+            raise ValueError("QTensor data must be a contiguous 1-D uint8 tensor")
+        if k % dtype.block_size():
+            raise ValueError(f"{dtype.type_name()}: k = {k} is not a multiple of {dtype.block_size()}")
+        need = n * (k // dtype.block_size()) * dtype.type_size()
+        if data.numel() != need:
+            raise ValueError(f"{dtype.type_name()}: {data.numel()} bytes for shape ({n}, {k}), expected {need}")
+        self.data = data
+        self._dtype = dtype
+        self._shape = (n, k)
+
+    @classmethod
+    def from_bytes(cls, raw, dtype: GgmlDType, shape: tuple[int, int], device="cuda") -> "QTensor":
+        """Upload raw GGUF block bytes (bytes / numpy uint8) to the device unchanged."""
+        host = torch.from_numpy(np.frombuffer(bytes(raw), dtype=np.uint8).copy()) if not isinstance(
+            raw, np.ndarray) else torch.from_numpy(np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1))
+        return cls(host.to(device), dtype, shape)
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor, dtype: GgmlDType) -> "QTensor":
+        """Quantise an f32 [n, k] device tensor to ``dtype`` blocks on the device."""
+        if w.dim() != 2:
+            raise ValueError("QTensor.quantize expects a 2-D (n, k) tensor")
+        n, k = w.shape
+        blocks = quantize_tensor(w.reshape(-1), dtype, _exact=True)
+        return cls(blocks, dtype, (n, k))
+
+    def dtype(self) -> GgmlDType:
+        return self._dtype
+
+    def shape(self) -> tuple[int, int]:
+        return self._shape
+
+    def storage_size_in_bytes(self) -> int:
+        return self.data.numel()
+
+    def dequantize(self) -> torch.Tensor:
+        """f32 [n, k], bit-exact with the reference's dequantisation."""
+        n, k = self._shape
+        return dequantize_tensor(self.data, self._dtype, n * k).reshape(n, k)
+
+    def __repr__(self) -> str:
+        return f"QTensor({self._dtype.type_name()}, shape={self._shape}, device={self.data.device})"
+
+
+# ---------------------------------------------------------------------------
+# QMatMul
+# ---------------------------------------------------------------------------
+class QMatMul:
+    """``QMatMul::from_qtensor`` + ``Module::forward`` over liblbq."""
+
+    def __init__(self, qtensor: QTensor, _handle: int, _ctx: int):
+        self._qt = qtensor
+        self._handle = _handle
+        self._ctx = _ctx
+
+    @classmethod
+    def from_qtensor(cls, qtensor: QTensor) -> "QMatMul":
+        dt = qtensor.dtype()
+        if dt not in SERVED:
+            raise ValueError(f"quantized matmul for {dt.type_name()} is not served by the GPU path")
+        n, k = qtensor.shape()
+        ctx = context(qtensor.data.device)
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().lbq_weight_wrap_device(ctx, int(dt), n, k, qtensor.data.data_ptr(),
+                                                     qtensor.data.numel(), ctypes.byref(h)))
+        return cls(qtensor, h.value, ctx)
+
+    def qtensor(self) -> QTensor:
+        return self._qt
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        n, k = self._qt.shape()
+        if xs.dtype != torch.float32:
+            raise ValueError(f"the lhs for quantized matmul must be f32, got {xs.dtype}")
+        if xs.dim() < 2:
+            raise ValueError(f"input tensor has only one dimension {tuple(xs.shape)}")
+        if xs.shape[-1] != k:
+            raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with {(n, k)}")
+        if not xs.is_contiguous():
+            raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
+        if xs.device != self._qt.data.device:
+            raise ValueError(f"input on {xs.device}, weights on {self._qt.data.device}")
+        m = xs.numel() // k
+        y = torch.empty(*xs.shape[:-1], n, dtype=torch.float32, device=xs.device)
+        if m:
+            _lib.check(_lib.lib().lbq_qmatmul_f32(self._ctx, self._handle, xs.data_ptr(), m, y.data_ptr(),
+                                                  _stream(xs.device)))
+        return y
+
+    __call__ = forward
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h:
+            try:
+                _lib.lib().lbq_weight_destroy(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    def __repr__(self) -> str:
+        return f"QMatMul({self._qt!r})"
+
+
+# ---------------------------------------------------------------------------
+# QuantizableLinear (src/model/quantizable_linear.rs)
+# ---------------------------------------------------------------------------
+class QuantizableLinear:
+    """Either ``Regular`` (dense f32 weight [n, k], optional bias) or ``Quantized(QMatMul)``."""
+
+    def __init__(self, kind: str, inner):
+        self.kind = kind
+        self.inner = inner
+
+    @classmethod
+    def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None) -> "QuantizableLinear":
+        return cls("Regular", (weight, bias))
+
+    @classmethod
+    def from_qmatmul(cls, qmatmul: QMatMul) -> "QuantizableLinear":
+        return cls("Quantized", qmatmul)
+
+    def is_quantized(self) -> bool:
+        return self.kind == "Quantized"
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        if self.kind == "Quantized":
+            return self.inner.forward(xs)
+        w, b = self.inner
+        y = xs.matmul(w.t())
+        return y + b if b is not None else y
+
+    __call__ = forward
+
+
+# ---------------------------------------------------------------------------
+# dequantize_tensor / quantize_tensor (src/quantization/mod.rs:158-327)
+# ---------------------------------------------------------------------------
+def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> torch.Tensor:
+    """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off."""
+    dtype = GgmlDType(dtype)
+    if dtype not in SERVED and dtype != GgmlDType.Q8K:
+        raise ValueError(f"Dequantization for {dtype.type_name()} not yet implemented")
+    bs, ts = dtype.block_size(), dtype.type_size()
+    num_blocks = (elem_count + bs - 1) // bs
+    expected = num_blocks * ts
+    if data.numel() < expected:
+        raise ValueError(f"Insufficient data for {dtype.type_name()}: got {data.numel()} bytes, "
+                         f"need {expected} bytes")
+    out = torch.empty(num_blocks * bs, dtype=torch.float32, device=data.device)
+    if num_blocks:
+        _lib.check(_lib.lib().lbq_dequantize_blocks_f32(int(dtype), data.data_ptr(), num_blocks * bs,
+                                                        out.data_ptr(), _stream(data.device)))
+    return out[:elem_count]
+
+
+def quantize_tensor(data: torch.Tensor, dtype: GgmlDType, _exact: bool = False) -> torch.Tensor:
+    """f32 device values -> GGUF blocks (uint8); the last block is zero-padded."""
+    dtype = GgmlDType(dtype)
+    if dtype not in SERVED:
+        raise ValueError(f"Quantization for {dtype.type_name()} not yet implemented")
+    if data.dtype != torch.float32:
+        raise ValueError("quantize_tensor expects f32 values")
+    flat = data.reshape(-1)
+    bs = dtype.block_size()
+    num_blocks = (flat.numel() + bs - 1) // bs
+    if num_blocks * bs != flat.numel():
+        if _exact:
+            raise ValueError(f"{flat.numel()} values are not a whole number of {bs}-value blocks")
+        padded = torch.zeros(num_blocks * bs, dtype=torch.float32, device=flat.device)
+        padded[:flat.numel()] = flat
+        flat = padded
+    flat = flat.contiguous()
+    out = torch.empty(num_blocks * dtype.type_size(), dtype=torch.uint8, device=flat.device)
+    if num_blocks:
+        _lib.check(_lib.lib().lbq_quantize_weights_f32(int(dtype), flat.data_ptr(), flat.numel(), out.data_ptr(),
+                                                       _stream(flat.device)))
+    return out
+
+
+def quantize_activations(x: torch.Tensor, act_type: GgmlDType) -> torch.Tensor:
+    """The activation step of QMatMul::forward on its own: x f32 [m, k] -> Q8_K / Q8_0 blocks (uint8)."""
+    act_type = GgmlDType(act_type)
+    if act_type not in (GgmlDType.Q8K, GgmlDType.Q8_0):
+        raise ValueError("activations quantise to Q8_K or Q8_0")
+    x = x.contiguous()
+    k = x.shape[-1]
+    m = x.numel() // k
+    out = torch.empty(m, k // act_type.block_size() * act_type.type_size(), dtype=torch.uint8, device=x.device)
+    if m:
+        _lib.check(_lib.lib().lbq_quantize_act(int(act_type), x.data_ptr(), m, k, out.data_ptr(), _stream(x.device)))
+    return out

@@ -1,0 +1,68 @@
+"""The C ABI library loads, exports every symbol include/lbq.h declares, and rejects
+bad arguments before touching a device (these run without a GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = (ROOT / "include" / "lbq.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lbq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(lbq):
+    from lightbulb_amd import _lib
+    names = declared_functions()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lbq, name), name
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_type_table_matches_reference(lbq):
+    # GgmlDType::block_size / type_size, /root/reference/src/quantization/mod.rs:99-126
+    for t, bs, ts in [(8, 32, 34), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 292)]:
+        assert lbq.lbq_type_block_size(t) == bs and lbq.lbq_type_size(t) == ts
+    for t in (0, 1, 2, 3, 9, 10, 11, 16, 999):
+        assert lbq.lbq_type_block_size(t) == 0 and lbq.lbq_type_size(t) == 0
+
+
+def test_argument_errors_without_device(lbq):
+    # unsupported types, bad shapes and null pointers are refused before any HIP call
+    dummy = ctypes.c_void_p(256)
+    assert lbq.lbq_quantize_act(12, dummy, 1, 256, dummy, None) == -2
+    assert lbq.lbq_quantize_act(15, dummy, 1, 255, dummy, None) == -3
+    assert lbq.lbq_quantize_act(15, None, 1, 256, dummy, None) == -1
+    assert lbq.lbq_dequantize_blocks_f32(2, dummy, 32, dummy, None) == -2
+    assert lbq.lbq_dequantize_blocks_f32(12, dummy, 100, dummy, None) == -3
+    assert lbq.lbq_quantize_weights_f32(15, dummy, 256, dummy, None) == -2
+    assert lbq.lbq_quantize_weights_f32(14, dummy, 300, dummy, None) == -3
+    assert lbq.lbq_qmatmul_f32(None, None, None, 1, None, None) == -1
+    assert lbq.lbq_weight_create(None, 12, 1, 256, None, 144, ctypes.byref(ctypes.c_void_p())) == -1
+    msg = lbq.lbq_last_error()
+    assert msg and b"null" in msg
+    assert lbq.lbq_init(0, None) == -1
+    assert lbq.lbq_weight_destroy(None) == 0 and lbq.lbq_ctx_destroy(None) == 0
+
+
+def test_product_does_not_import_oracle():
+    # the product path must never route through the test oracle
+    for p in (ROOT / "lightbulb_amd").rglob("*"):
+        if p.suffix in (".py", ".cpp", ".hip", ".hpp", ".h"):
+            src = p.read_text()
+            assert "import oracle" not in src and "from oracle" not in src and "lbq_oracle" not in src, p
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from lightbulb_amd import _lib
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    try:
+        _lib.lib()
+    except RuntimeError as e:
+        assert "missing" in str(e)
+    else:
+        raise AssertionError("no error without the library")

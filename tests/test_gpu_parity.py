@@ -1,0 +1,208 @@
+"""GPU parity: liblbq (through its C ABI) against the CPU oracle on the same inputs.
+
+Bars:
+* dequantisation, activation quantisation, weight quantisation: bit-exact;
+* QMatMul::forward: per output row, relative L2 error <= 2e-3 and max abs error
+  <= 1e-2 * ||row||_inf against the oracle's CPU QMatMul (the tolerance the
+  path is specified with).  Because the GPU reproduces the reference's Q8_K /
+  Q8_0 activation quantisation and integer sub-block sums, the observed error
+  is f32 summation order only (~1e-6); a tighter 1e-4 check guards that.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import blockpack as bp
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 8, 12, 13, 14, 15
+TOL_REL_L2 = 2e-3
+TOL_MAX_ABS = 1e-2
+
+
+def assert_rows_close(y: np.ndarray, ref: np.ndarray, tight: float = 1e-4):
+    y = y.reshape(ref.shape)
+    assert np.all(np.isfinite(y))
+    for r in range(ref.shape[0]):
+        diff = y[r].astype(np.float64) - ref[r]
+        nrm = np.linalg.norm(ref[r])
+        rel = np.linalg.norm(diff) / nrm if nrm > 0 else np.linalg.norm(diff)
+        assert rel <= TOL_REL_L2, f"row {r}: rel L2 {rel:.3e}"
+        assert np.abs(diff).max() <= TOL_MAX_ABS * np.abs(ref[r]).max() + 1e-30, f"row {r}: max abs"
+        assert rel <= tight, f"row {r}: rel L2 {rel:.3e} above the expected summation-order level"
+
+
+def to_dev(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def gpu_quant_weights(t: int, w: np.ndarray, dev) -> np.ndarray:
+    from lightbulb_amd.quantized import quantize_tensor
+    out = quantize_tensor(to_dev(w.astype(np.float32).reshape(-1), dev), t, _exact=True)
+    return out.cpu().numpy()
+
+
+def gpu_qmatmul(t: int, w_raw: np.ndarray, n: int, k: int, x: np.ndarray, dev) -> np.ndarray:
+    from lightbulb_amd.quantized import QMatMul, QTensor
+    qt = QTensor(to_dev(w_raw, dev), t, (n, k))
+    y = QMatMul.from_qtensor(qt).forward(to_dev(x.astype(np.float32), dev))
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# ---------------------------------------------------------------- dequantisation
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
+def test_dequant_bit_exact_random_blocks(oracle, lbq, dev, t):
+    rng = np.random.default_rng(10 + t)
+    nb = 1001
+    raw = bp.random_blocks(rng, t, nb, d_scale=0.5)
+    bs = oracle.block_size(t)
+    ref = oracle.dequantize(t, raw)
+    from lightbulb_amd.quantized import dequantize_tensor
+    got = dequantize_tensor(to_dev(raw, dev), t, nb * bs).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_q8k_and_truncation(oracle, lbq, dev):
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    q8k = oracle.quantize_act(Q8_K, x).reshape(-1)
+    from lightbulb_amd.quantized import dequantize_tensor
+    got = dequantize_tensor(to_dev(q8k, dev), Q8_K, 3 * 512).cpu().numpy()
+    assert np.array_equal(got, oracle.dequantize(Q8_K, q8k))
+    # reference semantics: blocks rounded up, output truncated to elem_count (mod.rs:165-187)
+    raw = bp.random_blocks(rng, Q4_K, 2)
+    got = dequantize_tensor(to_dev(raw, dev), Q4_K, 300).cpu().numpy()
+    assert got.shape == (300,) and np.array_equal(got, oracle.dequantize(Q4_K, raw)[:300])
+    with pytest.raises(ValueError, match="Insufficient data for Q4_K"):
+        dequantize_tensor(to_dev(raw[:200], dev), Q4_K, 512)
+
+
+# ---------------------------------------------------------------- activation quantisation
+def _special_rows(k: int) -> np.ndarray:
+    rows = np.zeros((6, k), dtype=np.float32)
+    rows[1, 17] = -3.0                       # single non-zero
+    rows[2, 3], rows[2, 7] = -2.0, 2.0       # tie with opposite signs, saturation at +128
+    rows[3, 0] = -128.0                      # iscale = 1: half-away-from-zero rounding
+    rows[3, 1:6] = [2.5, -2.5, 3.5, 0.5, -0.5]
+    rows[4, :] = np.linspace(-1, 1, k, dtype=np.float32)
+    rows[5, :] = 1e-30                       # tiny magnitudes
+    return rows
+
+
+@pytest.mark.parametrize("act", [Q8_K, Q8_0])
+def test_quantize_act_bit_exact(oracle, lbq, dev, act):
+    rng = np.random.default_rng(30 + act)
+    k = 4096
+    x = rng.standard_normal((9, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20      # outliers, as in the LM-head config
+    x = np.concatenate([x, _special_rows(k)])
+    from lightbulb_amd.quantized import quantize_activations
+    got = quantize_activations(to_dev(x, dev), act).cpu().numpy()
+    ref = oracle.quantize_act(act, x)
+    assert np.array_equal(got, ref)
+
+
+def test_quantize_act_unaligned_input(oracle, lbq, dev):
+    # an f32 view that is only 4-byte aligned takes the scalar-load variant
+    rng = np.random.default_rng(33)
+    base = torch.from_numpy(rng.standard_normal(2 * 256 + 1).astype(np.float32)).to(dev)
+    view = base[1:]
+    from lightbulb_amd.quantized import quantize_activations
+    got = quantize_activations(view.reshape(2, 256), Q8_K).cpu().numpy()
+    assert np.array_equal(got, oracle.quantize_act(Q8_K, view.cpu().numpy().reshape(2, 256)))
+
+
+# ---------------------------------------------------------------- weight quantisation
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
+def test_quantize_weights_bit_exact(oracle, lbq, dev, t):
+    rng = np.random.default_rng(40 + t)
+    w = (rng.standard_normal((64, 1024)) * 0.02).astype(np.float32)
+    w[0, :256] = 0.0            # all-zero block
+    w[1, :256] = 1e-3           # constant block
+    got = gpu_quant_weights(t, w, dev)
+    ref = oracle.quantize_weights(t, w)
+    assert np.array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- QMatMul::forward
+SMALL = [(48, 256), (100, 512), (257, 768), (1024, 1024)]
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17])
+def test_qmatmul_small(oracle, lbq, dev, t, m):
+    rng = np.random.default_rng(1000 * t + m)
+    for n, k in SMALL:
+        bs = oracle.block_size(t)
+        w_raw = bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+        assert_rows_close(gpu_qmatmul(t, w_raw, n, k, x, dev), ref)
+
+
+def test_qmatmul_q8_0_odd_block_count(oracle, lbq, dev):
+    rng = np.random.default_rng(51)
+    n, k = 129, 32 * 37  # 37 blocks per row: rows start 2 bytes into a dword
+    w_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-2)
+    for m in (1, 4, 12):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        assert_rows_close(gpu_qmatmul(Q8_0, w_raw, n, k, x, dev),
+                          oracle.qmatmul(Q8_0, w_raw, n, k, x, nthreads=8).astype(np.float64))
+
+
+def test_qmatmul_odd_superblock_count(oracle, lbq, dev):
+    rng = np.random.default_rng(52)
+    for t in (Q4_K, Q5_K, Q6_K):
+        n, k = 77, 256 * 5
+        w_raw = bp.random_blocks(rng, t, n * k // 256)
+        x = rng.standard_normal((3, k)).astype(np.float32)
+        assert_rows_close(gpu_qmatmul(t, w_raw, n, k, x, dev),
+                          oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64))
+
+
+def test_qmatmul_shapes_and_errors(oracle, lbq, dev):
+    from lightbulb_amd.quantized import QMatMul, QTensor, QuantizableLinear
+    rng = np.random.default_rng(53)
+    n, k = 64, 512
+    w_raw = bp.random_blocks(rng, Q4_K, n * k // 256)
+    qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), Q4_K, (n, k)))
+    lin = QuantizableLinear.from_qmatmul(qm)
+    assert lin.is_quantized()
+    x = rng.standard_normal((4, 1, k)).astype(np.float32)  # decode [B, 1, K]
+    y = lin.forward(to_dev(x, dev))
+    assert tuple(y.shape) == (4, 1, n)
+    ref = oracle.qmatmul(Q4_K, w_raw, n, k, x.reshape(4, k), nthreads=4)
+    assert_rows_close(y.cpu().numpy().reshape(4, n), ref.astype(np.float64))
+    with pytest.raises(ValueError, match="incompatible"):
+        qm.forward(torch.zeros(2, k + 256, device=dev))
+    with pytest.raises(ValueError, match="only one dimension"):
+        qm.forward(torch.zeros(k, device=dev))
+    with pytest.raises(ValueError, match="must be f32"):
+        qm.forward(torch.zeros(2, k, device=dev, dtype=torch.float16))
+    with pytest.raises(ValueError, match="not contiguous"):
+        qm.forward(torch.zeros(k, 2, device=dev).t())
+    assert qm.forward(torch.zeros(0, k, device=dev)).shape == (0, n)
+
+
+def test_c_abi_error_paths(lbq, dev):
+    from lightbulb_amd import _lib
+    from lightbulb_amd.quantized import context
+    ctx = context(dev)
+    h = ctypes.c_void_p()
+    buf = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
+    assert lbq.lbq_weight_wrap_device(ctx, 2, 4, 256, buf.data_ptr(), buf.numel(), ctypes.byref(h)) == -2
+    assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 255, buf.data_ptr(), buf.numel(), ctypes.byref(h)) == -3
+    assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 256, buf.data_ptr(), buf.numel() - 1, ctypes.byref(h)) == -3
+    assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 256, buf.data_ptr() + 4, 144 * 4, ctypes.byref(h)) == -1
+    assert b"16-byte" in lbq.lbq_last_error()
+    assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 256, buf.data_ptr(), buf.numel(), ctypes.byref(h)) == 0
+    assert lbq.lbq_qmatmul_f32(ctx, h, None, 1, None, None) == -1
+    assert lbq.lbq_qmatmul_f32(ctx, h, None, -1, None, None) == -1
+    assert lbq.lbq_qmatmul_f32(ctx, h, None, 0, None, None) == 0
+    assert lbq.lbq_weight_destroy(h) == 0
+    with pytest.raises(_lib.LbqError):
+        _lib.check(lbq.lbq_init(1 << 20, ctypes.byref(ctypes.c_void_p())))
