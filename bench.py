@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the GGUF quantized-linear hot path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): Q4_K batch-1 decode GEMV weight
+GB/s at Llama-3-8B layer shapes.  One step = QMatMul::forward (activation Q8_K
+quantisation + fused dequant/integer-dot GEMV) for the 7 projections of one
+Llama-3-8B layer (q, k, v, o 4096/1024 x 4096; gate, up 14336 x 4096;
+down 4096 x 14336), all Q4_K, x ~ N(0, 1) f32 [1, K].  Weights ~ N(0, 0.02)
+quantised on the device; 8 distinct layer copies (982 MB) rotate so the
+256 MB Infinity Cache cannot hold the working set.  Launches are replayed
+from HIP graphs so the host's issue rate does not limit the measurement.
+
+Also reported (extra keys): the dot kernel alone against the HBM roofline,
+per-shape kernel times, the 32-layer Q4_K_M stack in tokens/s at batch 1 and
+32, and the oracle (C restatement of the reference CPU QMatMul)
+on a bounded sample on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "Q4_K GEMV weight GB/s (% of HBM peak); 8B linear-stack tokens/s at batch 1"
+
+LAYER = [("q_proj", 4096, 4096), ("k_proj", 1024, 4096), ("v_proj", 1024, 4096), ("o_proj", 4096, 4096),
+         ("gate_proj", 14336, 4096), ("up_proj", 14336, 4096), ("down_proj", 4096, 14336)]
+VOCAB = 128256
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=800)
+    p.add_argument("--warmup", type=int, default=80)
+    p.add_argument("--copies", type=int, default=8, help="distinct weight copies rotated per step")
+    p.add_argument("--no-stack", action="store_true", help="skip the 32-layer stack measurement")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def make_weights(torch, qz, dtype, n, k, gen, dev):
+    w = torch.randn(n, k, generator=gen, device=dev, dtype=torch.float32).mul_(0.02)
+    qt = qz.QTensor.quantize(w, dtype)
+    del w
+    return qz.QMatMul.from_qtensor(qt)
+
+
+def timed_graph(torch, graph, reps, stream):
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e.record(stream)
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps  # ms per replay
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    fn()  # eager pass: sizes scratch and warms the allocator outside capture
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def cpu_baseline(layer_blocks, xs, budget_s):
+    """Oracle (C restatement of the reference CPU QMatMul) on one layer, all host cores."""
+    import numpy as np
+
+    import oracle
+    nthreads = oracle.nproc()
+    total_bytes = sum(b.size for b in layer_blocks)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        for (name, n, k), blk, x in zip(LAYER, layer_blocks, xs):
+            oracle.qmatmul(oracle.Q4_K, blk, n, k, x, nthreads=nthreads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 200:
+            break
+    per = el / reps
+    return {"value": round(total_bytes / per / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+            "sample": f"oracle qmatmul (Q8_K activation quant + integer vec_dot, rows split over {nthreads} "
+                      f"threads) on the 7 Q4_K projections of one layer at batch 1 ({total_bytes / 1e6:.1f} MB "
+                      f"of blocks), {reps} passes in {el:.1f} s; {per * 1e3:.2f} ms per layer",
+            "ms_per_step": round(per * 1e3, 3),
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from lightbulb_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from lightbulb_amd import build
+        build.build()
+    from lightbulb_amd import quantized as qz
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x1B1)
+    Q4K, Q6K = qz.GgmlDType.Q4K, qz.GgmlDType.Q6K
+
+    # ---------------------------------------------------------------- config 2 weights
+    t0 = time.perf_counter()
+    copies = [[make_weights(torch, qz, Q4K, n, k, gen, dev) for (_, n, k) in LAYER] for _ in range(args.copies)]
+    xs = [torch.randn(1, k, generator=gen, device=dev) for (_, n, k) in LAYER]
+    ys = [torch.empty(1, n, device=dev) for (_, n, k) in LAYER]
+    layer_bytes = sum(q.qtensor().storage_size_in_bytes() for q in copies[0])
+    io_bytes = sum(4 * (n + k) for (_, n, k) in LAYER)
+    log(f"weights ready: {args.copies} x {layer_bytes / 1e6:.1f} MB in {time.perf_counter() - t0:.1f} s")
+
+    def full_step_all_copies():
+        for layer in copies:
+            for qm, x in zip(layer, xs):
+                qm.forward(x)
+
+    # activation handles for the dot-only (roofline) graph
+    acts = {k: qz.QActivation(qz.GgmlDType.Q8K, 1, k, dev) for k in (4096, 14336)}
+    for (_, n, k), x in zip(LAYER, xs):
+        acts[k].quantize(x)
+
+    def dot_all_copies():
+        for layer in copies:
+            for qm, (_, n, k), y in zip(layer, LAYER, ys):
+                qm.forward_quantized(acts[k], y)
+
+    stream = torch.cuda.current_stream(dev)
+    g_full = capture(torch, full_step_all_copies)
+    g_dot = capture(torch, dot_all_copies)
+    reps = max(1, (args.steps + args.copies - 1) // args.copies)
+    wreps = max(1, (args.warmup + args.copies - 1) // args.copies)
+    steps = reps * args.copies
+    timed_graph(torch, g_full, wreps, stream)
+    ms_full = timed_graph(torch, g_full, reps, stream) / args.copies
+    timed_graph(torch, g_dot, wreps, stream)
+    ms_dot = timed_graph(torch, g_dot, reps, stream) / args.copies
+    value = layer_bytes / (ms_full * 1e-3) / 1e9
+    dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
+    log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
+        f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s")
+
+    # per-shape dot kernel times (same graphs, one shape at a time)
+    kernels = {}
+    for i, (name, n, k) in enumerate(LAYER):
+        if name in ("k_proj", "up_proj", "o_proj"):
+            continue  # same shape as v_proj / gate_proj / q_proj
+        def one_shape(i=i, k=k):
+            for layer in copies:
+                layer[i].forward_quantized(acts[k], ys[i])
+        g = capture(torch, one_shape)
+        timed_graph(torch, g, wreps, stream)
+        ms = timed_graph(torch, g, reps, stream) / args.copies
+        b = copies[0][i].qtensor().storage_size_in_bytes() + 4 * (n + k)
+        kernels[f"{name}_{n}x{k}"] = {"us": round(ms * 1e3, 3), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                      "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del g
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": wreps * args.copies,
+        "ms_per_step": round(ms_full, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q4_K batch-1 decode GEMV at Llama-3-8B layer shapes (configs[1]): one step = "
+                        "QMatMul::forward for q,k,v,o,gate,up,down of one layer, x f32 [1,K] ~ N(0,1), "
+                        f"weights N(0,0.02) -> Q4_K, {args.copies} layer copies rotated "
+                        f"({args.copies * layer_bytes / 1e6:.0f} MB working set), HIP-graph replay",
+            "weight_bytes_per_step": layer_bytes,
+            "arithmetic": "Q8_K activation codes x Q4_K codes in int8 sdot4, int32 sub-block sums, f32 combine",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dot_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dot_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "k_gemv<Q4_K> (the 7 dot launches of one step, average over launches)",
+            "us_per_step": round(ms_dot * 1e3, 3),
+        },
+        "kernels": kernels,
+    }
+    del g_full, g_dot
+
+    # ---------------------------------------------------------------- CPU baseline (bounded sample)
+    if not args.no_cpu:
+        try:
+            blocks = [q.qtensor().data.cpu().numpy() for q in copies[0]]
+            xh = [x.cpu().numpy() for x in xs]
+            result["cpu_baseline"] = cpu_baseline(blocks, xh, args.cpu_seconds)
+            log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s")
+        except Exception as e:  # the oracle is optional on a box without a compiler
+            result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": 0, "kind": "port",
+                                      "sample": f"unavailable: {e}"}
+    del copies, acts
+    torch.cuda.empty_cache()
+
+    # ---------------------------------------------------------------- config 5: 32-layer stack
+    if not args.no_stack:
+        result["stack"] = stack_bench(torch, qz, gen, dev, stream)
+
+    print(json.dumps(result), flush=True)
+
+
+def stack_bench(torch, qz, gen, dev, stream):
+    """Random-init Llama-3-8B linear stack, Q4_K_M mix: attn_v and even-layer ffn_down Q6_K,
+    the rest Q4_K, Q6_K output head; all 7 projections per layer plus the head per token."""
+    Q4K, Q6K = qz.GgmlDType.Q4K, qz.GgmlDType.Q6K
+    t0 = time.perf_counter()
+    layers = []
+    for li in range(32):
+        mats = []
+        for name, n, k in LAYER:
+            t = Q6K if name == "v_proj" or (name == "down_proj" and li % 2 == 0) else Q4K
+            mats.append(make_weights(torch, qz, t, n, k, gen, dev))
+        layers.append(mats)
+    head = make_weights(torch, qz, Q6K, VOCAB, 4096, gen, dev)
+    total = sum(q.qtensor().storage_size_in_bytes() for l in layers for q in l) + head.qtensor().storage_size_in_bytes()
+    log(f"stack ready: {total / 1e9:.3f} GB in {time.perf_counter() - t0:.1f} s")
+    out = {"weight_bytes": total}
+    for B in (1, 32):
+        xs = {k: torch.randn(B, k, generator=gen, device=dev) for k in (4096, 14336)}
+        ys = {n: torch.empty(B, n, device=dev) for n in (1024, 4096, 14336, VOCAB)}
+
+        def token_step():
+            for mats in layers:
+                for qm, (_, n, k) in zip(mats, LAYER):
+                    qm.forward(xs[k])
+            head.forward(xs[4096])
+
+        g = capture(torch, token_step)
+        timed_graph(torch, g, 2, stream)
+        reps = 20 if B == 1 else 5
+        ms = timed_graph(torch, g, reps, stream)
+        out[f"b{B}"] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
+                        "weight_GB/s": round(total / (ms * 1e-3) / 1e9, 1)}
+        log(f"stack B={B}: {ms:.3f} ms/step -> {B / (ms * 1e-3):.0f} tok/s")
+        del g, xs, ys
+    return out
+
+
+if __name__ == "__main__":
+    main()

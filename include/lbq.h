@@ -98,6 +98,21 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * sub-block dot products.  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
+/* Quantised-activation handle: the two halves of QMatMul::forward as separate
+ * calls.  candle's k_quants::matmul first quantises every row of x into
+ * vec-dot blocks and then runs vec_dot for all output columns; splitting the
+ * two lets call sites that feed one x to several weights -- q/k/v at
+ * /root/reference/src/model/custom_attention.rs:265-267, gate/up at
+ * mlp_wrapper.rs:190,193 -- quantise x once.  act_type is LBQ_TYPE_Q8_K for
+ * k-quant weights and LBQ_TYPE_Q8_0 for Q8_0 weights.  The handle owns device
+ * memory for m rows of k values. */
+typedef struct lbq_act lbq_act;
+int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act);
+int lbq_act_quantize(lbq_act *act, const float *d_x, void *stream);
+int lbq_act_destroy(lbq_act *act);
+/* y[m][n] from a quantised activation; act's k and vec-dot type must match w. */
+int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *act, float *d_y, void *stream);
+
 /* Dequantise the whole weight to f32 [n][k] -- QTensor::dequantize (used at
  * /root/reference/src/model/custom_transformer.rs:323,347 and
  * custom_transformer_block.rs:229,231).  Bit-exact with the reference. */

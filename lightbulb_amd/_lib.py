@@ -35,6 +35,10 @@ SIGNATURES = {
     "lbq_weight_destroy": (_c.c_int, [_VP]),
     "lbq_weight_info": (_c.c_int, [_VP, _c.POINTER(_U32), _c.POINTER(_I64), _c.POINTER(_I64)]),
     "lbq_qmatmul_f32": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
+    "lbq_act_create": (_c.c_int, [_VP, _U32, _I64, _I64, _c.POINTER(_VP)]),
+    "lbq_act_quantize": (_c.c_int, [_VP, _VP, _VP]),
+    "lbq_act_destroy": (_c.c_int, [_VP]),
+    "lbq_qmatmul_act_f32": (_c.c_int, [_VP, _VP, _VP, _VP, _VP]),
     "lbq_dequantize_f32": (_c.c_int, [_VP, _VP, _VP, _VP]),
     "lbq_dequantize_blocks_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
     "lbq_quantize_act": (_c.c_int, [_U32, _VP, _I64, _I64, _VP, _VP]),
@@ -60,6 +64,14 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build the HIP library first "
                 "(python -m lightbulb_amd.build, or __graft_entry__.build())")
+        # torch-ROCm bundles its own libamdhip64.so.7 / libhsa-runtime64.so.1.  If
+        # liblbq.so were loaded first, the system runtime would be mapped and torch
+        # would then map a second copy, and one of the two finds no device.  Loading
+        # torch first makes liblbq bind (by soname) to the one runtime in the process.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         handle = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)

@@ -31,7 +31,8 @@ HIP_FLAGS = [
 # Sources whose float arithmetic must be rounded op by op (bit-exact restatements).
 NO_CONTRACT = {"lbq_wquant.hip"}
 
-SOURCES = ["lbq_act.hip", "lbq_gemv.hip", "lbq_gemm.hip", "lbq_wquant.hip", "lbq_api.cpp"]
+SOURCES = ["lbq_act.hip", "lbq_gemv.hip", "lbq_gemv_q4k.hip", "lbq_gemv_q5k.hip", "lbq_gemv_q6k.hip",
+           "lbq_gemv_q8_0.hip", "lbq_gemm.hip", "lbq_wquant.hip", "lbq_api.cpp"]
 
 
 def _hipcc() -> str:

@@ -29,46 +29,11 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
     const int lane = threadIdx.x & 63;
     const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (blk >= nblocks) return;  // whole wave exits together
-    const float *src = x + blk * QK_K + lane * 4;
     float v[4];
-    if (VEC_IN) {
-        const float4 f = *reinterpret_cast<const float4 *>(src);
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-    } else {
-        for (int i = 0; i < 4; i++) v[i] = src[i];
-    }
-    float bk = -1.f, bv = 0.f;
-    int bi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = fabsf(v[i]);
-        const float key = (a == a) ? a : -1.f;
-        if (key > bk) { bk = key; bv = v[i]; bi = lane * 4 + i; }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ok = __shfl_xor(bk, off);
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ok > bk || (ok == bk && oi < bi)) { bk = ok; bv = ov; bi = oi; }
-    }
-    uint32_t packed = 0;
-    int s = 0;
-    float d = 0.f;
-    if (bk > 0.f) {
-        const float iscale = -128.f / bv;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float r = fminf(roundf(iscale * v[i]), 127.f);
-            r = fmaxf(r, -128.f);
-            const int q = (int)r;
-            s += q;
-            packed |= ((uint32_t)q & 0xffu) << (8 * i);
-        }
-        d = 1.f / iscale;
-    }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    load4f(x + blk * QK_K + lane * 4, VEC_IN, v);
+    int s;
+    float d;
+    const uint32_t packed = q8k_block_wave(v, lane, &s, &d);
     if (GGUF_OUT) {
         uint8_t *b = gguf + blk * 292;
         *reinterpret_cast<uint32_t *>(b + 4 + lane * 4) = packed;
@@ -83,9 +48,6 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
 
 // ---------------------------------------------------------------------------
 // Q8_0: 8 lanes per 32-value block, 8 blocks per wave.
-// candle: d = amax/127 (amax over |x|, NaN ignored by f32::max); id = 1/d or 0;
-// q = round(x*id) as i8 (saturating, NaN -> 0), using the unrounded d; the
-// stored scale is f16(d), so the value the dot product uses is f32(f16(d)).
 // ---------------------------------------------------------------------------
 template <bool GGUF_OUT, bool VEC_IN>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int64_t nblocks,
@@ -96,31 +58,9 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
     const int sub = threadIdx.x & 7;
     const bool ok = blk < nblocks;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (ok) {
-        const float *src = x + blk * QK8_0 + sub * 4;
-        if (VEC_IN) {
-            const float4 f = *reinterpret_cast<const float4 *>(src);
-            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        } else {
-            for (int i = 0; i < 4; i++) v[i] = src[i];
-        }
-    }
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    const float d = amax / 127.f;
-    const float id = d != 0.f ? 1.f / d : 0.f;
-    const __half dh = __float2half_rn(d);
-    uint32_t packed = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float r = roundf(v[i] * id);
-        int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.f), 127.f);
-        packed |= ((uint32_t)q & 0xffu) << (8 * i);
-    }
+    if (ok) load4f(x + blk * QK8_0 + sub * 4, VEC_IN, v);
+    __half dh;
+    const uint32_t packed = q8_0_block8(v, &dh);
     if (!ok) return;
     if (GGUF_OUT) {
         uint8_t *b = gguf + blk * 34;

@@ -34,6 +34,14 @@ struct lbq_weight {
     bool owned;
 };
 
+struct lbq_act {
+    lbq_ctx *ctx;
+    int act_type;
+    int64_t m, k;
+    uint8_t *buf;
+    lbq::ActView view;
+};
+
 namespace {
 
 thread_local std::string g_err;
@@ -105,6 +113,20 @@ int ensure_scratch(lbq_ctx *ctx, size_t bytes) {
     if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for activation scratch: %s", want, hipGetErrorString(e));
     ctx->scratch = static_cast<uint8_t *>(p);
     ctx->scratch_bytes = want;
+    return LBQ_OK;
+}
+
+lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
+    return lbq::ActView{reinterpret_cast<const int8_t *>(base + L.q_off), reinterpret_cast<const float *>(base + L.d_off),
+                        reinterpret_cast<const int16_t *>(base + L.bs_off), k, L.nb};
+}
+
+// The dot half of QMatMul::forward: decode GEMV for m <= 8, MFMA GEMM above.
+int run_dot(const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
+    hipError_t e;
+    if (m <= 8) e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
+    else e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, st);
+    if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
 }
 
@@ -253,19 +275,81 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const ActLayout L = act_layout(act_type, m, w->k);
+    if (m <= 8 && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
+        // decode: the GEMV quantises x in its own prologue -- one launch, no scratch
+        const lbq::ActView av{nullptr, nullptr, nullptr, w->k, L.nb};
+        hipError_t e = lbq::launch_gemv_x(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, d_x, (int)m, d_y, st);
+        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+        return LBQ_OK;
+    }
     std::lock_guard<std::mutex> lock(ctx->mu);
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
-    int8_t *xq = reinterpret_cast<int8_t *>(ctx->scratch + L.q_off);
-    float *xd = reinterpret_cast<float *>(ctx->scratch + L.d_off);
-    int16_t *xbs = reinterpret_cast<int16_t *>(ctx->scratch + L.bs_off);
-    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w->k, xq, xd, xbs, nullptr, st);
+    const lbq::ActView av = view_of(ctx->scratch, L, w->k);
+    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w->k, const_cast<int8_t *>(av.xq),
+                                         const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
-    lbq::ActView av{xq, xd, xbs, w->k, L.nb};
-    if (m <= 8) e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
-    else e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, st);
-    if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+    return run_dot(w, av, m, d_y, st);
+}
+
+int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act) {
+    if (!ctx || !out_act) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_act_create");
+    *out_act = nullptr;
+    if (act_type != LBQ_TYPE_Q8_K && act_type != LBQ_TYPE_Q8_0)
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15) or Q8_0 (8)", act_type);
+    const int bs = lbq_type_block_size(act_type);
+    if (m <= 0 || k <= 0 || k % bs) return fail(LBQ_ERR_SHAPE, "activation shape (%lld, %lld) invalid for %d-value blocks", (long long)m, (long long)k, bs);
+    if (m > (int64_t)1 << 24 || k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "activation shape exceeds the supported maximum");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    const ActLayout L = act_layout((int)act_type, m, k);
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, L.total);
+    if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for activations: %s", L.total, hipGetErrorString(e));
+    lbq_act *a = new (std::nothrow) lbq_act;
+    if (!a) {
+        (void)hipFree(p);
+        return fail(LBQ_ERR_OOM, "host allocation failed");
+    }
+    a->ctx = ctx;
+    a->act_type = (int)act_type;
+    a->m = m;
+    a->k = k;
+    a->buf = static_cast<uint8_t *>(p);
+    a->view = view_of(a->buf, L, k);
+    *out_act = a;
     return LBQ_OK;
+}
+
+int lbq_act_quantize(lbq_act *a, const float *d_x, void *stream) {
+    if (!a || !d_x) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_act_quantize");
+    if (reinterpret_cast<uintptr_t>(d_x) & 3u) return fail(LBQ_ERR_INVALID_ARG, "x must be a 4-byte aligned f32 buffer");
+    DeviceGuard g(a->ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = lbq::launch_quant_act(a->act_type, d_x, a->m, a->k, const_cast<int8_t *>(a->view.xq),
+                                         const_cast<float *>(a->view.xd), const_cast<int16_t *>(a->view.xbs),
+                                         nullptr, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    return LBQ_OK;
+}
+
+int lbq_act_destroy(lbq_act *a) {
+    if (!a) return LBQ_OK;
+    DeviceGuard g(a->ctx->device);
+    (void)hipFree(a->buf);
+    delete a;
+    return LBQ_OK;
+}
+
+int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *a, float *d_y, void *stream) {
+    if (!ctx || !w || !a || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_qmatmul_act_f32");
+    if (reinterpret_cast<uintptr_t>(d_y) & 3u) return fail(LBQ_ERR_INVALID_ARG, "y must be a 4-byte aligned f32 buffer");
+    const int want = w->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    if (a->act_type != want) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "weight type %d needs activation type %d, got %d", w->type, want, a->act_type);
+    if (a->k != w->k) return fail(LBQ_ERR_SHAPE, "activation k = %lld, weight k = %lld", (long long)a->k, (long long)w->k);
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    return run_dot(w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
 }
 
 int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream) {

@@ -45,14 +45,6 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { return *reinterpr
 
 __device__ __forceinline__ uint4 ld_u4(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-
-// Streaming (non-temporal) 16-byte load: weight bytes are read once per launch.
-__device__ __forceinline__ uint4 ld_u4_nt(const uint8_t *p) {
-    const u32x4v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 // 16 bytes starting at a 2-byte aligned address p.  Reads only aligned dwords that
 // hold at least one byte of [p, p+16), so it never touches a dword outside the
 // caller's buffer.
@@ -100,6 +92,85 @@ __device__ __forceinline__ void k4_scale_pair(uint32_t s0, uint32_t s1, uint32_t
     } else {
         *sc2 = (C & 0x0f0fu) | ((A >> 2) & 0x3030u);
         *m2 = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Activation quantisation, shared by the standalone kernels and the GEMV prologue.
+// ---------------------------------------------------------------------------
+
+// Q8_K (candle BlockQ8K::from_float) of one 256-value block by one 64-lane wave;
+// the lane holds values 4*lane .. 4*lane+3 in v.  The signed value of largest |x|
+// (first on ties, NaN never chosen) gives iscale = -128/max; q = min(127, round(iscale*x));
+// d = 1/iscale; amax == 0 gives d = 0 and all-zero codes.  Returns the 4 codes packed
+// little-endian; *sum4 gets the sum of 16 codes on every lane of each aligned lane quad.
+__device__ __forceinline__ uint32_t q8k_block_wave(const float v[4], int lane, int *sum16, float *d_out) {
+    float bk = -1.f, bv = 0.f;
+    int bi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = fabsf(v[i]);
+        const float key = (a == a) ? a : -1.f;
+        if (key > bk) { bk = key; bv = v[i]; bi = lane * 4 + i; }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ok = __shfl_xor(bk, off);
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ok > bk || (ok == bk && oi < bi)) { bk = ok; bv = ov; bi = oi; }
+    }
+    uint32_t packed = 0;
+    int s = 0;
+    float d = 0.f;
+    if (bk > 0.f) {
+        const float iscale = -128.f / bv;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float r = fminf(roundf(iscale * v[i]), 127.f);
+            r = fmaxf(r, -128.f);
+            const int q = (int)r;
+            s += q;
+            packed |= ((uint32_t)q & 0xffu) << (8 * i);
+        }
+        d = 1.f / iscale;
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    *sum16 = s;
+    *d_out = d;
+    return packed;
+}
+
+// Q8_0 (candle BlockQ8_0::from_float) of one 32-value block by 8 aligned lanes; sub =
+// lane % 8 holds values 4*sub .. 4*sub+3.  d = amax/127 (NaN ignored); q = round(x/d)
+// with the unrounded d, saturating, NaN -> 0.  *dh gets f16(d), the stored scale.
+__device__ __forceinline__ uint32_t q8_0_block8(const float v[4], __half *dh) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    *dh = __float2half_rn(d);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float r = roundf(v[i] * id);
+        const int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.f), 127.f);
+        packed |= ((uint32_t)q & 0xffu) << (8 * i);
+    }
+    return packed;
+}
+
+__device__ __forceinline__ void load4f(const float *p, bool vec, float v[4]) {
+    if (vec) {
+        const float4 f = *reinterpret_cast<const float4 *>(p);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else {
+        v[0] = p[0]; v[1] = p[1]; v[2] = p[2]; v[3] = p[3];
     }
 }
 

@@ -1,0 +1,475 @@
+// lbq_gemv_fast.hpp -- batch-1 decode GEMV.
+//
+// Same arithmetic as the general GEMV (exact int32 sub-block sums of Q8_K/Q8_0
+// codes x weight codes, f32 combine), organised for the m = 1 weight stream:
+//   - eight lanes share each weight block's header and read its 16-byte code
+//     pieces side by side, so a wave instruction reads whole 128-byte runs;
+//   - the quantised activation sits in LDS in a padded layout (odd multiples of
+//     16 bytes per block), so lanes reading different blocks hit different banks;
+//   - waves are persistent, each owning a contiguous range of row groups and
+//     double-buffering the weight loads of its next group;
+//   - with FUSED, the workgroup quantises x itself (Q8_K or Q8_0, bit-identical
+//     to the standalone kernels) into LDS first; the loads of the first row
+//     group are issued before the quantisation so their latency overlaps it;
+//   - row sums use DPP lane permutes and readlane, not LDS shuffles.
+#pragma once
+#include "lbq_device.hpp"
+#include "lbq_internal.hpp"
+
+namespace lbq {
+
+// ---------------------------------------------------------------------------
+// DPP helpers (gfx9 dpp_ctrl: quad_perm 0x00-0xFF, row_ror:n = 0x120+n)
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// every lane of each 16-lane row gets the row's max / min / sum
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max(v, dpp_u32<0x124>(v));  // row_ror:4
+    v = max(v, dpp_u32<0x128>(v));  // row_ror:8
+    return v;
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x124>(v));
+    v = min(v, dpp_u32<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ float row_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    return v;
+}
+__device__ __forceinline__ int quad_sum_i32(int v) {
+    v += (int)dpp_u32<0xB1>((uint32_t)v);
+    v += (int)dpp_u32<0x4E>((uint32_t)v);
+    return v;
+}
+__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+// Q8_K of one 256-value block by one wave (lane holds values 4*lane..4*lane+3).
+// Same selection and arithmetic as q8k_block_wave: the first value of largest |x|
+// (NaN never chosen) sets iscale = -128/max; q = min(127, round(iscale*x)); d = 1/iscale.
+__device__ __forceinline__ uint32_t q8k_block_wave_dpp(const float v[4], int lane, int *sum16, float *d_out) {
+    // |x| as ordered bits; NaN -> 0 (never selected, like candle's `amax < |x|`)
+    uint32_t a[4], am = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float f = fabsf(v[i]);
+        a[i] = (f == f) ? __float_as_uint(f) : 0u;
+        am = max(am, a[i]);
+    }
+    am = row_max_u32(am);
+    const uint32_t wmax = max(max(rl(am, 0), rl(am, 16)), max(rl(am, 32), rl(am, 48)));
+    uint32_t packed = 0;
+    int s = 0;
+    float d = 0.f;
+    if (wmax != 0u) {
+        // first index holding the maximum
+        uint32_t key = 0xffffffffu;
+#pragma unroll
+        for (int i = 3; i >= 0; i--)
+            if (a[i] == wmax) key = (uint32_t)(lane * 4 + i);
+        key = row_min_u32(key);
+        const uint32_t first = min(min(rl(key, 0), rl(key, 16)), min(rl(key, 32), rl(key, 48)));
+        const int src_lane = (int)(first >> 2), src_i = (int)(first & 3);
+        const float mine = src_i == 0 ? v[0] : src_i == 1 ? v[1] : src_i == 2 ? v[2] : v[3];
+        const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), src_lane));
+        const float iscale = -128.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float r = fminf(roundf(iscale * v[i]), 127.f);
+            r = fmaxf(r, -128.f);
+            const int q = (int)r;
+            s += q;
+            packed |= ((uint32_t)q & 0xffu) << (8 * i);
+        }
+        d = 1.f / iscale;
+    }
+    *sum16 = quad_sum_i32(s);
+    *d_out = d;
+    return packed;
+}
+
+// LDS layout of a quantised activation block.
+//   Q8_K: 304-byte blocks (19 x 16 B, odd, so lanes reading different blocks spread
+//         over all banks): codes [0,256), bsums int16[16] @256, d f32 @288.
+//   Q8_0: 48-byte blocks: codes [0,32), d f32 @32.
+constexpr int XS_K = 304;
+constexpr int XS_0 = 48;
+
+// ---------------------------------------------------------------------------
+// per-type register traits.  A piece is the unit a lane decodes (see the
+// general GEMV); XW is the number of activation dwords a lane keeps per block.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+struct Fast;
+
+__device__ __forceinline__ uint32_t pack_halves(uint32_t lo_word, uint32_t hi_word, int h) {
+    const uint32_t a = (lo_word >> (16 * h)) & 0xffffu, b = (hi_word >> (16 * h)) & 0xffffu;
+    return a | (b << 16);
+}
+
+template <int TYPE>
+struct FastK45 {  // Q4_K and Q5_K
+    static constexpr int PPB = 8, VALS = 256, XW = 10;
+    static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
+    struct Raw { uint4 hdr, qh, qs; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        Raw r;
+        r.hdr = ld_u4(blk);
+        if (TYPE == TYPE_Q5_K) r.qh = ld_u4(blk + 16 + 16 * (p & 1));
+        r.qs = ld_u4(blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 16 * p);
+        return r;
+    }
+    // activation registers for piece p of a block, from the LDS layout
+    __device__ static void xload_lds(const uint8_t *xb, int p, uint32_t *xr) {
+        const int c = p >> 1, h = p & 1;
+        const uint4 a = *reinterpret_cast<const uint4 *>(xb + 64 * c + 16 * h);
+        const uint4 b = *reinterpret_cast<const uint4 *>(xb + 64 * c + 32 + 16 * h);
+        const uint2 s = *reinterpret_cast<const uint2 *>(xb + 256 + 8 * c);
+        xr[0] = a.x; xr[1] = a.y; xr[2] = a.z; xr[3] = a.w;
+        xr[4] = b.x; xr[5] = b.y; xr[6] = b.z; xr[7] = b.w;
+        xr[8] = pack_halves(s.x, s.y, h);
+        xr[9] = *reinterpret_cast<const uint32_t *>(xb + 288);
+    }
+    // ... or from the split global layout (pre-quantised activations)
+    __device__ static void xload_glb(const ActView &a, int64_t blk, int p, uint32_t *xr) {
+        const int c = p >> 1, h = p & 1;
+        const int8_t *q = a.xq + blk * 256;
+        const uint4 u = *reinterpret_cast<const uint4 *>(q + 64 * c + 16 * h);
+        const uint4 v = *reinterpret_cast<const uint4 *>(q + 64 * c + 32 + 16 * h);
+        const uint2 s = *reinterpret_cast<const uint2 *>(a.xbs + blk * 16 + 4 * c);
+        xr[0] = u.x; xr[1] = u.y; xr[2] = u.z; xr[3] = u.w;
+        xr[4] = v.x; xr[5] = v.y; xr[6] = v.z; xr[7] = v.w;
+        xr[8] = pack_halves(s.x, s.y, h);
+        xr[9] = __float_as_uint(a.xd[blk]);
+    }
+    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+        const int c = p >> 1;
+        uint32_t sc2, m2;
+        k4_scale_pair(r.hdr.y, r.hdr.z, r.hdr.w, c, &sc2, &m2);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+        if (TYPE == TYPE_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = q[i] & 0x0f0f0f0fu;
+                hi[i] = (q[i] >> 4) & 0x0f0f0f0fu;
+            }
+        } else {
+            const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = (q[i] & 0x0f0f0f0fu) | (((qh[i] >> (2 * c)) & 0x01010101u) << 4);
+                hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            }
+        }
+        int s0 = dot4(lo[0], xr[0], 0);
+        s0 = dot4(lo[1], xr[1], s0);
+        s0 = dot4(lo[2], xr[2], s0);
+        s0 = dot4(lo[3], xr[3], s0);
+        int s1 = dot4(hi[0], xr[4], 0);
+        s1 = dot4(hi[1], xr[5], s1);
+        s1 = dot4(hi[2], xr[6], s1);
+        s1 = dot4(hi[3], xr[7], s1);
+        const int isum = __mul24((int)(sc2 & 0xffu), s0) + __mul24((int)(sc2 >> 8), s1);
+        const int msum = __mul24((int)(m2 & 0xffu), (int)(int16_t)(xr[8] & 0xffffu)) +
+                         __mul24((int)(m2 >> 8), (int)(int16_t)(xr[8] >> 16));
+        const float dx = __uint_as_float(xr[9]);
+        return (h2f(r.hdr.x & 0xffffu) * dx) * (float)isum - (h2f(r.hdr.x >> 16) * dx) * (float)msum;
+    }
+};
+template <> struct Fast<TYPE_Q4_K> : FastK45<TYPE_Q4_K> {};
+template <> struct Fast<TYPE_Q5_K> : FastK45<TYPE_Q5_K> {};
+
+// Q6_K piece p = (n, h) covers runs 128n+16h+32j (j < 4) with int8 scales 8n+h+2j.
+template <>
+struct Fast<TYPE_Q6_K> {
+    static constexpr int PPB = 4, VALS = 256, XW = 19, BYTES = 210;
+    struct Raw { uint32_t qa[4], qb[4], qh[4], s0, s1, dbits; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        const int n = p >> 1, h = p & 1;
+        Raw r;
+        ld16_a2(blk + 64 * n + 16 * h, r.qa);
+        ld16_a2(blk + 64 * n + 32 + 16 * h, r.qb);
+        ld16_a2(blk + 128 + 32 * n + 16 * h, r.qh);
+        r.s0 = ld4_a2(blk + 192 + 8 * n);
+        r.s1 = ld4_a2(blk + 196 + 8 * n);
+        r.dbits = ld2_a2(blk + 208);
+        return r;
+    }
+    // xr: 16 code dwords (run j at 4j), bsums packed (j=0,1) and (j=2,3), d
+    __device__ static void xload_lds(const uint8_t *xb, int p, uint32_t *xr) {
+        const int n = p >> 1, h = p & 1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(xb + 128 * n + 16 * h + 32 * j);
+            xr[4 * j] = a.x; xr[4 * j + 1] = a.y; xr[4 * j + 2] = a.z; xr[4 * j + 3] = a.w;
+        }
+        const uint4 s = *reinterpret_cast<const uint4 *>(xb + 256 + 16 * n);
+        xr[16] = pack_halves(s.x, s.y, h);
+        xr[17] = pack_halves(s.z, s.w, h);
+        xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
+    }
+    __device__ static void xload_glb(const ActView &a, int64_t blk, int p, uint32_t *xr) {
+        const int n = p >> 1, h = p & 1;
+        const int8_t *q = a.xq + blk * 256;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 u = *reinterpret_cast<const uint4 *>(q + 128 * n + 16 * h + 32 * j);
+            xr[4 * j] = u.x; xr[4 * j + 1] = u.y; xr[4 * j + 2] = u.z; xr[4 * j + 3] = u.w;
+        }
+        const uint4 s = *reinterpret_cast<const uint4 *>(a.xbs + blk * 16 + 8 * n);
+        xr[16] = pack_halves(s.x, s.y, h);
+        xr[17] = pack_halves(s.z, s.w, h);
+        xr[18] = __float_as_uint(a.xd[blk]);
+    }
+    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+        const int h = p & 1;
+        const int sh = 8 * h;
+        const int sc[4] = {(int)(int8_t)(r.s0 >> sh), (int)(int8_t)(r.s0 >> (sh + 16)), (int)(int8_t)(r.s1 >> sh),
+                           (int)(int8_t)(r.s1 >> (sh + 16))};
+        const int bs[4] = {(int)(int16_t)(xr[16] & 0xffffu), (int)(int16_t)(xr[16] >> 16),
+                           (int)(int16_t)(xr[17] & 0xffffu), (int)(int16_t)(xr[17] >> 16)};
+        int isum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t *qs = (j & 1) ? r.qb : r.qa;
+            const int shq = (j >> 1) * 4, shh = 2 * j;
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t v = ((qs[i] >> shq) & 0x0f0f0f0fu) | (((r.qh[i] >> shh) & 0x03030303u) << 4);
+                s = dot4(v, xr[4 * j + i], s);
+            }
+            isum += sc[j] * (s - 32 * bs[j]);
+        }
+        return (h2f(r.dbits) * __uint_as_float(xr[18])) * (float)isum;
+    }
+};
+
+// Q8_0: one 34-byte block (32 values) per piece.
+template <>
+struct Fast<TYPE_Q8_0> {
+    static constexpr int PPB = 1, VALS = 32, XW = 9, BYTES = 34;
+    struct Raw { uint32_t w[9]; uint32_t mis; };
+    __device__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
+        r.mis = (uint32_t)(ad & 3u);
+        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
+        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
+        const u32x4a4 a1 = *reinterpret_cast<const u32x4a4 *>(base + 16);
+        r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
+        r.w[4] = a1.x; r.w[5] = a1.y; r.w[6] = a1.z; r.w[7] = a1.w;
+        r.w[8] = *reinterpret_cast<const uint32_t *>(base + 32);
+        return r;
+    }
+    __device__ static void xload_lds(const uint8_t *xb, int, uint32_t *xr) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(xb);
+        const uint4 b = *reinterpret_cast<const uint4 *>(xb + 16);
+        xr[0] = a.x; xr[1] = a.y; xr[2] = a.z; xr[3] = a.w;
+        xr[4] = b.x; xr[5] = b.y; xr[6] = b.z; xr[7] = b.w;
+        xr[8] = *reinterpret_cast<const uint32_t *>(xb + 32);
+    }
+    __device__ static void xload_glb(const ActView &a, int64_t blk, int, uint32_t *xr) {
+        const int8_t *q = a.xq + blk * 32;
+        const uint4 u = *reinterpret_cast<const uint4 *>(q);
+        const uint4 v = *reinterpret_cast<const uint4 *>(q + 16);
+        xr[0] = u.x; xr[1] = u.y; xr[2] = u.z; xr[3] = u.w;
+        xr[4] = v.x; xr[5] = v.y; xr[6] = v.z; xr[7] = v.w;
+        xr[8] = __float_as_uint(a.xd[blk]);
+    }
+    __device__ static float dot(const Raw &r, int, const uint32_t *xr) {
+        const bool odd = r.mis != 0;
+        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xffffu));
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t q = odd ? r.w[i + 1] : __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+            s = dot4(q, xr[i], s);
+        }
+        return ((float)s * d) * __uint_as_float(xr[8]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Fused activation quantisation into LDS by the whole workgroup (m = 1).
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
+    if constexpr (TYPE != TYPE_Q8_0) {
+        // wave w quantises blocks w, w+4, ... (nbx <= 64: one pass); loads first
+        constexpr int MAXB = 16;
+        float v[MAXB][4];
+#pragma unroll
+        for (int j = 0; j < MAXB; j++) {
+            const int b = min(wave + 4 * j, nbx - 1);
+            load4f(x + (int64_t)b * QK_K + lane * 4, vec, v[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int jmax = (nbx - wave + 3) / 4;  // wave-uniform
+#pragma unroll
+        for (int j = 0; j < MAXB; j++) {
+            if (j < jmax) {
+                const int b = wave + 4 * j;
+                int s;
+                float d;
+                const uint32_t packed = q8k_block_wave_dpp(v[j], lane, &s, &d);
+                uint8_t *xb = sx + b * XS_K;
+                *reinterpret_cast<uint32_t *>(xb + lane * 4) = packed;
+                if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(xb + 256 + 2 * (lane >> 2)) = (int16_t)s;
+                if (lane == 0) *reinterpret_cast<float *>(xb + 288) = d;
+            }
+        }
+    } else {
+        // 8 lanes per 32-value block; thread t handles blocks t/8 + 32j (nbx <= 512: one pass)
+        constexpr int MAXJ = 16;
+        const int sub = threadIdx.x & 7, bt = threadIdx.x >> 3;
+        float v[MAXJ][4];
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++) {
+            const int b = min(bt + 32 * j, nbx - 1);
+            load4f(x + (int64_t)b * QK8_0 + sub * 4, vec, v[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < MAXJ; j++) {
+            if (32 * j < nbx) {  // uniform across the workgroup: shuffles stay convergent
+                __half dh;
+                const uint32_t packed = q8_0_block8(v[j], &dh);
+                const int b = min(bt + 32 * j, nbx - 1);  // clamped duplicates rewrite equal data
+                uint8_t *xb = sx + b * XS_0;
+                *reinterpret_cast<uint32_t *>(xb + sub * 4) = packed;
+                if (sub == 0) *reinterpret_cast<float *>(xb + 32) = __half2float(dh);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Pre-quantised activations (split global layout) -> the LDS layout.  Straight-line
+// code for nbx <= 64 (k <= 16384, the fast path's limit): every load is issued
+// before any store, with indices clamped into range instead of branches.
+template <int TYPE>
+__device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx) {
+    constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
+    constexpr int CPB = TYPE == TYPE_Q8_0 ? 2 : 16;  // 16-byte code chunks per block
+    constexpr int NC = TYPE == TYPE_Q8_0 ? 4 : 4;    // code chunks per thread (<= 1024 total)
+    const int t = (int)threadIdx.x;
+    const int ncode = nbx * CPB;
+    uint4 v[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) v[j] = *reinterpret_cast<const uint4 *>(a.xq + (int64_t)min(t + 256 * j, ncode - 1) * 16);
+    uint4 bsv = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (TYPE != TYPE_Q8_0) bsv = *reinterpret_cast<const uint4 *>(a.xbs + (int64_t)min(t, 2 * nbx - 1) * 8);
+    const float d = a.xd[min(t, nbx - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        const int i = min(t + 256 * j, ncode - 1);  // clamped duplicates rewrite equal data
+        *reinterpret_cast<uint4 *>(sx + (i / CPB) * XS + 16 * (i % CPB)) = v[j];
+    }
+    if constexpr (TYPE != TYPE_Q8_0) {
+        const int i = min(t, 2 * nbx - 1);
+        *reinterpret_cast<uint4 *>(sx + (i >> 1) * XS + 256 + 16 * (i & 1)) = bsv;
+    }
+    *reinterpret_cast<float *>(sx + min(t, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d;
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// The m = 1 kernel.  A row group is RPW rows; lane (r, li) decodes piece
+// li % PPB of blocks li / PPB + BPI*i (i < IT) of row r.  Requires nb <= BPI*IT.
+// ---------------------------------------------------------------------------
+template <int TYPE, int RPW, int IT, bool FUSED>
+__global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, int64_t n, int64_t row_bytes, int nb,
+                                               const float *__restrict__ x, ActView act, float *__restrict__ y) {
+    using F = Fast<TYPE>;
+    using Raw = typename F::Raw;
+    constexpr int LPR = 64 / RPW;
+    constexpr int BPI = LPR / F::PPB;
+    static_assert(BPI >= 1, "a row needs at least one whole block per sweep");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane / LPR, li = lane % LPR;
+    const int p = li % F::PPB, bs0 = li / F::PPB;
+    const int64_t ng = (n + RPW - 1) / RPW;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
+    const int64_t per = ng / nw, rem = ng % nw;
+    const int64_t g0 = gw * per + (gw < rem ? gw : rem), g1 = g0 + per + (gw < rem ? 1 : 0);
+
+    // loads are unconditional (row and block clamped into range); compute masks
+    auto load_group = [&](int64_t g, Raw *buf) {
+        const int64_t row = min(g * RPW + r, n - 1);
+        const uint8_t *wr = W + row * row_bytes;
+#pragma unroll
+        for (int i = 0; i < IT; i++) {
+            const int b = min(bs0 + BPI * i, nb - 1);
+            buf[i] = F::load(wr + (int64_t)b * F::BYTES, p);
+        }
+    };
+
+    Raw bufA[IT], bufB[IT];
+    load_group(g0 < g1 ? g0 : 0, bufA);
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the prologue
+
+    extern __shared__ __align__(16) uint8_t sx[];
+    constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
+    if constexpr (FUSED) quantise_x_lds<TYPE>(x, nb, sx);
+    else copy_x_lds<TYPE>(act, nb, sx);
+
+    auto compute_group = [&](int64_t g, const Raw *buf) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < IT; i++) {
+            const int b = bs0 + BPI * i;
+            uint32_t xr[F::XW];
+            F::xload_lds(sx + min(b, nb - 1) * XS, p, xr);
+            const float v = F::dot(buf[i], p, xr);
+            acc += b < nb ? v : 0.f;
+        }
+        acc = row_sum_f32(acc);
+        // row group q of this wave spans 16-lane rows LPR/16*q .. ; lane LPR*q writes it
+#pragma unroll
+        for (int q = 0; q < RPW; q++) {
+            float s;
+            if constexpr (LPR == 64) {
+                s = __int_as_float(rl(__float_as_uint(acc), 0)) + __int_as_float(rl(__float_as_uint(acc), 16)) +
+                    __int_as_float(rl(__float_as_uint(acc), 32)) + __int_as_float(rl(__float_as_uint(acc), 48));
+            } else if constexpr (LPR == 32) {
+                s = __int_as_float(rl(__float_as_uint(acc), 32 * q)) + __int_as_float(rl(__float_as_uint(acc), 32 * q + 16));
+            } else {
+                s = __int_as_float(rl(__float_as_uint(acc), 16 * q));
+            }
+            const int64_t rq = g * RPW + q;
+            if (lane == LPR * q && rq < n) y[rq] = s;
+        }
+    };
+
+    // rolling buffer: issue group g+1's loads, then compute group g
+    for (int64_t g = g0; g < g1; g++) {
+        const int64_t gn = g + 1 < g1 ? g + 1 : g;  // last pass reloads (cached) data: no branch
+        load_group(gn, bufB);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_group(g, bufA);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < IT; i++) bufA[i] = bufB[i];
+    }
+}
+
+}  // namespace lbq

@@ -1,0 +1,526 @@
+// lbq_gemv_impl.hpp -- decode GEMV (m <= 8) over GGUF blocks, fused dequant + integer dot.
+//
+// y[m][n] = sum_k W[n][k] * x[m][k] where x has been quantised to Q8_K (k-quant
+// weights) or Q8_0 (Q8_0 weights).  Each output is built the way the reference
+// CPU vec_dot builds it (candle-core 0.10.2 k_quants.rs, generic bodies of
+// vec_dot for Q8_0/Q4_K/Q5_K/Q6_K): exact int32 sums of code products per
+// sub-block, scaled by the integer sub-block scale, then combined in f32 with
+// d_w*d_x (and, for Q4_K/Q5_K, minus dmin_w*d_x*sum(m*bsum)).  Only the f32
+// summation order across blocks differs from the CPU.
+//
+// Work decomposition (64-lane waves, 256-thread workgroups):
+//   - a "piece" is the unit one lane decodes per step: 16 bytes of 4-bit codes
+//     (Q4_K/Q5_K: 32 values in two runs of 16), 32 bytes of Q6_K low bits plus
+//     16 of high bits (64 values), or one Q8_0 block (32 values);
+//   - a wave works on RPW weight rows at a time; LPR = 64/RPW lanes walk each
+//     row's pieces in order, so consecutive lanes read consecutive bytes of a
+//     row (coalesced); each row is reduced inside one wave (no atomics, so the
+//     result is deterministic).
+#pragma once
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "lbq_device.hpp"
+#include "lbq_gemv_fast.hpp"
+#include "lbq_internal.hpp"
+
+namespace lbq {
+
+template <int TYPE>
+struct Dec;
+
+// ---- Q4_K: piece p (0..7) = qs[16p .. 16p+16): c = p/2 (64-value chunk), h = p%2.
+// low nibbles -> values 64c+16h+[0,16) (sub-block 2c), high -> 64c+32+16h+[0,16) (2c+1).
+template <>
+struct Dec<TYPE_Q4_K> {
+    static constexpr int BYTES = 144, PPB = 8, VALS = 256;
+    struct Raw { uint4 hdr, qs; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        Raw r;
+        r.hdr = ld_u4(blk);
+        r.qs = ld_u4(blk + 16 + 16 * p);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int p, const ActView &a, int mrows, float *acc) {
+        const int c = p >> 1, h = p & 1;
+        uint32_t sc2, m2;
+        k4_scale_pair(r.hdr.y, r.hdr.z, r.hdr.w, c, &sc2, &m2);
+        const int sc0 = (int)(sc2 & 0xffu), sc1 = (int)(sc2 >> 8), mn0 = (int)(m2 & 0xffu), mn1 = (int)(m2 >> 8);
+        const float d = h2f(r.hdr.x & 0xffffu), dmin = h2f(r.hdr.x >> 16);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = q[i] & 0x0f0f0f0fu;
+            hi[i] = (q[i] >> 4) & 0x0f0f0f0fu;
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK_K + 64 * c + 16 * h;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
+                int s0 = dot4(lo[0], x0.x, 0);
+                s0 = dot4(lo[1], x0.y, s0);
+                s0 = dot4(lo[2], x0.z, s0);
+                s0 = dot4(lo[3], x0.w, s0);
+                int s1 = dot4(hi[0], x1.x, 0);
+                s1 = dot4(hi[1], x1.y, s1);
+                s1 = dot4(hi[2], x1.z, s1);
+                s1 = dot4(hi[3], x1.w, s1);
+                const int64_t sb = (int64_t)m * a.nb + b;
+                const uint2 bs = *reinterpret_cast<const uint2 *>(a.xbs + sb * 16 + 4 * c);
+                const int b0 = (int)(int16_t)(bs.x >> (16 * h)), b1 = (int)(int16_t)(bs.y >> (16 * h));
+                const int isum = sc0 * s0 + sc1 * s1;
+                const int msum = mn0 * b0 + mn1 * b1;
+                const float dx = a.xd[sb];
+                acc[m] += (d * dx) * (float)isum - (dmin * dx) * (float)msum;
+            }
+        }
+    }
+};
+
+// ---- Q5_K: as Q4_K with the fifth bit from qh[16h .. 16h+16): bit 2c for the low
+// run, bit 2c+1 for the high run.
+template <>
+struct Dec<TYPE_Q5_K> {
+    static constexpr int BYTES = 176, PPB = 8, VALS = 256;
+    struct Raw { uint4 hdr, qh, qs; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        Raw r;
+        r.hdr = ld_u4(blk);
+        r.qh = ld_u4(blk + 16 + 16 * (p & 1));
+        r.qs = ld_u4(blk + 48 + 16 * p);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int p, const ActView &a, int mrows, float *acc) {
+        const int c = p >> 1, h = p & 1;
+        uint32_t sc2, m2;
+        k4_scale_pair(r.hdr.y, r.hdr.z, r.hdr.w, c, &sc2, &m2);
+        const int sc0 = (int)(sc2 & 0xffu), sc1 = (int)(sc2 >> 8), mn0 = (int)(m2 & 0xffu), mn1 = (int)(m2 >> 8);
+        const float d = h2f(r.hdr.x & 0xffffu), dmin = h2f(r.hdr.x >> 16);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = (q[i] & 0x0f0f0f0fu) | (((qh[i] >> (2 * c)) & 0x01010101u) << 4);
+            hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK_K + 64 * c + 16 * h;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 32);
+                int s0 = dot4(lo[0], x0.x, 0);
+                s0 = dot4(lo[1], x0.y, s0);
+                s0 = dot4(lo[2], x0.z, s0);
+                s0 = dot4(lo[3], x0.w, s0);
+                int s1 = dot4(hi[0], x1.x, 0);
+                s1 = dot4(hi[1], x1.y, s1);
+                s1 = dot4(hi[2], x1.z, s1);
+                s1 = dot4(hi[3], x1.w, s1);
+                const int64_t sb = (int64_t)m * a.nb + b;
+                const uint2 bs = *reinterpret_cast<const uint2 *>(a.xbs + sb * 16 + 4 * c);
+                const int b0 = (int)(int16_t)(bs.x >> (16 * h)), b1 = (int)(int16_t)(bs.y >> (16 * h));
+                const int isum = sc0 * s0 + sc1 * s1;
+                const int msum = mn0 * b0 + mn1 * b1;
+                const float dx = a.xd[sb];
+                acc[m] += (d * dx) * (float)isum - (dmin * dx) * (float)msum;
+            }
+        }
+    }
+};
+
+// ---- Q6_K: piece p (0..3): n = p/2 (128-value half), h = p%2.  It covers
+// ql[64n+16h..+16] (qa), ql[64n+32+16h..+16] (qb) and qh[32n+16h..+16]; its four
+// runs of 16 values start at 128n+16h+32j (j = 0..3) with int8 scale 8n+h+2j:
+//   j=0: qa low | qh bits 0-1;  j=1: qb low | qh bits 2-3;
+//   j=2: qa high | qh bits 4-5; j=3: qb high | qh bits 6-7.
+// Codes v in [0,63] go through sdot4 unshifted; q = v-32 is restored with the
+// Q8_K block sums: sum (v-32)*x = sum v*x - 32*bsum.
+template <>
+struct Dec<TYPE_Q6_K> {
+    static constexpr int BYTES = 210, PPB = 4, VALS = 256;
+    struct Raw { uint32_t qa[4], qb[4], qh[4], s0, s1, dbits; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        const int n = p >> 1, h = p & 1;
+        Raw r;
+        ld16_a2(blk + 64 * n + 16 * h, r.qa);
+        ld16_a2(blk + 64 * n + 32 + 16 * h, r.qb);
+        ld16_a2(blk + 128 + 32 * n + 16 * h, r.qh);
+        r.s0 = ld4_a2(blk + 192 + 8 * n);
+        r.s1 = ld4_a2(blk + 196 + 8 * n);
+        r.dbits = ld2_a2(blk + 208);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int p, const ActView &a, int mrows, float *acc) {
+        const int n = p >> 1, h = p & 1;
+        const float d = h2f(r.dbits);
+        const int sh = 8 * h;
+        const int sc[4] = {(int)(int8_t)(r.s0 >> sh), (int)(int8_t)(r.s0 >> (sh + 16)), (int)(int8_t)(r.s1 >> sh),
+                           (int)(int8_t)(r.s1 >> (sh + 16))};
+        uint32_t v[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[0][i] = (r.qa[i] & 0x0f0f0f0fu) | ((r.qh[i] & 0x03030303u) << 4);
+            v[1][i] = (r.qb[i] & 0x0f0f0f0fu) | (((r.qh[i] >> 2) & 0x03030303u) << 4);
+            v[2][i] = ((r.qa[i] >> 4) & 0x0f0f0f0fu) | (((r.qh[i] >> 4) & 0x03030303u) << 4);
+            v[3][i] = ((r.qb[i] >> 4) & 0x0f0f0f0fu) | (((r.qh[i] >> 6) & 0x03030303u) << 4);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK_K + 128 * n + 16 * h;
+                const int64_t sb = (int64_t)m * a.nb + b;
+                const uint4 bs = *reinterpret_cast<const uint4 *>(a.xbs + sb * 16 + 8 * n);
+                const uint32_t bsw[4] = {bs.x, bs.y, bs.z, bs.w};
+                int isum = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + 32 * j);
+                    int s = dot4(v[j][0], xv.x, 0);
+                    s = dot4(v[j][1], xv.y, s);
+                    s = dot4(v[j][2], xv.z, s);
+                    s = dot4(v[j][3], xv.w, s);
+                    const int bsum = (int)(int16_t)(bsw[j] >> (16 * h));
+                    isum += sc[j] * (s - 32 * bsum);
+                }
+                acc[m] += (d * a.xd[sb]) * (float)isum;
+            }
+        }
+    }
+};
+
+// ---- Q8_0: piece = one 34-byte block (2-byte aligned): 9 aligned dwords cover it.
+template <>
+struct Dec<TYPE_Q8_0> {
+    static constexpr int BYTES = 34, PPB = 1, VALS = 32;
+    struct Raw { uint32_t w[9]; uint32_t mis; };
+    __device__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
+        r.mis = (uint32_t)(ad & 3u);
+        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
+        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
+        const u32x4a4 a1 = *reinterpret_cast<const u32x4a4 *>(base + 16);
+        r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
+        r.w[4] = a1.x; r.w[5] = a1.y; r.w[6] = a1.z; r.w[7] = a1.w;
+        r.w[8] = *reinterpret_cast<const uint32_t *>(base + 32);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int, const ActView &a, int mrows, float *acc) {
+        const bool odd = r.mis != 0;  // block starts 2 bytes into a dword
+        const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xffffu));
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = odd ? r.w[i + 1] : __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK8_0;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 16);
+                int s = dot4(q[0], x0.x, 0);
+                s = dot4(q[1], x0.y, s);
+                s = dot4(q[2], x0.z, s);
+                s = dot4(q[3], x0.w, s);
+                s = dot4(q[4], x1.x, s);
+                s = dot4(q[5], x1.y, s);
+                s = dot4(q[6], x1.z, s);
+                s = dot4(q[7], x1.w, s);
+                acc[m] += ((float)s * d) * a.xd[(int64_t)m * a.nb + b];
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Persistent GEMV.  The rows are cut into groups of RPW rows; each wave owns a
+// contiguous range of groups and walks each group's rows in chunks of
+// CH = (64/RPW)*IT pieces, double-buffering the weight loads of the next chunk
+// while it computes the current one.  With FUSED the workgroup first quantises
+// x itself (the same code as the standalone Q8_K/Q8_0 kernels) into LDS, after
+// issuing the loads of its first chunk so that the quantisation overlaps their
+// latency; the dot products then read x from LDS.
+// ---------------------------------------------------------------------------
+struct PGeom {
+    int64_t n_rows, row_bytes;
+    int nb;                  // weight blocks per row
+    int pieces;              // pieces per row
+    int cpg;                 // chunks per group
+    int64_t ngroups;
+};
+
+template <int TYPE, int M, int RPW, int IT, bool FUSED>
+__global__ __launch_bounds__(256) void k_gemv_p(const uint8_t *__restrict__ W, PGeom g, ActView act,
+                                                const float *__restrict__ x, int mrows, float *__restrict__ y) {
+    using D = Dec<TYPE>;
+    using Raw = typename D::Raw;
+    constexpr int LPR = 64 / RPW;
+    constexpr int CH = LPR * IT;
+    constexpr bool KQ = TYPE != TYPE_Q8_0;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane / LPR, li = lane % LPR;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
+    const int64_t per = g.ngroups / nw, rem = g.ngroups % nw;
+    const int64_t g0 = gw * per + (gw < rem ? gw : rem);
+    const int64_t u0 = g0 * g.cpg, u1 = (g0 + per + (gw < rem ? 1 : 0)) * g.cpg;
+
+    auto load_unit = [&](int64_t u, Raw *raw) {
+        const int64_t grp = u / g.cpg;
+        const int c = (int)(u - grp * g.cpg);
+        const int64_t row = grp * RPW + r;
+        const uint8_t *wrow = W + (row < g.n_rows ? row : 0) * g.row_bytes;
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int q = c * CH + it * LPR + li;
+            if (row < g.n_rows && q < g.pieces) raw[it] = D::load(wrow + (int64_t)(q / D::PPB) * D::BYTES, q % D::PPB);
+        }
+    };
+
+    Raw bufA[IT], bufB[IT];
+    if (u0 < u1) load_unit(u0, bufA);
+
+    ActView a = act;
+    if constexpr (FUSED) {
+        extern __shared__ __align__(16) uint8_t smem[];
+        const int64_t k = act.k;
+        int8_t *sxq = reinterpret_cast<int8_t *>(smem);
+        float *sxd = reinterpret_cast<float *>(smem + ((mrows * k + 15) & ~(int64_t)15));
+        int16_t *sxbs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(sxd) + ((mrows * act.nb * 4 + 15) & ~15));
+        const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+        if constexpr (KQ) {
+            const int nblk = mrows * act.nb;
+            for (int b = wave; b < nblk; b += 4) {
+                float v[4];
+                load4f(x + (int64_t)b * QK_K + lane * 4, vec, v);
+                int s;
+                float d;
+                const uint32_t packed = q8k_block_wave(v, lane, &s, &d);
+                *reinterpret_cast<uint32_t *>(sxq + (int64_t)b * QK_K + lane * 4) = packed;
+                if ((lane & 3) == 0) sxbs[b * 16 + (lane >> 2)] = (int16_t)s;
+                if (lane == 0) sxd[b] = d;
+            }
+        } else {
+            const int nblk = mrows * act.nb;
+            for (int b0 = 0; b0 < nblk; b0 += 32) {
+                const int b = b0 + (threadIdx.x >> 3), sub = threadIdx.x & 7;
+                float v[4] = {0.f, 0.f, 0.f, 0.f};
+                if (b < nblk) load4f(x + (int64_t)b * QK8_0 + sub * 4, vec, v);
+                __half dh;
+                const uint32_t packed = q8_0_block8(v, &dh);
+                if (b < nblk) {
+                    *reinterpret_cast<uint32_t *>(sxq + (int64_t)b * QK8_0 + sub * 4) = packed;
+                    if (sub == 0) sxd[b] = __half2float(dh);
+                }
+            }
+        }
+        __syncthreads();
+        a.xq = sxq;
+        a.xd = sxd;
+        a.xbs = sxbs;
+    }
+
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.f;
+
+    auto compute_unit = [&](int64_t u, const Raw *raw) {
+        const int64_t grp = u / g.cpg;
+        const int c = (int)(u - grp * g.cpg);
+        const int64_t row = grp * RPW + r;
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int q = c * CH + it * LPR + li;
+            if (row < g.n_rows && q < g.pieces) D::template dot<M>(raw[it], q / D::PPB, q % D::PPB, a, mrows, acc);
+        }
+        if (c == g.cpg - 1) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+#pragma unroll
+                for (int off = LPR / 2; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off);
+            }
+            if (li == 0 && row < g.n_rows) {
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    if (m < mrows) y[(int64_t)m * g.n_rows + row] = acc[m];
+            }
+#pragma unroll
+            for (int m = 0; m < M; m++) acc[m] = 0.f;
+        }
+    };
+
+    for (int64_t u = u0; u < u1; u += 2) {
+        if (u + 1 < u1) load_unit(u + 1, bufB);
+        compute_unit(u, bufA);
+        if (u + 1 < u1) {
+            if (u + 2 < u1) load_unit(u + 2, bufA);
+            compute_unit(u + 1, bufB);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch
+// ---------------------------------------------------------------------------
+struct GemvCfg {
+    int rpw, it, wpc;  // rows per wave, pieces per lane per chunk, target waves per CU
+    bool fused;
+};
+
+static int env_int(const char *s, int def) { return s ? atoi(s) : def; }
+
+// LBQ_GEMV="rpw,it,wpc,fused" overrides the choice (tuning; any value is correct).
+static GemvCfg pick_cfg(int type, int64_t n, int pieces, int m, int64_t k) {
+    GemvCfg c;
+    c.fused = (int64_t)m * k <= 32768;
+    const int ppb = type == TYPE_Q6_K ? 4 : type == TYPE_Q8_0 ? 1 : 8;
+    (void)ppb;
+    // rows per wave: enough lanes per row to cover a row in a few chunks
+    // must name a pair that run_m compiles for every m
+    if (pieces >= 384) { c.rpw = 1; c.it = 7; }
+    else if (pieces >= 128) { c.rpw = 2; c.it = 4; }
+    else { c.rpw = 4; c.it = 4; }
+    c.wpc = 8;
+    if (const char *e = getenv("LBQ_GEMV")) {
+        int v[4] = {c.rpw, c.it, c.wpc, c.fused ? 1 : 0};
+        sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]);
+        c.rpw = v[0]; c.it = v[1]; c.wpc = v[2]; c.fused = v[3] != 0 && (int64_t)m * k <= 65536;
+    }
+    (void)n;
+    return c;
+}
+
+static int num_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+template <int TYPE, int M, int RPW, int IT, bool FUSED>
+static hipError_t run_p(const uint8_t *w, const PGeom &g0, const ActView &act, const float *x, int m, float *y,
+                        int wpc, hipStream_t st) {
+    PGeom g = g0;
+    constexpr int CH = (64 / RPW) * IT;
+    g.cpg = (g.pieces + CH - 1) / CH;
+    g.ngroups = (g.n_rows + RPW - 1) / RPW;
+    int64_t waves = (int64_t)num_cus() * wpc;
+    if (waves > g.ngroups) waves = g.ngroups;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    size_t lds = 0;
+    if (FUSED) {
+        lds = ((size_t)m * act.k + 15) / 16 * 16 + ((size_t)m * act.nb * 4 + 15) / 16 * 16;
+        if (TYPE != TYPE_Q8_0) lds += (size_t)m * (act.k / 16) * 2;
+    }
+    k_gemv_p<TYPE, M, RPW, IT, FUSED><<<grid, 256, lds, st>>>(w, g, act, x, m, y);
+    return hipGetLastError();
+}
+
+// (rpw, it) pairs compiled: the ones pick_cfg returns.
+template <int TYPE, int M>
+static hipError_t run_m(const GemvCfg &c, const uint8_t *w, const PGeom &g, const ActView &act, const float *x, int m,
+                        float *y, hipStream_t st) {
+#define LBQ_CASE(R, I)                                                                               \
+    if (c.rpw == R && c.it == I) return run_p<TYPE, M, R, I, false>(w, g, act, x, m, y, c.wpc, st);
+    LBQ_CASE(1, 7)
+    LBQ_CASE(2, 4)
+    LBQ_CASE(4, 4)
+#undef LBQ_CASE
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// m = 1: the register-activation kernel (lbq_gemv_fast.hpp)
+// ---------------------------------------------------------------------------
+template <int TYPE>
+static bool fast_shape(int nb, int *rpw, int *it) {
+    constexpr int PPB = Fast<TYPE>::PPB;
+    if (PPB == 8) {  // Q4_K, Q5_K
+        if (nb <= 4) { *rpw = 2; *it = 1; return true; }
+        if (nb <= 8) { *rpw = 2; *it = 2; return true; }
+        if (nb <= 16) { *rpw = 2; *it = 4; return true; }
+        if (nb <= 32) { *rpw = 1; *it = 4; return true; }
+        if (nb <= 56) { *rpw = 1; *it = 7; return true; }
+        if (nb <= 64) { *rpw = 1; *it = 8; return true; }
+    } else if (PPB == 4) {  // Q6_K
+        if (nb <= 8) { *rpw = 2; *it = 1; return true; }
+        if (nb <= 16) { *rpw = 2; *it = 2; return true; }
+        if (nb <= 32) { *rpw = 1; *it = 2; return true; }
+        if (nb <= 64) { *rpw = 1; *it = 4; return true; }
+    } else {  // Q8_0: nb counts 32-value blocks
+        if (nb <= 64) { *rpw = 1; *it = 1; return true; }
+        if (nb <= 128) { *rpw = 1; *it = 2; return true; }
+        if (nb <= 256) { *rpw = 1; *it = 4; return true; }
+        if (nb <= 448) { *rpw = 1; *it = 7; return true; }
+        if (nb <= 512) { *rpw = 1; *it = 8; return true; }
+    }
+    return false;
+}
+
+template <int TYPE, int RPW, int IT>
+static hipError_t launch_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int nb, const float *x,
+                              const ActView &act, float *y, hipStream_t st) {
+    const int64_t ng = (n + RPW - 1) / RPW;
+    int wpc = 8;
+    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : 8;
+    int64_t waves = (int64_t)num_cus() * wpc;
+    if (waves > ng) waves = ng;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    const size_t lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
+    if (x) k_gemv1<TYPE, RPW, IT, true><<<grid, 256, lds, st>>>(w, n, row_bytes, nb, x, act, y);
+    else k_gemv1<TYPE, RPW, IT, false><<<grid, 256, lds, st>>>(w, n, row_bytes, nb, x, act, y);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t run_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int nb, const float *x, const ActView &act,
+                           float *y, hipStream_t st) {
+    int rpw, it;
+    if (!fast_shape<TYPE>(nb, &rpw, &it)) return hipErrorNotSupported;
+#define LBQ_FAST(R, I) \
+    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(w, n, row_bytes, nb, x, act, y, st);
+    if constexpr (Fast<TYPE>::PPB == 8) {
+        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
+    } else if constexpr (Fast<TYPE>::PPB == 4) {
+        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(1, 2) LBQ_FAST(1, 4)
+    } else {
+        LBQ_FAST(1, 1) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
+    }
+#undef LBQ_FAST
+    return hipErrorNotSupported;
+}
+
+template <int TYPE>
+static hipError_t run_type(const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                           const float *x, int m, float *y, hipStream_t st) {
+    using D = Dec<TYPE>;
+    PGeom g{};
+    g.n_rows = n;
+    g.row_bytes = row_bytes;
+    g.nb = (int)(k / D::VALS);
+    g.pieces = g.nb * D::PPB;
+    if (m == 1) {
+        const hipError_t e = run_fast<TYPE>(w, n, row_bytes, g.nb, x, act, y, st);
+        if (e != hipErrorNotSupported) return e;
+    }
+    GemvCfg c = pick_cfg(TYPE, n, g.pieces, m, k);
+    c.fused = false;  // m > 1: x arrives quantised (separate kernel)
+    if (x) return hipErrorInvalidValue;
+    if (m <= 1) return run_m<TYPE, 1>(c, w, g, act, x, m, y, st);
+    if (m <= 2) return run_m<TYPE, 2>(c, w, g, act, x, m, y, st);
+    if (m <= 4) return run_m<TYPE, 4>(c, w, g, act, x, m, y, st);
+    return run_m<TYPE, 8>(c, w, g, act, x, m, y, st);
+}
+
+}  // namespace lbq

@@ -23,6 +23,15 @@ hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float 
 hipError_t launch_gemv(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                        int m, float *y, hipStream_t st);
 
+// True when the decode GEMV quantises x itself (m = 1, k within the fast path,
+// x 16-byte aligned).
+bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x);
+
+// Decode GEMV that quantises raw f32 x [m][k] in its prologue (act supplies k and
+// the scale-block count only).  x == nullptr means act holds quantised codes.
+hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                         const float *x, int m, float *y, hipStream_t st);
+
 // Batched path (m > 8): dequantise weight tiles into LDS and run them through MFMA.
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                        int64_t m, float *y, hipStream_t st);

@@ -212,6 +212,19 @@ class QMatMul:
 
     __call__ = forward
 
+    def forward_quantized(self, act: "QActivation", out: torch.Tensor | None = None) -> torch.Tensor:
+        """The dot half of ``forward`` on an activation quantised once by ``QActivation``."""
+        n, k = self._qt.shape()
+        if act.k != k:
+            raise ValueError(f"activation k = {act.k} incompatible with {(n, k)}")
+        if out is None:
+            out = torch.empty(act.m, n, dtype=torch.float32, device=self._qt.data.device)
+        elif out.dtype != torch.float32 or not out.is_contiguous() or out.numel() != act.m * n:
+            raise ValueError("out must be a contiguous f32 tensor of m*n values")
+        _lib.check(_lib.lib().lbq_qmatmul_act_f32(self._ctx, self._handle, act._handle, out.data_ptr(),
+                                                  _stream(out.device)))
+        return out
+
     def __del__(self):
         h = getattr(self, "_handle", None)
         if h:
@@ -223,6 +236,40 @@ class QMatMul:
 
     def __repr__(self) -> str:
         return f"QMatMul({self._qt!r})"
+
+
+class QActivation:
+    """x [m, k] quantised once (Q8_K for k-quant weights, Q8_0 for Q8_0 weights),
+    reusable by every QMatMul that reads the same x -- q/k/v and gate/up."""
+
+    def __init__(self, act_type: GgmlDType, m: int, k: int, device="cuda"):
+        self.act_type = GgmlDType(act_type)
+        self.m, self.k = int(m), int(k)
+        self.device = torch.device(device)
+        h = ctypes.c_void_p()
+        _lib.check(_lib.lib().lbq_act_create(context(self.device), int(self.act_type), self.m, self.k,
+                                             ctypes.byref(h)))
+        self._handle = h.value
+
+    @classmethod
+    def for_weight(cls, qmatmul: "QMatMul", m: int) -> "QActivation":
+        t = GgmlDType.Q8_0 if qmatmul.qtensor().dtype() == GgmlDType.Q8_0 else GgmlDType.Q8K
+        return cls(t, m, qmatmul.qtensor().shape()[1], qmatmul.qtensor().data.device)
+
+    def quantize(self, x: torch.Tensor) -> "QActivation":
+        if x.dtype != torch.float32 or not x.is_contiguous() or x.numel() != self.m * self.k:
+            raise ValueError(f"x must be a contiguous f32 tensor of {self.m}x{self.k} values")
+        _lib.check(_lib.lib().lbq_act_quantize(self._handle, x.data_ptr(), _stream(x.device)))
+        return self
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h:
+            try:
+                _lib.lib().lbq_act_destroy(h)
+            except Exception:
+                pass
+            self._handle = None
 
 
 # ---------------------------------------------------------------------------
