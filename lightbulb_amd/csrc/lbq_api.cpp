@@ -22,6 +22,8 @@ struct lbq_ctx {
     std::mutex mu;        // guards scratch growth
     uint8_t *scratch;     // quantised activations (split layout)
     size_t scratch_bytes;
+    uint8_t *ws;          // batched GEMM workspace (fp16 activations, split-k partials)
+    size_t ws_bytes;
 };
 
 struct lbq_weight {
@@ -41,6 +43,19 @@ struct lbq_act {
     uint8_t *buf;
     lbq::ActView view;
 };
+
+namespace lbq {
+int num_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+}  // namespace lbq
 
 namespace {
 
@@ -97,23 +112,28 @@ ActLayout act_layout(int act_type, int64_t m, int64_t k) {
     return L;
 }
 
-int ensure_scratch(lbq_ctx *ctx, size_t bytes) {
-    if (ctx->scratch_bytes >= bytes) return LBQ_OK;
-    const size_t want = align_up(bytes > ctx->scratch_bytes * 2 ? bytes : ctx->scratch_bytes * 2, 1 << 20);
-    if (ctx->scratch) {
+// Grows a context buffer to at least `bytes` (what: message tag).
+int ensure_buffer(uint8_t **buf, size_t *have, size_t bytes, const char *what) {
+    if (*have >= bytes) return LBQ_OK;
+    const size_t want = align_up(bytes > *have * 2 ? bytes : *have * 2, 1 << 20);
+    if (*buf) {
         // in-flight kernels on any stream may still read the old buffer
         hipError_t e = hipDeviceSynchronize();
         if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
-        (void)hipFree(ctx->scratch);
-        ctx->scratch = nullptr;
-        ctx->scratch_bytes = 0;
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *have = 0;
     }
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, want);
-    if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for activation scratch: %s", want, hipGetErrorString(e));
-    ctx->scratch = static_cast<uint8_t *>(p);
-    ctx->scratch_bytes = want;
+    if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for %s: %s", want, what, hipGetErrorString(e));
+    *buf = static_cast<uint8_t *>(p);
+    *have = want;
     return LBQ_OK;
+}
+
+int ensure_scratch(lbq_ctx *ctx, size_t bytes) {
+    return ensure_buffer(&ctx->scratch, &ctx->scratch_bytes, bytes, "activation scratch");
 }
 
 lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
@@ -122,10 +142,19 @@ lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
 }
 
 // The dot half of QMatMul::forward: decode GEMV for m <= 8, MFMA GEMM above.
-int run_dot(const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
+// Caller holds ctx->mu (the GEMM's split-k workspace lives in the context).
+int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
     hipError_t e;
-    if (m <= 8) e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
-    else e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, st);
+    if (m <= 8) {
+        e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
+    } else {
+        const size_t wsb = lbq::gemm_workspace_bytes(w->type, w->n, w->k, m);
+        if (wsb) {
+            int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
+            if (s) return s;
+        }
+        e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, ctx->ws, st);
+    }
     if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
 }
@@ -197,6 +226,8 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
     c->device = device;
     c->scratch = nullptr;
     c->scratch_bytes = 0;
+    c->ws = nullptr;
+    c->ws_bytes = 0;
     *out_ctx = c;
     return LBQ_OK;
 }
@@ -204,9 +235,10 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
 int lbq_ctx_destroy(lbq_ctx *ctx) {
     if (!ctx) return LBQ_OK;
     DeviceGuard g(ctx->device);
-    if (ctx->scratch) {
+    if (ctx->scratch || ctx->ws) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->scratch);
+        if (ctx->scratch) (void)hipFree(ctx->scratch);
+        if (ctx->ws) (void)hipFree(ctx->ws);
     }
     delete ctx;
     return LBQ_OK;
@@ -289,7 +321,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w->k, const_cast<int8_t *>(av.xq),
                                          const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
-    return run_dot(w, av, m, d_y, st);
+    return run_dot(ctx, w, av, m, d_y, st);
 }
 
 int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act) {
@@ -349,7 +381,8 @@ int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *a, flo
     if (a->k != w->k) return fail(LBQ_ERR_SHAPE, "activation k = %lld, weight k = %lld", (long long)a->k, (long long)w->k);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-    return run_dot(w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return run_dot(ctx, w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
 }
 
 int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream) {

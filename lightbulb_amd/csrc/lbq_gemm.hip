@@ -1,21 +1,39 @@
-// lbq_gemm.hip -- batched path (m > 8): k-quant weight tiles dequantised into LDS,
-// multiplied on MFMA.
+// lbq_gemm.hip -- batched path (m > 8): k-quant weights dequantised in registers
+// straight into MFMA operands, activation codes staged through LDS.
 //
-// y[m][n] = sum_b d_x[m][b] * sum_{k in block b} q8[m][k] * w[n][k]
-//   q8, d_x : the Q8_K activation codes and block scales (as the reference
-//             quantises them); the codes are integers in [-128, 127], exact in fp16;
-//   w       : the weight dequantised as the reference does it (d*sc)*q - dmin*m in
-//             f32, rounded once to fp16 (relative error <= 2^-11 per weight).
-// Each 256-value block is accumulated on v_mfma_f32_32x32x16_f16 into its own
-// accumulator, which is then scaled by d_x[m][b] and added to the total.  The
-// only differences from the reference's integer path are that one rounding of w
-// and f32 summation order (about 3e-4 relative on a row).
+// y[m][n] = 2^e_m * sum_k a[m][k] * w[n][k]   (v_mfma_f32_32x32x16_f16, f32 accumulation)
+//   a[m][k] = f16(q8[m][k] * d_x[m][b] * 2^-e_m): the Q8_K activation value as the
+//             reference quantises it (codes q8, block scale d_x), rounded once to
+//             fp16 after a power-of-two row normalisation e_m chosen so that the
+//             row's largest |value| lies in [2^14, 2^15) -- no overflow, and
+//             every block within 2^14 of the row's largest keeps full precision;
+//   w[n][k] = the weight value the reference's integer path implies,
+//             (d*sc)*q - dmin*m (Q4_K/Q5_K) or (d*sc)*(q-32) (Q6_K), formed at f32
+//             precision and rounded once to fp16.
+// So the products differ from the reference's by two fp16 roundings (relative
+// <= 2^-11 each) and the sum by f32 summation order: about 4e-4 relative on a row.
 //
-// Tiles: BM x BN = 128 x 128 outputs per 256-thread workgroup, BK = 64 values
-// of k per step (a quarter of a block), four waves each owning 64 x 64 outputs
-// as 2 x 2 MFMA tiles of 32 x 32.  LDS is double-buffered: while the MFMAs run
-// on one step, the next step's weight bytes and codes are already in registers,
-// and are dequantised into the other buffer afterwards.
+// Work split.  A 256-thread workgroup owns BM = 32*MT rows of y and BN = 256
+// columns; wave w owns columns 64w..64w+63 (two 32-column MFMA tiles) for all BM
+// rows (MT 32-row tiles).  Lane l serves weight rows 32j + l%32 (j = 0, 1) and the
+// half h = l/32 of every 256-value block: it loads that half's raw bytes one block
+// ahead into registers and expands them into the B operands of the block's 16
+// MFMA k-steps.  No weight byte goes through LDS and each is dequantised once per
+// workgroup.  The activations are turned into fp16 operands once, by a pre-pass
+// (k_act_f16), and each block of them (BM x 256) is loaded one block ahead and
+// copied into a double-buffered LDS tile that all four waves read as A operands.
+//
+// k order.  For k-step s (0..15), lane half h supplies the 8 values
+// 128h + 8s + pi(e), e = 0..7, pi = (0,2,1,3,4,6,5,7): nibbles of bytes 0 and 2 of
+// a dword land in one f16 pair, bytes 1 and 3 in the next, which saves a shift
+// per pair.  The activation tile is stored in the same order (position 4a + e
+// holds value 4a + pi(e)), so each A operand is one contiguous 16-byte LDS read.
+//
+// Shapes with few output tiles split k over S workgroups (split-K) that write
+// partial sums to the workspace; a second kernel adds them in a fixed order, so
+// results do not depend on scheduling.
+#include <algorithm>
+
 #include "lbq_device.hpp"
 #include "lbq_internal.hpp"
 
@@ -25,248 +43,487 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int GBM = 128, GBN = 128, GBK = 64;
-constexpr int GLD = GBK + 8;  // LDS row stride in halfs (144 bytes: conflict-free b128 reads)
+constexpr int KB = 256;      // values per block (weights and Q8_K activations)
+constexpr int ALD = KB + 8;  // activation tile row stride in halfs: 528 B, conflict-free b128 reads
+constexpr int BN = 256;      // output columns per workgroup
 
-__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
-    const half2v h = {(_Float16)a, (_Float16)b};
-    return __builtin_bit_cast(uint32_t, h);
+// Weight operands are built from f16 subnormals: the bit pattern u (u < 1024) is
+// the f16 value u * 2^-24, exactly, so masking a nibble (or a nibble plus high
+// bits) in place in bytes 0 and 2 of a dword yields two f16 operands at once; a
+// nibble left in bits 4..7 reads as 16u * 2^-24.  The per-sub-block scale is
+// pre-multiplied by 2^24 (or 2^20), and v_fma_mix forms u*d1 - m1 at f32
+// precision (the subnormal converts exactly) and rounds it to f16 once.
+__device__ __forceinline__ uint32_t scale2(uint32_t p, float d1s, float c1) {
+    const half2v h = __builtin_bit_cast(half2v, p);
+    const half2v r = {(_Float16)fmaf((float)h.x, d1s, c1), (_Float16)fmaf((float)h.y, d1s, c1)};
+    return __builtin_bit_cast(uint32_t, r);
 }
 
-// byte I of v as f32 (the compiler emits v_cvt_f32_ubyteI)
-template <int I>
-__device__ __forceinline__ float ubyte_f32(uint32_t v) { return (float)((v >> (8 * I)) & 0xffu); }
-
-// 4 int8 codes (one dword) -> 4 exact fp16 values (two dwords): byte u = q ^ 0x80 is
-// placed in the mantissa of 1024.0 (0x6400 | u = 1024 + u), then 1152 is subtracted.
-__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t *lo, uint32_t *hi) {
+// 4 int8 codes times the scale sx -> f16 pairs (x0, x2) and (x1, x3).  Byte
+// q ^ 0x80 goes into the mantissa of 1024.0 (the f16 1152 + q, exact), and
+// (1152 + q)*sx + c with c = -1152*sx is evaluated at f32 precision and rounded
+// once (c carries an f32 rounding, <= 2^-24 * 1152 * |sx|, far below the f16 one).
+__device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint32_t *lo, uint32_t *hi) {
     const uint32_t u = w ^ 0x80808080u;
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    const half2v bias = {(_Float16)-1152.f, (_Float16)-1152.f};
-    *lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, a) + bias);
-    *hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, b) + bias);
+    const half2v a = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u));
+    const half2v b = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u));
+    const half2v ra = {(_Float16)fmaf((float)a.x, sx, c), (_Float16)fmaf((float)a.y, sx, c)};
+    const half2v rb = {(_Float16)fmaf((float)b.x, sx, c), (_Float16)fmaf((float)b.y, sx, c)};
+    *lo = __builtin_bit_cast(uint32_t, ra);
+    *hi = __builtin_bit_cast(uint32_t, rb);
 }
 
 // ---------------------------------------------------------------------------
-// Weight staging: one thread owns 32 consecutive values of a row inside the
-// step's 64-value window: values 64*kk + 32*hf + [0, 32) of block b.
+// Pre-pass: Q8_K rows (codes + block scales) -> fp16 operand rows in the GEMM's k
+// order, and the row exponent e_m.  One wave per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
+                                                 int *__restrict__ erow) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t m = (int64_t)blockIdx.x * 4 + wave;
+    if (m >= M) return;
+    const int nb = act.nb;
+    const float *xd = act.xd + m * nb;
+    float mx = 0.f;
+    for (int b = lane; b < nb; b += 64) mx = fmaxf(mx, fabsf(xd[b]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    // max |d_x| = f*2^E, f in [0.5, 1): |q8*d_x| < 128*2^E, so e = E - 8 keeps the
+    // row's values below 2^15 and its largest at or above 2^14
+    const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;
+    if (lane == 0) erow[m] = e;
+    const int8_t *q = act.xq + m * act.k;
+    _Float16 *a = A + m * act.k;
+    for (int64_t c = 16 * lane; c < act.k; c += 1024) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(q + c);
+        const float sx = __builtin_amdgcn_ldexpf(xd[c / KB], -e);
+        const float cc = -1152.f * sx;
+        uint32_t v[8];
+        codes_to_f16(w.x, sx, cc, &v[0], &v[1]);
+        codes_to_f16(w.y, sx, cc, &v[2], &v[3]);
+        codes_to_f16(w.z, sx, cc, &v[4], &v[5]);
+        codes_to_f16(w.w, sx, cc, &v[6], &v[7]);
+        uint4 *dst = reinterpret_cast<uint4 *>(a + c);
+        dst[0] = make_uint4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_uint4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// B-operand sources.  A lane's raw bytes of one block come in NL loads
+// (load_part(i), so the kernel can spread them over its MFMA stream); prep()
+// derives the per-block scales; dw(s, d) gives f16 values 2d, 2d+1 of the 8 the
+// lane supplies to k-step s.
 // ---------------------------------------------------------------------------
 template <int TYPE>
-struct GemmW;
+struct GB;
+
+// Q4_K / Q5_K: lane half h holds qs bytes 64h..64h+63 (sub-blocks 4h..4h+3) and,
+// for Q5_K, all 32 qh bytes (high bit of value 64c + 32*hi + i is bit 2c+hi of qh[i]).
+template <int TYPE>
+struct GBK45 {
+    static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
+    static constexpr int QS = TYPE == TYPE_Q4_K ? 16 : 48;
+    static constexpr int NL = TYPE == TYPE_Q4_K ? 5 : 7;
+    struct Raw { uint4 v[NL]; };  // header, qs x4, (qh x2)
+    struct Prep { float d1[4], c1[4]; uint32_t q[16], qh[8]; };
+    __device__ static void load_part(const uint8_t *blk, int h, Raw &r, int i) {
+        if (i == 0) r.v[0] = ld_u4(blk);
+        else if (i <= 4) r.v[i] = ld_u4(blk + QS + 64 * h + 16 * (i - 1));
+        else r.v[i] = ld_u4(blk + 16 + 16 * (i - 5));
+    }
+    // lane sub-block j (0..3) is block sub-block 4h + j: low nibbles for even j,
+    // high nibbles (read as 16u) for odd j
+    __device__ static void prep(const Raw &r, int h, Prep &p) {
+        const uint4 hdr = r.v[0];
+        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+#pragma unroll
+        for (int cl = 0; cl < 2; cl++) {
+            uint32_t sc2, m2;
+            k4_scale_pair(hdr.y, hdr.z, hdr.w, 2 * h + cl, &sc2, &m2);
+#pragma unroll
+            for (int hi = 0; hi < 2; hi++) {
+                p.d1[2 * cl + hi] = d * (float)((sc2 >> (8 * hi)) & 0xffu) * (hi ? 1048576.f : 16777216.f);
+                p.c1[2 * cl + hi] = -(dmin * (float)((m2 >> (8 * hi)) & 0xffu));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint4 q = r.v[1 + i];
+            p.q[4 * i] = q.x; p.q[4 * i + 1] = q.y; p.q[4 * i + 2] = q.z; p.q[4 * i + 3] = q.w;
+        }
+        if (TYPE == TYPE_Q5_K) {
+            // bring bit 4h (sub-block 4h) of every qh byte to bit 0
+            const uint32_t sh = 4u * (uint32_t)h;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint4 q = r.v[NL - 2 + i];
+                p.qh[4 * i] = q.x >> sh; p.qh[4 * i + 1] = q.y >> sh;
+                p.qh[4 * i + 2] = q.z >> sh; p.qh[4 * i + 3] = q.w >> sh;
+            }
+        }
+    }
+    // dword d (f16 slots 2d, 2d+1 = bytes 0,2 or 1,3 of a qs dword) of the operand of k-step s
+    __device__ static uint32_t dw(const Prep &p, int s, int d) {
+        const int js = s >> 2, hi = js & 1;
+        uint32_t q = p.q[8 * (s >> 3) + 2 * (s & 3) + (d >> 1)];
+        if (d & 1) q >>= 8;
+        uint32_t v = q & (hi ? 0x00f000f0u : 0x000f000fu);
+        if (TYPE == TYPE_Q5_K) {
+            // fifth bit: bit js of the qh byte, to bit 4 (8 for high nibbles) of the f16
+            uint32_t hq = p.qh[2 * (s & 3) + (d >> 1)];
+            if (d & 1) hq >>= 8;
+            v |= (hq << ((hi ? 8 : 4) - js)) & (hi ? 0x01000100u : 0x00100010u);
+        }
+        return scale2(v, p.d1[js], p.c1[js]);
+    }
+};
+template <> struct GB<TYPE_Q4_K> : GBK45<TYPE_Q4_K> {};
+template <> struct GB<TYPE_Q5_K> : GBK45<TYPE_Q5_K> {};
+
+// Q6_K: lane half h holds the 128-value half h: ql bytes 64h..64h+63, qh bytes
+// 32h..32h+31, scales 8h..8h+7.  Value 128h + 32q + l (l < 32): low bits from
+// ql[64h + 32(q%2) + l] (nibble q/2), high bits from qh[32h + l] (bits 2q, 2q+1),
+// scale 8h + 2q + l/16.  Blocks are 210 bytes, only 2-byte aligned: each field is
+// read as the aligned dwords that hold it (the last one re-read when the field
+// is 4-byte aligned, so no dword outside it is touched) and funnel-shifted.
+template <>
+struct GB<TYPE_Q6_K> {
+    static constexpr int BYTES = 210;
+    static constexpr int NL = 12;
+    struct Raw { u32x4a4 ql[4], qh[2]; uint32_t qlt, qht, sc[3], dw; };
+    struct Prep { float d1[8], c1[8]; uint32_t l[16], qh[8]; };
+    __device__ static const uint8_t *al4(const uint8_t *p) {
+        return reinterpret_cast<const uint8_t *>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
+    }
+    __device__ static void load_part(const uint8_t *blk, int h, Raw &r, int i) {
+        const bool mis = (reinterpret_cast<uintptr_t>(blk) & 3u) != 0;
+        const uint8_t *ql = al4(blk + 64 * h), *qh = al4(blk + 128 + 32 * h), *sc = al4(blk + 192 + 8 * h);
+        if (i < 4) r.ql[i] = *reinterpret_cast<const u32x4a4 *>(ql + 16 * i);
+        else if (i < 6) r.qh[i - 4] = *reinterpret_cast<const u32x4a4 *>(qh + 16 * (i - 4));
+        else if (i == 6) r.qlt = *reinterpret_cast<const uint32_t *>(ql + (mis ? 64 : 60));
+        else if (i == 7) r.qht = *reinterpret_cast<const uint32_t *>(qh + (mis ? 32 : 28));
+        else if (i < 10) r.sc[i - 8] = *reinterpret_cast<const uint32_t *>(sc + 4 * (i - 8));
+        else if (i == 10) r.sc[2] = *reinterpret_cast<const uint32_t *>(sc + (mis ? 8 : 4));
+        else r.dw = ld2_a2(blk + 208);
+    }
+    // mis: byte misalignment of the block (0 or 2)
+    __device__ static void prep(const Raw &r, uint32_t mis, Prep &p) {
+        uint32_t w[17], x[9];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { w[4 * i] = r.ql[i].x; w[4 * i + 1] = r.ql[i].y; w[4 * i + 2] = r.ql[i].z; w[4 * i + 3] = r.ql[i].w; }
+        w[16] = r.qlt;
+#pragma unroll
+        for (int i = 0; i < 2; i++) { x[4 * i] = r.qh[i].x; x[4 * i + 1] = r.qh[i].y; x[4 * i + 2] = r.qh[i].z; x[4 * i + 3] = r.qh[i].w; }
+        x[8] = r.qht;
+#pragma unroll
+        for (int i = 0; i < 16; i++) p.l[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], mis);
+#pragma unroll
+        for (int i = 0; i < 8; i++) p.qh[i] = __builtin_amdgcn_alignbyte(x[i + 1], x[i], mis);
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc[1], r.sc[0], mis), s1 = __builtin_amdgcn_alignbyte(r.sc[2], r.sc[1], mis);
+        const float d = h2f(r.dw);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            // scale i covers quarter q = i/2 of the half: high nibbles (read as 16u) for i >= 4
+            const int8_t sc = (int8_t)(((i < 4 ? s0 : s1) >> (8 * (i & 3))) & 0xffu);
+            const float d1 = d * (float)sc;
+            p.d1[i] = d1 * (i >= 4 ? 1048576.f : 16777216.f);
+            p.c1[i] = -32.f * d1;  // (u - 32)*d1
+        }
+    }
+    __device__ static uint32_t dw(const Prep &p, int s, int d) {
+        const int q = s >> 2, hi = q >> 1;
+        uint32_t l = p.l[8 * (q & 1) + 2 * (s & 3) + (d >> 1)], hq = p.qh[2 * (s & 3) + (d >> 1)];
+        if (d & 1) { l >>= 8; hq >>= 8; }
+        // bits (2q, 2q+1) of the qh byte -> bits 4,5 of the f16 (8,9 for high nibbles)
+        const uint32_t v = (l & (hi ? 0x00f000f0u : 0x000f000fu)) |
+                           ((hq << ((hi ? 8 : 4) - 2 * q)) & (hi ? 0x03000300u : 0x00300030u));
+        return scale2(v, p.d1[s >> 1], p.c1[s >> 1]);
+    }
+};
 
 template <int TYPE>
-struct GemmWK45 {
-    static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
-    struct Raw { uint4 hdr, q0, q1, h0, h1; };
-    __device__ static Raw load(const uint8_t *blk, int kk, int hf) {
-        (void)hf;
-        Raw r;
-        r.hdr = ld_u4(blk);
-        const uint8_t *qs = blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 32 * kk;
-        r.q0 = ld_u4(qs);
-        r.q1 = ld_u4(qs + 16);
-        if (TYPE == TYPE_Q5_K) {
-            r.h0 = ld_u4(blk + 16);
-            r.h1 = ld_u4(blk + 32);
-        }
-        return r;
-    }
-    // 32 dequantised values -> 16 packed fp16 pairs
-    __device__ static void deq(const Raw &r, int kk, int hf, uint32_t out[16]) {
-        uint32_t sc2, m2;
-        k4_scale_pair(r.hdr.y, r.hdr.z, r.hdr.w, kk, &sc2, &m2);
-        const uint32_t sc = hf ? (sc2 >> 8) : (sc2 & 0xffu);
-        const uint32_t mn = hf ? (m2 >> 8) : (m2 & 0xffu);
-        const float d1 = h2f(r.hdr.x & 0xffffu) * (float)sc;
-        const float m1 = h2f(r.hdr.x >> 16) * (float)mn;
-        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t v = hf ? ((q[i] >> 4) & 0x0f0f0f0fu) : (q[i] & 0x0f0f0f0fu);
-            if (TYPE == TYPE_Q5_K) v |= ((qh[i] >> (2 * kk + hf)) & 0x01010101u) << 4;
-            const float f0 = d1 * ubyte_f32<0>(v) - m1;
-            const float f1 = d1 * ubyte_f32<1>(v) - m1;
-            const float f2 = d1 * ubyte_f32<2>(v) - m1;
-            const float f3 = d1 * ubyte_f32<3>(v) - m1;
-            out[2 * i] = pack_f16x2(f0, f1);
-            out[2 * i + 1] = pack_f16x2(f2, f3);
-        }
-    }
-};
-template <> struct GemmW<TYPE_Q4_K> : GemmWK45<TYPE_Q4_K> {};
-template <> struct GemmW<TYPE_Q5_K> : GemmWK45<TYPE_Q5_K> {};
-
-// Q6_K: window values 64*kk + 32*hf + l (l < 32) are 128n + 32s + l with n = kk/2,
-// s = 2*(kk%2) + hf: low bits from ql[64n + 32*(s%2) + l] (nibble s/2), high bits
-// from qh[32n + l] (bits 2s, 2s+1), scale index 8n + 2s + l/16.
-template <>
-struct GemmW<TYPE_Q6_K> {
-    static constexpr int BYTES = 210;
-    struct Raw { uint32_t ql[8], qh[8], sc, dbits; };
-    __device__ static Raw load(const uint8_t *blk, int kk, int hf) {
-        const int n = kk >> 1, s = 2 * (kk & 1) + hf;
-        Raw r;
-        ld16_a2(blk + 64 * n + 32 * (s & 1), r.ql);
-        ld16_a2(blk + 64 * n + 32 * (s & 1) + 16, r.ql + 4);
-        ld16_a2(blk + 128 + 32 * n, r.qh);
-        ld16_a2(blk + 128 + 32 * n + 16, r.qh + 4);
-        r.sc = ld4_a2(blk + 192 + 8 * n + 2 * s);
-        r.dbits = ld2_a2(blk + 208);
-        return r;
-    }
-    __device__ static void deq(const Raw &r, int kk, int hf, uint32_t out[16]) {
-        const int s = 2 * (kk & 1) + hf;
-        const float d = h2f(r.dbits);
-        const float d1a = d * (float)(int8_t)(r.sc & 0xffu);        // l < 16
-        const float d1b = d * (float)(int8_t)((r.sc >> 8) & 0xffu); // l >= 16
-        const int shq = 4 * (s >> 1), shh = 2 * s;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t v = ((r.ql[i] >> shq) & 0x0f0f0f0fu) | (((r.qh[i] >> shh) & 0x03030303u) << 4);
-            const float d1 = i < 4 ? d1a : d1b;
-            const float f0 = d1 * (ubyte_f32<0>(v) - 32.f);
-            const float f1 = d1 * (ubyte_f32<1>(v) - 32.f);
-            const float f2 = d1 * (ubyte_f32<2>(v) - 32.f);
-            const float f3 = d1 * (ubyte_f32<3>(v) - 32.f);
-            out[2 * i] = pack_f16x2(f0, f1);
-            out[2 * i + 1] = pack_f16x2(f2, f3);
-        }
-    }
-};
+__device__ __forceinline__ void gb_prep(const typename GB<TYPE>::Raw &r, int h, const uint8_t *blk, typename GB<TYPE>::Prep &p) {
+    if constexpr (TYPE == TYPE_Q6_K) GB<TYPE>::prep(r, (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u), p);
+    else { (void)blk; GB<TYPE>::prep(r, h, p); }
+}
 
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
-template <int TYPE>
-__global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
-                                                 ActView act, int64_t M, float *__restrict__ y) {
-    using GW = GemmW<TYPE>;
-    __shared__ __align__(16) _Float16 As[2][GBM][GLD];
-    __shared__ __align__(16) _Float16 Bs[2][GBN][GLD];
-    __shared__ float Xd[2][GBM];
+struct GemmGrid {
+    int tiles_m, tiles_n, bps;  // bps: blocks of k per split
+    int64_t split_stride;       // floats between the partial outputs of two splits (0: no split)
+};
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-    const int64_t m0 = (int64_t)blockIdx.x * GBM, n0 = (int64_t)blockIdx.y * GBN;
-    const int nb = act.nb;
-    const int steps = nb * 4;
+// resident workgroups per CU the register budget allows
+template <int TYPE, int MT>
+constexpr int gemm_occupancy() { return (MT == 4 || TYPE == TYPE_Q6_K || (TYPE == TYPE_Q5_K && MT == 2)) ? 1 : 2; }
 
-    // staging roles: row t/2 of the tile, half hf = t%2 of the 64-value window
-    const int srow = t >> 1, hf = t & 1;
-    const int64_t am = min(m0 + srow, M - 1);  // clamped: loads stay in range
-    const int64_t wn_row = min(n0 + srow, N - 1);
-    const int8_t *arow = act.xq + am * act.k;
-    const uint8_t *wrow = W + wn_row * row_bytes;
+// Pipeline.  The MFMAs of a block run as 16 k-steps of 2*MT MFMAs; each MFMA sits
+// in its own scheduling region (sched_barrier) together with a share of the
+// other work, so that work issues in the MFMA shadow instead of as a bubble
+// (on gfx950 only about four VALU per MFMA co-issue for free):
+//   every step s < 15 : the B operands (one dword per MFMA at MT = 4) and the A
+//                       operands of step s+1;
+//   step 0            : the next block's activation loads;
+//   steps 1..3        : the next block's weight loads;
+//   step 4            : barrier -- every wave is done with the other LDS buffer;
+//   step 8            : the next block's activations into the other LDS buffer;
+//   step 13           : barrier -- that buffer is complete;
+//   step 14           : the next block's first A operands;
+//   step 15           : the next block's scales and first B operands.
+template <int TYPE, int MT>
+__global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(const uint8_t *__restrict__ W, int64_t N,
+                                                               int64_t row_bytes, const _Float16 *__restrict__ A,
+                                                               const int *__restrict__ erow, int64_t K, int64_t M,
+                                                               float *__restrict__ out, GemmGrid g) {
+    using B = GB<TYPE>;
+    constexpr int BM = 32 * MT;
+    constexpr int NG = 2 * MT;                 // MFMAs (regions) per k-step
+    constexpr int ALOADS = BM / 8;             // 16-byte activation loads per thread and block (= 2 NG)
+    constexpr int WL = 2 * B::NL;              // weight loads per lane and block
+    constexpr int WPR = (WL + 3 * NG - 1) / (3 * NG);
+    constexpr int PER = 8 / NG;                // B-operand dwords built per region
+    constexpr int NPR = (8 + NG - 2) / (NG - 1 > 0 ? NG - 1 : 1);  // step 15: dwords per region after the scales
+    __shared__ __align__(16) _Float16 As[2][BM][ALD];
+    __shared__ int Es[BM];
 
-    uint4 ra0, ra1;
-    typename GW::Raw rw;
-    float rxd = 0.f;
-    auto load_step = [&](int s) {
-        const int b = s >> 2, kk = s & 3;
-        const int8_t *ap = arow + (int64_t)s * GBK + 32 * hf;
-        ra0 = *reinterpret_cast<const uint4 *>(ap);
-        ra1 = *reinterpret_cast<const uint4 *>(ap + 16);
-        rw = GW::load(wrow + (int64_t)b * GW::BYTES, kk, hf);
-        if (t < GBM) rxd = act.xd[min(m0 + t, M - 1) * nb + b];
+    // tile of this workgroup: consecutive workgroup ids go to different XCDs, so
+    // renumber them such that each XCD receives a contiguous run of tiles; tiles
+    // are ordered split-major, then by column tile, then by row tile, so the row
+    // tiles that share weight columns share an L2.
+    const int G = (int)gridDim.x, L = (int)blockIdx.x;
+    const int T = (G & 7) == 0 ? (L & 7) * (G >> 3) + (L >> 3) : L;
+    const int tm = T % g.tiles_m, tn = (T / g.tiles_m) % g.tiles_n, z = T / (g.tiles_m * g.tiles_n);
+    const int nb = (int)(K / KB);
+    const int b0 = z * g.bps, b1 = min(nb, b0 + g.bps);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    float *y = out + (int64_t)z * g.split_stride;
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
+    const uint8_t *wrow[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) wrow[j] = W + min(n0 + 64 * wave + 32 * j + lr, N - 1) * row_bytes;
+    // activation staging: a block row is 256 halfs = 32 16-byte pieces; load i of
+    // thread t moves piece t%32 of tile row 8i + t/32, so every load instruction
+    // reads two whole 512-byte rows.  The operand buffer holds whole tiles of rows
+    // (rows past M are never stored), so the addresses need no clamping.
+    const int pc = t & 31, pr = t >> 5;
+    const _Float16 *abase = A + (m0 + pr) * K + pc * 8;
+    if (t < BM) Es[t] = erow[min(m0 + t, M - 1)];
+
+    typename B::Raw raw[2];
+    typename B::Prep p[2];
+    uint4 ra[ALOADS];
+    auto a_load = [&](int b, int i) { ra[i] = *reinterpret_cast<const uint4 *>(abase + 8 * i * K + (int64_t)b * KB); };
+    auto a_store = [&](int buf, int i) {
+        *reinterpret_cast<uint4 *>(&As[buf][8 * i + pr][8 * pc]) = make_uint4(ra[i].x, ra[i].y, ra[i].z, ra[i].w);
     };
-    auto store_step = [&](int s, int buf) {
-        const int kk = s & 3;
-        uint32_t a16[16];
-        const uint32_t aw[8] = {ra0.x, ra0.y, ra0.z, ra0.w, ra1.x, ra1.y, ra1.z, ra1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) i8x4_to_f16(aw[i], &a16[2 * i], &a16[2 * i + 1]);
-        uint4 *adst = reinterpret_cast<uint4 *>(&As[buf][srow][32 * hf]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) adst[i] = make_uint4(a16[4 * i], a16[4 * i + 1], a16[4 * i + 2], a16[4 * i + 3]);
-        uint32_t w16[16];
-        GW::deq(rw, kk, hf, w16);
-        uint4 *bdst = reinterpret_cast<uint4 *>(&Bs[buf][srow][32 * hf]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) bdst[i] = make_uint4(w16[4 * i], w16[4 * i + 1], w16[4 * i + 2], w16[4 * i + 3]);
-        if (kk == 0 && t < GBM) Xd[(s >> 2) & 1][t] = rxd;
-    };
+    auto w_load = [&](int b, int q) { B::load_part(wrow[q / B::NL] + (int64_t)b * B::BYTES, h, raw[q / B::NL], q % B::NL); };
+    auto w_prep = [&](int b, int j) { gb_prep<TYPE>(raw[j], h, wrow[j] + (int64_t)b * B::BYTES, p[j]); };
 
-    floatx16 acc[2][2], blk[2][2];
+    floatx16 acc[MT][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
-    load_step(0);
-    store_step(0, 0);
+    // prologue: block b0 into LDS buffer 0, its scales and first operands
+#pragma unroll
+    for (int i = 0; i < ALOADS; i++) a_load(b0, i);
+#pragma unroll
+    for (int q = 0; q < WL; q++) w_load(b0, q);
+#pragma unroll
+    for (int i = 0; i < ALOADS; i++) a_store(0, i);
     __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; j++) w_prep(b0, j);
+    const _Float16 *al0 = &As[0][lr][128 * h], *al1 = &As[1][lr][128 * h];
+    half8 acur[MT];
+    uint32_t bcur[2][4];
+#pragma unroll
+    for (int i = 0; i < MT; i++) acur[i] = *reinterpret_cast<const half8 *>(al0 + 32 * i * ALD);
+#pragma unroll
+    for (int q = 0; q < 8; q++) bcur[q >> 2][q & 3] = B::dw(p[q >> 2], 0, q & 3);
 
-    const int lr = lane & 31, lk = 8 * (lane >> 5);
-    for (int s = 0; s < steps; s++) {
-        const int buf = s & 1;
-        if (s + 1 < steps) load_step(s + 1);
-        if ((s & 3) == 0) {
+    auto block = [&](int b, int buf) {
+        const int bn = min(b + 1, b1 - 1);  // clamped: the last block re-stages itself, harmlessly
+        const _Float16 *al = buf ? al1 : al0, *aln = buf ? al0 : al1;
+        half8 ablk[MT];
+        uint32_t bblk[2][4];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+        for (int s = 0; s < 16; s++) {
+            half8 anxt[MT];
+            uint32_t bnxt[2][4];
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+            for (int i = 0; i < MT; i++) {
 #pragma unroll
-                    for (int v = 0; v < 16; v++) blk[i][j][v] = 0.f;
-        }
+                for (int j = 0; j < 2; j++) {
+                    const int rg = 2 * i + j;
+                    const half8 bo = __builtin_bit_cast(half8, make_uint4(bcur[j][0], bcur[j][1], bcur[j][2], bcur[j][3]));
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(acur[i], bo, acc[i][j], 0, 0, 0);
+                    if (s < 15) {
 #pragma unroll
-        for (int ks = 0; ks < GBK / 16; ks++) {
-            half8 a[2], b[2];
+                        for (int q = rg * PER; q < (rg + 1) * PER; q++) bnxt[q >> 2][q & 3] = B::dw(p[q >> 2], s + 1, q & 3);
+                        if (j == 1) anxt[i] = *reinterpret_cast<const half8 *>(al + 32 * i * ALD + 8 * (s + 1));
+                    }
+                    if (s == 0) { a_load(bn, 2 * rg); a_load(bn, 2 * rg + 1); }
+                    if (s >= 1 && s <= 3) {
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                a[i] = *reinterpret_cast<const half8 *>(&As[buf][64 * wm + 32 * i + lr][16 * ks + lk]);
+                        for (int w = ((s - 1) * NG + rg) * WPR; w < ((s - 1) * NG + rg + 1) * WPR; w++)
+                            if (w < WL) w_load(bn, w);
+                    }
+                    if (s == 4 && rg == 0) __syncthreads();
+                    if (s == 8) { a_store(buf ^ 1, 2 * rg); a_store(buf ^ 1, 2 * rg + 1); }
+                    if (s == 13 && rg == 0) __syncthreads();
+                    if (s == 14 && j == 1) ablk[i] = *reinterpret_cast<const half8 *>(aln + 32 * i * ALD);
+                    if (s == 15) {
+                        if (rg == 0) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                b[j] = *reinterpret_cast<const half8 *>(&Bs[buf][64 * wn + 32 * j + lr][16 * ks + lk]);
+                            for (int jj = 0; jj < 2; jj++) w_prep(bn, jj);
+                        }
+                        if (NG == 1 || rg > 0) {
+                            const int r0 = NG == 1 ? 0 : (rg - 1) * NPR;
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], blk[i][j], 0, 0, 0);
-        }
-        if ((s & 3) == 3) {
-            // block done: scale by the activation block scale of each output row
-            const float *xd = Xd[(s >> 2) & 1];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const float sx = xd[64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
-#pragma unroll
-                    for (int j = 0; j < 2; j++) acc[i][j][v] += blk[i][j][v] * sx;
+                            for (int q = r0; q < r0 + (NG == 1 ? 8 : NPR); q++)
+                                if (q < 8) bblk[q >> 2][q & 3] = B::dw(p[q >> 2], 0, q & 3);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-        }
-        if (s + 1 < steps) store_step(s + 1, buf ^ 1);
-        __syncthreads();
-    }
-
-    // write y[m][n]: for a fixed v, lanes 0..31 cover 32 consecutive n
+            if (s < 15) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+                for (int i = 0; i < MT; i++) acur[i] = anxt[i];
+#pragma unroll
+                for (int q = 0; q < 8; q++) bcur[q >> 2][q & 3] = bnxt[q >> 2][q & 3];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MT; i++) acur[i] = ablk[i];
+#pragma unroll
+        for (int q = 0; q < 8; q++) bcur[q >> 2][q & 3] = bblk[q >> 2][q & 3];
+    };
+
+    int b = b0;
+    for (; b + 1 < b1; b += 2) {
+        block(b, 0);
+        block(b + 1, 1);
+    }
+    if (b < b1) block(b, 0);
+
+    // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            const int64_t m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int64_t m = m0 + r;
+            const int e = Es[r];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                const int64_t n = n0 + 64 * wn + 32 * j + lr;
-                if (m < M && n < N) y[m * N + n] = acc[i][j][v];
+                const int64_t n = n0 + 64 * wave + 32 * j + lr;
+                if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][v], e);
             }
         }
     }
 }
 
+// y = sum over s < S of part[s] (fixed order), count values.
+__global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int S, int64_t count,
+                                                   float *__restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    float s = part[i];
+    for (int z = 1; z < S; z++) s += part[(int64_t)z * count + i];
+    y[i] = s;
+}
+
+namespace {
+
+struct Plan {
+    int mt, tiles_m, tiles_n, splits, bps;
+};
+
+Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
+    Plan p;
+    p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
+    p.tiles_m = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
+    p.tiles_n = (int)((n + BN - 1) / BN);
+    const int nb = (int)(k / KB);
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    const int occ = (p.mt == 4 || type == TYPE_Q6_K || (type == TYPE_Q5_K && p.mt == 2)) ? 1 : 2;  // gemm_occupancy
+    const int64_t slots = (int64_t)num_cus() * occ;
+    int s = 1;
+    if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
+    p.bps = (nb + s - 1) / s;
+    p.splits = (nb + p.bps - 1) / p.bps;
+    return p;
+}
+
+template <int TYPE>
+hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_bytes, const _Float16 *a,
+                        const int *erow, int64_t k, int64_t m, float *out, int64_t split_stride, hipStream_t st) {
+    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride};
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
+    switch (p.mt) {
+    case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+    case 2: k_gemm<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+    default:
+        if constexpr (TYPE != TYPE_Q6_K) k_gemm<TYPE, 4><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+        break;
+    }
+    return hipGetLastError();
+}
+
+// workspace: fp16 operand rows [m][k] | row exponents [m] | split-k partials [S][m][n]
+struct WsLayout {
+    size_t a_off, e_off, part_off, total;
+};
+
+WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
+    auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    WsLayout L;
+    L.a_off = 0;
+    L.e_off = up((size_t)p.tiles_m * 32 * p.mt * (size_t)k * sizeof(_Float16));  // whole row tiles
+    L.part_off = L.e_off + up((size_t)m * sizeof(int));
+    L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
+    return L;
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
+    if (type == TYPE_Q8_0) return 0;
+    return ws_layout(plan_for(type, n, k, m), n, k, m).total;
+}
+
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       int64_t m, float *y, hipStream_t st) {
+                       int64_t m, float *y, void *ws, hipStream_t st) {
     if (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K) {
-        const dim3 grid((unsigned)((m + GBM - 1) / GBM), (unsigned)((n + GBN - 1) / GBN));
+        if (!ws) return hipErrorInvalidValue;
+        const Plan p = plan_for(type, n, k, m);
+        const WsLayout L = ws_layout(p, n, k, m);
+        uint8_t *base = static_cast<uint8_t *>(ws);
+        _Float16 *a = reinterpret_cast<_Float16 *>(base + L.a_off);
+        int *erow = reinterpret_cast<int *>(base + L.e_off);
+        float *part = reinterpret_cast<float *>(base + L.part_off);
+        k_act_f16<<<(unsigned)((m + 3) / 4), 256, 0, st>>>(act, m, a, erow);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        float *out = p.splits > 1 ? part : y;
+        const int64_t stride = p.splits > 1 ? m * n : 0;
         switch (type) {
-        case TYPE_Q4_K: k_gemm<TYPE_Q4_K><<<grid, 256, 0, st>>>(w, n, row_bytes, act, m, y); break;
-        case TYPE_Q5_K: k_gemm<TYPE_Q5_K><<<grid, 256, 0, st>>>(w, n, row_bytes, act, m, y); break;
-        case TYPE_Q6_K: k_gemm<TYPE_Q6_K><<<grid, 256, 0, st>>>(w, n, row_bytes, act, m, y); break;
+        case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+        case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+        default: e = launch_typed<TYPE_Q6_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
         }
+        if (e != hipSuccess || p.splits == 1) return e;
+        const int64_t count = m * n;
+        k_split_sum<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(part, p.splits, count, y);
         return hipGetLastError();
     }
     // Q8_0 (activation scale every 32 values): the decode GEMV over row chunks of 8

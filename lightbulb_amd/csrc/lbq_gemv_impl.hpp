@@ -397,17 +397,6 @@ static GemvCfg pick_cfg(int type, int64_t n, int pieces, int m, int64_t k) {
     return c;
 }
 
-static int num_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        hipDeviceProp_t p;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
-        if (cus <= 0) cus = 256;
-    }
-    return cus;
-}
-
 template <int TYPE, int M, int RPW, int IT, bool FUSED>
 static hipError_t run_p(const uint8_t *w, const PGeom &g0, const ActView &act, const float *x, int m, float *y,
                         int wpc, hipStream_t st) {

@@ -32,9 +32,15 @@ bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x);
 hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                          const float *x, int m, float *y, hipStream_t st);
 
-// Batched path (m > 8): dequantise weight tiles into LDS and run them through MFMA.
+// Batched path (m > 8): weights dequantised in registers into MFMA operands.
+// Needs gemm_workspace_bytes(type, n, k, m) bytes of device memory at ws (fp16
+// activation operands and, for shapes that split k, the partial sums).
+size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       int64_t m, float *y, hipStream_t st);
+                       int64_t m, float *y, void *ws, hipStream_t st);
+
+// Compute units of the current device (cached after the first call).
+int num_cus();
 
 // f32 weights -> GGUF blocks on the device (ggml reference quantisers).
 hipError_t launch_quant_weights(int type, const float *w, int64_t nelem, uint8_t *out, hipStream_t st);
