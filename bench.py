@@ -10,10 +10,16 @@ quantised on the device; 8 distinct layer copies (982 MB) rotate so the
 256 MB Infinity Cache cannot hold the working set.  Launches are replayed
 from HIP graphs so the host's issue rate does not limit the measurement.
 
-Also reported (extra keys): the dot kernel alone against the HBM roofline,
-per-shape kernel times, the 32-layer Q4_K_M stack in tokens/s at batch 1 and
-32, and the oracle (C restatement of the reference CPU QMatMul)
-on a bounded sample on the host cores.
+roofline: the step's kernel (the fused quantise + GEMV, one launch per
+projection), algorithmic bytes (weights + x + y) per launch over its average
+launch time; traffic: HBM bytes per launch from the committed rocprofv3
+FETCH_SIZE/WRITE_SIZE summary (profiles/traffic_q4k_gemv.json), when present.
+
+Also reported (extra keys): the dot kernel alone, per-shape kernel times, the
+batched MFMA path at M = 512 in TFLOP/s against dense bf16 peak,
+the 32-layer Q4_K_M stack in tokens/s at batch 1 and 32, and the
+oracle (C restatement of the reference CPU QMatMul) on a bounded sample on the
+host cores.
 """
 from __future__ import annotations
 
@@ -49,7 +55,30 @@ def parse():
     p.add_argument("--no-stack", action="store_true", help="skip the 32-layer stack measurement")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-gemm", action="store_true", help="skip the M = 512 MFMA measurement")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="first run a 256 MiB device copy 4 times (reference kernel of known size for "
+                        "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+def copy_probe(torch, dev):
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy probe: 4 x {src.numel() * 4} B copies")
+    del src, dst
+
+
+def load_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed PMC summary."""
+    f = ROOT / "profiles" / "traffic_q4k_gemv.json"
+    try:
+        return json.loads(f.read_text())
+    except (OSError, ValueError):
+        return None
 
 
 def make_weights(torch, qz, dtype, n, k, gen, dev):
@@ -132,6 +161,8 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        copy_probe(torch, dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B1)
     Q4K, Q6K = qz.GgmlDType.Q4K, qz.GgmlDType.Q6K
@@ -171,6 +202,7 @@ def main():
     timed_graph(torch, g_dot, wreps, stream)
     ms_dot = timed_graph(torch, g_dot, reps, stream) / args.copies
     value = layer_bytes / (ms_full * 1e-3) / 1e9
+    full_gbs = (layer_bytes + io_bytes) / (ms_full * 1e-3) / 1e9
     dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
     log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
         f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s")
@@ -214,17 +246,25 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(dot_gbs, 1),
+            "achieved": round(full_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(dot_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(full_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "k_gemv<Q4_K> (the 7 dot launches of one step, average over launches)",
-            "us_per_step": round(ms_dot * 1e3, 3),
+            "kernel": "k_gemv1<Q4_K, fused> (quantise x + dequant/int-dot GEMV, one launch per projection); "
+                      "algorithmic bytes per launch = N*K/256*144 + 4K + 4N, averaged over the 7 launches",
+            "us_per_launch": round(ms_full * 1e3 / len(LAYER), 3),
+            "algorithmic_bytes_per_launch": round((layer_bytes + io_bytes) / len(LAYER)),
         },
+        "dot_only": {"us_per_step": round(ms_dot * 1e3, 3), "GB/s": round(dot_gbs, 1),
+                     "kernel": "k_gemv1<Q4_K> on pre-quantised activations (forward_quantized)"},
         "kernels": kernels,
     }
     del g_full, g_dot
+    tr = load_traffic()
+    if tr and "bytes_per_launch" in tr:
+        result["roofline"]["traffic"] = tr["bytes_per_launch"]
+        result["roofline"]["traffic_source"] = "profiles/traffic_q4k_gemv.json (" + tr.get("method", "") + ")"
 
     # ---------------------------------------------------------------- CPU baseline (bounded sample)
     if not args.no_cpu:
@@ -239,11 +279,44 @@ def main():
     del copies, acts
     torch.cuda.empty_cache()
 
+    # ---------------------------------------------------------------- config 4: M = 512 MFMA path
+    if not args.no_gemm:
+        result["prefill_gemm"] = gemm_bench(torch, qz, gen, dev, stream, reps)
+
     # ---------------------------------------------------------------- config 5: 32-layer stack
     if not args.no_stack:
         result["stack"] = stack_bench(torch, qz, gen, dev, stream)
 
     print(json.dumps(result), flush=True)
+
+
+def gemm_bench(torch, qz, gen, dev, stream, reps):
+    """Q4_K gate_proj / down_proj at M = 512: QMatMul::forward (quantise, operand pre-pass, MFMA
+    GEMM) and the dot half alone, 2*M*N*K flops over the time, against dense bf16 peak."""
+    out = {}
+    M = 512
+    for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
+        qm = make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev)
+        x = torch.randn(M, k, generator=gen, device=dev)
+        y = torch.empty(M, n, device=dev)
+        act = qz.QActivation.for_weight(qm, M).quantize(x)
+        g_f = capture(torch, lambda: qm.forward(x))
+        g_d = capture(torch, lambda: qm.forward_quantized(act, y))
+        r = max(5, reps // 4)
+        timed_graph(torch, g_f, 3, stream)
+        ms_f = timed_graph(torch, g_f, r, stream)
+        timed_graph(torch, g_d, 3, stream)
+        ms_d = timed_graph(torch, g_d, r, stream)
+        fl = 2.0 * M * n * k
+        out[f"{name}_{n}x{k}_m{M}"] = {
+            "us_forward": round(ms_f * 1e3, 2), "us_dot": round(ms_d * 1e3, 2),
+            "TFLOP/s_forward": round(fl / (ms_f * 1e-3) / 1e12, 1),
+            "TFLOP/s_dot": round(fl / (ms_d * 1e-3) / 1e12, 1),
+            "frac_bf16_peak_dot": round(fl / (ms_d * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        log(f"gemm {name} M={M}: forward {ms_f * 1e3:.1f} us, dot {ms_d * 1e3:.1f} us "
+            f"({fl / (ms_d * 1e-3) / 1e12:.0f} TFLOP/s)")
+        del g_f, g_d, qm, x, y, act
+    return out
 
 
 def stack_bench(torch, qz, gen, dev, stream):
