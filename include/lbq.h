@@ -20,10 +20,11 @@
  *   - Weights are GGUF blocks in their on-disk byte layout: row-major
  *     [n][k / block_size] blocks, rows contiguous along k
  *     (GGUF ne0 = k; /root/reference/src/gguf/parser.rs:180-199).
- *   - A context owns per-device scratch (quantised activations).  Calls that
- *     share a context must be ordered on one stream (the reference runs every
- *     forward on one model thread, src/engine/model_runner.rs:236,383).
- *     Weight handles are immutable and may be read concurrently.
+ *   - A context owns per-device scratch (quantised activations, the batched
+ *     GEMM's workspace), grown on demand.  Calls that share a context must be
+ *     ordered on one stream (the reference runs every forward on one model
+ *     thread, src/engine/model_runner.rs:236,383).  Weight handles are
+ *     immutable and may be read concurrently.
  */
 #ifndef LBQ_H
 #define LBQ_H
@@ -94,8 +95,10 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * x and y are contiguous f32 device buffers; any leading dims of the
  * reference's [.., k] tensor are flattened into m.  The activation is
  * quantised to Q8_K (k-quant weights) or Q8_0 (Q8_0 weights) exactly as the
- * reference CPU path does, and each output is formed from integer
- * sub-block dot products.  m == 0 is a no-op. */
+ * reference CPU path does.  For m <= 8 (and Q8_0) each output is formed from
+ * integer sub-block dot products as in the reference; for k-quant weights at
+ * m > 8 the products run on MFMA from fp16 roundings of the same activation
+ * and weight values (about 4e-4 relative on a row).  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
 /* Quantised-activation handle: the two halves of QMatMul::forward as separate
