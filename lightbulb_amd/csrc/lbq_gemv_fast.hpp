@@ -6,8 +6,9 @@
 //     pieces side by side, so a wave instruction reads whole 128-byte runs;
 //   - the quantised activation sits in LDS in a padded layout (odd multiples of
 //     16 bytes per block), so lanes reading different blocks hit different banks;
-//   - waves are persistent, each owning a contiguous range of row groups and
-//     double-buffering the weight loads of its next group;
+//   - waves are persistent, each owning a contiguous range of row groups with
+//     the weight loads of the next one (Q6_K, Q8_0) or two (Q4_K, Q5_K) groups
+//     in flight while a group is computed;
 //   - with FUSED, the workgroup quantises x itself (Q8_K or Q8_0, bit-identical
 //     to the standalone kernels) into LDS first; the loads of the first row
 //     group are issued before the quantisation so their latency overlaps it;
@@ -121,14 +122,20 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t lo_word, uint32_t hi_wo
     return a | (b << 16);
 }
 
+// Q4_K / Q5_K: piece p (0..7) of a block is qs bytes 16p..16p+15, i.e. values
+// 64c + 16h + [0,16) (low nibbles) and 64c + 32 + 16h + [0,16) (high) with c = p/2,
+// h = p%2.  The eight lanes of a block each load one dword of its 16-byte header
+// (dword p%4) and share the four through DPP quad broadcasts, instead of each
+// holding the whole header.
 template <int TYPE>
 struct FastK45 {  // Q4_K and Q5_K
     static constexpr int PPB = 8, VALS = 256, XW = 10;
     static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
-    struct Raw { uint4 hdr, qh, qs; };
+    static constexpr int NBUF = 3;  // three-buffer ring allowed (see k_gemv1)
+    struct Raw { uint32_t hw; uint4 qh, qs; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         Raw r;
-        r.hdr = ld_u4(blk);
+        r.hw = *reinterpret_cast<const uint32_t *>(blk + 4 * (p & 3));
         if (TYPE == TYPE_Q5_K) r.qh = ld_u4(blk + 16 + 16 * (p & 1));
         r.qs = ld_u4(blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 16 * p);
         return r;
@@ -158,8 +165,11 @@ struct FastK45 {  // Q4_K and Q5_K
     }
     __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
         const int c = p >> 1;
+        // header dword i sits in lane i of every quad (quad_perm [i,i,i,i])
+        const uint32_t h0 = dpp_u32<0x00>(r.hw), s0 = dpp_u32<0x55>(r.hw);
+        const uint32_t s1 = dpp_u32<0xAA>(r.hw), s2 = dpp_u32<0xFF>(r.hw);
         uint32_t sc2, m2;
-        k4_scale_pair(r.hdr.y, r.hdr.z, r.hdr.w, c, &sc2, &m2);
+        k4_scale_pair(s0, s1, s2, c, &sc2, &m2);
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
         uint32_t lo[4], hi[4];
         if (TYPE == TYPE_Q4_K) {
@@ -176,19 +186,19 @@ struct FastK45 {  // Q4_K and Q5_K
                 hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
             }
         }
-        int s0 = dot4(lo[0], xr[0], 0);
-        s0 = dot4(lo[1], xr[1], s0);
-        s0 = dot4(lo[2], xr[2], s0);
-        s0 = dot4(lo[3], xr[3], s0);
-        int s1 = dot4(hi[0], xr[4], 0);
-        s1 = dot4(hi[1], xr[5], s1);
-        s1 = dot4(hi[2], xr[6], s1);
-        s1 = dot4(hi[3], xr[7], s1);
-        const int isum = __mul24((int)(sc2 & 0xffu), s0) + __mul24((int)(sc2 >> 8), s1);
+        int sl = dot4(lo[0], xr[0], 0);
+        sl = dot4(lo[1], xr[1], sl);
+        sl = dot4(lo[2], xr[2], sl);
+        sl = dot4(lo[3], xr[3], sl);
+        int sh = dot4(hi[0], xr[4], 0);
+        sh = dot4(hi[1], xr[5], sh);
+        sh = dot4(hi[2], xr[6], sh);
+        sh = dot4(hi[3], xr[7], sh);
+        const int isum = __mul24((int)(sc2 & 0xffu), sl) + __mul24((int)(sc2 >> 8), sh);
         const int msum = __mul24((int)(m2 & 0xffu), (int)(int16_t)(xr[8] & 0xffffu)) +
                          __mul24((int)(m2 >> 8), (int)(int16_t)(xr[8] >> 16));
         const float dx = __uint_as_float(xr[9]);
-        return (h2f(r.hdr.x & 0xffffu) * dx) * (float)isum - (h2f(r.hdr.x >> 16) * dx) * (float)msum;
+        return (h2f(h0 & 0xffffu) * dx) * (float)isum - (h2f(h0 >> 16) * dx) * (float)msum;
     }
 };
 template <> struct Fast<TYPE_Q4_K> : FastK45<TYPE_Q4_K> {};
@@ -198,6 +208,7 @@ template <> struct Fast<TYPE_Q5_K> : FastK45<TYPE_Q5_K> {};
 template <>
 struct Fast<TYPE_Q6_K> {
     static constexpr int PPB = 4, VALS = 256, XW = 19, BYTES = 210;
+    static constexpr int NBUF = 2;
     struct Raw { uint32_t qa[4], qb[4], qh[4], s0, s1, dbits; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         const int n = p >> 1, h = p & 1;
@@ -264,6 +275,7 @@ struct Fast<TYPE_Q6_K> {
 template <>
 struct Fast<TYPE_Q8_0> {
     static constexpr int PPB = 1, VALS = 32, XW = 9, BYTES = 34;
+    static constexpr int NBUF = 2;
     struct Raw { uint32_t w[9]; uint32_t mis; };
     __device__ static Raw load(const uint8_t *blk, int) {
         Raw r;
@@ -382,7 +394,7 @@ __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *s
 #pragma unroll
     for (int j = 0; j < NC; j++) {
         const int i = min(t + 256 * j, ncode - 1);  // clamped duplicates rewrite equal data
-        *reinterpret_cast<uint4 *>(sx + (i / CPB) * XS + 16 * (i % CPB)) = v[j];
+        *reinterpret_cast<uint4 *>(sx + (i / CPB) * XS + 16 * (i % CPB)) = make_uint4(v[j].x, v[j].y, v[j].z, v[j].w);
     }
     if constexpr (TYPE != TYPE_Q8_0) {
         const int i = min(t, 2 * nbx - 1);
@@ -423,8 +435,21 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
         }
     };
 
-    Raw bufA[IT], bufB[IT];
-    load_group(g0 < g1 ? g0 : 0, bufA);
+    // group indices are clamped into the wave's range (a wave without groups
+    // touches row group 0), so every load is unconditional
+    const int64_t glast = g0 < g1 ? g1 - 1 : 0;
+    auto gc = [&](int64_t g) { return g < glast ? g : glast; };
+    // Ring of NBUF row-group buffers: NBUF - 1 groups are in flight while one is
+    // computed, and the first NBUF - 1 are issued before the x prologue so the
+    // weight stream overlaps it.  Loads are clamped, not skipped (no branches
+    // around loads).  Three buffers measured best: deeper rings, and issuing a
+    // wave's whole stream up front, leave every wave waiting for its first rows
+    // while the whole matrix is in flight, and bunch the compute at the end.
+    // Deep rows (IT > 4) keep two buffers (registers).
+    constexpr int NBUF = (F::NBUF == 3 && IT <= 4) ? 3 : 2;
+    Raw ring[NBUF][IT];
+#pragma unroll
+    for (int k = 0; k < NBUF - 1; k++) load_group(gc(g0 + k), ring[k]);
     __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the prologue
 
     extern __shared__ __align__(16) uint8_t sx[];
@@ -460,15 +485,14 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
         }
     };
 
-    // rolling buffer: issue group g+1's loads, then compute group g
-    for (int64_t g = g0; g < g1; g++) {
-        const int64_t gn = g + 1 < g1 ? g + 1 : g;  // last pass reloads (cached) data: no branch
-        load_group(gn, bufB);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_group(g, bufA);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int64_t g = g0; g < g1; g += NBUF) {
 #pragma unroll
-        for (int i = 0; i < IT; i++) bufA[i] = bufB[i];
+        for (int k = 0; k < NBUF; k++) {
+            load_group(gc(g + k + NBUF - 1), ring[(k + NBUF - 1) % NBUF]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k == 0 || g + k < g1) compute_group(g + k, ring[k]);  // wave-uniform
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 }
 

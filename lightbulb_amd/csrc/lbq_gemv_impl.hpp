@@ -435,10 +435,17 @@ static hipError_t run_m(const GemvCfg &c, const uint8_t *w, const PGeom &g, cons
 template <int TYPE>
 static bool fast_shape(int nb, int *rpw, int *it) {
     constexpr int PPB = Fast<TYPE>::PPB;
+    if (const char *e = getenv("LBQ_GEMV1_CFG")) {  // tuning override "rpw,it"
+        int r = 0, i = 0;
+        if (sscanf(e, "%d,%d", &r, &i) == 2 && r >= 1 && i >= 1 && (64 / r / PPB) * i >= nb) {
+            *rpw = r; *it = i;
+            return true;
+        }
+    }
     if (PPB == 8) {  // Q4_K, Q5_K
         if (nb <= 4) { *rpw = 2; *it = 1; return true; }
         if (nb <= 8) { *rpw = 2; *it = 2; return true; }
-        if (nb <= 16) { *rpw = 2; *it = 4; return true; }
+        if (nb <= 16) { *rpw = 1; *it = 2; return true; }
         if (nb <= 32) { *rpw = 1; *it = 4; return true; }
         if (nb <= 56) { *rpw = 1; *it = 7; return true; }
         if (nb <= 64) { *rpw = 1; *it = 8; return true; }
@@ -480,7 +487,7 @@ static hipError_t run_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int n
 #define LBQ_FAST(R, I) \
     if (rpw == R && it == I) return launch_fast<TYPE, R, I>(w, n, row_bytes, nb, x, act, y, st);
     if constexpr (Fast<TYPE>::PPB == 8) {
-        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
+        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
     } else if constexpr (Fast<TYPE>::PPB == 4) {
         LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(1, 2) LBQ_FAST(1, 4)
     } else {

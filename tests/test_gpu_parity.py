@@ -182,6 +182,26 @@ def test_qmatmul_mfma_ragged(oracle, lbq, dev, t):
                           oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64), tight_bound(t, m))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_decode_row_partition(oracle, lbq, dev, t, k):
+    # m = 1 at the Llama-3 row lengths: every row split across waves (1 .. 8 rows
+    # per wave), ragged row counts, fused quantisation and pre-quantised x
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    rng = np.random.default_rng(70 + t + k)
+    for n in (1, 3, 257, 1000, 5000):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+        xd = to_dev(x, dev)
+        y1 = qm.forward(xd)
+        y2 = qm.forward_quantized(QActivation.for_weight(qm, 1).quantize(xd))
+        torch.cuda.synchronize()
+        assert_rows_close(y1.cpu().numpy(), ref)
+        assert_rows_close(y2.cpu().numpy(), ref)
+
+
 def test_qmatmul_shapes_and_errors(oracle, lbq, dev):
     from lightbulb_amd.quantized import QMatMul, QTensor, QuantizableLinear
     rng = np.random.default_rng(53)
