@@ -325,27 +325,67 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
     if constexpr (TYPE != TYPE_Q8_0) {
-        // wave w quantises blocks w, w+4, ... (nbx <= 64: one pass); loads first
-        constexpr int MAXB = 16;
-        float v[MAXB][4];
+        // 16 lanes per 256-value block, 16 consecutive values per lane, so the
+        // workgroup quantises 16 blocks per pass (nbx <= 64: at most 4 passes).
+        // Selection and arithmetic as q8k_block_wave: the first value of largest
+        // |x| (NaN never chosen) sets iscale = -128/max; q = min(127, round(iscale*x));
+        // d = 1/iscale; a lane's 16 codes are exactly one bsums entry.
+        constexpr int MAXP = 4;
+        const int t = threadIdx.x, sub = t & 15;
+        const int np = (nbx + 15) >> 4;  // workgroup-uniform
+        float v[MAXP][16];
 #pragma unroll
-        for (int j = 0; j < MAXB; j++) {
-            const int b = min(wave + 4 * j, nbx - 1);
-            load4f(x + (int64_t)b * QK_K + lane * 4, vec, v[j]);
+        for (int j = 0; j < MAXP; j++) {
+            const int b = min(16 * j + (t >> 4), nbx - 1);
+            const float4 *src = reinterpret_cast<const float4 *>(x + (int64_t)b * QK_K + 16 * sub);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 f = src[i];
+                v[j][4 * i] = f.x; v[j][4 * i + 1] = f.y; v[j][4 * i + 2] = f.z; v[j][4 * i + 3] = f.w;
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
-        const int jmax = (nbx - wave + 3) / 4;  // wave-uniform
 #pragma unroll
-        for (int j = 0; j < MAXB; j++) {
-            if (j < jmax) {
-                const int b = wave + 4 * j;
-                int s;
-                float d;
-                const uint32_t packed = q8k_block_wave_dpp(v[j], lane, &s, &d);
-                uint8_t *xb = sx + b * XS_K;
-                *reinterpret_cast<uint32_t *>(xb + lane * 4) = packed;
-                if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(xb + 256 + 2 * (lane >> 2)) = (int16_t)s;
-                if (lane == 0) *reinterpret_cast<float *>(xb + 288) = d;
+        for (int j = 0; j < MAXP; j++) {
+            if (j < np) {
+                // |x| as ordered bits (NaN -> 0); the lane's max and its first index
+                uint32_t am = 0, key = 0xffffffffu;
+#pragma unroll
+                for (int i = 15; i >= 0; i--) {
+                    const float f = fabsf(v[j][i]);
+                    const uint32_t a = (f == f) ? __float_as_uint(f) : 0u;
+                    if (a >= am) {  // scanning down: ties keep the lower index
+                        key = a == am ? min(key, (uint32_t)(2 * (16 * sub + i)) | (__float_as_uint(v[j][i]) >> 31))
+                                      : (uint32_t)(2 * (16 * sub + i)) | (__float_as_uint(v[j][i]) >> 31);
+                        am = a;
+                    }
+                }
+                const uint32_t bmax = row_max_u32(am);
+                key = am == bmax ? key : 0xffffffffu;
+                key = row_min_u32(key);  // (first index of the block max) << 1 | its sign
+                uint32_t packed[4] = {0u, 0u, 0u, 0u};
+                int sum = 0;
+                float d = 0.f;
+                if (bmax != 0u) {  // uniform within the 16-lane block
+                    const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
+                    const float iscale = -128.f / mx;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        float r = fminf(roundf(iscale * v[j][i]), 127.f);
+                        r = fmaxf(r, -128.f);
+                        const int q = (int)r;
+                        sum += q;
+                        packed[i >> 2] |= ((uint32_t)q & 0xffu) << (8 * (i & 3));
+                    }
+                    d = 1.f / iscale;
+                }
+                const int b = 16 * j + (t >> 4);
+                if (b < nbx) {
+                    uint8_t *xb = sx + b * XS_K;
+                    *reinterpret_cast<uint4 *>(xb + 16 * sub) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                    *reinterpret_cast<int16_t *>(xb + 256 + 2 * sub) = (int16_t)sum;
+                    if (sub == 0) *reinterpret_cast<float *>(xb + 288) = d;
+                }
             }
         }
     } else {

@@ -202,6 +202,26 @@ def test_decode_row_partition(oracle, lbq, dev, t, k):
         assert_rows_close(y2.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t):
+    # At m = 1 and k <= 4096 the GEMV quantises x in its own prologue.  The same
+    # kernel fed x quantised by the standalone (bit-exact) kernel runs the same
+    # integer arithmetic, so the two outputs must agree to the bit.
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    rng = np.random.default_rng(90 + t)
+    n, k = 300, 4096
+    w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
+    qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+    xs = np.concatenate([_special_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
+    xs[-1, rng.random(k) < 0.01] *= 20
+    for row in xs:
+        xd = to_dev(row[None, :], dev)
+        y_fused = qm.forward(xd)
+        y_act = qm.forward_quantized(QActivation.for_weight(qm, 1).quantize(xd))
+        torch.cuda.synchronize()
+        assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
+
+
 def test_qmatmul_shapes_and_errors(oracle, lbq, dev):
     from lightbulb_amd.quantized import QMatMul, QTensor, QuantizableLinear
     rng = np.random.default_rng(53)
