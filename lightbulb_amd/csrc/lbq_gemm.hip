@@ -32,6 +32,8 @@
 // Shapes with few output tiles split k over S workgroups (split-K) that write
 // partial sums to the workspace; a second kernel adds them in a fixed order, so
 // results do not depend on scheduling.
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "lbq_device.hpp"
@@ -75,26 +77,25 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint
 
 // ---------------------------------------------------------------------------
 // Pre-pass: Q8_K rows (codes + block scales) -> fp16 operand rows in the GEMM's k
-// order, and the row exponent e_m.  One wave per row.
+// order, and the row exponent e_m.  One 256-thread workgroup per row; every
+// thread reads the row's block scales (the same few addresses across the
+// workgroup), takes their maximum, and converts 16-code chunks.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
                                                  int *__restrict__ erow) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t m = (int64_t)blockIdx.x * 4 + wave;
-    if (m >= M) return;
+    const int64_t m = blockIdx.x;
+    const int t = threadIdx.x;
     const int nb = act.nb;
     const float *xd = act.xd + m * nb;
     float mx = 0.f;
-    for (int b = lane; b < nb; b += 64) mx = fmaxf(mx, fabsf(xd[b]));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int b = 0; b < nb; b++) mx = fmaxf(mx, fabsf(xd[b]));
     // max |d_x| = f*2^E, f in [0.5, 1): |q8*d_x| < 128*2^E, so e = E - 8 keeps the
     // row's values below 2^15 and its largest at or above 2^14
     const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;
-    if (lane == 0) erow[m] = e;
+    if (t == 0) erow[m] = e;
     const int8_t *q = act.xq + m * act.k;
     _Float16 *a = A + m * act.k;
-    for (int64_t c = 16 * lane; c < act.k; c += 1024) {
+    for (int64_t c = 16 * t; c < act.k; c += 16 * 256) {
         const uint4 w = *reinterpret_cast<const uint4 *>(q + c);
         const float sx = __builtin_amdgcn_ldexpf(xd[c / KB], -e);
         const float cc = -1152.f * sx;
@@ -432,6 +433,152 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// Tall tiles for m >= 256: each wave owns 256 rows x 32 columns (8 x 1 MFMA
+// tiles), so every B operand it builds feeds 8 MFMAs (about 2.3 VALU per MFMA
+// including the scale prep -- within what gfx950 co-issues next to MFMA, where
+// the 128-row kernel needs 4+).  Workgroup tile 256 x 128.  The activation tile
+// is staged in two stages per block: stage t holds, for lane half h, values
+// 128h + 64t + [0, 64) -- exactly k-steps 8t..8t+7 of the k order above -- so a
+// double-buffered stage (256 rows x 128 values) fits in LDS.
+// ---------------------------------------------------------------------------
+constexpr int TBM = 256, TBN = 128;
+constexpr int TSLD = 136;  // stage row stride in halfs (272 B: conflict-free b128 reads)
+
+// Per stage (8 k-steps x 8 MFMA regions), besides the A operands of the k-step
+// AH ahead and the B operand of the next one:
+//   k-step 0    : the next stage's activation loads (2 per region);
+//   k-steps 1-2 : in stage 0, the next block's weight loads;
+//   k-step 2    : barrier -- every wave is done with the other buffer;
+//   k-step 5    : the next stage's activations into the other buffer;
+//   k-step 6    : barrier -- that buffer is complete; from k-step 8 - AH on, the
+//                 next stage's first A operands are read from it;
+//   k-step 7    : in stage 1, the next block's scales and first B operand.
+template <int TYPE>
+__global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
+                                                   const _Float16 *__restrict__ A, const int *__restrict__ erow,
+                                                   int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
+    using B = GB<TYPE>;
+    __shared__ __align__(16) _Float16 As[2][TBM][TSLD];
+    __shared__ int Es[TBM];
+
+    const int G = (int)gridDim.x, L = (int)blockIdx.x;
+    const int T = (G & 7) == 0 ? (L & 7) * (G >> 3) + (L >> 3) : L;
+    const int tm = T % g.tiles_m, tn = (T / g.tiles_m) % g.tiles_n, z = T / (g.tiles_m * g.tiles_n);
+    const int nb = (int)(K / KB);
+    const int b0 = z * g.bps, b1 = min(nb, b0 + g.bps);
+    const int64_t m0 = (int64_t)tm * TBM, n0 = (int64_t)tn * TBN;
+    float *y = out + (int64_t)z * g.split_stride;
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
+    const uint8_t *wrow = W + min(n0 + 32 * wave + lr, N - 1) * row_bytes;
+    // staging: piece f = 256 i + t of a stage is row f/16, half (f/8)%2 (values
+    // 128*half + 64t + ...), 16-byte piece f%8; rows past M exist in the operand
+    // buffer (whole tiles), so no clamping
+    const int srow = t >> 4, shh = (t >> 3) & 1, spc = t & 7;
+    const _Float16 *abase = A + (m0 + srow) * K + 128 * shh + 8 * spc;
+    Es[t] = erow[min(m0 + t, M - 1)];
+
+    typename B::Raw raw;
+    typename B::Prep p;
+    uint4 ra[16];
+    auto a_load = [&](int u, int i) {
+        ra[i] = *reinterpret_cast<const uint4 *>(abase + (int64_t)i * 16 * K + (int64_t)(u >> 1) * KB + 64 * (u & 1));
+    };
+    auto a_store = [&](int buf, int i) {
+        *reinterpret_cast<uint4 *>(&As[buf][16 * i + srow][64 * shh + 8 * spc]) = make_uint4(ra[i].x, ra[i].y, ra[i].z, ra[i].w);
+    };
+    auto w_load = [&](int b, int q) { B::load_part(wrow + (int64_t)b * B::BYTES, h, raw, q); };
+    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, p); };
+
+    floatx16 acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
+
+#pragma unroll
+    for (int i = 0; i < 16; i++) a_load(2 * b0, i);
+#pragma unroll
+    for (int q = 0; q < B::NL; q++) w_load(b0, q);
+#pragma unroll
+    for (int i = 0; i < 16; i++) a_store(0, i);
+    __syncthreads();
+    w_prep(b0);
+    const _Float16 *al0 = &As[0][lr][64 * h], *al1 = &As[1][lr][64 * h];
+    // A operands are read AH k-steps ahead (ar[j] holds k-step ks + j): with one
+    // wave per SIMD, 8 KB of reads per k-step need that depth to keep the LDS
+    // busy.  Q6_K's larger weight state leaves registers for one step only.
+    constexpr int AH = TYPE == TYPE_Q6_K ? 1 : 2;
+    half8 ar[AH][8];
+    uint32_t bcur[4];
+#pragma unroll
+    for (int j = 0; j < AH; j++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) ar[j][i] = *reinterpret_cast<const half8 *>(al0 + 32 * i * TSLD + 8 * j);
+#pragma unroll
+    for (int d = 0; d < 4; d++) bcur[d] = B::dw(p, 0, d);
+
+    const int u_end = 2 * b1;
+    auto stage = [&](int u, int buf) {
+        const int ts = u & 1;
+        const int un = min(u + 1, u_end - 1);          // clamped: the last stage re-stages itself
+        const int bn = min((u >> 1) + 1, b1 - 1);
+        const _Float16 *al = buf ? al1 : al0, *aln = buf ? al0 : al1;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const int s = 8 * ts + ks;  // k-step within the block
+            half8 an[8];
+            uint32_t bnxt[4];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (ks == 2 && i == 0) __syncthreads();  // every wave is done with the other buffer
+                if (ks == 6 && i == 0) __syncthreads();  // the other buffer holds the next stage
+                const half8 bo = __builtin_bit_cast(half8, make_uint4(bcur[0], bcur[1], bcur[2], bcur[3]));
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ar[0][i], bo, acc[i], 0, 0, 0);
+                if (ks + AH < 8) an[i] = *reinterpret_cast<const half8 *>(al + 32 * i * TSLD + 8 * (ks + AH));
+                else an[i] = *reinterpret_cast<const half8 *>(aln + 32 * i * TSLD + 8 * (ks + AH - 8));
+                if (s < 15) {
+                    if (i < 4) bnxt[i] = B::dw(p, s + 1, i);
+                } else {
+                    if (i == 0) w_prep(bn);
+                    else if (i <= 4) bnxt[i - 1] = B::dw(p, 0, i - 1);
+                }
+                if (ks == 0) { a_load(un, 2 * i); a_load(un, 2 * i + 1); }
+                if (ts == 0 && (ks == 1 || ks == 2)) {
+                    const int q = 8 * (ks - 1) + i;
+                    if (q < B::NL) w_load(bn, q);
+                }
+                if (ks == 5) { a_store(buf ^ 1, 2 * i); a_store(buf ^ 1, 2 * i + 1); }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+#pragma unroll
+                for (int j = 0; j + 1 < AH; j++) ar[j][i] = ar[j + 1][i];
+                ar[AH - 1][i] = an[i];
+            }
+#pragma unroll
+            for (int d = 0; d < 4; d++) bcur[d] = bnxt[d];
+        }
+    };
+    for (int u = 2 * b0; u < u_end; u += 2) {
+        stage(u, 0);
+        stage(u + 1, 1);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int64_t m = m0 + r;
+            const int64_t n = n0 + 32 * wave + lr;
+            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r]);
+        }
+    }
+}
+
 // y = sum over s < S of part[s] (fixed order), count values.
 __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int S, int64_t count,
                                                    float *__restrict__ y) {
@@ -448,14 +595,16 @@ struct Plan {
     int mt, tiles_m, tiles_n, splits, bps;
 };
 
+// mt = 8 selects the tall kernel (256 x 128 tiles) for m >= 256
 Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     Plan p;
-    p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
+    if (m >= 256 && !getenv("LBQ_GEMM_NO_TALL")) p.mt = 8;
+    else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
     p.tiles_m = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
-    p.tiles_n = (int)((n + BN - 1) / BN);
+    p.tiles_n = (int)((n + (p.mt == 8 ? TBN : BN) - 1) / (p.mt == 8 ? TBN : BN));
     const int nb = (int)(k / KB);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-    const int occ = (p.mt == 4 || type == TYPE_Q6_K || (type == TYPE_Q5_K && p.mt == 2)) ? 1 : 2;  // gemm_occupancy
+    const int occ = (p.mt >= 4 || type == TYPE_Q6_K || (type == TYPE_Q5_K && p.mt == 2)) ? 1 : 2;  // gemm_occupancy
     const int64_t slots = (int64_t)num_cus() * occ;
     int s = 1;
     if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
@@ -470,6 +619,7 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
     const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
     switch (p.mt) {
+    case 8: k_gemm_t<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 2: k_gemm<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     default:
@@ -511,7 +661,7 @@ hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t
         _Float16 *a = reinterpret_cast<_Float16 *>(base + L.a_off);
         int *erow = reinterpret_cast<int *>(base + L.e_off);
         float *part = reinterpret_cast<float *>(base + L.part_off);
-        k_act_f16<<<(unsigned)((m + 3) / 4), 256, 0, st>>>(act, m, a, erow);
+        k_act_f16<<<(unsigned)m, 256, 0, st>>>(act, m, a, erow);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         float *out = p.splits > 1 ? part : y;

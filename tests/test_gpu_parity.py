@@ -222,6 +222,19 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t):
         assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
+    # m >= 256 takes the 256 x 128 tile kernel: ragged m and n, odd and even block counts
+    rng = np.random.default_rng(80 + t)
+    for (m, n, k) in ((256, 128, 256), (300, 200, 256 * 3), (520, 390, 256 * 4)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        rows = np.r_[0:4, m // 2:m // 2 + 4, m - 4:m]
+        y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y[rows], ref, tight_bound(t, m))
+
+
 def test_qmatmul_shapes_and_errors(oracle, lbq, dev):
     from lightbulb_amd.quantized import QMatMul, QTensor, QuantizableLinear
     rng = np.random.default_rng(53)
