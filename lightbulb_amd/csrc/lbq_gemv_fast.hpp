@@ -320,8 +320,11 @@ struct Fast<TYPE_Q8_0> {
 // ---------------------------------------------------------------------------
 // Fused activation quantisation into LDS by the whole workgroup (m = 1).
 // ---------------------------------------------------------------------------
-template <int TYPE>
-__device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx) {
+// `between` runs after the x loads are issued and before any of them is used:
+// loads issued there (the weight ring) queue behind x, so the in-order memory
+// counter lets the quantisation start as soon as x has arrived.
+template <int TYPE, class Between>
+__device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
     if constexpr (TYPE != TYPE_Q8_0) {
@@ -345,37 +348,49 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < MAXP; j++) {
-            if (j < np) {
-                // |x| as ordered bits (NaN -> 0); the lane's max and its first index
-                uint32_t am = 0, key = 0xffffffffu;
+            if (j == 0 || j < np) {  // pass 0 unconditional: its loads stay ahead of the ring
+                // the lane's largest |x| and the first value holding it (ascending
+                // scan, strict >: ties keep the lower index; a NaN compares false
+                // and is never chosen)
+                float am = 0.f, av = 0.f;
 #pragma unroll
-                for (int i = 15; i >= 0; i--) {
-                    const float f = fabsf(v[j][i]);
-                    const uint32_t a = (f == f) ? __float_as_uint(f) : 0u;
-                    if (a >= am) {  // scanning down: ties keep the lower index
-                        key = a == am ? min(key, (uint32_t)(2 * (16 * sub + i)) | (__float_as_uint(v[j][i]) >> 31))
-                                      : (uint32_t)(2 * (16 * sub + i)) | (__float_as_uint(v[j][i]) >> 31);
-                        am = a;
-                    }
+                for (int i = 0; i < 16; i++) {
+                    const bool gt = fabsf(v[j][i]) > am;
+                    av = gt ? v[j][i] : av;
+                    am = gt ? fabsf(v[j][i]) : am;
                 }
-                const uint32_t bmax = row_max_u32(am);
-                key = am == bmax ? key : 0xffffffffu;
-                key = row_min_u32(key);  // (first index of the block max) << 1 | its sign
+                const uint32_t bmax = row_max_u32(__float_as_uint(am));  // non-negative: bits order as values
+                uint32_t key = __float_as_uint(am) == bmax ? ((uint32_t)sub << 1) | (__float_as_uint(av) >> 31) : 0xffffffffu;
+                key = row_min_u32(key);  // the first lane holding the block max, and that value's sign
                 uint32_t packed[4] = {0u, 0u, 0u, 0u};
                 int sum = 0;
                 float d = 0.f;
                 if (bmax != 0u) {  // uniform within the 16-lane block
                     const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
                     const float iscale = -128.f / mx;
+                    int q[16];
 #pragma unroll
                     for (int i = 0; i < 16; i++) {
-                        float r = fminf(roundf(iscale * v[j][i]), 127.f);
-                        r = fmaxf(r, -128.f);
-                        const int q = (int)r;
-                        sum += q;
-                        packed[i >> 2] |= ((uint32_t)q & 0xffu) << (8 * (i & 3));
+#pragma clang fp contract(off)
+                        // min(roundf(iscale * x), 127): for |t| <= 2^23, adding 0.5 - 2^-25
+                        // with t's sign and truncating rounds exactly the halves (and
+                        // everything above them) away from zero -- checked for every
+                        // such float; fminf sends NaN to 127 as the reference's min
+                        // does.  Separate roundings: no fma contraction.
+                        const float tt = iscale * v[j][i];
+                        const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
+                        q[i] = max(-128, (int)r);
+                        sum += q[i];
+                    }
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+                        const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
+                        const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
+                        packed[w] = lo | (hi << 16);
                     }
                     d = 1.f / iscale;
                 }
@@ -399,6 +414,8 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             load4f(x + (int64_t)b * QK8_0 + sub * 4, vec, v[j]);
         }
         __builtin_amdgcn_sched_barrier(0);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < MAXJ; j++) {
             if (32 * j < nbx) {  // uniform across the workgroup: shuffles stay convergent
@@ -416,9 +433,10 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
 
 // Pre-quantised activations (split global layout) -> the LDS layout.  Straight-line
 // code for nbx <= 64 (k <= 16384, the fast path's limit): every load is issued
-// before any store, with indices clamped into range instead of branches.
-template <int TYPE>
-__device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx) {
+// before any store, with indices clamped into range instead of branches;
+// `between` as for quantise_x_lds.
+template <int TYPE, class Between>
+__device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx, Between between) {
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
     constexpr int CPB = TYPE == TYPE_Q8_0 ? 2 : 16;  // 16-byte code chunks per block
     constexpr int NC = TYPE == TYPE_Q8_0 ? 4 : 4;    // code chunks per thread (<= 1024 total)
@@ -429,7 +447,11 @@ __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *s
     for (int j = 0; j < NC; j++) v[j] = *reinterpret_cast<const uint4 *>(a.xq + (int64_t)min(t + 256 * j, ncode - 1) * 16);
     uint4 bsv = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (TYPE != TYPE_Q8_0) bsv = *reinterpret_cast<const uint4 *>(a.xbs + (int64_t)min(t, 2 * nbx - 1) * 8);
-    const float d = a.xd[min(t, nbx - 1)];
+    // block scales: nbx <= 512, so two per thread cover every block
+    const float d0 = a.xd[min(t, nbx - 1)];
+    const float d1 = a.xd[min(t + 256, nbx - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    between();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NC; j++) {
@@ -440,7 +462,8 @@ __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *s
         const int i = min(t, 2 * nbx - 1);
         *reinterpret_cast<uint4 *>(sx + (i >> 1) * XS + 256 + 16 * (i & 1)) = bsv;
     }
-    *reinterpret_cast<float *>(sx + min(t, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d;
+    *reinterpret_cast<float *>(sx + min(t, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d0;
+    *reinterpret_cast<float *>(sx + min(t + 256, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d1;
     __syncthreads();
 }
 
@@ -480,24 +503,26 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
     const int64_t glast = g0 < g1 ? g1 - 1 : 0;
     auto gc = [&](int64_t g) { return g < glast ? g : glast; };
     // Ring of NBUF row-group buffers: NBUF - 1 groups are in flight while one is
-    // computed, and the first NBUF - 1 are issued before the x prologue so the
-    // weight stream overlaps it.  Loads are clamped, not skipped (no branches
+    // computed, and the first NBUF - 1 are issued inside the x prologue, right
+    // after its x loads, so the weight stream overlaps the prologue without the
+    // prologue waiting for it.  Loads are clamped, not skipped (no branches
     // around loads).  Three buffers measured best: deeper rings, and issuing a
     // wave's whole stream up front, leave every wave waiting for its first rows
     // while the whole matrix is in flight, and bunch the compute at the end.
     // Deep rows (IT > 4) keep two buffers (registers).
     constexpr int NBUF = (F::NBUF == 3 && IT <= 4) ? 3 : 2;
     Raw ring[NBUF][IT];
+    auto issue_ring = [&] {
 #pragma unroll
-    for (int k = 0; k < NBUF - 1; k++) load_group(gc(g0 + k), ring[k]);
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the prologue
+        for (int k = 0; k < NBUF - 1; k++) load_group(gc(g0 + k), ring[k]);
+    };
 
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
-    if constexpr (FUSED) quantise_x_lds<TYPE>(x, nb, sx);
-    else copy_x_lds<TYPE>(act, nb, sx);
+    if constexpr (FUSED) quantise_x_lds<TYPE>(x, nb, sx, issue_ring);
+    else copy_x_lds<TYPE>(act, nb, sx, issue_ring);
 
-    auto compute_group = [&](int64_t g, const Raw *buf) {
+    auto compute_group = [&](int64_t g, const Raw *buf, bool store) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < IT; i++) {
@@ -521,18 +546,22 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
                 s = __int_as_float(rl(__float_as_uint(acc), 16 * q));
             }
             const int64_t rq = g * RPW + q;
-            if (lane == LPR * q && rq < n) y[rq] = s;
+            if (store && lane == LPR * q && rq < n) y[rq] = s;
         }
     };
 
-    for (int64_t g = g0; g < g1; g += NBUF) {
+    // The first pass runs even for a wave without groups (it stores nothing):
+    // the ring's first loads then have an unconditional use and stay where they
+    // are issued, ahead of the prologue, instead of being sunk into the loop.
+    for (int64_t g = g0;; g += NBUF) {
 #pragma unroll
         for (int k = 0; k < NBUF; k++) {
             load_group(gc(g + k + NBUF - 1), ring[(k + NBUF - 1) % NBUF]);
             __builtin_amdgcn_sched_barrier(0);
-            if (k == 0 || g + k < g1) compute_group(g + k, ring[k]);  // wave-uniform
+            if (k == 0 || g + k < g1) compute_group(g + k, ring[k], g + k < g1);  // wave-uniform
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (g + NBUF >= g1) break;
     }
 }
 

@@ -468,8 +468,12 @@ template <int TYPE, int RPW, int IT>
 static hipError_t launch_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int nb, const float *x,
                               const ActView &act, float *y, hipStream_t st) {
     const int64_t ng = (n + RPW - 1) / RPW;
-    int wpc = 8;
-    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : 8;
+    // Waves per CU.  With the fused prologue every workgroup quantises all of x,
+    // so for fewer rows (less weight per CU to hide it behind) one workgroup per
+    // CU does better; measured on Q4_K: 4096 x 4096 5.3 us at 4 vs 5.8 at 8,
+    // 14336 x 4096 9.1 us at 8 vs 9.8 at 4.
+    int wpc = (x && n < 8192) ? 4 : 8;
+    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);

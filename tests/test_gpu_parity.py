@@ -89,13 +89,18 @@ def test_dequant_q8k_and_truncation(oracle, lbq, dev):
 
 # ---------------------------------------------------------------- activation quantisation
 def _special_rows(k: int) -> np.ndarray:
-    rows = np.zeros((6, k), dtype=np.float32)
+    rows = np.zeros((7, k), dtype=np.float32)
     rows[1, 17] = -3.0                       # single non-zero
     rows[2, 3], rows[2, 7] = -2.0, 2.0       # tie with opposite signs, saturation at +128
     rows[3, 0] = -128.0                      # iscale = 1: half-away-from-zero rounding
     rows[3, 1:6] = [2.5, -2.5, 3.5, 0.5, -0.5]
     rows[4, :] = np.linspace(-1, 1, k, dtype=np.float32)
     rows[5, :] = 1e-30                       # tiny magnitudes
+    near_half = np.array([0.49999997, -0.49999997, 1.4999999, -1.4999999, 2.5000002, -2.4999998,
+                          126.5, -127.5, 127.49999, -127.50001, 0.5000001, 63.5], dtype=np.float32)
+    for b in range(0, k, 256):               # iscale = 1 in every block: rounding at and next to halves
+        rows[6, b] = -128.0
+        rows[6, b + 1:b + 1 + len(near_half)] = near_half
     return rows
 
 
@@ -182,15 +187,16 @@ def test_qmatmul_mfma_ragged(oracle, lbq, dev, t):
                           oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64), tight_bound(t, m))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
 @pytest.mark.parametrize("k", [4096, 14336])
 def test_decode_row_partition(oracle, lbq, dev, t, k):
     # m = 1 at the Llama-3 row lengths: every row split across waves (1 .. 8 rows
     # per wave), ragged row counts, fused quantisation and pre-quantised x
+    # (Q8_0 at k = 14336: 448 blocks, more block scales than threads)
     from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
     rng = np.random.default_rng(70 + t + k)
     for n in (1, 3, 257, 1000, 5000):
-        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
         x = rng.standard_normal((1, k)).astype(np.float32)
         ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
         qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
@@ -203,13 +209,15 @@ def test_decode_row_partition(oracle, lbq, dev, t, k):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
-def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t):
-    # At m = 1 and k <= 4096 the GEMV quantises x in its own prologue.  The same
-    # kernel fed x quantised by the standalone (bit-exact) kernel runs the same
-    # integer arithmetic, so the two outputs must agree to the bit.
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
+    # At m = 1 the GEMV quantises x in its own prologue (k = 14336: four passes
+    # of 16 Q8_K blocks).  The same kernel fed x quantised by the standalone
+    # (bit-exact) kernel runs the same integer arithmetic, so the two outputs
+    # must agree to the bit.
     from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
     rng = np.random.default_rng(90 + t)
-    n, k = 300, 4096
+    n = 300
     w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
     qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
     xs = np.concatenate([_special_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
