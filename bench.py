@@ -181,6 +181,15 @@ def main():
             for qm, x in zip(layer, xs):
                 qm.forward(x)
 
+    # the same step through the grouped entry point (q|k|v and gate|up as the
+    # reference's call sites feed them one x): 4 launches instead of 7
+    def grouped_step_all_copies():
+        for layer in copies:
+            qz.qmatmul_group(layer[0:3], xs[0])
+            layer[3].forward(xs[3])
+            qz.qmatmul_group(layer[4:6], xs[4])
+            layer[6].forward(xs[6])
+
     # activation handles for the dot-only (roofline) graph
     acts = {k: qz.QActivation(qz.GgmlDType.Q8K, 1, k, dev) for k in (4096, 14336)}
     for (_, n, k), x in zip(LAYER, xs):
@@ -194,6 +203,7 @@ def main():
     stream = torch.cuda.current_stream(dev)
     g_full = capture(torch, full_step_all_copies)
     g_dot = capture(torch, dot_all_copies)
+    g_grp = capture(torch, grouped_step_all_copies)
     reps = max(1, (args.steps + args.copies - 1) // args.copies)
     wreps = max(1, (args.warmup + args.copies - 1) // args.copies)
     steps = reps * args.copies
@@ -201,11 +211,14 @@ def main():
     ms_full = timed_graph(torch, g_full, reps, stream) / args.copies
     timed_graph(torch, g_dot, wreps, stream)
     ms_dot = timed_graph(torch, g_dot, reps, stream) / args.copies
+    timed_graph(torch, g_grp, wreps, stream)
+    ms_grp = timed_graph(torch, g_grp, reps, stream) / args.copies
     value = layer_bytes / (ms_full * 1e-3) / 1e9
     full_gbs = (layer_bytes + io_bytes) / (ms_full * 1e-3) / 1e9
     dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
     log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
-        f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s")
+        f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s; "
+        f"grouped (4 launches) {ms_grp * 1e3:.2f} us -> {layer_bytes / (ms_grp * 1e-3) / 1e9:.0f} GB/s")
 
     # per-shape dot kernel times (same graphs, one shape at a time)
     kernels = {}
@@ -258,9 +271,15 @@ def main():
         },
         "dot_only": {"us_per_step": round(ms_dot * 1e3, 3), "GB/s": round(dot_gbs, 1),
                      "kernel": "k_gemv1<Q4_K> on pre-quantised activations (forward_quantized)"},
+        "grouped": {"us_per_step": round(ms_grp * 1e3, 3),
+                    "GB/s": round(layer_bytes / (ms_grp * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(layer_bytes / (ms_grp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "launches": 4,
+                    "path": "lbq_qmatmul_group_f32 for q|k|v and gate|up (one fused launch each), "
+                            "lbq_qmatmul_f32 for o and down; outputs bit-identical to the 7 separate calls"},
         "kernels": kernels,
     }
-    del g_full, g_dot
+    del g_full, g_dot, g_grp
     tr = load_traffic()
     if tr and "bytes_per_launch" in tr:
         result["roofline"]["traffic"] = tr["bytes_per_launch"]
@@ -345,14 +364,32 @@ def stack_bench(torch, qz, gen, dev, stream):
                     qm.forward(xs[k])
             head.forward(xs[4096])
 
-        g = capture(torch, token_step)
-        timed_graph(torch, g, 2, stream)
+        def token_step_grouped():  # q|k|v, gate|up grouped where the types agree
+            for mats in layers:
+                for grp in ((0, 1, 2), (3,), (4, 5), (6,)):
+                    qs = [mats[i] for i in grp]
+                    k = LAYER[grp[0]][2]
+                    if len(qs) > 1 and len({q.qtensor().dtype() for q in qs}) == 1:
+                        qz.qmatmul_group(qs, xs[k])
+                    elif len(qs) > 1 and qs[0].qtensor().dtype() == qs[1].qtensor().dtype():
+                        qz.qmatmul_group(qs[:2], xs[k])
+                        for q in qs[2:]:
+                            q.forward(xs[k])
+                    else:
+                        for q in qs:
+                            q.forward(xs[k])
+            head.forward(xs[4096])
+
         reps = 20 if B == 1 else 5
-        ms = timed_graph(torch, g, reps, stream)
-        out[f"b{B}"] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
+        for tag, fn in ((f"b{B}", token_step), (f"b{B}_grouped", token_step_grouped)):
+            g = capture(torch, fn)
+            timed_graph(torch, g, 2, stream)
+            ms = timed_graph(torch, g, reps, stream)
+            out[tag] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
                         "weight_GB/s": round(total / (ms * 1e-3) / 1e9, 1)}
-        log(f"stack B={B}: {ms:.3f} ms/step -> {B / (ms * 1e-3):.0f} tok/s")
-        del g, xs, ys
+            log(f"stack {tag}: {ms:.3f} ms/step -> {B / (ms * 1e-3):.0f} tok/s")
+            del g
+        del xs, ys
     return out
 
 

@@ -101,6 +101,17 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * and weight values (about 4e-4 relative on a row).  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
+/* Several weights applied to one x: ys[i][m][n_i] = x . W_i^T, exactly as
+ * `count` separate lbq_qmatmul_f32 calls compute them (bit-identical), with x
+ * quantised once and, at m = 1, every weight's rows streamed by one launch.
+ * Replaces the runs of QMatMul::forward calls on the same input at the q/k/v
+ * projections (/root/reference/src/model/custom_attention.rs:265-267) and the
+ * gate/up projections (/root/reference/src/model/mlp_wrapper.rs:190,193).
+ * 1 <= count <= LBQ_GROUP_MAX; all weights share the ggml type and k. */
+#define LBQ_GROUP_MAX 4
+int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
+                          float *const *d_ys, void *stream);
+
 /* Quantised-activation handle: the two halves of QMatMul::forward as separate
  * calls.  candle's k_quants::matmul first quantises every row of x into
  * vec-dot blocks and then runs vec_dot for all output columns; splitting the

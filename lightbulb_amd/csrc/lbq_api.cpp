@@ -7,6 +7,7 @@
 // never an abort.  Here that is a negative status plus a thread-local message.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -16,6 +17,8 @@
 #include "../../include/lbq.h"
 #include "lbq_device.hpp"
 #include "lbq_internal.hpp"
+
+static_assert(LBQ_GROUP_MAX == lbq::GROUP_MAX, "one group limit for the ABI and the kernels");
 
 struct lbq_ctx {
     int device;
@@ -165,6 +168,7 @@ int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
     if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
     if (k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "k = %lld exceeds the supported maximum", (long long)k);
+    if (n > lbq::MAX_ROWS) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)n);
     const size_t want = (size_t)n * (size_t)(k / bs) * (size_t)lbq_type_size(type);
     if (nbytes != want)
         return fail(LBQ_ERR_SHAPE, "byte count %zu does not match n*(k/%d)*%d = %zu", nbytes, bs, lbq_type_size(type), want);
@@ -322,6 +326,60 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
                                          const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     return run_dot(ctx, w, av, m, d_y, st);
+}
+
+int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
+                          float *const *d_ys, void *stream) {
+    if (!ctx || !ws || !d_ys) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_qmatmul_group_f32");
+    if (count < 1 || count > LBQ_GROUP_MAX) return fail(LBQ_ERR_LIMIT, "count = %d outside 1..%d", count, LBQ_GROUP_MAX);
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !d_ys[i]) return fail(LBQ_ERR_INVALID_ARG, "null weight or output %d", i);
+        if (reinterpret_cast<uintptr_t>(d_ys[i]) & 3u) return fail(LBQ_ERR_INVALID_ARG, "output %d must be a 4-byte aligned f32 buffer", i);
+        if (ws[i]->type != ws[0]->type || ws[i]->k != ws[0]->k)
+            return fail(LBQ_ERR_SHAPE, "weight %d (type %d, k = %lld) differs from weight 0 (type %d, k = %lld)", i, ws[i]->type,
+                        (long long)ws[i]->k, ws[0]->type, (long long)ws[0]->k);
+    }
+    if (m == 0) return LBQ_OK;
+    if (!d_x) return fail(LBQ_ERR_INVALID_ARG, "null activation pointer");
+    if (reinterpret_cast<uintptr_t>(d_x) & 3u) return fail(LBQ_ERR_INVALID_ARG, "x must be a 4-byte aligned f32 buffer");
+    if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    const lbq_weight *w0 = ws[0];
+    const int act_type = w0->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const ActLayout L = act_layout(act_type, m, w0->k);
+    // m = 1: every weight's rows in one launch (one row space)
+    lbq::RowMap rm = lbq::single_row_map(w0->d_blocks, w0->n, d_ys[0]);
+    int64_t rows = 0;
+    for (int i = 0; i < count; i++) {
+        rm.w[i] = ws[i]->d_blocks;
+        rm.y[i] = d_ys[i];
+        rows += ws[i]->n;
+        rm.end[i] = (int32_t)std::min<int64_t>(rows, lbq::MAX_ROWS);
+    }
+    rm.n = rows;
+    const bool one_launch = rows <= lbq::MAX_ROWS;  // else weight by weight
+    if (one_launch && m == 1 && lbq::gemv_fuses_quant(w0->type, rows, w0->k, 1, d_x)) {
+        const lbq::ActView av{nullptr, nullptr, nullptr, w0->k, L.nb};
+        hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, av, d_x, st);
+        if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
+    }
+    // otherwise x is quantised once into the context's scratch and shared by
+    // one launch per weight
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    int s = ensure_scratch(ctx, L.total);
+    if (s) return s;
+    const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
+    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w0->k, const_cast<int8_t *>(av.xq),
+                                         const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    for (int i = 0; i < count; i++) {
+        s = run_dot(ctx, ws[i], av, m, d_ys[i], st);
+        if (s) return s;
+    }
+    return LBQ_OK;
 }
 
 int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act) {

@@ -3,10 +3,10 @@
 
 namespace lbq {
 
-hipError_t gemv_q4k(int64_t, int64_t, int64_t, const ActView &, const float *, int, float *, hipStream_t, const uint8_t *);
-hipError_t gemv_q5k(int64_t, int64_t, int64_t, const ActView &, const float *, int, float *, hipStream_t, const uint8_t *);
-hipError_t gemv_q6k(int64_t, int64_t, int64_t, const ActView &, const float *, int, float *, hipStream_t, const uint8_t *);
-hipError_t gemv_q8_0(int64_t, int64_t, int64_t, const ActView &, const float *, int, float *, hipStream_t, const uint8_t *);
+hipError_t gemv_q4k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, hipStream_t);
+hipError_t gemv_q5k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, hipStream_t);
+hipError_t gemv_q6k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, hipStream_t);
+hipError_t gemv_q8_0(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, hipStream_t);
 
 bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     (void)n;
@@ -31,15 +31,37 @@ hipError_t launch_gemv(int type, const uint8_t *w, int64_t n, int64_t k, int64_t
     return launch_gemv_x(type, w, n, k, row_bytes, act, nullptr, m, y, st);
 }
 
-hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                         const float *x, int m, float *y, hipStream_t st) {
+RowMap single_row_map(const uint8_t *w, int64_t n, float *y) {
+    RowMap rm;
+    for (int s = 0; s < GROUP_MAX; s++) {
+        rm.w[s] = w;
+        rm.y[s] = y;
+        rm.end[s] = INT32_MAX;
+    }
+    rm.end[0] = (int32_t)n;
+    rm.n = n;
+    return rm;
+}
+
+static hipError_t dispatch(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x,
+                           int m, hipStream_t st) {
     switch (type) {
-    case TYPE_Q4_K: return gemv_q4k(n, k, row_bytes, act, x, m, y, st, w);
-    case TYPE_Q5_K: return gemv_q5k(n, k, row_bytes, act, x, m, y, st, w);
-    case TYPE_Q6_K: return gemv_q6k(n, k, row_bytes, act, x, m, y, st, w);
-    case TYPE_Q8_0: return gemv_q8_0(n, k, row_bytes, act, x, m, y, st, w);
+    case TYPE_Q4_K: return gemv_q4k(rm, k, row_bytes, act, x, m, st);
+    case TYPE_Q5_K: return gemv_q5k(rm, k, row_bytes, act, x, m, st);
+    case TYPE_Q6_K: return gemv_q6k(rm, k, row_bytes, act, x, m, st);
+    case TYPE_Q8_0: return gemv_q8_0(rm, k, row_bytes, act, x, m, st);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                         const float *x, int m, float *y, hipStream_t st) {
+    return dispatch(type, single_row_map(w, n, y), k, row_bytes, act, x, m, st);
+}
+
+hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act,
+                             const float *x, hipStream_t st) {
+    return dispatch(type, rm, k, row_bytes, act, x, 1, st);
 }
 
 }  // namespace lbq

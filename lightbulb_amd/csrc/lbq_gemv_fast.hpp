@@ -467,19 +467,78 @@ __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *s
     __syncthreads();
 }
 
+// A row map held in scalar registers (named fields, no arrays: nothing is
+// indexed).  Each field passes through an empty asm statement, so lookups
+// select between values; a select between the kernel argument's fields would
+// otherwise become a load from a selected address, whose wait would also wait
+// for every load issued before it.  Lookups take wave-uniform rows and run on
+// the scalar unit.
+static_assert(GROUP_MAX == 4, "RowMapS has four segments");
+struct RowMapS {
+    uint64_t w0, w1, w2, w3, y0, y1, y2, y3;
+    int32_t e0, e1, e2;
+};
+__device__ __forceinline__ uint64_t sreg(uint64_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+__device__ __forceinline__ int32_t sreg32(int32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+__device__ __forceinline__ RowMapS map_regs(const RowMap &rm) {
+    RowMapS r;
+    r.w0 = sreg(reinterpret_cast<uint64_t>(rm.w[0]));
+    r.w1 = sreg(reinterpret_cast<uint64_t>(rm.w[1]));
+    r.w2 = sreg(reinterpret_cast<uint64_t>(rm.w[2]));
+    r.w3 = sreg(reinterpret_cast<uint64_t>(rm.w[3]));
+    r.y0 = sreg(reinterpret_cast<uint64_t>(rm.y[0]));
+    r.y1 = sreg(reinterpret_cast<uint64_t>(rm.y[1]));
+    r.y2 = sreg(reinterpret_cast<uint64_t>(rm.y[2]));
+    r.y3 = sreg(reinterpret_cast<uint64_t>(rm.y[3]));
+    r.e0 = sreg32(rm.end[0]);
+    r.e1 = sreg32(rm.end[1]);
+    r.e2 = sreg32(rm.end[2]);
+    return r;
+}
+// (segment base pointer, first row of the segment) for a row of the space
+__device__ __forceinline__ void map_seg(const RowMapS &rm, int32_t row, uint64_t a0, uint64_t a1, uint64_t a2,
+                                        uint64_t a3, uint64_t *ptr, int32_t *base) {
+    uint64_t p = a0;
+    int32_t b = 0;
+    if (row >= rm.e0) { p = a1; b = rm.e0; }
+    if (row >= rm.e1) { p = a2; b = rm.e1; }
+    if (row >= rm.e2) { p = a3; b = rm.e2; }
+    *ptr = p;
+    *base = b;
+}
+// Global-address-space views of looked-up pointers, so accesses through them
+// stay global loads and stores.
+typedef const __attribute__((address_space(1))) uint8_t *gbytes;
+typedef __attribute__((address_space(1))) float *gfloats;
+
 // ---------------------------------------------------------------------------
 // The m = 1 kernel.  A row group is RPW rows; lane (r, li) decodes piece
 // li % PPB of blocks li / PPB + BPI*i (i < IT) of row r.  Requires nb <= BPI*IT.
 // ---------------------------------------------------------------------------
-template <int TYPE, int RPW, int IT, bool FUSED>
-__global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, int64_t n, int64_t row_bytes, int nb,
-                                               const float *__restrict__ x, ActView act, float *__restrict__ y) {
+// GROUPED: rm may hold several weights (rows looked up per group); otherwise it
+// is one weight, addressed directly.
+template <int TYPE, int RPW, int IT, bool FUSED, bool GROUPED>
+__global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
+                                               ActView act) {
+    const int64_t n = rm.n;
+    const uint8_t *__restrict__ W = rm.w[0];
+    float *__restrict__ y = rm.y[0];
+    RowMapS rs{};
+    if constexpr (GROUPED) rs = map_regs(rm);
     using F = Fast<TYPE>;
     using Raw = typename F::Raw;
     constexpr int LPR = 64 / RPW;
     constexpr int BPI = LPR / F::PPB;
     static_assert(BPI >= 1, "a row needs at least one whole block per sweep");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // grouped: the wave index as a scalar, so row-group indices (and row lookups) are scalar
+    const int lane = threadIdx.x & 63,
+              wave = GROUPED ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
     const int r = lane / LPR, li = lane % LPR;
     const int p = li % F::PPB, bs0 = li / F::PPB;
     const int64_t ng = (n + RPW - 1) / RPW;
@@ -487,10 +546,29 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
     const int64_t per = ng / nw, rem = ng % nw;
     const int64_t g0 = gw * per + (gw < rem ? gw : rem), g1 = g0 + per + (gw < rem ? 1 : 0);
 
-    // loads are unconditional (row and block clamped into range); compute masks
+    // loads are unconditional (row and block clamped into range); compute masks.
+    // Grouped: the group's rows are looked up once each (g is wave-uniform),
+    // and each lane takes its own row's base.
     auto load_group = [&](int64_t g, Raw *buf) {
-        const int64_t row = min(g * RPW + r, n - 1);
-        const uint8_t *wr = W + row * row_bytes;
+        const uint8_t *wr;
+        if constexpr (GROUPED) {
+            uint64_t rp = 0;
+            int64_t roff = 0;
+#pragma unroll
+            for (int q = 0; q < RPW; q++) {
+                const int32_t row = (int32_t)min(g * RPW + q, n - 1);
+                uint64_t sp;
+                int32_t sb;
+                map_seg(rs, row, rs.w0, rs.w1, rs.w2, rs.w3, &sp, &sb);
+                if (q == 0 || r == q) {
+                    rp = sp;
+                    roff = (int64_t)(row - sb) * row_bytes;
+                }
+            }
+            wr = (const uint8_t *)((gbytes)rp + roff);
+        } else {
+            wr = W + min(g * RPW + r, n - 1) * row_bytes;
+        }
 #pragma unroll
         for (int i = 0; i < IT; i++) {
             const int b = min(bs0 + BPI * i, nb - 1);
@@ -546,7 +624,14 @@ __global__ __launch_bounds__(256) void k_gemv1(const uint8_t *__restrict__ W, in
                 s = __int_as_float(rl(__float_as_uint(acc), 16 * q));
             }
             const int64_t rq = g * RPW + q;
-            if (store && lane == LPR * q && rq < n) y[rq] = s;
+            if constexpr (GROUPED) {
+                uint64_t yp;
+                int32_t yb;
+                map_seg(rs, (int32_t)min(rq, n - 1), rs.y0, rs.y1, rs.y2, rs.y3, &yp, &yb);
+                if (store && lane == LPR * q && rq < n) *(float *)((gfloats)yp + (rq - yb)) = s;
+            } else {
+                if (store && lane == LPR * q && rq < n) y[rq] = s;
+            }
         }
     };
 

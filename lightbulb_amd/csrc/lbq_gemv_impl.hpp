@@ -465,8 +465,9 @@ static bool fast_shape(int nb, int *rpw, int *it) {
 }
 
 template <int TYPE, int RPW, int IT>
-static hipError_t launch_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int nb, const float *x,
-                              const ActView &act, float *y, hipStream_t st) {
+static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act,
+                              hipStream_t st) {
+    const int64_t n = rm.n;
     const int64_t ng = (n + RPW - 1) / RPW;
     // Waves per CU.  With the fused prologue every workgroup quantises all of x,
     // so for fewer rows (less weight per CU to hide it behind) one workgroup per
@@ -478,18 +479,24 @@ static hipError_t launch_fast(const uint8_t *w, int64_t n, int64_t row_bytes, in
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     const size_t lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
-    if (x) k_gemv1<TYPE, RPW, IT, true><<<grid, 256, lds, st>>>(w, n, row_bytes, nb, x, act, y);
-    else k_gemv1<TYPE, RPW, IT, false><<<grid, 256, lds, st>>>(w, n, row_bytes, nb, x, act, y);
+    if (rm.end[0] < n) {  // several weights: fused quantisation only (the caller runs the rest one by one)
+        if (!x) return hipErrorNotSupported;
+        k_gemv1<TYPE, RPW, IT, true, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+    } else if (x) {
+        k_gemv1<TYPE, RPW, IT, true, false><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+    } else {
+        k_gemv1<TYPE, RPW, IT, false, false><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+    }
     return hipGetLastError();
 }
 
 template <int TYPE>
-static hipError_t run_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int nb, const float *x, const ActView &act,
-                           float *y, hipStream_t st) {
+static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act,
+                           hipStream_t st) {
     int rpw, it;
     if (!fast_shape<TYPE>(nb, &rpw, &it)) return hipErrorNotSupported;
 #define LBQ_FAST(R, I) \
-    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(w, n, row_bytes, nb, x, act, y, st);
+    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, st);
     if constexpr (Fast<TYPE>::PPB == 8) {
         LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
     } else if constexpr (Fast<TYPE>::PPB == 4) {
@@ -501,19 +508,24 @@ static hipError_t run_fast(const uint8_t *w, int64_t n, int64_t row_bytes, int n
     return hipErrorNotSupported;
 }
 
+// One weight (rm.n rows, single segment) or, at m = 1, a multi-weight row map.
 template <int TYPE>
-static hipError_t run_type(const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                           const float *x, int m, float *y, hipStream_t st) {
+static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
+                           hipStream_t st) {
     using D = Dec<TYPE>;
+    const uint8_t *w = rm.w[0];
+    const int64_t n = rm.n;
+    float *y = rm.y[0];
     PGeom g{};
     g.n_rows = n;
     g.row_bytes = row_bytes;
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
     if (m == 1) {
-        const hipError_t e = run_fast<TYPE>(w, n, row_bytes, g.nb, x, act, y, st);
+        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, st);
         if (e != hipErrorNotSupported) return e;
     }
+    if (rm.end[0] != n) return hipErrorNotSupported;  // row maps: m = 1 fast path only
     GemvCfg c = pick_cfg(TYPE, n, g.pieces, m, k);
     c.fused = false;  // m > 1: x arrives quantised (separate kernel)
     if (x) return hipErrorInvalidValue;

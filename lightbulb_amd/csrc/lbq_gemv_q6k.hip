@@ -4,9 +4,9 @@
 
 namespace lbq {
 
-hipError_t gemv_q6k(int64_t n, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m, float *y,
-                       hipStream_t st, const uint8_t *w) {
-    return run_type<TYPE_Q6_K>(w, n, k, row_bytes, act, x, m, y, st);
+hipError_t gemv_q6k(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
+                       hipStream_t st) {
+    return run_type<TYPE_Q6_K>(rm, k, row_bytes, act, x, m, st);
 }
 
 }  // namespace lbq

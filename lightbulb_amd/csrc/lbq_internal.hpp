@@ -10,6 +10,21 @@ enum : int { TYPE_Q8_0 = 8, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE
 
 struct ActView;
 
+// The rows of up to GROUP_MAX weights of one type and k, seen as one row space
+// (weights applied to the same x: q|k|v, gate|up).  Segment s holds rows
+// [end[s-1], end[s]) of the space, its blocks at w[s] and its outputs at y[s];
+// entries past the last segment have end = INT32_MAX.  A plain single weight is
+// the one-segment map.  A row space has fewer than 2^31 - 1 rows.
+constexpr int GROUP_MAX = 4;
+constexpr int64_t MAX_ROWS = 0x7ffffffe;
+struct RowMap {
+    const uint8_t *w[GROUP_MAX];
+    float *y[GROUP_MAX];
+    int32_t end[GROUP_MAX];
+    int64_t n;  // rows in all segments
+};
+RowMap single_row_map(const uint8_t *w, int64_t n, float *y);
+
 // Quantise x[m][k] to Q8_K (act_type 15) or Q8_0 (act_type 8).  Writes the split
 // internal layout (xq/xd/xbs) when gguf == nullptr, else GGUF blocks to gguf.
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
@@ -31,6 +46,12 @@ bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x);
 // the scale-block count only).  x == nullptr means act holds quantised codes.
 hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                          const float *x, int m, float *y, hipStream_t st);
+
+// m = 1 over a multi-weight row map in one launch, quantising x in the prologue
+// (x != nullptr).  hipErrorNotSupported when k is outside the single-row fast
+// path or x is not given; the caller then runs the weights one by one.
+hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act,
+                             const float *x, hipStream_t st);
 
 // Batched path (m > 8): weights dequantised in registers into MFMA operands.
 // Needs gemm_workspace_bytes(type, n, k, m) bytes of device memory at ws (fp16

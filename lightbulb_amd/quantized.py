@@ -238,6 +238,43 @@ class QMatMul:
         return f"QMatMul({self._qt!r})"
 
 
+GROUP_MAX = 4  # LBQ_GROUP_MAX
+
+
+def qmatmul_group(qmatmuls, xs: torch.Tensor) -> list[torch.Tensor]:
+    """``[q.forward(xs) for q in qmatmuls]`` in one call: the runs of
+    ``QMatMul::forward`` on one input at the q/k/v projections
+    (src/model/custom_attention.rs:265-267) and gate/up (src/model/mlp_wrapper.rs:190,193).
+    x is quantised once and, at m = 1, all weights stream in one launch; the
+    outputs are bit-identical to separate ``forward`` calls.  The weights must
+    share the ggml type and k."""
+    qmatmuls = list(qmatmuls)
+    if not 1 <= len(qmatmuls) <= GROUP_MAX:
+        raise ValueError(f"between 1 and {GROUP_MAX} weights per group, got {len(qmatmuls)}")
+    q0 = qmatmuls[0]
+    n0, k = q0.qtensor().shape()
+    for q in qmatmuls[1:]:
+        if q.qtensor().dtype() != q0.qtensor().dtype() or q.qtensor().shape()[1] != k:
+            raise ValueError("grouped weights must share the ggml type and k")
+    if xs.dtype != torch.float32:
+        raise ValueError(f"the lhs for quantized matmul must be f32, got {xs.dtype}")
+    if xs.dim() < 2:
+        raise ValueError(f"input tensor has only one dimension {tuple(xs.shape)}")
+    if xs.shape[-1] != k:
+        raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with {(n0, k)}")
+    if not xs.is_contiguous():
+        raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
+    m = xs.numel() // k
+    ys = [torch.empty(*xs.shape[:-1], q.qtensor().shape()[0], dtype=torch.float32, device=xs.device)
+          for q in qmatmuls]
+    if m:
+        cnt = len(qmatmuls)
+        hs = (ctypes.c_void_p * cnt)(*[q._handle for q in qmatmuls])
+        outs = (ctypes.c_void_p * cnt)(*[y.data_ptr() for y in ys])
+        _lib.check(_lib.lib().lbq_qmatmul_group_f32(q0._ctx, hs, cnt, xs.data_ptr(), m, outs, _stream(xs.device)))
+    return ys
+
+
 class QActivation:
     """x [m, k] quantised once (Q8_K for k-quant weights, Q8_0 for Q8_0 weights),
     reusable by every QMatMul that reads the same x -- q/k/v and gate/up."""

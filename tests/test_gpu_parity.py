@@ -230,6 +230,57 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
         assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+def test_qmatmul_group_matches_separate_calls(oracle, lbq, dev, t):
+    # q|k|v- and gate|up-like groups in one call: every output bit-identical to
+    # its own forward (m = 1 streams all weights in one launch; m > 1 shares the
+    # quantised x), checked against the oracle too; x offset by one float takes
+    # the unfused m = 1 path
+    from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
+    rng = np.random.default_rng(110 + t)
+    for k, ns in ((4096, (512, 128, 128)), (1024, (300, 77)), (14336, (64, 33, 96, 5))):
+        raws = [bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3) for n in ns]
+        qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
+        for m in (1, 3, 20):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            for shift in ((0, 1) if m == 1 else (0,)):
+                buf = to_dev(np.concatenate([np.zeros(shift, np.float32), x.ravel()]), dev)
+                xd = buf[shift:].view(m, k)
+                ys = qmatmul_group(qms, xd)
+                singles = [q.forward(xd) for q in qms]
+                torch.cuda.synchronize()
+                for y, y1 in zip(ys, singles):
+                    assert np.array_equal(y.cpu().numpy().view(np.uint32), y1.cpu().numpy().view(np.uint32))
+            if m == 1:
+                for y, r, n in zip(ys, raws, ns):
+                    assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, x, nthreads=8).astype(np.float64))
+
+
+def test_qmatmul_group_errors(oracle, lbq, dev):
+    from lightbulb_amd import _lib
+    from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
+    rng = np.random.default_rng(120)
+    a = QMatMul.from_qtensor(QTensor(to_dev(bp.random_blocks(rng, Q4_K, 8 * 2), dev), Q4_K, (8, 512)))
+    b = QMatMul.from_qtensor(QTensor(to_dev(bp.random_blocks(rng, Q4_K, 8 * 1), dev), Q4_K, (8, 256)))
+    c = QMatMul.from_qtensor(QTensor(to_dev(bp.random_blocks(rng, Q5_K, 8 * 2), dev), Q5_K, (8, 512)))
+    x = torch.zeros(1, 512, device=dev)
+    with pytest.raises(ValueError, match="share"):
+        qmatmul_group([a, b], x)
+    with pytest.raises(ValueError, match="between 1 and 4"):
+        qmatmul_group([a] * 5, x)
+    assert [tuple(y.shape) for y in qmatmul_group([a], torch.zeros(0, 512, device=dev))] == [(0, 8)]
+    # the C ABI checks the same things itself
+    L = _lib.lib()
+    y = torch.empty(1, 8, device=dev)
+    for ws, cnt, want in (([a, c], 2, -3), ([a, b], 2, -3), ([a], 0, -6), ([a] * 4 + [a], 5, -6)):
+        hs = (ctypes.c_void_p * len(ws))(*[q._handle for q in ws])
+        outs = (ctypes.c_void_p * len(ws))(*([y.data_ptr()] * len(ws)))
+        assert L.lbq_qmatmul_group_f32(a._ctx, hs, cnt, x.data_ptr(), 1, outs, None) == want
+    hs = (ctypes.c_void_p * 2)(a._handle, None)
+    outs = (ctypes.c_void_p * 2)(y.data_ptr(), y.data_ptr())
+    assert L.lbq_qmatmul_group_f32(a._ctx, hs, 2, x.data_ptr(), 1, outs, None) == -1
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
     # m >= 256 takes the 256 x 128 tile kernel: ragged m and n, odd and even block counts
