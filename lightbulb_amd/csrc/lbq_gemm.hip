@@ -443,23 +443,34 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 // double-buffered stage (256 rows x 128 values) fits in LDS.
 // ---------------------------------------------------------------------------
 constexpr int TBM = 256, TBN = 128;
-constexpr int TSLD = 136;  // stage row stride in halfs (272 B: conflict-free b128 reads)
+constexpr int TROW = 256;  // stage row: 128 halfs, no padding (chunks are swizzled instead)
 
+// Stage layout: row r of a stage is 256 B = 16 chunks of 8 halfs; logical chunk
+// c = 8h + j (lane half h, k-step j of the stage) sits in slot c ^ (r & 15).  A
+// wave's A-operand read (rows lr, lr + 32.., one chunk each) then touches 16
+// distinct slots per 16 rows: every bank once, with no padding, so a stage is
+// exactly 64 KB and fills by direct-to-LDS loads (16 B per lane, a wave writes
+// 4 whole rows per instruction; each lane fetches the chunk its slot holds).
+//
 // Per stage (8 k-steps x 8 MFMA regions), besides the A operands of the k-step
 // AH ahead and the B operand of the next one:
-//   k-step 0    : the next stage's activation loads (2 per region);
-//   k-steps 1-2 : in stage 0, the next block's weight loads;
-//   k-step 2    : barrier -- every wave is done with the other buffer;
-//   k-step 5    : the next stage's activations into the other buffer;
-//   k-step 6    : barrier -- that buffer is complete; from k-step 8 - AH on, the
-//                 next stage's first A operands are read from it;
+//   k-step 0    : barrier -- every wave is done with the other buffer; then the
+//                 next stage's direct-to-LDS loads into it (2 per region);
+//   k-step 6    : wait for this wave's loads, barrier -- the other buffer is
+//                 complete; from k-step 8 - AH on, the next stage's first A
+//                 operands are read from it;
+//   k-steps 6-7 : in stage 0, the next block's weight loads (after the wait, so
+//                 they are not waited for until the next stage's k-step 6);
 //   k-step 7    : in stage 1, the next block's scales and first B operand.
 template <int TYPE>
 __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
                                                    const _Float16 *__restrict__ A, const int *__restrict__ erow,
                                                    int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
     using B = GB<TYPE>;
-    __shared__ __align__(16) _Float16 As[2][TBM][TSLD];
+    // two separate arrays, so the compiler tells the buffers apart when it
+    // places waits for the direct-to-LDS loads
+    __shared__ __align__(1024) uint8_t As0[TBM * TROW];
+    __shared__ __align__(1024) uint8_t As1[TBM * TROW];
     __shared__ int Es[TBM];
 
     const int G = (int)gridDim.x, L = (int)blockIdx.x;
@@ -470,24 +481,50 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     const int64_t m0 = (int64_t)tm * TBM, n0 = (int64_t)tn * TBN;
     float *y = out + (int64_t)z * g.split_stride;
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
+    // the wave index as a scalar: staging addresses and LDS targets are then
+    // scalar too (the direct-to-LDS target goes through M0)
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
+              lr = lane & 31;
     const uint8_t *wrow = W + min(n0 + 32 * wave + lr, N - 1) * row_bytes;
-    // staging: piece f = 256 i + t of a stage is row f/16, half (f/8)%2 (values
-    // 128*half + 64t + ...), 16-byte piece f%8; rows past M exist in the operand
-    // buffer (whole tiles), so no clamping
-    const int srow = t >> 4, shh = (t >> 3) & 1, spc = t & 7;
-    const _Float16 *abase = A + (m0 + srow) * K + 128 * shh + 8 * spc;
     Es[t] = erow[min(m0 + t, M - 1)];
+
+    // direct-to-LDS staging: instruction j of a wave fills stage rows
+    // 64 wave + 4j + [0, 4); lane l writes row 64 wave + 4j + l/16, slot l%16,
+    // so it fetches logical chunk (l%16) ^ (row & 15), whose pattern repeats
+    // every 4 instructions: a scalar base plus one of four 32-bit lane offsets.
+    // Rows past M exist in the operand buffer (whole tiles), so no clamping.
+    const char *dma_base = reinterpret_cast<const char *>(A + (m0 + 64 * wave) * K);
+    uint32_t voff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int c = (lane & 15) ^ ((4 * q + (lane >> 4)) & 15);
+        voff[q] = (uint32_t)(((lane >> 4) * (int)K + 128 * (c >> 3) + 8 * (c & 7)) * 2);
+    }
+    auto a_dma = [&](int u, int buf, int j) {
+        const char *src = dma_base + ((int64_t)j * 4 * K + (int64_t)(u >> 1) * KB + 64 * (u & 1)) * 2 + voff[j & 3];
+        uint8_t *dst = (buf ? As1 : As0) + (64 * wave + 4 * j) * TROW;
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    };
+    // A-operand read addresses: row lr (+32 i, an immediate offset), chunk 8h + j
+    // in slot (8h + j) ^ (lr & 15); one register per k-step and buffer
+    // (the offsets pass through an empty asm statement per buffer, so neither
+    // buffer's addresses are rebuilt from the other's -- a VALU op per read --
+    // while each pointer still names its array, which the placement of waits
+    // for the direct-to-LDS loads relies on)
+    const uint8_t *rb[2][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int o0 = lr * TROW + 16 * ((8 * h + j) ^ (lr & 15)), o1 = o0;
+        asm volatile("" : "+v"(o0), "+v"(o1));
+        rb[0][j] = As0 + o0;
+        rb[1][j] = As1 + o1;
+    }
+    auto a_read = [&](int buf, int j, int i) -> half8 {
+        return *reinterpret_cast<const half8 *>(rb[buf][j] + 32 * i * TROW);
+    };
 
     typename B::Raw raw;
     typename B::Prep p;
-    uint4 ra[16];
-    auto a_load = [&](int u, int i) {
-        ra[i] = *reinterpret_cast<const uint4 *>(abase + (int64_t)i * 16 * K + (int64_t)(u >> 1) * KB + 64 * (u & 1));
-    };
-    auto a_store = [&](int buf, int i) {
-        *reinterpret_cast<uint4 *>(&As[buf][16 * i + srow][64 * shh + 8 * spc]) = make_uint4(ra[i].x, ra[i].y, ra[i].z, ra[i].w);
-    };
     auto w_load = [&](int b, int q) { B::load_part(wrow + (int64_t)b * B::BYTES, h, raw, q); };
     auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, p); };
 
@@ -498,14 +535,12 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
         for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
 
 #pragma unroll
-    for (int i = 0; i < 16; i++) a_load(2 * b0, i);
+    for (int j = 0; j < 16; j++) a_dma(2 * b0, 0, j);
 #pragma unroll
     for (int q = 0; q < B::NL; q++) w_load(b0, q);
-#pragma unroll
-    for (int i = 0; i < 16; i++) a_store(0, i);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     w_prep(b0);
-    const _Float16 *al0 = &As[0][lr][64 * h], *al1 = &As[1][lr][64 * h];
     // A operands are read AH k-steps ahead (ar[j] holds k-step ks + j): with one
     // wave per SIMD, 8 KB of reads per k-step need that depth to keep the LDS
     // busy.  Q6_K's larger weight state leaves registers for one step only.
@@ -515,7 +550,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
 #pragma unroll
     for (int j = 0; j < AH; j++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) ar[j][i] = *reinterpret_cast<const half8 *>(al0 + 32 * i * TSLD + 8 * j);
+        for (int i = 0; i < 8; i++) ar[j][i] = a_read(0, j, i);
 #pragma unroll
     for (int d = 0; d < 4; d++) bcur[d] = B::dw(p, 0, d);
 
@@ -524,7 +559,6 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
         const int ts = u & 1;
         const int un = min(u + 1, u_end - 1);          // clamped: the last stage re-stages itself
         const int bn = min((u >> 1) + 1, b1 - 1);
-        const _Float16 *al = buf ? al1 : al0, *aln = buf ? al0 : al1;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             const int s = 8 * ts + ks;  // k-step within the block
@@ -532,24 +566,30 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
             uint32_t bnxt[4];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                if (ks == 2 && i == 0) __syncthreads();  // every wave is done with the other buffer
-                if (ks == 6 && i == 0) __syncthreads();  // the other buffer holds the next stage
+                if (ks == 0 && i == 0) __syncthreads();  // every wave is done with the other buffer
+                if (ks == 6 && i == 0) {
+                    // this wave's direct-to-LDS loads (and nothing later is in
+                    // flight: the weight loads come after), then all waves'
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                }
                 const half8 bo = __builtin_bit_cast(half8, make_uint4(bcur[0], bcur[1], bcur[2], bcur[3]));
                 acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ar[0][i], bo, acc[i], 0, 0, 0);
-                if (ks + AH < 8) an[i] = *reinterpret_cast<const half8 *>(al + 32 * i * TSLD + 8 * (ks + AH));
-                else an[i] = *reinterpret_cast<const half8 *>(aln + 32 * i * TSLD + 8 * (ks + AH - 8));
+                if (ks + AH < 8) an[i] = a_read(buf, ks + AH, i);
+                else an[i] = a_read(buf ^ 1, ks + AH - 8, i);
+                // B-operand dwords two at a time, so the half-register writes of one
+                // interleave with the other's (no hazard stall between them)
                 if (s < 15) {
-                    if (i < 4) bnxt[i] = B::dw(p, s + 1, i);
+                    if (i == 0 || i == 2) { bnxt[i] = B::dw(p, s + 1, i); bnxt[i + 1] = B::dw(p, s + 1, i + 1); }
                 } else {
                     if (i == 0) w_prep(bn);
-                    else if (i <= 4) bnxt[i - 1] = B::dw(p, 0, i - 1);
+                    else if (i == 1 || i == 3) { bnxt[i - 1] = B::dw(p, 0, i - 1); bnxt[i] = B::dw(p, 0, i); }
                 }
-                if (ks == 0) { a_load(un, 2 * i); a_load(un, 2 * i + 1); }
-                if (ts == 0 && (ks == 1 || ks == 2)) {
-                    const int q = 8 * (ks - 1) + i;
+                if (ks == 0) { a_dma(un, buf ^ 1, 2 * i); a_dma(un, buf ^ 1, 2 * i + 1); }
+                if (ts == 0 && (ks == 6 || ks == 7)) {
+                    const int q = 8 * (ks - 6) + i;
                     if (q < B::NL) w_load(bn, q);
                 }
-                if (ks == 5) { a_store(buf ^ 1, 2 * i); a_store(buf ^ 1, 2 * i + 1); }
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
