@@ -156,7 +156,7 @@ int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m
             int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
             if (s) return s;
         }
-        e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, m, d_y, ctx->ws, st);
+        e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ctx->ws, st);
     }
     if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
@@ -319,6 +319,15 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
         return LBQ_OK;
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
+    if (m > 8 && w->type != LBQ_TYPE_Q8_0 && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
+        // batched: the operand pre-pass quantises x itself
+        int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), "GEMM workspace");
+        if (s) return s;
+        const lbq::ActView none{nullptr, nullptr, nullptr, w->k, L.nb};
+        hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, none, d_x, m, d_y, ctx->ws, st);
+        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+        return LBQ_OK;
+    }
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
     const lbq::ActView av = view_of(ctx->scratch, L, w->k);
@@ -366,9 +375,35 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, av, d_x, st);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    if (m > 8 && w0->type != LBQ_TYPE_Q8_0) {
+        // batched: one operand pre-pass (quantising x itself when it can) shared
+        // by every weight's GEMM
+        size_t wsb = 0;
+        for (int i = 0; i < count; i++) wsb = std::max(wsb, lbq::gemm_workspace_bytes(w0->type, ws[i]->n, w0->k, m));
+        int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
+        if (s) return s;
+        hipError_t e;
+        if (lbq::gemm_prepass_fuses_quant(w0->k, d_x)) {
+            const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, L.nb};
+            e = lbq::gemm_prepass(w0->type, w0->k, none, d_x, m, ctx->ws, st);
+        } else {
+            s = ensure_scratch(ctx, L.total);
+            if (s) return s;
+            const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
+            e = lbq::launch_quant_act(act_type, d_x, m, w0->k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
+                                      const_cast<int16_t *>(av.xbs), nullptr, st);
+            if (e == hipSuccess) e = lbq::gemm_prepass(w0->type, w0->k, av, nullptr, m, ctx->ws, st);
+        }
+        if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
+        for (int i = 0; i < count; i++) {
+            e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i], ctx->ws, st);
+            if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
+        }
+        return LBQ_OK;
+    }
     // otherwise x is quantised once into the context's scratch and shared by
     // one launch per weight
-    std::lock_guard<std::mutex> lock(ctx->mu);
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
     const lbq::ActView av = view_of(ctx->scratch, L, w0->k);

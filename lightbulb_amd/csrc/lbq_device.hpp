@@ -18,6 +18,98 @@
 
 namespace lbq {
 
+// ---------------------------------------------------------------------------
+// DPP helpers (gfx9 dpp_ctrl: quad_perm 0x00-0xFF, row_ror:n = 0x120+n)
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// every lane of each 16-lane row gets the row's max / min / sum
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max(v, dpp_u32<0x124>(v));  // row_ror:4
+    v = max(v, dpp_u32<0x128>(v));  // row_ror:8
+    return v;
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x124>(v));
+    v = min(v, dpp_u32<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ float row_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    return v;
+}
+__device__ __forceinline__ int quad_sum_i32(int v) {
+    v += (int)dpp_u32<0xB1>((uint32_t)v);
+    v += (int)dpp_u32<0x4E>((uint32_t)v);
+    return v;
+}
+__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+// Q8_K quantisation of one 256-value block by 16 aligned lanes, 16 consecutive
+// values per lane (lane sub = lane % 16 holds values 16 sub .. 16 sub + 15).
+// Candle's BlockQ8K::from_float: the first value of largest |x| (NaN never
+// chosen) sets iscale = -128/max; q = min(127, round(iscale*x)); d = 1/iscale;
+// an all-zero block gives d = 0 and zero codes.  Out: the lane's 16 codes packed
+// little-endian, their sum (one bsums entry) and the block's d.
+__device__ __forceinline__ void q8k_lane16(const float *v, int sub, uint32_t packed[4], int *sum_out, float *d_out) {
+    // the lane's largest |x| and the first value holding it (ascending
+    // scan, strict >: ties keep the lower index; a NaN compares false
+    // and is never chosen)
+    float am = 0.f, av = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const bool gt = fabsf(v[i]) > am;
+        av = gt ? v[i] : av;
+        am = gt ? fabsf(v[i]) : am;
+    }
+    const uint32_t bmax = row_max_u32(__float_as_uint(am));  // non-negative: bits order as values
+    uint32_t key = __float_as_uint(am) == bmax ? ((uint32_t)sub << 1) | (__float_as_uint(av) >> 31) : 0xffffffffu;
+    key = row_min_u32(key);  // the first lane holding the block max, and that value's sign
+    packed[0] = packed[1] = packed[2] = packed[3] = 0u;
+    int sum = 0;
+    float d = 0.f;
+    if (bmax != 0u) {  // uniform within the 16-lane block
+        const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
+        const float iscale = -128.f / mx;
+        int q[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+#pragma clang fp contract(off)
+            // min(roundf(iscale * x), 127): for |t| <= 2^23, adding 0.5 - 2^-25
+            // with t's sign and truncating rounds exactly the halves (and
+            // everything above them) away from zero -- checked for every
+            // such float; fminf sends NaN to 127 as the reference's min
+            // does.  Separate roundings: no fma contraction.
+            const float tt = iscale * v[i];
+            const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
+            q[i] = max(-128, (int)r);
+            sum += q[i];
+        }
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
+            packed[w] = lo | (hi << 16);
+        }
+        d = 1.f / iscale;
+    }
+    *sum_out = sum;
+    *d_out = d;
+}
+
 constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 

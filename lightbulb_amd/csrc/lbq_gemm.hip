@@ -110,6 +110,69 @@ __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float1
     }
 }
 
+// The same operand rows straight from f32 x (k <= 16384): the workgroup
+// quantises its row to Q8_K in registers (q8k_lane16, as the standalone
+// quantiser), shares the block scales through LDS for the row exponent, and
+// converts with the same arithmetic as k_act_f16 -- one launch instead of two,
+// bit-identical operands.
+__global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
+                                                   int *__restrict__ erow) {
+    constexpr int MAXP = 4;  // passes of 16 blocks
+    __shared__ float ds[16 * MAXP];
+    const int64_t m = blockIdx.x;
+    const int t = threadIdx.x, sub = t & 15;
+    const int nbx = (int)(K / KB), np = (nbx + 15) >> 4;
+    const float *xr = x + m * K;
+    float v[MAXP][16];
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        const int b = min(16 * j + (t >> 4), nbx - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(xr + (int64_t)b * KB + 16 * sub);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = src[i];
+            v[j][4 * i] = f.x; v[j][4 * i + 1] = f.y; v[j][4 * i + 2] = f.z; v[j][4 * i + 3] = f.w;
+        }
+    }
+    uint4 codes[MAXP];
+    float dj[MAXP];
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        codes[j] = make_uint4(0u, 0u, 0u, 0u);
+        dj[j] = 0.f;
+        if (j < np) {  // workgroup-uniform
+            uint32_t packed[4];
+            int sum;
+            q8k_lane16(v[j], sub, packed, &sum, &dj[j]);
+            codes[j] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            const int b = 16 * j + (t >> 4);
+            if (sub == 0 && b < nbx) ds[b] = dj[j];
+        }
+    }
+    __syncthreads();
+    float mx = 0.f;
+    for (int b = 0; b < nbx; b++) mx = fmaxf(mx, fabsf(ds[b]));
+    const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;  // as k_act_f16
+    if (t == 0) erow[m] = e;
+    _Float16 *a = A + m * K;
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        const int b = 16 * j + (t >> 4);
+        if (j < np && b < nbx) {
+            const float sx = __builtin_amdgcn_ldexpf(dj[j], -e);
+            const float cc = -1152.f * sx;
+            uint32_t w8[8];
+            codes_to_f16(codes[j].x, sx, cc, &w8[0], &w8[1]);
+            codes_to_f16(codes[j].y, sx, cc, &w8[2], &w8[3]);
+            codes_to_f16(codes[j].z, sx, cc, &w8[4], &w8[5]);
+            codes_to_f16(codes[j].w, sx, cc, &w8[6], &w8[7]);
+            uint4 *dst = reinterpret_cast<uint4 *>(a + (int64_t)b * KB + 16 * sub);
+            dst[0] = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+            dst[1] = make_uint4(w8[4], w8[5], w8[6], w8[7]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // B-operand sources.  A lane's raw bytes of one block come in NL loads
 // (load_part(i), so the kernel can spread them over its MFMA stream); prep()
@@ -691,31 +754,57 @@ size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
     return ws_layout(plan_for(type, n, k, m), n, k, m).total;
 }
 
-hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       int64_t m, float *y, void *ws, hipStream_t st) {
-    if (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K) {
-        if (!ws) return hipErrorInvalidValue;
-        const Plan p = plan_for(type, n, k, m);
-        const WsLayout L = ws_layout(p, n, k, m);
-        uint8_t *base = static_cast<uint8_t *>(ws);
-        _Float16 *a = reinterpret_cast<_Float16 *>(base + L.a_off);
-        int *erow = reinterpret_cast<int *>(base + L.e_off);
-        float *part = reinterpret_cast<float *>(base + L.part_off);
+bool gemm_prepass_fuses_quant(int64_t k, const float *x) {
+    return x && k % KB == 0 && k / KB <= 64 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st) {
+    if (!ws || type == TYPE_Q8_0) return hipErrorInvalidValue;
+    const Plan p = plan_for(type, 1, k, m);  // the operand rows do not depend on n
+    const WsLayout L = ws_layout(p, 1, k, m);
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    _Float16 *a = reinterpret_cast<_Float16 *>(base + L.a_off);
+    int *erow = reinterpret_cast<int *>(base + L.e_off);
+    if (x) {
+        if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
+        k_quant_f16<<<(unsigned)m, 256, 0, st>>>(x, k, a, erow);
+    } else {
         k_act_f16<<<(unsigned)m, 256, 0, st>>>(act, m, a, erow);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        float *out = p.splits > 1 ? part : y;
-        const int64_t stride = p.splits > 1 ? m * n : 0;
-        switch (type) {
-        case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
-        case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
-        default: e = launch_typed<TYPE_Q6_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
-        }
-        if (e != hipSuccess || p.splits == 1) return e;
-        const int64_t count = m * n;
-        k_split_sum<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(part, p.splits, count, y);
-        return hipGetLastError();
     }
+    return hipGetLastError();
+}
+
+hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int64_t m, float *y, void *ws,
+                     hipStream_t st) {
+    if (!ws || type == TYPE_Q8_0) return hipErrorInvalidValue;
+    const Plan p = plan_for(type, n, k, m);
+    const WsLayout L = ws_layout(p, n, k, m);
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    const _Float16 *a = reinterpret_cast<const _Float16 *>(base + L.a_off);
+    const int *erow = reinterpret_cast<const int *>(base + L.e_off);
+    float *part = reinterpret_cast<float *>(base + L.part_off);
+    float *out = p.splits > 1 ? part : y;
+    const int64_t stride = p.splits > 1 ? m * n : 0;
+    hipError_t e;
+    switch (type) {
+    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    default: e = launch_typed<TYPE_Q6_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    }
+    if (e != hipSuccess || p.splits == 1) return e;
+    const int64_t count = m * n;
+    k_split_sum<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(part, p.splits, count, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
+                       const float *x, int64_t m, float *y, void *ws, hipStream_t st) {
+    if (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K) {
+        hipError_t e = gemm_prepass(type, k, act, x, m, ws, st);
+        if (e != hipSuccess) return e;
+        return gemm_main(type, w, n, k, row_bytes, m, y, ws, st);
+    }
+    if (x) return hipErrorInvalidValue;  // Q8_0 takes quantised activations
     // Q8_0 (activation scale every 32 values): the decode GEMV over row chunks of 8
     for (int64_t m0 = 0; m0 < m; m0 += 8) {
         const int mc = (int)(m - m0 < 8 ? m - m0 : 8);

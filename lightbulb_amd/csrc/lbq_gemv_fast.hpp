@@ -19,45 +19,7 @@
 
 namespace lbq {
 
-// ---------------------------------------------------------------------------
-// DPP helpers (gfx9 dpp_ctrl: quad_perm 0x00-0xFF, row_ror:n = 0x120+n)
-// ---------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-// every lane of each 16-lane row gets the row's max / min / sum
-__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = max(v, dpp_u32<0x124>(v));  // row_ror:4
-    v = max(v, dpp_u32<0x128>(v));  // row_ror:8
-    return v;
-}
-__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
-    v = min(v, dpp_u32<0xB1>(v));
-    v = min(v, dpp_u32<0x4E>(v));
-    v = min(v, dpp_u32<0x124>(v));
-    v = min(v, dpp_u32<0x128>(v));
-    return v;
-}
-__device__ __forceinline__ float row_sum_f32(float v) {
-    v += dpp_f32<0xB1>(v);
-    v += dpp_f32<0x4E>(v);
-    v += dpp_f32<0x124>(v);
-    v += dpp_f32<0x128>(v);
-    return v;
-}
-__device__ __forceinline__ int quad_sum_i32(int v) {
-    v += (int)dpp_u32<0xB1>((uint32_t)v);
-    v += (int)dpp_u32<0x4E>((uint32_t)v);
-    return v;
-}
-__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
 
 // Q8_K of one 256-value block by one wave (lane holds values 4*lane..4*lane+3).
 // Same selection and arithmetic as q8k_block_wave: the first value of largest |x|
@@ -328,11 +290,9 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
     if constexpr (TYPE != TYPE_Q8_0) {
-        // 16 lanes per 256-value block, 16 consecutive values per lane, so the
-        // workgroup quantises 16 blocks per pass (nbx <= 64: at most 4 passes).
-        // Selection and arithmetic as q8k_block_wave: the first value of largest
-        // |x| (NaN never chosen) sets iscale = -128/max; q = min(127, round(iscale*x));
-        // d = 1/iscale; a lane's 16 codes are exactly one bsums entry.
+        // 16 lanes per 256-value block, 16 consecutive values per lane
+        // (q8k_lane16), so the workgroup quantises 16 blocks per pass (nbx <= 64:
+        // at most 4 passes); a lane's 16 codes are exactly one bsums entry.
         constexpr int MAXP = 4;
         const int t = threadIdx.x, sub = t & 15;
         const int np = (nbx + 15) >> 4;  // workgroup-uniform
@@ -353,47 +313,10 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
 #pragma unroll
         for (int j = 0; j < MAXP; j++) {
             if (j == 0 || j < np) {  // pass 0 unconditional: its loads stay ahead of the ring
-                // the lane's largest |x| and the first value holding it (ascending
-                // scan, strict >: ties keep the lower index; a NaN compares false
-                // and is never chosen)
-                float am = 0.f, av = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const bool gt = fabsf(v[j][i]) > am;
-                    av = gt ? v[j][i] : av;
-                    am = gt ? fabsf(v[j][i]) : am;
-                }
-                const uint32_t bmax = row_max_u32(__float_as_uint(am));  // non-negative: bits order as values
-                uint32_t key = __float_as_uint(am) == bmax ? ((uint32_t)sub << 1) | (__float_as_uint(av) >> 31) : 0xffffffffu;
-                key = row_min_u32(key);  // the first lane holding the block max, and that value's sign
-                uint32_t packed[4] = {0u, 0u, 0u, 0u};
-                int sum = 0;
-                float d = 0.f;
-                if (bmax != 0u) {  // uniform within the 16-lane block
-                    const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
-                    const float iscale = -128.f / mx;
-                    int q[16];
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-#pragma clang fp contract(off)
-                        // min(roundf(iscale * x), 127): for |t| <= 2^23, adding 0.5 - 2^-25
-                        // with t's sign and truncating rounds exactly the halves (and
-                        // everything above them) away from zero -- checked for every
-                        // such float; fminf sends NaN to 127 as the reference's min
-                        // does.  Separate roundings: no fma contraction.
-                        const float tt = iscale * v[j][i];
-                        const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
-                        q[i] = max(-128, (int)r);
-                        sum += q[i];
-                    }
-#pragma unroll
-                    for (int w = 0; w < 4; w++) {
-                        const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
-                        const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
-                        packed[w] = lo | (hi << 16);
-                    }
-                    d = 1.f / iscale;
-                }
+                uint32_t packed[4];
+                int sum;
+                float d;
+                q8k_lane16(v[j], sub, packed, &sum, &d);
                 const int b = 16 * j + (t >> 4);
                 if (b < nbx) {
                     uint8_t *xb = sx + b * XS_K;

@@ -55,10 +55,18 @@ hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_
 
 // Batched path (m > 8): weights dequantised in registers into MFMA operands.
 // Needs gemm_workspace_bytes(type, n, k, m) bytes of device memory at ws (fp16
-// activation operands and, for shapes that split k, the partial sums).
+// activation operands and, for shapes that split k, the partial sums).  For
+// k-quants it is a pre-pass that writes the operand rows -- from raw f32 x
+// (quantised to Q8_K on the way) when x != nullptr, else from act's codes --
+// and the GEMM proper, which weights of one type, k and m can share a pre-pass
+// for (the operand rows do not depend on n).
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
+bool gemm_prepass_fuses_quant(int64_t k, const float *x);
+hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st);
+hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int64_t m, float *y, void *ws,
+                     hipStream_t st);
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       int64_t m, float *y, void *ws, hipStream_t st);
+                       const float *x, int64_t m, float *y, void *ws, hipStream_t st);
 
 // Compute units of the current device (cached after the first call).
 int num_cus();

@@ -230,6 +230,26 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
         assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_batched_prepass_quantisation_is_bit_exact(oracle, lbq, dev, t):
+    # At m > 8 forward() quantises x inside the GEMM's operand pre-pass; fed the
+    # standalone kernel's codes instead, the same GEMM must give the same bits
+    # (both tile kernels, one and four quantisation passes, special rows)
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    rng = np.random.default_rng(130 + t)
+    for m, n, k in ((20, 200, 4096), (300, 130, 4096), (40, 96, 14336)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[:7] = _special_rows(k)
+        x[-1, rng.random(k) < 0.01] *= 20
+        xd = to_dev(x, dev)
+        y_fused = qm.forward(xd)
+        y_act = qm.forward_quantized(QActivation.for_weight(qm, m).quantize(xd))
+        torch.cuda.synchronize()
+        assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
 def test_qmatmul_group_matches_separate_calls(oracle, lbq, dev, t):
     # q|k|v- and gate|up-like groups in one call: every output bit-identical to
