@@ -190,6 +190,17 @@ def main():
             qz.qmatmul_group(layer[4:6], xs[4])
             layer[6].forward(xs[6])
 
+    # the layer as its call sites would run it: q|k|v grouped, o, then the MLP
+    # with gate/up and the SiLU product in one launch feeding down_proj
+    h_mlp = torch.empty(1, 14336, device=dev)
+
+    def fused_step_all_copies():
+        for layer in copies:
+            qz.qmatmul_group(layer[0:3], xs[0])
+            layer[3].forward(xs[3])
+            h = qz.gate_up_silu(layer[4], layer[5], xs[4])
+            layer[6].forward(h)
+
     # activation handles for the dot-only (roofline) graph
     acts = {k: qz.QActivation(qz.GgmlDType.Q8K, 1, k, dev) for k in (4096, 14336)}
     for (_, n, k), x in zip(LAYER, xs):
@@ -204,6 +215,7 @@ def main():
     g_full = capture(torch, full_step_all_copies)
     g_dot = capture(torch, dot_all_copies)
     g_grp = capture(torch, grouped_step_all_copies)
+    g_fus = capture(torch, fused_step_all_copies)
     reps = max(1, (args.steps + args.copies - 1) // args.copies)
     wreps = max(1, (args.warmup + args.copies - 1) // args.copies)
     steps = reps * args.copies
@@ -213,12 +225,15 @@ def main():
     ms_dot = timed_graph(torch, g_dot, reps, stream) / args.copies
     timed_graph(torch, g_grp, wreps, stream)
     ms_grp = timed_graph(torch, g_grp, reps, stream) / args.copies
+    timed_graph(torch, g_fus, wreps, stream)
+    ms_fus = timed_graph(torch, g_fus, reps, stream) / args.copies
     value = layer_bytes / (ms_full * 1e-3) / 1e9
     full_gbs = (layer_bytes + io_bytes) / (ms_full * 1e-3) / 1e9
     dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
     log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
         f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s; "
-        f"grouped (4 launches) {ms_grp * 1e3:.2f} us -> {layer_bytes / (ms_grp * 1e-3) / 1e9:.0f} GB/s")
+        f"grouped (4 launches) {ms_grp * 1e3:.2f} us -> {layer_bytes / (ms_grp * 1e-3) / 1e9:.0f} GB/s; "
+        f"call-site fused (q|k|v, o, gate|up+SiLU, down) {ms_fus * 1e3:.2f} us")
 
     # per-shape dot kernel times (same graphs, one shape at a time)
     kernels = {}
@@ -277,9 +292,15 @@ def main():
                     "launches": 4,
                     "path": "lbq_qmatmul_group_f32 for q|k|v and gate|up (one fused launch each), "
                             "lbq_qmatmul_f32 for o and down; outputs bit-identical to the 7 separate calls"},
+        "call_site_fused": {"us_per_step": round(ms_fus * 1e3, 3),
+                            "GB/s": round(layer_bytes / (ms_fus * 1e-3) / 1e9, 1),
+                            "launches": 4,
+                            "path": "lbq_qmatmul_group_f32 (q|k|v), lbq_qmatmul_f32 (o), lbq_gate_up_silu_f32 "
+                                    "(gate|up with silu(gate)*up in the GEMV epilogue), lbq_qmatmul_f32 (down on "
+                                    "that product): the data flow of the reference's attention/MLP call sites"},
         "kernels": kernels,
     }
-    del g_full, g_dot, g_grp
+    del g_full, g_dot, g_grp, g_fus
     tr = load_traffic()
     if tr and "bytes_per_launch" in tr:
         result["roofline"]["traffic"] = tr["bytes_per_launch"]
@@ -364,24 +385,20 @@ def stack_bench(torch, qz, gen, dev, stream):
                     qm.forward(xs[k])
             head.forward(xs[4096])
 
-        def token_step_grouped():  # q|k|v, gate|up grouped where the types agree
+        def token_step_grouped():  # q|k|v grouped where the types agree; gate|up+SiLU fused into down
             for mats in layers:
-                for grp in ((0, 1, 2), (3,), (4, 5), (6,)):
-                    qs = [mats[i] for i in grp]
-                    k = LAYER[grp[0]][2]
-                    if len(qs) > 1 and len({q.qtensor().dtype() for q in qs}) == 1:
-                        qz.qmatmul_group(qs, xs[k])
-                    elif len(qs) > 1 and qs[0].qtensor().dtype() == qs[1].qtensor().dtype():
-                        qz.qmatmul_group(qs[:2], xs[k])
-                        for q in qs[2:]:
-                            q.forward(xs[k])
-                    else:
-                        for q in qs:
-                            q.forward(xs[k])
+                q, kp, v, o, gate, up, down = mats
+                if v.qtensor().dtype() == q.qtensor().dtype():
+                    qz.qmatmul_group([q, kp, v], xs[4096])
+                else:
+                    qz.qmatmul_group([q, kp], xs[4096])
+                    v.forward(xs[4096])
+                o.forward(xs[4096])
+                down.forward(qz.gate_up_silu(gate, up, xs[4096]))
             head.forward(xs[4096])
 
         reps = 20 if B == 1 else 5
-        for tag, fn in ((f"b{B}", token_step), (f"b{B}_grouped", token_step_grouped)):
+        for tag, fn in ((f"b{B}", token_step), (f"b{B}_call_site_fused", token_step_grouped)):
             g = capture(torch, fn)
             timed_graph(torch, g, 2, stream)
             ms = timed_graph(torch, g, reps, stream)

@@ -112,6 +112,17 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
 int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
                           float *const *d_ys, void *stream);
 
+/* The gate/up half of the reference's MLP forward (/root/reference/src/model/
+ * mlp_wrapper.rs:190-194: `silu(gate_proj.forward(x)) * up_proj.forward(x)`):
+ * d_out[m][n] = silu(x . Wg^T) * (x . Wu^T), silu(v) = v / (1 + exp(-v)) in f32.
+ * The two products are computed exactly as lbq_qmatmul_f32 computes them.  At
+ * m = 1 both weights stream through one launch and the product is formed in its
+ * epilogue, so neither product is written out; otherwise the grouped path fills
+ * context memory and one elementwise launch combines it.  gate and up share the
+ * ggml type, n and k. */
+int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
+                         float *d_out, void *stream);
+
 /* Quantised-activation handle: the two halves of QMatMul::forward as separate
  * calls.  candle's k_quants::matmul first quantises every row of x into
  * vec-dot blocks and then runs vec_dot for all output columns; splitting the

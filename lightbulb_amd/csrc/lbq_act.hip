@@ -181,4 +181,20 @@ hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float 
     return hipGetLastError();
 }
 
+// out = silu(g) * u with candle's f32 silu, v / (1 + exp(-v)) (the gate/up
+// product of mlp_wrapper.rs:190-194 when it is not fused into the GEMV)
+__global__ __launch_bounds__(256) void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u, int64_t count,
+                                                  float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    const float v = g[i];
+    out[i] = v / (1.f + expf(-v)) * u[i];
+}
+
+hipError_t launch_silu_mul(const float *g, const float *u, int64_t count, float *out, hipStream_t st) {
+    if (count <= 0) return hipSuccess;
+    k_silu_mul<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(g, u, count, out);
+    return hipGetLastError();
+}
+
 }  // namespace lbq

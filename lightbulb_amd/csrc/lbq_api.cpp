@@ -27,6 +27,8 @@ struct lbq_ctx {
     size_t scratch_bytes;
     uint8_t *ws;          // batched GEMM workspace (fp16 activations, split-k partials)
     size_t ws_bytes;
+    uint8_t *tmp;         // gate and up outputs when their product is not fused
+    size_t tmp_bytes;
 };
 
 struct lbq_weight {
@@ -232,6 +234,8 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
     c->scratch_bytes = 0;
     c->ws = nullptr;
     c->ws_bytes = 0;
+    c->tmp = nullptr;
+    c->tmp_bytes = 0;
     *out_ctx = c;
     return LBQ_OK;
 }
@@ -239,10 +243,11 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
 int lbq_ctx_destroy(lbq_ctx *ctx) {
     if (!ctx) return LBQ_OK;
     DeviceGuard g(ctx->device);
-    if (ctx->scratch || ctx->ws) {
+    if (ctx->scratch || ctx->ws || ctx->tmp) {
         (void)hipDeviceSynchronize();
         if (ctx->scratch) (void)hipFree(ctx->scratch);
         if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->tmp) (void)hipFree(ctx->tmp);
     }
     delete ctx;
     return LBQ_OK;
@@ -414,6 +419,46 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         s = run_dot(ctx, ws[i], av, m, d_ys[i], st);
         if (s) return s;
     }
+    return LBQ_OK;
+}
+
+int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
+                         float *d_out, void *stream) {
+    if (!ctx || !w_gate || !w_up || !d_out) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_gate_up_silu_f32");
+    if (w_gate->type != w_up->type || w_gate->n != w_up->n || w_gate->k != w_up->k)
+        return fail(LBQ_ERR_SHAPE, "gate (type %d, %lld x %lld) and up (type %d, %lld x %lld) differ", w_gate->type,
+                    (long long)w_gate->n, (long long)w_gate->k, w_up->type, (long long)w_up->n, (long long)w_up->k);
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    if (m == 0) return LBQ_OK;
+    if (!d_x) return fail(LBQ_ERR_INVALID_ARG, "null activation pointer");
+    if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_out)) & 3u)
+        return fail(LBQ_ERR_INVALID_ARG, "x and out must be 4-byte aligned f32 buffers");
+    if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (m == 1 && lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
+        // one launch: both weights' rows interleaved, the product in the epilogue
+        hipError_t e = lbq::launch_gemv_silu_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n, w_gate->k,
+                                                  w_gate->row_bytes, d_x, d_out, st);
+        if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "gate/up launch");
+    }
+    // otherwise gate and up through the grouped path into context memory, then
+    // one elementwise launch
+    const size_t half = ((size_t)m * (size_t)w_gate->n * sizeof(float) + 255) / 256 * 256;
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        int s = ensure_buffer(&ctx->tmp, &ctx->tmp_bytes, 2 * half, "gate/up outputs");
+        if (s) return s;
+    }
+    float *gy = reinterpret_cast<float *>(ctx->tmp), *uy = reinterpret_cast<float *>(ctx->tmp + half);
+    const lbq_weight *pair[2] = {w_gate, w_up};
+    float *outs[2] = {gy, uy};
+    int s = lbq_qmatmul_group_f32(ctx, pair, 2, d_x, m, outs, stream);
+    if (s) return s;
+    hipError_t e = lbq::launch_silu_mul(gy, uy, m * w_gate->n, d_out, st);
+    if (e != hipSuccess) return hip_fail(e, "silu-mul launch");
     return LBQ_OK;
 }
 

@@ -444,30 +444,45 @@ typedef __attribute__((address_space(1))) float *gfloats;
 // The m = 1 kernel.  A row group is RPW rows; lane (r, li) decodes piece
 // li % PPB of blocks li / PPB + BPI*i (i < IT) of row r.  Requires nb <= BPI*IT.
 // ---------------------------------------------------------------------------
-// GROUPED: rm may hold several weights (rows looked up per group); otherwise it
-// is one weight, addressed directly.
-template <int TYPE, int RPW, int IT, bool FUSED, bool GROUPED>
+// Row maps: MAP_ONE is one weight, addressed directly; MAP_SEGMENTS holds
+// several weights (rows looked up per group); MAP_SILU_PAIRS interleaves the
+// rows of a gate (w[0]) and an up (w[1]) weight -- row 2i is gate row i, 2i + 1
+// up row i -- and writes silu(gate_i) * up_i to y[0][i]: the gate/up half of
+// an MLP in one launch, with no gate/up round trip.
+enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
+
+// candle's silu for f32: v / (1 + exp(-v))
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
+
+template <int TYPE, int RPW, int IT, bool FUSED, int MAP>
 __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                ActView act) {
+    constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
+    static_assert(!PAIRED || RPW <= 2, "a silu pair spans two row groups or one");
     const int64_t n = rm.n;
     const uint8_t *__restrict__ W = rm.w[0];
     float *__restrict__ y = rm.y[0];
     RowMapS rs{};
-    if constexpr (GROUPED) rs = map_regs(rm);
+    if constexpr (MAP != MAP_ONE) rs = map_regs(rm);
+    // silu pairs: up row i is (w1 - w0) past gate row i (arithmetic, not a select
+    // between fields, which the compiler would turn into an indexed copy)
+    const uint64_t wdiff = rs.w1 - rs.w0;
     using F = Fast<TYPE>;
     using Raw = typename F::Raw;
     constexpr int LPR = 64 / RPW;
     constexpr int BPI = LPR / F::PPB;
     static_assert(BPI >= 1, "a row needs at least one whole block per sweep");
-    // grouped: the wave index as a scalar, so row-group indices (and row lookups) are scalar
+    // row maps: the wave index as a scalar, so row-group indices (and row lookups) are scalar
     const int lane = threadIdx.x & 63,
-              wave = GROUPED ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
+              wave = MAP != MAP_ONE ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
     const int r = lane / LPR, li = lane % LPR;
     const int p = li % F::PPB, bs0 = li / F::PPB;
-    const int64_t ng = (n + RPW - 1) / RPW;
+    // silu pairs are never split between waves: ranges are counted in pairs
+    constexpr int GPU_ = PAIRED ? 2 / RPW : 1;  // row groups per unit
+    const int64_t ng = PAIRED ? n / 2 : (n + RPW - 1) / RPW;
     const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
     const int64_t per = ng / nw, rem = ng % nw;
-    const int64_t g0 = gw * per + (gw < rem ? gw : rem), g1 = g0 + per + (gw < rem ? 1 : 0);
+    const int64_t g0 = (gw * per + (gw < rem ? gw : rem)) * GPU_, g1 = g0 + (per + (gw < rem ? 1 : 0)) * GPU_;
 
     // loads are unconditional (row and block clamped into range); compute masks.
     // Grouped: the group's rows are looked up once each (g is wave-uniform),
@@ -486,6 +501,18 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
                 if (q == 0 || r == q) {
                     rp = sp;
                     roff = (int64_t)(row - sb) * row_bytes;
+                }
+            }
+            wr = (const uint8_t *)((gbytes)rp + roff);
+        } else if constexpr (PAIRED) {
+            uint64_t rp = 0;
+            int64_t roff = 0;
+#pragma unroll
+            for (int q = 0; q < RPW; q++) {
+                const int64_t v = min(g * RPW + q, n - 1);
+                if (q == 0 || r == q) {
+                    rp = rs.w0 + (uint64_t)(v & 1) * wdiff;
+                    roff = (v >> 1) * row_bytes;
                 }
             }
             wr = (const uint8_t *)((gbytes)rp + roff);
@@ -523,6 +550,7 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     if constexpr (FUSED) quantise_x_lds<TYPE>(x, nb, sx, issue_ring);
     else copy_x_lds<TYPE>(act, nb, sx, issue_ring);
 
+    float pend = 0.f;  // silu pairs: the gate sum waiting for its up sum (wave-uniform)
     auto compute_group = [&](int64_t g, const Raw *buf, bool store) {
         float acc = 0.f;
 #pragma unroll
@@ -547,7 +575,13 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
                 s = __int_as_float(rl(__float_as_uint(acc), 16 * q));
             }
             const int64_t rq = g * RPW + q;
-            if constexpr (GROUPED) {
+            if constexpr (PAIRED) {
+                if ((rq & 1) == 0) {
+                    pend = s;
+                } else if (store && lane == LPR * q && rq < n) {
+                    y[rq >> 1] = silu_f32(pend) * s;
+                }
+            } else if constexpr (GROUPED) {
                 uint64_t yp;
                 int32_t yb;
                 map_seg(rs, (int32_t)min(rq, n - 1), rs.y0, rs.y1, rs.y2, rs.y3, &yp, &yb);

@@ -465,7 +465,7 @@ static bool fast_shape(int nb, int *rpw, int *it) {
 }
 
 template <int TYPE, int RPW, int IT>
-static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act,
+static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
                               hipStream_t st) {
     const int64_t n = rm.n;
     const int64_t ng = (n + RPW - 1) / RPW;
@@ -479,24 +479,32 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     const size_t lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
-    if (rm.end[0] < n) {  // several weights: fused quantisation only (the caller runs the rest one by one)
+    // row maps take the fused quantisation only (the caller runs the rest weight by weight)
+    if (map == MAP_SILU_PAIRS) {
+        if constexpr (RPW <= 2) {
+            if (!x || (n & 1)) return hipErrorNotSupported;
+            k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        } else {
+            return hipErrorNotSupported;
+        }
+    } else if (rm.end[0] < n) {
         if (!x) return hipErrorNotSupported;
-        k_gemv1<TYPE, RPW, IT, true, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
     } else if (x) {
-        k_gemv1<TYPE, RPW, IT, true, false><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        k_gemv1<TYPE, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
     } else {
-        k_gemv1<TYPE, RPW, IT, false, false><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        k_gemv1<TYPE, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
     }
     return hipGetLastError();
 }
 
 template <int TYPE>
-static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act,
+static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
                            hipStream_t st) {
     int rpw, it;
     if (!fast_shape<TYPE>(nb, &rpw, &it)) return hipErrorNotSupported;
 #define LBQ_FAST(R, I) \
-    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, st);
+    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, map, st);
     if constexpr (Fast<TYPE>::PPB == 8) {
         LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
     } else if constexpr (Fast<TYPE>::PPB == 4) {
@@ -508,10 +516,11 @@ static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const fl
     return hipErrorNotSupported;
 }
 
-// One weight (rm.n rows, single segment) or, at m = 1, a multi-weight row map.
+// One weight (rm.n rows, single segment) or, at m = 1, a multi-weight row map
+// (map: MAP_ONE / MAP_SEGMENTS, or MAP_SILU_PAIRS for a gate/up pair).
 template <int TYPE>
 static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
-                           hipStream_t st) {
+                           int map, hipStream_t st) {
     using D = Dec<TYPE>;
     const uint8_t *w = rm.w[0];
     const int64_t n = rm.n;
@@ -522,10 +531,10 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
     if (m == 1) {
-        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, st);
+        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, st);
         if (e != hipErrorNotSupported) return e;
     }
-    if (rm.end[0] != n) return hipErrorNotSupported;  // row maps: m = 1 fast path only
+    if (map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // row maps: m = 1 fast path only
     GemvCfg c = pick_cfg(TYPE, n, g.pieces, m, k);
     c.fused = false;  // m > 1: x arrives quantised (separate kernel)
     if (x) return hipErrorInvalidValue;

@@ -5,8 +5,8 @@
 namespace lbq {
 
 hipError_t gemv_q4k(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
-                       hipStream_t st) {
-    return run_type<TYPE_Q4_K>(rm, k, row_bytes, act, x, m, st);
+                       int map, hipStream_t st) {
+    return run_type<TYPE_Q4_K>(rm, k, row_bytes, act, x, m, map, st);
 }
 
 }  // namespace lbq

@@ -53,6 +53,15 @@ hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64
 hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act,
                              const float *x, hipStream_t st);
 
+// m = 1 gate/up pair (same type, n, k): out[i] = silu(x . gate_i) * (x . up_i)
+// in one launch that quantises x in its prologue.  hipErrorNotSupported when the
+// single-row fast path does not cover k (or x is not 16-byte aligned); the
+// caller then computes gate and up and combines them with launch_silu_mul.
+hipError_t launch_gemv_silu_pair(int type, const uint8_t *w_gate, const uint8_t *w_up, int64_t n, int64_t k,
+                                 int64_t row_bytes, const float *x, float *out, hipStream_t st);
+// out[i] = silu(g[i]) * u[i], count values
+hipError_t launch_silu_mul(const float *g, const float *u, int64_t count, float *out, hipStream_t st);
+
 // Batched path (m > 8): weights dequantised in registers into MFMA operands.
 // Needs gemm_workspace_bytes(type, n, k, m) bytes of device memory at ws (fp16
 // activation operands and, for shapes that split k, the partial sums).  For

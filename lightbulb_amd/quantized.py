@@ -275,6 +275,49 @@ def qmatmul_group(qmatmuls, xs: torch.Tensor) -> list[torch.Tensor]:
     return ys
 
 
+def gate_up_silu(gate: "QMatMul", up: "QMatMul", xs: torch.Tensor) -> torch.Tensor:
+    """``silu(gate.forward(xs)) * up.forward(xs)`` -- the gate/up half of the
+    reference's MLP forward (src/model/mlp_wrapper.rs:190-194) -- in one call
+    (one launch at m = 1).  gate and up share the ggml type, n and k."""
+    (n, k), (nu, ku) = gate.qtensor().shape(), up.qtensor().shape()
+    if gate.qtensor().dtype() != up.qtensor().dtype() or (n, k) != (nu, ku):
+        raise ValueError("gate and up must share the ggml type and shape")
+    if xs.dtype != torch.float32:
+        raise ValueError(f"the lhs for quantized matmul must be f32, got {xs.dtype}")
+    if xs.dim() < 2:
+        raise ValueError(f"input tensor has only one dimension {tuple(xs.shape)}")
+    if xs.shape[-1] != k:
+        raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with {(n, k)}")
+    if not xs.is_contiguous():
+        raise ValueError(f"input tensor is not contiguous {tuple(xs.shape)}")
+    m = xs.numel() // k
+    out = torch.empty(*xs.shape[:-1], n, dtype=torch.float32, device=xs.device)
+    if m:
+        _lib.check(_lib.lib().lbq_gate_up_silu_f32(gate._ctx, gate._handle, up._handle, xs.data_ptr(), m,
+                                                   out.data_ptr(), _stream(xs.device)))
+    return out
+
+
+class Mlp:
+    """``Mlp`` (src/model/mlp_wrapper.rs): ``down_proj(silu(gate_proj(x)) * up_proj(x))``
+    over ``QuantizableLinear`` projections; quantized gate/up pairs take the fused
+    ``gate_up_silu`` path."""
+
+    def __init__(self, gate_proj: "QuantizableLinear", up_proj: "QuantizableLinear", down_proj: "QuantizableLinear"):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def forward(self, xs: torch.Tensor) -> torch.Tensor:
+        g, u = self.gate_proj, self.up_proj
+        if (g.is_quantized() and u.is_quantized() and g.inner.qtensor().dtype() == u.inner.qtensor().dtype()
+                and g.inner.qtensor().shape() == u.inner.qtensor().shape()):
+            h = gate_up_silu(g.inner, u.inner, xs)
+        else:
+            h = torch.nn.functional.silu(g.forward(xs)) * u.forward(xs)
+        return self.down_proj.forward(h)
+
+    __call__ = forward
+
+
 class QActivation:
     """x [m, k] quantised once (Q8_K for k-quant weights, Q8_0 for Q8_0 weights),
     reusable by every QMatMul that reads the same x -- q/k/v and gate/up."""

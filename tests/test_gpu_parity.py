@@ -276,6 +276,46 @@ def test_qmatmul_group_matches_separate_calls(oracle, lbq, dev, t):
                     assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, x, nthreads=8).astype(np.float64))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+def test_gate_up_silu(oracle, lbq, dev, t):
+    # silu(x.Wg^T) * (x.Wu^T): one launch at m = 1 (the product in the GEMV
+    # epilogue), the grouped path plus an elementwise launch otherwise; against
+    # the oracle's two products combined in float64, and through Mlp.forward
+    from lightbulb_amd.quantized import Mlp, QMatMul, QTensor, QuantizableLinear, gate_up_silu
+    rng = np.random.default_rng(140 + t)
+    bs = oracle.block_size(t)
+    for k, n in ((4096, 300), (14336, 77), (1024, 513)):
+        g_raw = bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3)
+        u_raw = bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3)
+        qg = QMatMul.from_qtensor(QTensor(to_dev(g_raw, dev), t, (n, k)))
+        qu = QMatMul.from_qtensor(QTensor(to_dev(u_raw, dev), t, (n, k)))
+        for m in (1, 3, 20):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            for shift in ((0, 1) if m == 1 else (0,)):
+                buf = to_dev(np.concatenate([np.zeros(shift, np.float32), x.ravel()]), dev)
+                y = gate_up_silu(qg, qu, buf[shift:].view(m, k))
+                torch.cuda.synchronize()
+                gr = oracle.qmatmul(t, g_raw, n, k, x, nthreads=8).astype(np.float64)
+                ur = oracle.qmatmul(t, u_raw, n, k, x, nthreads=8).astype(np.float64)
+                ref = gr / (1.0 + np.exp(-gr)) * ur
+                assert_rows_close(y.cpu().numpy(), ref, tight_bound(t, m))
+    # the MLP forward end to end (down_proj on the fused gate/up output)
+    k, n = 512, 256
+    raws = [bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3) for _ in range(2)]
+    d_raw = bp.random_blocks(rng, t, k * n // bs, d_scale=1e-3)
+    lin = lambda raw, shape: QuantizableLinear.from_qmatmul(QMatMul.from_qtensor(QTensor(to_dev(raw, dev), t, shape)))
+    mlp = Mlp(lin(raws[0], (n, k)), lin(raws[1], (n, k)), lin(d_raw, (k, n)))
+    x = rng.standard_normal((2, 1, k)).astype(np.float32)
+    y = mlp.forward(to_dev(x, dev))
+    assert tuple(y.shape) == (2, 1, k)
+    xf = x.reshape(2, k)
+    gr = oracle.qmatmul(t, raws[0], n, k, xf, nthreads=4).astype(np.float64)
+    ur = oracle.qmatmul(t, raws[1], n, k, xf, nthreads=4).astype(np.float64)
+    h = (gr / (1.0 + np.exp(-gr)) * ur).astype(np.float32)
+    ref = oracle.qmatmul(t, d_raw, k, n, h, nthreads=4).astype(np.float64)
+    assert_rows_close(y.cpu().numpy().reshape(2, k), ref, 2e-3)
+
+
 def test_qmatmul_group_errors(oracle, lbq, dev):
     from lightbulb_amd import _lib
     from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
@@ -299,6 +339,12 @@ def test_qmatmul_group_errors(oracle, lbq, dev):
     hs = (ctypes.c_void_p * 2)(a._handle, None)
     outs = (ctypes.c_void_p * 2)(y.data_ptr(), y.data_ptr())
     assert L.lbq_qmatmul_group_f32(a._ctx, hs, 2, x.data_ptr(), 1, outs, None) == -1
+    # gate/up pairs must match in type and shape
+    from lightbulb_amd.quantized import gate_up_silu
+    with pytest.raises(ValueError, match="share"):
+        gate_up_silu(a, c, x)
+    assert L.lbq_gate_up_silu_f32(a._ctx, a._handle, c._handle, x.data_ptr(), 1, y.data_ptr(), None) == -3
+    assert L.lbq_gate_up_silu_f32(a._ctx, a._handle, None, x.data_ptr(), 1, y.data_ptr(), None) == -1
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
