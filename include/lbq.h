@@ -46,7 +46,10 @@ enum lbq_status {
     LBQ_ERR_SHAPE = -3,            /* k not a multiple of the block size, byte count mismatch */
     LBQ_ERR_OOM = -4,              /* device allocation failed */
     LBQ_ERR_HIP = -5,              /* a HIP runtime call failed */
-    LBQ_ERR_LIMIT = -6             /* size beyond a documented maximum */
+    LBQ_ERR_LIMIT = -6,            /* size beyond a documented maximum */
+    LBQ_ERR_FORMAT = -7,           /* malformed or unsupported GGUF container */
+    LBQ_ERR_NOT_FOUND = -8,        /* no tensor or metadata key of that name */
+    LBQ_ERR_IO = -9                /* a file could not be opened or mapped */
 };
 
 /* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
@@ -158,6 +161,48 @@ int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, 
  * of `ggml_type` -- quantize_tensor (/root/reference/src/quantization/mod.rs:257-327),
  * extended to Q5_K/Q6_K.  Runs on the device. */
 int lbq_quantize_weights_f32(uint32_t ggml_type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * GGUF container (v3, little-endian) and the direct GGUF -> device upload.
+ * lbq_gguf_open maps the file and parses it as the reference's parse_gguf does
+ * (/root/reference/src/gguf/parser.rs:136-213, reached from Content::read,
+ * src/gguf/mod.rs:62-92): magic, version 3 only, metadata (types 0..12, arrays),
+ * tensor infos, data section at the infos' end rounded up to general.alignment
+ * (UInt32; default 32).  Every read is bounds-checked: a malformed file gives
+ * LBQ_ERR_FORMAT with the reference's message, never a fault.  Parsing and the
+ * byte accessors are host-only.  Strings returned point into the handle and live
+ * until lbq_gguf_close.
+ * ------------------------------------------------------------------------- */
+typedef struct lbq_gguf lbq_gguf;
+int lbq_gguf_open(const char *path, lbq_gguf **out);
+int lbq_gguf_close(lbq_gguf *g);
+/* GGUFHeader fields (parser.rs:112-121) and the file size; any pointer may be NULL. */
+int lbq_gguf_header(const lbq_gguf *g, uint32_t *version, int64_t *tensor_count, int64_t *metadata_count,
+                    uint64_t *alignment, uint64_t *tensor_data_offset, uint64_t *file_size);
+/* TensorInfo of tensor `index` in file order (parser.rs:103-109): name, ggml type,
+ * dims (ne0 first; dims must hold n_dims <= 8 values), offset within the data section. */
+int lbq_gguf_tensor_info(const lbq_gguf *g, int64_t index, const char **name, uint32_t *ggml_type, uint32_t *n_dims,
+                         uint64_t *dims, uint64_t *offset);
+int lbq_gguf_find_tensor(const lbq_gguf *g, const char *name, int64_t *index);
+/* A tensor's bytes in the mapped file, as extract_tensor_bytes
+ * (src/quantization/gguf_ops.rs:19-59): ceil(numel / block_size) * type_size
+ * bytes at data_offset + offset, for every GgmlDType (quantization/mod.rs:58-127). */
+int lbq_gguf_tensor_bytes(const lbq_gguf *g, const char *name, const void **data, size_t *nbytes);
+/* Metadata (parser.rs:24-81): key and MetadataValueType by index; typed reads by
+ * key (integers of any width and bool; f32/f64; strings; array element type and
+ * length).  A missing key gives LBQ_ERR_NOT_FOUND, a type mismatch LBQ_ERR_FORMAT. */
+int lbq_gguf_meta_key(const lbq_gguf *g, int64_t index, const char **key, uint32_t *value_type);
+int lbq_gguf_meta_int(const lbq_gguf *g, const char *key, int64_t *out);
+int lbq_gguf_meta_float(const lbq_gguf *g, const char *key, double *out);
+int lbq_gguf_meta_string(const lbq_gguf *g, const char *key, const char **data, size_t *len);
+int lbq_gguf_meta_array(const lbq_gguf *g, const char *key, uint32_t *elem_type, uint64_t *len);
+/* Copy a tensor's bytes into device memory through pinned staging (synchronous). */
+int lbq_gguf_copy_tensor(const lbq_gguf *g, const char *name, void *d_dst, size_t dst_bytes);
+/* A weight handle straight from the file: the tensor (2-D, ne0 = k, ne1 = n, a
+ * served type) goes through pinned staging into device memory the handle owns.
+ * Replaces Content::tensor -> QMatMul::from_qtensor (src/gguf/mod.rs:274-282 and
+ * the call sites listed at lbq_weight_create). */
+int lbq_weight_from_gguf(lbq_ctx *ctx, const lbq_gguf *g, const char *name, lbq_weight **out_w);
 
 #ifdef __cplusplus
 }

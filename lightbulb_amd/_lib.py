@@ -19,6 +19,9 @@ STATUS_NAMES = {
     -4: "LBQ_ERR_OOM",
     -5: "LBQ_ERR_HIP",
     -6: "LBQ_ERR_LIMIT",
+    -7: "LBQ_ERR_FORMAT",
+    -8: "LBQ_ERR_NOT_FOUND",
+    -9: "LBQ_ERR_IO",
 }
 
 # name -> (restype, argtypes); must list every function include/lbq.h declares
@@ -45,6 +48,21 @@ SIGNATURES = {
     "lbq_dequantize_blocks_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
     "lbq_quantize_act": (_c.c_int, [_U32, _VP, _I64, _I64, _VP, _VP]),
     "lbq_quantize_weights_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
+    "lbq_gguf_open": (_c.c_int, [_c.c_char_p, _c.POINTER(_VP)]),
+    "lbq_gguf_close": (_c.c_int, [_VP]),
+    "lbq_gguf_header": (_c.c_int, [_VP, _c.POINTER(_U32), _c.POINTER(_I64), _c.POINTER(_I64), _c.POINTER(_c.c_uint64),
+                                   _c.POINTER(_c.c_uint64), _c.POINTER(_c.c_uint64)]),
+    "lbq_gguf_tensor_info": (_c.c_int, [_VP, _I64, _c.POINTER(_c.c_char_p), _c.POINTER(_U32), _c.POINTER(_U32),
+                                        _c.POINTER(_c.c_uint64), _c.POINTER(_c.c_uint64)]),
+    "lbq_gguf_find_tensor": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_I64)]),
+    "lbq_gguf_tensor_bytes": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_VP), _c.POINTER(_SZ)]),
+    "lbq_gguf_meta_key": (_c.c_int, [_VP, _I64, _c.POINTER(_c.c_char_p), _c.POINTER(_U32)]),
+    "lbq_gguf_meta_int": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_I64)]),
+    "lbq_gguf_meta_float": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_c.c_double)]),
+    "lbq_gguf_meta_string": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_VP), _c.POINTER(_SZ)]),
+    "lbq_gguf_meta_array": (_c.c_int, [_VP, _c.c_char_p, _c.POINTER(_U32), _c.POINTER(_c.c_uint64)]),
+    "lbq_gguf_copy_tensor": (_c.c_int, [_VP, _c.c_char_p, _VP, _SZ]),
+    "lbq_weight_from_gguf": (_c.c_int, [_VP, _VP, _c.c_char_p, _c.POINTER(_VP)]),
 }
 
 

@@ -195,6 +195,16 @@ int make_weight(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const uint8_t
 
 }  // namespace
 
+// shared with lbq_gguf.cpp
+int lbq_fail_status(int status, const char *msg) { return fail(status, "%s", msg); }
+int lbq_ctx_device(const lbq_ctx *ctx) { return ctx->device; }
+int lbq_make_owned_weight(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, void *d_blocks, size_t nbytes,
+                          lbq_weight **out) {
+    const int s = check_weight_args(type, n, k, nbytes);
+    if (s) return s;
+    return make_weight(ctx, type, n, k, static_cast<const uint8_t *>(d_blocks), nbytes, true, out);
+}
+
 extern "C" {
 
 const char *lbq_last_error(void) { return g_err.c_str(); }

@@ -316,6 +316,48 @@ def test_gate_up_silu(oracle, lbq, dev, t):
     assert_rows_close(y.cpu().numpy().reshape(2, k), ref, 2e-3)
 
 
+def test_gguf_to_qmatmul(oracle, lbq, dev, tmp_path):
+    # GGUF file -> device through pinned staging, both ways (Content.tensor and
+    # lbq_weight_from_gguf), then QMatMul::forward against the oracle on the
+    # same bytes; the two loads give the same bits
+    import gguf_writer as gw
+    from lightbulb_amd import _lib
+    from lightbulb_amd.gguf import Content
+    from lightbulb_amd.quantized import QMatMul, context
+    rng = np.random.default_rng(150)
+    w = {t: (bp.random_blocks(rng, t, n * k // oracle.block_size(t)), n, k)
+         for t, n, k in ((Q4_K, 300, 512), (Q6_K, 64, 1024), (Q8_0, 33, 256))}
+    tensors = [("token_norm", [512], 0, rng.standard_normal(512).astype(np.float32).tobytes())]
+    tensors += [(f"blk.0.w{t}", [k, n], t, raw.tobytes()) for t, (raw, n, k) in w.items()]
+    blob, _, _ = gw.build([("general.architecture", gw.STR, "llama"), ("general.alignment", gw.U32, 64)], tensors,
+                          alignment=64)
+    path = tmp_path / "w.gguf"
+    path.write_bytes(blob)
+    L = _lib.lib()
+    with Content.read(path) as c:
+        for t, (raw, n, k) in w.items():
+            qt = c.tensor(f"blk.0.w{t}", dev)
+            assert qt.shape() == (n, k) and int(qt.dtype()) == t
+            assert np.array_equal(qt.data.cpu().numpy(), raw)
+            x = rng.standard_normal((3, k)).astype(np.float32)
+            y = QMatMul.from_qtensor(qt).forward(to_dev(x, dev))
+            ref = oracle.qmatmul(t, raw, n, k, x, nthreads=4).astype(np.float64)
+            assert_rows_close(y.cpu().numpy(), ref)
+            h = ctypes.c_void_p()
+            ctx = context(dev)
+            _lib.check(L.lbq_weight_from_gguf(ctx, c._h, f"blk.0.w{t}".encode(), ctypes.byref(h)))
+            y2 = torch.empty(3, n, device=dev)
+            _lib.check(L.lbq_qmatmul_f32(ctx, h.value, to_dev(x, dev).data_ptr(), 3, y2.data_ptr(), None))
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+            L.lbq_weight_destroy(h.value)
+        # a 1-D tensor is not a weight
+        h = ctypes.c_void_p()
+        assert L.lbq_weight_from_gguf(context(dev), c._h, b"token_norm", ctypes.byref(h)) == -3
+        with pytest.raises(ValueError, match="2"):
+            c.tensor("token_norm", dev)
+
+
 def test_qmatmul_group_errors(oracle, lbq, dev):
     from lightbulb_amd import _lib
     from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
