@@ -190,15 +190,16 @@ def main():
             qz.qmatmul_group(layer[4:6], xs[4])
             layer[6].forward(xs[6])
 
-    # the layer as its call sites would run it: q|k|v grouped, o, then the MLP
-    # with gate/up and the SiLU product in one launch feeding down_proj
-    h_mlp = torch.empty(1, 14336, device=dev)
+    # the layer as its call sites would run it: input RMS norm + q|k|v in one
+    # launch, o, then post-attention RMS norm + gate/up + SiLU product in one
+    # launch feeding down_proj
+    norm_w = [1.0 + 0.1 * torch.randn(4096, generator=gen, device=dev) for _ in range(2)]
 
     def fused_step_all_copies():
         for layer in copies:
-            qz.qmatmul_group(layer[0:3], xs[0])
+            qz.rmsnorm_qmatmul_group(layer[0:3], xs[0], norm_w[0], 1e-5)
             layer[3].forward(xs[3])
-            h = qz.gate_up_silu(layer[4], layer[5], xs[4])
+            h = qz.rmsnorm_gate_up_silu(layer[4], layer[5], xs[4], norm_w[1], 1e-5)
             layer[6].forward(h)
 
     # activation handles for the dot-only (roofline) graph
@@ -233,7 +234,7 @@ def main():
     log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
         f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s; "
         f"grouped (4 launches) {ms_grp * 1e3:.2f} us -> {layer_bytes / (ms_grp * 1e-3) / 1e9:.0f} GB/s; "
-        f"call-site fused (q|k|v, o, gate|up+SiLU, down) {ms_fus * 1e3:.2f} us")
+        f"call-site fused (norm+q|k|v, o, norm+gate|up+SiLU, down) {ms_fus * 1e3:.2f} us")
 
     # per-shape dot kernel times (same graphs, one shape at a time)
     kernels = {}
@@ -295,9 +296,10 @@ def main():
         "call_site_fused": {"us_per_step": round(ms_fus * 1e3, 3),
                             "GB/s": round(layer_bytes / (ms_fus * 1e-3) / 1e9, 1),
                             "launches": 4,
-                            "path": "lbq_qmatmul_group_f32 (q|k|v), lbq_qmatmul_f32 (o), lbq_gate_up_silu_f32 "
-                                    "(gate|up with silu(gate)*up in the GEMV epilogue), lbq_qmatmul_f32 (down on "
-                                    "that product): the data flow of the reference's attention/MLP call sites"},
+                            "path": "lbq_rmsnorm_qmatmul_group_f32 (input RMS norm + q|k|v, the norm in the GEMV "
+                                    "prologue), lbq_qmatmul_f32 (o), lbq_rmsnorm_gate_up_silu_f32 (post-attention "
+                                    "norm + gate|up, silu(gate)*up in the epilogue), lbq_qmatmul_f32 (down on that "
+                                    "product): the reference's layer data flow, its two RMS norms included"},
         "kernels": kernels,
     }
     del g_full, g_dot, g_grp, g_fus

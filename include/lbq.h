@@ -126,6 +126,20 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
 int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
                          float *d_out, void *stream);
 
+/* The RMS norm that precedes those projections (input_layernorm before q/k/v,
+ * post_attention_layernorm before gate/up: /root/reference/src/model/
+ * custom_transformer_block.rs:329 and the MLP path; candle's RmsNorm in f32:
+ * x_norm = x / sqrt(sum(x^2) / k + eps) * norm_w), then the grouped projections or
+ * the gate/up product of x_norm.  At m = 1 (k-quants, k <= 8192, x and norm_w
+ * 16-byte aligned) the norm and the Q8_K quantisation run in the GEMV prologue
+ * -- one launch, x_norm never written; otherwise x_norm goes to context memory
+ * first.  lbq_rmsnorm_f32 is the norm alone. */
+int lbq_rmsnorm_f32(const float *d_x, const float *d_w, float eps, int64_t m, int64_t k, float *d_y, void *stream);
+int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x,
+                                  const float *d_norm_w, float eps, int64_t m, float *const *d_ys, void *stream);
+int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x,
+                                 const float *d_norm_w, float eps, int64_t m, float *d_out, void *stream);
+
 /* Quantised-activation handle: the two halves of QMatMul::forward as separate
  * calls.  candle's k_quants::matmul first quantises every row of x into
  * vec-dot blocks and then runs vec_dot for all output columns; splitting the

@@ -40,6 +40,10 @@ SIGNATURES = {
     "lbq_qmatmul_f32": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
     "lbq_qmatmul_group_f32": (_c.c_int, [_VP, _c.POINTER(_VP), _c.c_int, _VP, _I64, _c.POINTER(_VP), _VP]),
     "lbq_gate_up_silu_f32": (_c.c_int, [_VP, _VP, _VP, _VP, _I64, _VP, _VP]),
+    "lbq_rmsnorm_f32": (_c.c_int, [_VP, _VP, _c.c_float, _I64, _I64, _VP, _VP]),
+    "lbq_rmsnorm_qmatmul_group_f32": (_c.c_int, [_VP, _c.POINTER(_VP), _c.c_int, _VP, _VP, _c.c_float, _I64,
+                                                 _c.POINTER(_VP), _VP]),
+    "lbq_rmsnorm_gate_up_silu_f32": (_c.c_int, [_VP, _VP, _VP, _VP, _VP, _c.c_float, _I64, _VP, _VP]),
     "lbq_act_create": (_c.c_int, [_VP, _U32, _I64, _I64, _c.POINTER(_VP)]),
     "lbq_act_quantize": (_c.c_int, [_VP, _VP, _VP]),
     "lbq_act_destroy": (_c.c_int, [_VP]),

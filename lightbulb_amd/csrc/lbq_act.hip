@@ -181,6 +181,30 @@ hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float 
     return hipGetLastError();
 }
 
+// candle's RmsNorm (f32): y = x / sqrt(sum(x^2) / k + eps) * w, one workgroup per row
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float eps,
+                                                 int64_t k, float *__restrict__ y) {
+    __shared__ float red[4];
+    const int64_t m = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float *xr = x + m * k;
+    float ss = 0.f;
+    for (int64_t i = t; i < k; i += 256) ss += xr[i] * xr[i];
+    ss = row_sum_f32(ss);
+    ss = __int_as_float(rl(__float_as_uint(ss), 0)) + __int_as_float(rl(__float_as_uint(ss), 16)) +
+         __int_as_float(rl(__float_as_uint(ss), 32)) + __int_as_float(rl(__float_as_uint(ss), 48));
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)k + eps);
+    for (int64_t i = t; i < k; i += 256) y[m * k + i] = xr[i] / rms * w[i];
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int64_t m, int64_t k, float *y, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    k_rmsnorm<<<(unsigned)m, 256, 0, st>>>(x, w, eps, k, y);
+    return hipGetLastError();
+}
+
 // out = silu(g) * u with candle's f32 silu, v / (1 + exp(-v)) (the gate/up
 // product of mlp_wrapper.rs:190-194 when it is not fused into the GEMV)
 __global__ __launch_bounds__(256) void k_silu_mul(const float *__restrict__ g, const float *__restrict__ u, int64_t count,

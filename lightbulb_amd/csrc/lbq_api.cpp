@@ -472,6 +472,104 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
     return LBQ_OK;
 }
 
+int lbq_rmsnorm_f32(const float *d_x, const float *d_w, float eps, int64_t m, int64_t k, float *d_y, void *stream) {
+    if (!d_x || !d_w || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_rmsnorm_f32");
+    if (m < 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "rmsnorm shape (%lld, %lld) invalid", (long long)m, (long long)k);
+    if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_w) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
+        return fail(LBQ_ERR_INVALID_ARG, "x, w and y must be 4-byte aligned f32 buffers");
+    if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    hipError_t e = lbq::launch_rmsnorm(d_x, d_w, eps, m, k, d_y, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? LBQ_OK : hip_fail(e, "rmsnorm launch");
+}
+
+namespace {
+// x_norm = rmsnorm(x) in the context's gate/up memory (first m*k floats of tmp,
+// after `skip` bytes); the caller holds no lock
+int norm_into_tmp(lbq_ctx *ctx, const float *d_x, const float *d_w, float eps, int64_t m, int64_t k, size_t skip,
+                  hipStream_t st, float **out) {
+    const size_t need = skip + (size_t)m * (size_t)k * sizeof(float);
+    {
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        int s = ensure_buffer(&ctx->tmp, &ctx->tmp_bytes, need, "normalised activations");
+        if (s) return s;
+    }
+    *out = reinterpret_cast<float *>(ctx->tmp + skip);
+    hipError_t e = lbq::launch_rmsnorm(d_x, d_w, eps, m, k, *out, st);
+    return e == hipSuccess ? LBQ_OK : hip_fail(e, "rmsnorm launch");
+}
+}  // namespace
+
+int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x,
+                                  const float *d_norm_w, float eps, int64_t m, float *const *d_ys, void *stream) {
+    if (!ctx || !ws || !d_ys || !d_norm_w) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_rmsnorm_qmatmul_group_f32");
+    if (count < 1 || count > LBQ_GROUP_MAX) return fail(LBQ_ERR_LIMIT, "count = %d outside 1..%d", count, LBQ_GROUP_MAX);
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !d_ys[i]) return fail(LBQ_ERR_INVALID_ARG, "null weight or output %d", i);
+        if (ws[i]->type != ws[0]->type || ws[i]->k != ws[0]->k)
+            return fail(LBQ_ERR_SHAPE, "weight %d differs from weight 0 in type or k", i);
+    }
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    if (m == 0) return LBQ_OK;
+    if (!d_x || ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_norm_w)) & 3u))
+        return fail(LBQ_ERR_INVALID_ARG, "x and the norm weight must be 4-byte aligned f32 buffers");
+    const lbq_weight *w0 = ws[0];
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int64_t rows = 0;
+    for (int i = 0; i < count; i++) rows += ws[i]->n;
+    if (m == 1 && rows <= lbq::MAX_ROWS && !((reinterpret_cast<uintptr_t>(d_norm_w)) & 15u) &&
+        lbq::gemv_fuses_quant(w0->type, rows, w0->k, 1, d_x)) {
+        // one launch: the norm and the quantisation in the GEMV prologue
+        lbq::RowMap rm = lbq::single_row_map(w0->d_blocks, w0->n, d_ys[0]);
+        int64_t r = 0;
+        for (int i = 0; i < count; i++) {
+            rm.w[i] = ws[i]->d_blocks;
+            rm.y[i] = d_ys[i];
+            r += ws[i]->n;
+            rm.end[i] = (int32_t)r;
+        }
+        rm.n = rows;
+        const int act_type = w0->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+        const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, act_layout(act_type, 1, w0->k).nb};
+        hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, none, d_x, st, d_norm_w, eps);
+        if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
+    }
+    float *xn;
+    int s = norm_into_tmp(ctx, d_x, d_norm_w, eps, m, w0->k, 0, st, &xn);
+    if (s) return s;
+    return lbq_qmatmul_group_f32(ctx, ws, count, xn, m, d_ys, stream);
+}
+
+int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x,
+                                 const float *d_norm_w, float eps, int64_t m, float *d_out, void *stream) {
+    if (!ctx || !w_gate || !w_up || !d_out || !d_norm_w)
+        return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_rmsnorm_gate_up_silu_f32");
+    if (w_gate->type != w_up->type || w_gate->n != w_up->n || w_gate->k != w_up->k)
+        return fail(LBQ_ERR_SHAPE, "gate and up differ in type or shape");
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    if (m == 0) return LBQ_OK;
+    if (!d_x || ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_norm_w) |
+                  reinterpret_cast<uintptr_t>(d_out)) & 3u))
+        return fail(LBQ_ERR_INVALID_ARG, "x, the norm weight and out must be 4-byte aligned f32 buffers");
+    if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (m == 1 && !((reinterpret_cast<uintptr_t>(d_norm_w)) & 15u) &&
+        lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
+        hipError_t e = lbq::launch_gemv_silu_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n,
+                                                  w_gate->k, w_gate->row_bytes, d_x, d_out, st, d_norm_w, eps);
+        if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "gate/up launch");
+    }
+    // the normalised x sits after the gate/up halves lbq_gate_up_silu_f32 uses
+    const size_t half = ((size_t)m * (size_t)w_gate->n * sizeof(float) + 255) / 256 * 256;
+    float *xn;
+    int s = norm_into_tmp(ctx, d_x, d_norm_w, eps, m, w_gate->k, 2 * half, st, &xn);
+    if (s) return s;
+    return lbq_gate_up_silu_f32(ctx, w_gate, w_up, xn, m, d_out, stream);
+}
+
 int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act) {
     if (!ctx || !out_act) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_act_create");
     *out_act = nullptr;

@@ -3,10 +3,10 @@
 
 namespace lbq {
 
-hipError_t gemv_q4k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, hipStream_t);
-hipError_t gemv_q5k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, hipStream_t);
-hipError_t gemv_q6k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, hipStream_t);
-hipError_t gemv_q8_0(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, hipStream_t);
+hipError_t gemv_q4k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float, hipStream_t);
+hipError_t gemv_q5k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float, hipStream_t);
+hipError_t gemv_q6k(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float, hipStream_t);
+hipError_t gemv_q8_0(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float, hipStream_t);
 
 bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     (void)n;
@@ -44,12 +44,12 @@ RowMap single_row_map(const uint8_t *w, int64_t n, float *y) {
 }
 
 static hipError_t dispatch(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x,
-                           int m, int map, hipStream_t st) {
+                           int m, int map, hipStream_t st, const float *alpha = nullptr, float eps = 0.f) {
     switch (type) {
-    case TYPE_Q4_K: return gemv_q4k(rm, k, row_bytes, act, x, m, map, st);
-    case TYPE_Q5_K: return gemv_q5k(rm, k, row_bytes, act, x, m, map, st);
-    case TYPE_Q6_K: return gemv_q6k(rm, k, row_bytes, act, x, m, map, st);
-    case TYPE_Q8_0: return gemv_q8_0(rm, k, row_bytes, act, x, m, map, st);
+    case TYPE_Q4_K: return gemv_q4k(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
+    case TYPE_Q5_K: return gemv_q5k(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
+    case TYPE_Q6_K: return gemv_q6k(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
+    case TYPE_Q8_0: return gemv_q8_0(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -60,16 +60,17 @@ hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64
 }
 
 hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act,
-                             const float *x, hipStream_t st) {
-    return dispatch(type, rm, k, row_bytes, act, x, 1, MAP_SEGMENTS, st);
+                             const float *x, hipStream_t st, const float *norm_w, float eps) {
+    return dispatch(type, rm, k, row_bytes, act, x, 1, MAP_SEGMENTS, st, norm_w, eps);
 }
 
 hipError_t launch_gemv_silu_pair(int type, const uint8_t *w_gate, const uint8_t *w_up, int64_t n, int64_t k,
-                                 int64_t row_bytes, const float *x, float *out, hipStream_t st) {
+                                 int64_t row_bytes, const float *x, float *out, hipStream_t st, const float *norm_w,
+                                 float eps) {
     RowMap rm = single_row_map(w_gate, 2 * n, out);
     rm.w[1] = w_up;
     const ActView none{nullptr, nullptr, nullptr, k, 0};
-    return dispatch(type, rm, k, row_bytes, none, x, 1, MAP_SILU_PAIRS, st);
+    return dispatch(type, rm, k, row_bytes, none, x, 1, MAP_SILU_PAIRS, st, norm_w, eps);
 }
 
 }  // namespace lbq

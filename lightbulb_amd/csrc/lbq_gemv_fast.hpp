@@ -285,18 +285,23 @@ struct Fast<TYPE_Q8_0> {
 // `between` runs after the x loads are issued and before any of them is used:
 // loads issued there (the weight ring) queue behind x, so the in-order memory
 // counter lets the quantisation start as soon as x has arrived.
-template <int TYPE, class Between>
-__device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between) {
+//
+// NORM (k-quants, nbx <= 32): x is first RMS-normalised as candle's RmsNorm does
+// in f32 -- x / sqrt(sum(x^2) / k + eps) * alpha -- with the sum of squares taken
+// over the whole workgroup (every workgroup holds all of x).
+template <int TYPE, bool NORM, class Between>
+__device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between,
+                                               const float *__restrict__ alpha, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
     if constexpr (TYPE != TYPE_Q8_0) {
         // 16 lanes per 256-value block, 16 consecutive values per lane
         // (q8k_lane16), so the workgroup quantises 16 blocks per pass (nbx <= 64:
         // at most 4 passes); a lane's 16 codes are exactly one bsums entry.
-        constexpr int MAXP = 4;
+        constexpr int MAXP = NORM ? 2 : 4;
         const int t = threadIdx.x, sub = t & 15;
         const int np = (nbx + 15) >> 4;  // workgroup-uniform
-        float v[MAXP][16];
+        float v[MAXP][16], al[NORM ? MAXP : 1][16];
 #pragma unroll
         for (int j = 0; j < MAXP; j++) {
             const int b = min(16 * j + (t >> 4), nbx - 1);
@@ -306,10 +311,39 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
                 const float4 f = src[i];
                 v[j][4 * i] = f.x; v[j][4 * i + 1] = f.y; v[j][4 * i + 2] = f.z; v[j][4 * i + 3] = f.w;
             }
+            if constexpr (NORM) {
+                const float4 *wsrc = reinterpret_cast<const float4 *>(alpha + (int64_t)b * QK_K + 16 * sub);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 f = wsrc[i];
+                    al[j][4 * i] = f.x; al[j][4 * i + 1] = f.y; al[j][4 * i + 2] = f.z; al[j][4 * i + 3] = f.w;
+                }
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         between();
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NORM) {
+            __shared__ float red[4];
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < MAXP; j++) {
+                if (j < np && 16 * j + (t >> 4) < nbx) {  // clamped duplicates do not count
+#pragma unroll
+                    for (int i = 0; i < 16; i++) ss += v[j][i] * v[j][i];
+                }
+            }
+            ss = row_sum_f32(ss);
+            ss = __int_as_float(rl(__float_as_uint(ss), 0)) + __int_as_float(rl(__float_as_uint(ss), 16)) +
+                 __int_as_float(rl(__float_as_uint(ss), 32)) + __int_as_float(rl(__float_as_uint(ss), 48));
+            if (lane == 0) red[wave] = ss;
+            __syncthreads();
+            const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)(nbx * QK_K) + eps);
+#pragma unroll
+            for (int j = 0; j < MAXP; j++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[j][i] = v[j][i] / rms * al[j][i];
+        }
 #pragma unroll
         for (int j = 0; j < MAXP; j++) {
             if (j == 0 || j < np) {  // pass 0 unconditional: its loads stay ahead of the ring
@@ -454,9 +488,10 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
-template <int TYPE, int RPW, int IT, bool FUSED, int MAP>
+template <int TYPE, int RPW, int IT, bool FUSED, int MAP, bool NORM = false>
 __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
-                                               ActView act) {
+                                               ActView act, const float *__restrict__ alpha, float eps) {
+    static_assert(!NORM || (FUSED && TYPE != TYPE_Q8_0), "the RMS norm runs in the quantising prologue");
     constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
     static_assert(!PAIRED || RPW <= 2, "a silu pair spans two row groups or one");
     const int64_t n = rm.n;
@@ -547,7 +582,7 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
 
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
-    if constexpr (FUSED) quantise_x_lds<TYPE>(x, nb, sx, issue_ring);
+    if constexpr (FUSED) quantise_x_lds<TYPE, NORM>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE>(act, nb, sx, issue_ring);
 
     float pend = 0.f;  // silu pairs: the gate sum waiting for its up sum (wave-uniform)

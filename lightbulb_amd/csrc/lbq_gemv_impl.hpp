@@ -466,7 +466,7 @@ static bool fast_shape(int nb, int *rpw, int *it) {
 
 template <int TYPE, int RPW, int IT>
 static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
-                              hipStream_t st) {
+                              const float *alpha, float eps, hipStream_t st) {
     const int64_t n = rm.n;
     const int64_t ng = (n + RPW - 1) / RPW;
     // Waves per CU.  With the fused prologue every workgroup quantises all of x,
@@ -479,32 +479,45 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
     const size_t lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
-    // row maps take the fused quantisation only (the caller runs the rest weight by weight)
+    // row maps take the fused quantisation only (the caller runs the rest weight by
+    // weight); the RMS norm (alpha != nullptr) only k-quant row maps with k <= 8192
+    constexpr bool NORM_OK = TYPE != TYPE_Q8_0 && (64 / RPW / Fast<TYPE>::PPB) * IT <= 32;
+    if (alpha && (!NORM_OK || nb > 32 || !x || map == MAP_ONE)) return hipErrorNotSupported;
     if (map == MAP_SILU_PAIRS) {
         if constexpr (RPW <= 2) {
             if (!x || (n & 1)) return hipErrorNotSupported;
-            k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+            if constexpr (NORM_OK)
+                if (alpha) {
+                    k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                    return hipGetLastError();
+                }
+            k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
         } else {
             return hipErrorNotSupported;
         }
-    } else if (rm.end[0] < n) {
+    } else if (map == MAP_SEGMENTS) {
         if (!x) return hipErrorNotSupported;
-        k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        if constexpr (NORM_OK)
+            if (alpha) {
+                k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                return hipGetLastError();
+            }
+        k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else if (x) {
-        k_gemv1<TYPE, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        k_gemv1<TYPE, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else {
-        k_gemv1<TYPE, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act);
+        k_gemv1<TYPE, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     }
     return hipGetLastError();
 }
 
 template <int TYPE>
 static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
-                           hipStream_t st) {
+                           const float *alpha, float eps, hipStream_t st) {
     int rpw, it;
     if (!fast_shape<TYPE>(nb, &rpw, &it)) return hipErrorNotSupported;
 #define LBQ_FAST(R, I) \
-    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, map, st);
+    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, map, alpha, eps, st);
     if constexpr (Fast<TYPE>::PPB == 8) {
         LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
     } else if constexpr (Fast<TYPE>::PPB == 4) {
@@ -520,7 +533,7 @@ static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const fl
 // (map: MAP_ONE / MAP_SEGMENTS, or MAP_SILU_PAIRS for a gate/up pair).
 template <int TYPE>
 static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
-                           int map, hipStream_t st) {
+                           int map, const float *alpha, float eps, hipStream_t st) {
     using D = Dec<TYPE>;
     const uint8_t *w = rm.w[0];
     const int64_t n = rm.n;
@@ -531,10 +544,10 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
     if (m == 1) {
-        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, st);
+        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
         if (e != hipErrorNotSupported) return e;
     }
-    if (map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // row maps: m = 1 fast path only
+    if (alpha || map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // m = 1 fast path only
     GemvCfg c = pick_cfg(TYPE, n, g.pieces, m, k);
     c.fused = false;  // m > 1: x arrives quantised (separate kernel)
     if (x) return hipErrorInvalidValue;

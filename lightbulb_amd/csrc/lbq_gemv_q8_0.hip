@@ -5,8 +5,8 @@
 namespace lbq {
 
 hipError_t gemv_q8_0(const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act, const float *x, int m,
-                       int map, hipStream_t st) {
-    return run_type<TYPE_Q8_0>(rm, k, row_bytes, act, x, m, map, st);
+                       int map, const float *alpha, float eps, hipStream_t st) {
+    return run_type<TYPE_Q8_0>(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
 }
 
 }  // namespace lbq

@@ -50,15 +50,19 @@ hipError_t launch_gemv_x(int type, const uint8_t *w, int64_t n, int64_t k, int64
 // m = 1 over a multi-weight row map in one launch, quantising x in the prologue
 // (x != nullptr).  hipErrorNotSupported when k is outside the single-row fast
 // path or x is not given; the caller then runs the weights one by one.
+// With norm_w, x is first RMS-normalised in the prologue (k-quants, k <= 8192).
 hipError_t launch_gemv_group(int type, const RowMap &rm, int64_t k, int64_t row_bytes, const ActView &act,
-                             const float *x, hipStream_t st);
+                             const float *x, hipStream_t st, const float *norm_w = nullptr, float eps = 0.f);
 
 // m = 1 gate/up pair (same type, n, k): out[i] = silu(x . gate_i) * (x . up_i)
 // in one launch that quantises x in its prologue.  hipErrorNotSupported when the
 // single-row fast path does not cover k (or x is not 16-byte aligned); the
 // caller then computes gate and up and combines them with launch_silu_mul.
 hipError_t launch_gemv_silu_pair(int type, const uint8_t *w_gate, const uint8_t *w_up, int64_t n, int64_t k,
-                                 int64_t row_bytes, const float *x, float *out, hipStream_t st);
+                                 int64_t row_bytes, const float *x, float *out, hipStream_t st,
+                                 const float *norm_w = nullptr, float eps = 0.f);
+// candle's RmsNorm in f32, one workgroup per row: y = x / sqrt(sum(x^2)/k + eps) * w
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int64_t m, int64_t k, float *y, hipStream_t st);
 // out[i] = silu(g[i]) * u[i], count values
 hipError_t launch_silu_mul(const float *g, const float *u, int64_t count, float *out, hipStream_t st);
 

@@ -298,6 +298,66 @@ def gate_up_silu(gate: "QMatMul", up: "QMatMul", xs: torch.Tensor) -> torch.Tens
     return out
 
 
+def _check_norm(xs: torch.Tensor, weight: torch.Tensor, k: int):
+    if weight.dtype != torch.float32 or not weight.is_contiguous() or weight.numel() != k:
+        raise ValueError(f"the norm weight must be a contiguous f32 tensor of {k} values")
+    if weight.device != xs.device:
+        raise ValueError(f"norm weight on {weight.device}, input on {xs.device}")
+
+
+def rms_norm(xs: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """candle's ``RmsNorm`` in f32: ``x / sqrt(mean(x^2) + eps) * weight`` over the last dim."""
+    if xs.dtype != torch.float32 or not xs.is_contiguous():
+        raise ValueError("rms_norm takes a contiguous f32 tensor")
+    k = xs.shape[-1]
+    _check_norm(xs, weight, k)
+    y = torch.empty_like(xs)
+    m = xs.numel() // k
+    if m:
+        _lib.check(_lib.lib().lbq_rmsnorm_f32(xs.data_ptr(), weight.data_ptr(), float(eps), m, k, y.data_ptr(),
+                                              _stream(xs.device)))
+    return y
+
+
+def rmsnorm_qmatmul_group(qmatmuls, xs: torch.Tensor, weight: torch.Tensor, eps: float) -> list[torch.Tensor]:
+    """``qmatmul_group(qmatmuls, rms_norm(xs, weight, eps))`` -- the input norm
+    and the q/k/v projections that read it in one call (one launch at m = 1)."""
+    qmatmuls = list(qmatmuls)
+    if not 1 <= len(qmatmuls) <= GROUP_MAX:
+        raise ValueError(f"between 1 and {GROUP_MAX} weights per group, got {len(qmatmuls)}")
+    k = qmatmuls[0].qtensor().shape()[1]
+    if xs.dtype != torch.float32 or not xs.is_contiguous() or xs.shape[-1] != k:
+        raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with k = {k}")
+    _check_norm(xs, weight, k)
+    m = xs.numel() // k
+    ys = [torch.empty(*xs.shape[:-1], q.qtensor().shape()[0], dtype=torch.float32, device=xs.device) for q in qmatmuls]
+    if m:
+        cnt = len(qmatmuls)
+        hs = (ctypes.c_void_p * cnt)(*[q._handle for q in qmatmuls])
+        outs = (ctypes.c_void_p * cnt)(*[y.data_ptr() for y in ys])
+        _lib.check(_lib.lib().lbq_rmsnorm_qmatmul_group_f32(qmatmuls[0]._ctx, hs, cnt, xs.data_ptr(), weight.data_ptr(),
+                                                            float(eps), m, outs, _stream(xs.device)))
+    return ys
+
+
+def rmsnorm_gate_up_silu(gate: "QMatMul", up: "QMatMul", xs: torch.Tensor, weight: torch.Tensor,
+                         eps: float) -> torch.Tensor:
+    """``gate_up_silu(gate, up, rms_norm(xs, weight, eps))`` in one call."""
+    n, k = gate.qtensor().shape()
+    if gate.qtensor().dtype() != up.qtensor().dtype() or up.qtensor().shape() != (n, k):
+        raise ValueError("gate and up must share the ggml type and shape")
+    if xs.dtype != torch.float32 or not xs.is_contiguous() or xs.shape[-1] != k:
+        raise ValueError(f"input tensor {tuple(xs.shape)} incompatible with k = {k}")
+    _check_norm(xs, weight, k)
+    m = xs.numel() // k
+    out = torch.empty(*xs.shape[:-1], n, dtype=torch.float32, device=xs.device)
+    if m:
+        _lib.check(_lib.lib().lbq_rmsnorm_gate_up_silu_f32(gate._ctx, gate._handle, up._handle, xs.data_ptr(),
+                                                           weight.data_ptr(), float(eps), m, out.data_ptr(),
+                                                           _stream(xs.device)))
+    return out
+
+
 class Mlp:
     """``Mlp`` (src/model/mlp_wrapper.rs): ``down_proj(silu(gate_proj(x)) * up_proj(x))``
     over ``QuantizableLinear`` projections; quantized gate/up pairs take the fused

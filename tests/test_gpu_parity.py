@@ -358,6 +358,51 @@ def test_gguf_to_qmatmul(oracle, lbq, dev, tmp_path):
             c.tensor("token_norm", dev)
 
 
+def _rms_norm_ref(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    # candle RmsNorm in f32: x / sqrt(sum(x^2) / k + eps) * w
+    x32 = x.astype(np.float32)
+    ss = (x32 * x32).sum(axis=-1, dtype=np.float32, keepdims=True)
+    rms = np.sqrt(ss / np.float32(x.shape[-1]) + np.float32(eps)).astype(np.float32)
+    return (x32 / rms * w.astype(np.float32)).astype(np.float32)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+def test_rmsnorm_fused_projections(oracle, lbq, dev, t):
+    # the input norm in the GEMV prologue (m = 1, k-quants, k <= 8192) or in its
+    # own launch (otherwise), then grouped projections / the gate-up product;
+    # against the oracle on the numpy-normalised x
+    from lightbulb_amd.quantized import (QMatMul, QTensor, qmatmul_group, rms_norm, rmsnorm_gate_up_silu,
+                                         rmsnorm_qmatmul_group)
+    rng = np.random.default_rng(160 + t)
+    bs = oracle.block_size(t)
+    for k, ns in ((4096, (256, 64, 64)), (1024, (96, 33)), (14336, (40, 24))):
+        raws = [bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3) for n in ns]
+        qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
+        w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        wd = to_dev(w, dev)
+        for m in (1, 3):
+            x = (3.0 * rng.standard_normal((m, k)) + 0.5).astype(np.float32)
+            xd = to_dev(x, dev)
+            xn = _rms_norm_ref(x, w, 1e-5)
+            got_norm = rms_norm(xd, wd, 1e-5).cpu().numpy()
+            assert np.allclose(got_norm, xn, rtol=2e-6, atol=1e-6)
+            ys = rmsnorm_qmatmul_group(qms, xd, wd, 1e-5)
+            torch.cuda.synchronize()
+            for y, r, n in zip(ys, raws, ns):
+                assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, xn, nthreads=8).astype(np.float64), 2e-3)
+            if ns[0] == ns[1]:
+                continue
+            # gate/up product over the first two weights cut to a common n
+            n2 = min(ns[0], ns[1])
+            cut = [r[: n2 * (r.size // n)] for r, n in zip(raws[:2], ns[:2])]  # the first n2 rows
+            gq = [QMatMul.from_qtensor(QTensor(to_dev(c, dev), t, (n2, k))) for c in cut]
+            out = rmsnorm_gate_up_silu(gq[0], gq[1], xd, wd, 1e-5)
+            torch.cuda.synchronize()
+            gr = oracle.qmatmul(t, cut[0], n2, k, xn, nthreads=8).astype(np.float64)
+            ur = oracle.qmatmul(t, cut[1], n2, k, xn, nthreads=8).astype(np.float64)
+            assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, 2e-3)
+
+
 def test_qmatmul_group_errors(oracle, lbq, dev):
     from lightbulb_amd import _lib
     from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
