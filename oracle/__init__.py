@@ -46,9 +46,11 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 _BUILD = HERE / "_build"
 
-Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 8, 12, 13, 14, 15
-BLOCK_SIZE = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
-TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 2, 3, 6, 7, 8, 9, 12, 13, 14, 15
+BLOCK_SIZE = {Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
+TYPE_SIZE = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
+# the activation type each weight type's vec_dot takes (candle GgmlType::VecDotType)
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_1: Q8_1, Q5_1: Q8_1, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
 
 _libs: dict[str, ctypes.CDLL] = {}
 
@@ -117,7 +119,7 @@ def dequantize(t: int, blocks: np.ndarray) -> np.ndarray:
 
 
 def quantize_act(t: int, x: np.ndarray) -> np.ndarray:
-    """x f32 [m, k] -> GGUF blocks of Q8_K (t=15) or Q8_0 (t=8) as uint8 [m, k/QK*TS]."""
+    """x f32 [m, k] -> GGUF blocks of Q8_K (t=15), Q8_0 (t=8) or Q8_1 (t=9) as uint8 [m, k/QK*TS]."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     if x.ndim == 1:
         x = x[None]

@@ -19,7 +19,9 @@
  *   - activation quantisation to Q8_K (k-quant weights) or Q8_0 (Q8_0
  *     weights): candle k_quants.rs BlockQ8K::from_float / BlockQ8_0::from_float
  *   - the generic (non-SIMD) integer vec_dot for Q8_0.Q8_0, Q4_K.Q8_K,
- *     Q5_K.Q8_K and Q6_K.Q8_K with its 8-lane partial sums
+ *     Q5_K.Q8_K and Q6_K.Q8_K with its 8-lane partial sums, and for the
+ *     32-value legacy blocks Q4_0.Q8_0, Q5_0.Q8_0, Q4_1.Q8_1, Q5_1.Q8_1
+ *     (activation quantisation to Q8_1: BlockQ8_1::from_float)
  *   - the k_quants::matmul driver: quantise all M rows, then for each row a
  *     parallel loop over N output columns (rayon, chunks of 128..512)
  *   - dequantisation (GgmlType::to_float; lightbulb's own dequantize_tensor,
@@ -52,19 +54,30 @@ typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; } b
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; } blk_q5_k;
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_k;
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_k;
+/* 32-value blocks (ggml legacy types) */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_q4_0;
+typedef struct { uint16_t d, m; uint8_t qs[16]; } blk_q4_1;
+typedef struct { uint16_t d; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_0;
+typedef struct { uint16_t d, m; uint8_t qh[4]; uint8_t qs[16]; } blk_q5_1;
+typedef struct { uint16_t d, s; int8_t qs[32]; } blk_q8_1;
 
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0 size");
 _Static_assert(sizeof(blk_q4_k) == 144, "q4_k size");
 _Static_assert(sizeof(blk_q5_k) == 176, "q5_k size");
 _Static_assert(sizeof(blk_q6_k) == 210, "q6_k size");
 _Static_assert(sizeof(blk_q8_k) == 292, "q8_k size");
+_Static_assert(sizeof(blk_q4_0) == 18, "q4_0 size");
+_Static_assert(sizeof(blk_q4_1) == 20, "q4_1 size");
+_Static_assert(sizeof(blk_q5_0) == 22, "q5_0 size");
+_Static_assert(sizeof(blk_q5_1) == 24, "q5_1 size");
+_Static_assert(sizeof(blk_q8_1) == 36, "q8_1 size");
 
 /* ------------------------------------------------------------------ */
 /* type table: reference src/quantization/mod.rs:58-126                */
 /* ------------------------------------------------------------------ */
 int oracle_block_size(uint32_t type) {
     switch (type) {
-    case ORACLE_Q8_0: return 32;
+    case ORACLE_Q8_0: case ORACLE_Q4_0: case ORACLE_Q4_1: case ORACLE_Q5_0: case ORACLE_Q5_1: case ORACLE_Q8_1: return 32;
     case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: case ORACLE_Q8_K: return 256;
     default: return 0;
     }
@@ -73,6 +86,11 @@ int oracle_block_size(uint32_t type) {
 int oracle_type_size(uint32_t type) {
     switch (type) {
     case ORACLE_Q8_0: return 34;
+    case ORACLE_Q4_0: return 18;
+    case ORACLE_Q4_1: return 20;
+    case ORACLE_Q5_0: return 22;
+    case ORACLE_Q5_1: return 24;
+    case ORACLE_Q8_1: return 36;
     case ORACLE_Q4_K: return 144;
     case ORACLE_Q5_K: return 176;
     case ORACLE_Q6_K: return 210;
@@ -239,6 +257,54 @@ static void deq_q8_k(const blk_q8_k *b, float *y) {
     for (int i = 0; i < QK_K; i++) y[i] = b->d * (float)b->qs[i];
 }
 
+/* 32-value blocks (candle k_quants to_float): element j from the low nibble of
+ * qs[j], element j + 16 from its high nibble; Q5 fifth bits from the u32 qh,
+ * bit j (element j) and bit j + 16 (element j + 16). */
+static uint32_t qh_u32(const uint8_t qh[4]) {
+    return (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+}
+
+static void deq_q4_0(const blk_q4_0 *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d);
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)((int)(b->qs[j] & 0xF) - 8) * d;
+        y[j + 16] = (float)((int)(b->qs[j] >> 4) - 8) * d;
+    }
+}
+
+static void deq_q4_1(const blk_q4_1 *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d), m = oracle_f16_to_f32(b->m);
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)(b->qs[j] & 0xF) * d + m;
+        y[j + 16] = (float)(b->qs[j] >> 4) * d + m;
+    }
+}
+
+static void deq_q5_0(const blk_q5_0 *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d);
+    const uint32_t qh = qh_u32(b->qh);
+    for (int j = 0; j < 16; j++) {
+        const uint32_t h0 = ((qh >> j) << 4) & 0x10, h1 = (qh >> (j + 12)) & 0x10;
+        y[j] = (float)((int)((b->qs[j] & 0xF) | h0) - 16) * d;
+        y[j + 16] = (float)((int)((b->qs[j] >> 4) | h1) - 16) * d;
+    }
+}
+
+static void deq_q5_1(const blk_q5_1 *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d), m = oracle_f16_to_f32(b->m);
+    const uint32_t qh = qh_u32(b->qh);
+    for (int j = 0; j < 16; j++) {
+        const uint32_t h0 = ((qh >> j) << 4) & 0x10, h1 = (qh >> (j + 12)) & 0x10;
+        y[j] = (float)((b->qs[j] & 0xF) | h0) * d + m;
+        y[j + 16] = (float)((b->qs[j] >> 4) | h1) * d + m;
+    }
+}
+
+static void deq_q8_1(const blk_q8_1 *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d);
+    for (int j = 0; j < 32; j++) y[j] = (float)b->qs[j] * d;
+}
+
 int oracle_dequantize(uint32_t type, const void *blocks, int64_t nblocks, float *out) {
     const uint8_t *p = (const uint8_t *)blocks;
     const int ts = oracle_type_size(type), bs = oracle_block_size(type);
@@ -252,6 +318,11 @@ int oracle_dequantize(uint32_t type, const void *blocks, int64_t nblocks, float 
         case ORACLE_Q5_K: deq_q5_k((const blk_q5_k *)b, y); break;
         case ORACLE_Q6_K: deq_q6_k((const blk_q6_k *)b, y); break;
         case ORACLE_Q8_K: deq_q8_k((const blk_q8_k *)b, y); break;
+        case ORACLE_Q4_0: deq_q4_0((const blk_q4_0 *)b, y); break;
+        case ORACLE_Q4_1: deq_q4_1((const blk_q4_1 *)b, y); break;
+        case ORACLE_Q5_0: deq_q5_0((const blk_q5_0 *)b, y); break;
+        case ORACLE_Q5_1: deq_q5_1((const blk_q5_1 *)b, y); break;
+        case ORACLE_Q8_1: deq_q8_1((const blk_q8_1 *)b, y); break;
         }
     }
     return 0;
@@ -308,7 +379,31 @@ static void quant_row_q8_0(const float *x, blk_q8_0 *y, int64_t nb) {
     }
 }
 
+/* candle BlockQ8_1::from_float: as Q8_0 (d = amax/127, q = round(x / d) with
+ * the unrounded d, stored f16(d)), plus s = f16(sum of the codes) * f16(d) taken
+ * in f16 (the half crate multiplies in f32 and rounds back). */
+static void quant_row_q8_1(const float *x, blk_q8_1 *y, int64_t nb) {
+    for (int64_t i = 0; i < nb; i++, x += 32, y++) {
+        float amax = 0.f;
+        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+        const float d = amax / 127.f;
+        const float id = d != 0.f ? 1.f / d : 0.f;
+        y->d = oracle_f32_to_f16(d);
+        int sum = 0;
+        for (int j = 0; j < 32; j++) {
+            y->qs[j] = round_sat_i8(x[j] * id);
+            sum += y->qs[j];
+        }
+        y->s = oracle_f32_to_f16(oracle_f16_to_f32(oracle_f32_to_f16((float)sum)) * oracle_f16_to_f32(y->d));
+    }
+}
+
 int oracle_quantize_act(uint32_t type, const float *x, int64_t m, int64_t k, void *out) {
+    if (type == ORACLE_Q8_1) {
+        if (k % 32) return -1;
+        quant_row_q8_1(x, (blk_q8_1 *)out, m * (k / 32));
+        return 0;
+    }
     if (type == ORACLE_Q8_K) {
         if (k % QK_K) return -1;
         quant_row_q8_k(x, (blk_q8_k *)out, m * (k / QK_K));
@@ -469,8 +564,80 @@ static float vec_dot_q6_k(int64_t n, const blk_q6_k *xs, const blk_q8_k *ys) {
     return s;
 }
 
+/* the generic candle/ggml bodies of the 32-block vec_dots */
+static float vec_dot_q4_0(int64_t n, const blk_q4_0 *xs, const blk_q8_0 *ys) {
+    float sumf = 0.f;
+    for (int64_t i = 0; i < n / 32; i++) {
+        int sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            const int v0 = (int)(xs[i].qs[j] & 0xF) - 8, v1 = (int)(xs[i].qs[j] >> 4) - 8;
+            sumi += v0 * (int)ys[i].qs[j] + v1 * (int)ys[i].qs[j + 16];
+        }
+        sumf += (float)sumi * oracle_f16_to_f32(xs[i].d) * oracle_f16_to_f32(ys[i].d);
+    }
+    return sumf;
+}
+
+static float vec_dot_q4_1(int64_t n, const blk_q4_1 *xs, const blk_q8_1 *ys) {
+    float sumf = 0.f;
+    for (int64_t i = 0; i < n / 32; i++) {
+        int sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            const int v0 = xs[i].qs[j] & 0xF, v1 = xs[i].qs[j] >> 4;
+            sumi += v0 * (int)ys[i].qs[j] + v1 * (int)ys[i].qs[j + 16];
+        }
+        sumf += (oracle_f16_to_f32(xs[i].d) * oracle_f16_to_f32(ys[i].d)) * (float)sumi +
+                oracle_f16_to_f32(xs[i].m) * oracle_f16_to_f32(ys[i].s);
+    }
+    return sumf;
+}
+
+static float vec_dot_q5_0(int64_t n, const blk_q5_0 *xs, const blk_q8_0 *ys) {
+    float sumf = 0.f;
+    for (int64_t i = 0; i < n / 32; i++) {
+        const uint32_t qh = qh_u32(xs[i].qh);
+        int sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            const uint32_t h0 = ((qh >> j) << 4) & 0x10, h1 = (qh >> (j + 12)) & 0x10;
+            const int v0 = (int)((xs[i].qs[j] & 0xF) | h0) - 16, v1 = (int)((xs[i].qs[j] >> 4) | h1) - 16;
+            sumi += v0 * (int)ys[i].qs[j] + v1 * (int)ys[i].qs[j + 16];
+        }
+        sumf += (oracle_f16_to_f32(xs[i].d) * oracle_f16_to_f32(ys[i].d)) * (float)sumi;
+    }
+    return sumf;
+}
+
+static float vec_dot_q5_1(int64_t n, const blk_q5_1 *xs, const blk_q8_1 *ys) {
+    float sumf = 0.f;
+    for (int64_t i = 0; i < n / 32; i++) {
+        const uint32_t qh = qh_u32(xs[i].qh);
+        int sumi = 0;
+        for (int j = 0; j < 16; j++) {
+            const uint32_t h0 = ((qh >> j) << 4) & 0x10, h1 = (qh >> (j + 12)) & 0x10;
+            const int v0 = (int)((xs[i].qs[j] & 0xF) | h0), v1 = (int)((xs[i].qs[j] >> 4) | h1);
+            sumi += v0 * (int)ys[i].qs[j] + v1 * (int)ys[i].qs[j + 16];
+        }
+        sumf += (oracle_f16_to_f32(xs[i].d) * oracle_f16_to_f32(ys[i].d)) * (float)sumi +
+                oracle_f16_to_f32(xs[i].m) * oracle_f16_to_f32(ys[i].s);
+    }
+    return sumf;
+}
+
+uint32_t oracle_vec_dot_type(uint32_t type) {
+    switch (type) {
+    case ORACLE_Q8_0: case ORACLE_Q4_0: case ORACLE_Q5_0: return ORACLE_Q8_0;
+    case ORACLE_Q4_1: case ORACLE_Q5_1: return ORACLE_Q8_1;
+    case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: return ORACLE_Q8_K;
+    default: return 0;
+    }
+}
+
 int oracle_vec_dot(uint32_t type, int64_t k, const void *wrow, const void *xrow, float *out) {
     switch (type) {
+    case ORACLE_Q4_0: *out = vec_dot_q4_0(k, (const blk_q4_0 *)wrow, (const blk_q8_0 *)xrow); return 0;
+    case ORACLE_Q4_1: *out = vec_dot_q4_1(k, (const blk_q4_1 *)wrow, (const blk_q8_1 *)xrow); return 0;
+    case ORACLE_Q5_0: *out = vec_dot_q5_0(k, (const blk_q5_0 *)wrow, (const blk_q8_0 *)xrow); return 0;
+    case ORACLE_Q5_1: *out = vec_dot_q5_1(k, (const blk_q5_1 *)wrow, (const blk_q8_1 *)xrow); return 0;
     case ORACLE_Q8_0: *out = vec_dot_q8_0(k, (const blk_q8_0 *)wrow, (const blk_q8_0 *)xrow); return 0;
     case ORACLE_Q4_K: *out = vec_dot_q4_k(k, (const blk_q4_k *)wrow, (const blk_q8_k *)xrow); return 0;
     case ORACLE_Q5_K: *out = vec_dot_q5_k(k, (const blk_q5_k *)wrow, (const blk_q8_k *)xrow); return 0;
@@ -499,7 +666,7 @@ typedef struct {
 static void *mm_worker(void *arg) {
     mm_job *j = (mm_job *)arg;
     const int64_t w_row_bytes = (j->k / oracle_block_size(j->type)) * oracle_type_size(j->type);
-    const uint32_t vt = j->type == ORACLE_Q8_0 ? ORACLE_Q8_0 : ORACLE_Q8_K;
+    const uint32_t vt = oracle_vec_dot_type(j->type);
     const int64_t x_row_bytes = (j->k / oracle_block_size(vt)) * oracle_type_size(vt);
     const uint8_t *xrow = j->xq + j->row * x_row_bytes;
     float *dst = j->y + j->row * j->n;
@@ -516,10 +683,10 @@ static void *mm_worker(void *arg) {
 }
 
 int oracle_qmatmul(uint32_t type, const void *w, int64_t n, int64_t k, const float *x, int64_t m, float *y, int nthreads) {
-    if (type != ORACLE_Q8_0 && type != ORACLE_Q4_K && type != ORACLE_Q5_K && type != ORACLE_Q6_K) return -1;
+    const uint32_t vt = oracle_vec_dot_type(type);
+    if (!vt) return -1;
     if (k % oracle_block_size(type)) return -1;
     if (m == 0 || n == 0) return 0;
-    const uint32_t vt = type == ORACLE_Q8_0 ? ORACLE_Q8_0 : ORACLE_Q8_K;
     const int64_t x_row_bytes = (k / oracle_block_size(vt)) * oracle_type_size(vt);
     uint8_t *xq = (uint8_t *)malloc((size_t)(m * x_row_bytes));
     if (!xq) return -2;
@@ -800,6 +967,84 @@ static void quantize_q6_k(const float *x, blk_q6_k *y) {
     }
 }
 
+/* ggml quantize_row_q4_0/q4_1/q5_0/q5_1 reference quantisers (fixtures) */
+static void quantize_q4_0(const float *x, blk_q4_0 *y) {
+    float amax = 0.f, max = 0.f;
+    for (int j = 0; j < 32; j++) {
+        const float v = x[j];
+        if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+    }
+    const float d = max / -8.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    y->d = oracle_f32_to_f16(d);
+    for (int j = 0; j < 16; j++) {
+        int8_t a = (int8_t)(x[j] * id + 8.5f), b2 = (int8_t)(x[j + 16] * id + 8.5f);
+        const uint8_t xi0 = (uint8_t)(a < 15 ? a : 15), xi1 = (uint8_t)(b2 < 15 ? b2 : 15);
+        y->qs[j] = (uint8_t)(xi0 | (xi1 << 4));
+    }
+}
+
+static void minmax32(const float *x, float *mn, float *mx) {
+    float lo = x[0], hi = x[0];
+    for (int j = 1; j < 32; j++) {
+        if (x[j] < lo) lo = x[j];
+        if (x[j] > hi) hi = x[j];
+    }
+    *mn = lo;
+    *mx = hi;
+}
+
+static void quantize_q4_1(const float *x, blk_q4_1 *y) {
+    float min, max;
+    minmax32(x, &min, &max);
+    const float d = (max - min) / 15.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    y->d = oracle_f32_to_f16(d);
+    y->m = oracle_f32_to_f16(min);
+    for (int j = 0; j < 16; j++) {
+        int8_t a = (int8_t)((x[j] - min) * id + 0.5f), b2 = (int8_t)((x[j + 16] - min) * id + 0.5f);
+        const uint8_t xi0 = (uint8_t)(a < 15 ? a : 15), xi1 = (uint8_t)(b2 < 15 ? b2 : 15);
+        y->qs[j] = (uint8_t)(xi0 | (xi1 << 4));
+    }
+}
+
+static void quantize_q5_0(const float *x, blk_q5_0 *y) {
+    float amax = 0.f, max = 0.f;
+    for (int j = 0; j < 32; j++) {
+        const float v = x[j];
+        if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+    }
+    const float d = max / -16.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    y->d = oracle_f32_to_f16(d);
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; j++) {
+        int8_t a = (int8_t)(x[j] * id + 16.5f), b2 = (int8_t)(x[j + 16] * id + 16.5f);
+        const uint8_t xi0 = (uint8_t)(a < 31 ? a : 31), xi1 = (uint8_t)(b2 < 31 ? b2 : 31);
+        y->qs[j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+        qh |= ((uint32_t)(xi0 & 0x10) >> 4) << j;
+        qh |= ((uint32_t)(xi1 & 0x10) >> 4) << (j + 16);
+    }
+    memcpy(y->qh, &qh, 4);
+}
+
+static void quantize_q5_1(const float *x, blk_q5_1 *y) {
+    float min, max;
+    minmax32(x, &min, &max);
+    const float d = (max - min) / 31.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    y->d = oracle_f32_to_f16(d);
+    y->m = oracle_f32_to_f16(min);
+    uint32_t qh = 0;
+    for (int j = 0; j < 16; j++) {
+        const uint8_t xi0 = (uint8_t)(int8_t)((x[j] - min) * id + 0.5f), xi1 = (uint8_t)(int8_t)((x[j + 16] - min) * id + 0.5f);
+        y->qs[j] = (uint8_t)((xi0 & 0x0F) | ((xi1 & 0x0F) << 4));
+        qh |= ((uint32_t)(xi0 & 0x10) >> 4) << j;
+        qh |= ((uint32_t)(xi1 & 0x10) >> 4) << (j + 16);
+    }
+    memcpy(y->qh, &qh, 4);
+}
+
 int oracle_quantize_weights(uint32_t type, const float *w, int64_t nelem, void *out) {
     const int bs = oracle_block_size(type);
     if (!bs || nelem % bs) return -1;
@@ -816,6 +1061,10 @@ int oracle_quantize_weights(uint32_t type, const float *w, int64_t nelem, void *
     case ORACLE_Q6_K:
         for (int64_t i = 0; i < nb; i++) quantize_q6_k(w + i * QK_K, (blk_q6_k *)(o + i * 210));
         return 0;
+    case ORACLE_Q4_0: for (int64_t i = 0; i < nb; i++) quantize_q4_0(w + i * 32, (blk_q4_0 *)(o + i * 18)); return 0;
+    case ORACLE_Q4_1: for (int64_t i = 0; i < nb; i++) quantize_q4_1(w + i * 32, (blk_q4_1 *)(o + i * 20)); return 0;
+    case ORACLE_Q5_0: for (int64_t i = 0; i < nb; i++) quantize_q5_0(w + i * 32, (blk_q5_0 *)(o + i * 22)); return 0;
+    case ORACLE_Q5_1: for (int64_t i = 0; i < nb; i++) quantize_q5_1(w + i * 32, (blk_q5_1 *)(o + i * 24)); return 0;
     default: return -1;
     }
 }

@@ -9,7 +9,12 @@ extern "C" {
 #endif
 
 /* GGUF type ids, /root/reference/src/quantization/mod.rs:58-75 */
-enum { ORACLE_Q8_0 = 8, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14, ORACLE_Q8_K = 15 };
+enum {
+    ORACLE_Q4_0 = 2, ORACLE_Q4_1 = 3, ORACLE_Q5_0 = 6, ORACLE_Q5_1 = 7, ORACLE_Q8_0 = 8, ORACLE_Q8_1 = 9,
+    ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14, ORACLE_Q8_K = 15
+};
+/* the activation type a weight type's vec_dot takes (0 if none) */
+uint32_t oracle_vec_dot_type(uint32_t type);
 
 int oracle_block_size(uint32_t type);
 int oracle_type_size(uint32_t type);
@@ -19,7 +24,7 @@ void oracle_unpack_scales_k4(const uint8_t scales[12], uint8_t sc[8], uint8_t mn
 
 /* out: nblocks*block_size floats */
 int oracle_dequantize(uint32_t type, const void *blocks, int64_t nblocks, float *out);
-/* type: ORACLE_Q8_K or ORACLE_Q8_0; x is [m][k] f32; out is m*(k/QK) blocks */
+/* type: ORACLE_Q8_K, ORACLE_Q8_0 or ORACLE_Q8_1; x is [m][k] f32; out is m*(k/QK) blocks */
 int oracle_quantize_act(uint32_t type, const float *x, int64_t m, int64_t k, void *out);
 /* one output element: dot of a weight row (k/QK blocks) with a quantised activation row */
 int oracle_vec_dot(uint32_t type, int64_t k, const void *wrow, const void *xrow, float *out);

@@ -21,6 +21,12 @@ Spec (ggml block layouts, as used by candle-core 0.10.2 / ggml-quants 0.1.0):
         scale index v//16: x = d*scale*q.
   Q8_0: d f16, qs[32] int8: x = d*q.
   Q8_K: d f32, qs[256] int8, bsums[16] int16.
+  32-value legacy blocks: value j (j<16) is the low nibble of qs[j], value
+  j+16 its high nibble; Q5_* take bit 4 of value v from bit v of the little-
+  endian u32 qh.
+  Q4_0: d f16, qs[16]: x = d*(q-8).     Q4_1: d f16, m f16, qs[16]: x = d*q + m.
+  Q5_0: d f16, qh[4], qs[16]: x = d*(q-16).  Q5_1: d, m f16, qh[4], qs[16]: x = d*q + m.
+  Q8_1: d f16, s f16, qs[32] int8 (s = d * sum(qs), kept in f16).
 """
 from __future__ import annotations
 
@@ -136,13 +142,65 @@ def unpack_q8_0(raw: np.ndarray):
     return d, qs
 
 
+def _nib_pack(q) -> bytes:
+    q = [int(v) for v in q]
+    return bytes((q[j] & 15) | ((q[j + 16] & 15) << 4) for j in range(16))
+
+
+def _qh_pack(q) -> bytes:
+    h = 0
+    for v in range(32):
+        h |= ((int(q[v]) >> 4) & 1) << v
+    return h.to_bytes(4, "little")
+
+
+def pack_q4_0(d: int, q) -> bytes:
+    return d.to_bytes(2, "little") + _nib_pack(q)
+
+
+def pack_q4_1(d: int, m: int, q) -> bytes:
+    return d.to_bytes(2, "little") + m.to_bytes(2, "little") + _nib_pack(q)
+
+
+def pack_q5_0(d: int, q) -> bytes:
+    return d.to_bytes(2, "little") + _qh_pack(q) + _nib_pack(q)
+
+
+def pack_q5_1(d: int, m: int, q) -> bytes:
+    return d.to_bytes(2, "little") + m.to_bytes(2, "little") + _qh_pack(q) + _nib_pack(q)
+
+
+def unpack_legacy(t: int, raw: np.ndarray):
+    """(d, m, codes) per block of the 32-value weight types; codes unsigned
+    (0..15 or 0..31), m = 0 for Q4_0/Q5_0 (whose offset is -8 / -16)."""
+    ts = {2: 18, 3: 20, 6: 22, 7: 24}[t]
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, ts)
+    f16 = lambda c: raw[:, c:c + 2].copy().view(np.float16).astype(np.float64).reshape(-1)
+    d = f16(0)
+    m = f16(2) if t in (3, 7) else np.zeros(raw.shape[0])
+    qs = raw[:, ts - 16:].astype(np.int64)
+    q = np.concatenate([qs & 15, qs >> 4], axis=1)
+    if t in (6, 7):
+        off = 2 if t == 6 else 4
+        h = raw[:, off:off + 4].copy().view("<u4").astype(np.int64).reshape(-1)
+        q = q | (((h[:, None] >> np.arange(32)) & 1) << 4)
+    return d, m, q
+
+
+def unpack_q8_1(raw: np.ndarray):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, 36)
+    d = raw[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    s = raw[:, 2:4].copy().view(np.float16).astype(np.float32).reshape(-1)
+    return d, s, raw[:, 4:36].copy().view(np.int8)
+
+
 def random_blocks(rng: np.random.Generator, t: int, nblocks: int, d_scale: float = 1e-3) -> np.ndarray:
     """Random bytes in every field, with finite, moderate f16 scales."""
-    ts = {8: 34, 12: 144, 13: 176, 14: 210}[t]
+    ts = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 12: 144, 13: 176, 14: 210}[t]
     raw = rng.integers(0, 256, size=(nblocks, ts), dtype=np.uint8)
     def f16col(n):
         return (rng.standard_normal(n) * d_scale).astype(np.float16).view(np.uint8).reshape(n, 2)
-    if t in (12, 13):
+    if t in (12, 13, 3, 7):
         raw[:, 0:2] = f16col(nblocks)
         raw[:, 2:4] = f16col(nblocks)
     elif t == 14:

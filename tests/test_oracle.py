@@ -253,3 +253,98 @@ def test_weight_quantisers_valid(oracle):
         deq = oracle.dequantize(t, raw)
         rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
         assert rel < tol, (t, rel)
+
+
+# ---------------------------------------------------------------- 32-value legacy blocks
+LEGACY = [2, 3, 6, 7]  # Q4_0, Q4_1, Q5_0, Q5_1
+
+
+@pytest.mark.parametrize("t", LEGACY)
+def test_dequant_legacy_known_answers(oracle, t):
+    # every code value in both nibble halves (and, for Q5_*, both qh halves),
+    # through an independent packer: x = d*(q - off) or d*q + m, in f32
+    rng = np.random.default_rng(200 + t)
+    five = t in (6, 7)
+    top = 32 if five else 16
+    blobs, want = [], []
+    for rep in range(4):
+        q = rng.permutation(np.arange(32) % top)
+        d = bp.f16_bits(float(rng.uniform(0.01, 2.0)) * (1 if rep % 2 else -1))
+        m = bp.f16_bits(float(rng.uniform(-3, 3)))
+        if t == 2:
+            blobs.append(bp.pack_q4_0(d, q))
+            want.append((q.astype(np.float32) - np.float32(8)) * bp.f16_val(d))
+        elif t == 3:
+            blobs.append(bp.pack_q4_1(d, m, q))
+            want.append(q.astype(np.float32) * bp.f16_val(d) + bp.f16_val(m))
+        elif t == 6:
+            blobs.append(bp.pack_q5_0(d, q))
+            want.append((q.astype(np.float32) - np.float32(16)) * bp.f16_val(d))
+        else:
+            blobs.append(bp.pack_q5_1(d, m, q))
+            want.append(q.astype(np.float32) * bp.f16_val(d) + bp.f16_val(m))
+    got = oracle.dequantize(t, np.frombuffer(b"".join(blobs), dtype=np.uint8))
+    assert np.array_equal(got, np.concatenate(want).astype(np.float32))
+
+
+def test_q8_1_known_answers(oracle):
+    # as Q8_0 (d = amax/127 kept in f16, codes from the unrounded d), plus
+    # s = f16(f16(sum q) * d) -- candle's half-precision product
+    rng = np.random.default_rng(210)
+    x = rng.standard_normal((3, 64)).astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, 5] = -40.0
+    d, s, qs = bp.unpack_q8_1(oracle.quantize_act(9, x))
+    d8, q8 = bp.unpack_q8_0(oracle.quantize_act(8, x))
+    assert np.array_equal(d, d8) and np.array_equal(qs, q8)   # the Q8_0 half is Q8_0's
+    assert d[0] == 0 and not qs[0].any() and s[0] == 0
+    assert qs[2, 5] == -127
+    sums = qs.astype(np.int64).sum(axis=1).astype(np.float32)
+    want_s = (sums.astype(np.float16).astype(np.float32) * d).astype(np.float16).astype(np.float32)
+    assert np.array_equal(s, want_s)
+
+
+@pytest.mark.parametrize("t", LEGACY)
+@pytest.mark.parametrize("k", [32, 256, 544])
+def test_legacy_vec_dot_float64(oracle, t, k):
+    # sum over blocks of d_w*d_x*sum(q_w*q_x) (q_w with its -8/-16 offset), plus
+    # m_w*s_x for the _1 types, in float64 from independently unpacked fields
+    rng = np.random.default_rng(220 + t + k)
+    n, m = 20, 3
+    w_raw = bp.random_blocks(rng, t, n * k // 32, d_scale=0.05)
+    x = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+    y = oracle.qmatmul(t, w_raw, n, k, x)
+    dw, mw, qw = bp.unpack_legacy(t, w_raw)
+    off = {2: 8, 3: 0, 6: 16, 7: 0}[t]
+    at = oracle.VEC_DOT_TYPE[t]
+    xq = oracle.quantize_act(at, x)
+    if at == 9:
+        dx, sx, qx = bp.unpack_q8_1(xq.reshape(-1))
+    else:
+        dx, qx = bp.unpack_q8_0(xq.reshape(-1))
+        sx = np.zeros_like(dx)
+    nb = k // 32
+    dw, mw, qw = dw.reshape(n, nb), mw.reshape(n, nb), (qw - off).reshape(n, nb, 32)
+    dx, sx, qx = (a.astype(np.float64).reshape(m, nb) for a in (dx, sx)), None, qx.astype(np.int64).reshape(m, nb, 32)
+    dx, sx = list(dx)
+    ref = np.zeros((m, n))
+    for r in range(m):
+        isum = (qw * qx[r][None]).sum(axis=2)                    # [n, nb] exact integers
+        ref[r] = (dw * dx[r][None] * isum + mw * sx[r][None]).sum(axis=1)
+    scale = np.abs(ref).max(axis=1, keepdims=True) + 1e-30
+    assert (np.abs(y - ref) / scale).max() < 1e-5
+    xr = xq[1]
+    rb = k // 32 * oracle.type_size(t)
+    assert oracle.vec_dot(t, k, w_raw[3 * rb:4 * rb], xr) == y[1, 3]
+
+
+def test_legacy_weight_quantisers_valid(oracle):
+    # parity unpinned (ggml quantize_row_q4_0/q4_1/q5_0/q5_1 reference choices):
+    # the blocks are well-formed and reconstruct the weights
+    rng = np.random.default_rng(230)
+    w = (rng.standard_normal(64 * 32) * 0.02).astype(np.float32)
+    for t, tol in [(2, 0.15), (3, 0.12), (6, 0.08), (7, 0.06)]:
+        raw = oracle.quantize_weights(t, w)
+        assert raw.size == w.size // 32 * oracle.type_size(t)
+        rel = np.linalg.norm(oracle.dequantize(t, raw) - w) / np.linalg.norm(w)
+        assert rel < tol, (t, rel)
