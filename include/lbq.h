@@ -54,7 +54,12 @@ enum lbq_status {
 
 /* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
 enum lbq_ggml_type {
+    LBQ_TYPE_Q4_0 = 2, /* 32-value blocks, Q8_0 activations */
+    LBQ_TYPE_Q4_1 = 3, /* 32-value blocks, Q8_1 activations */
+    LBQ_TYPE_Q5_0 = 6, /* 32-value blocks, Q8_0 activations */
+    LBQ_TYPE_Q5_1 = 7, /* 32-value blocks, Q8_1 activations */
     LBQ_TYPE_Q8_0 = 8,
+    LBQ_TYPE_Q8_1 = 9, /* activation-only type (vec-dot partner of Q4_1/Q5_1) */
     LBQ_TYPE_Q4_K = 12,
     LBQ_TYPE_Q5_K = 13,
     LBQ_TYPE_Q6_K = 14,
@@ -65,7 +70,7 @@ enum lbq_ggml_type {
 const char *lbq_last_error(void);
 
 /* GgmlDType::block_size / type_size (/root/reference/src/quantization/mod.rs:99-126)
- * for the five types above; 0 for any other id. */
+ * for the types above; 0 for any other id. */
 int lbq_type_block_size(uint32_t ggml_type);
 int lbq_type_size(uint32_t ggml_type);
 
@@ -146,8 +151,8 @@ int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const l
  * two lets call sites that feed one x to several weights -- q/k/v at
  * /root/reference/src/model/custom_attention.rs:265-267, gate/up at
  * mlp_wrapper.rs:190,193 -- quantise x once.  act_type is LBQ_TYPE_Q8_K for
- * k-quant weights and LBQ_TYPE_Q8_0 for Q8_0 weights.  The handle owns device
- * memory for m rows of k values. */
+ * k-quant weights, LBQ_TYPE_Q8_0 for Q8_0/Q4_0/Q5_0 weights and LBQ_TYPE_Q8_1
+ * for Q4_1/Q5_1 weights.  The handle owns device memory for m rows of k values. */
 typedef struct lbq_act lbq_act;
 int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act);
 int lbq_act_quantize(lbq_act *act, const float *d_x, void *stream);
@@ -161,19 +166,21 @@ int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *act, f
 int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream);
 
 /* Dequantise nelem values of raw device blocks -- dequantize_tensor
- * (/root/reference/src/quantization/mod.rs:158-247), extended to Q5_K/Q6_K/Q8_K.
+ * (/root/reference/src/quantization/mod.rs:158-247), extended to Q5_K/Q6_K/Q8_K and
+ * the remaining 32-value types (Q4_1, Q5_0, Q5_1, Q8_1).
  * nelem must be a multiple of the block size. */
 int lbq_dequantize_blocks_f32(uint32_t ggml_type, const void *d_blocks, int64_t nelem, float *d_y, void *stream);
 
 /* Quantise activations x[m][k] to GGUF blocks of `act_type` (LBQ_TYPE_Q8_K:
- * 292-byte blocks; LBQ_TYPE_Q8_0: 34-byte blocks) -- the activation
- * quantisation inside QMatMul::forward (candle BlockQ8K::from_float /
- * BlockQ8_0::from_float).  Exposed so the step can be checked on its own. */
+ * 292-byte blocks; LBQ_TYPE_Q8_0: 34-byte blocks; LBQ_TYPE_Q8_1: 36-byte
+ * blocks) -- the activation quantisation inside QMatMul::forward (candle
+ * BlockQ8K / BlockQ8_0 / BlockQ8_1 ::from_float).  Exposed so the step can be
+ * checked on its own. */
 int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, void *d_out_blocks, void *stream);
 
 /* Quantise f32 weights (nelem values, row-major, rows along k) to GGUF blocks
  * of `ggml_type` -- quantize_tensor (/root/reference/src/quantization/mod.rs:257-327),
- * extended to Q5_K/Q6_K.  Runs on the device. */
+ * extended to Q5_K/Q6_K and Q4_1/Q5_0/Q5_1.  Runs on the device. */
 int lbq_quantize_weights_f32(uint32_t ggml_type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream);
 
 /* ---------------------------------------------------------------------------

@@ -1,7 +1,7 @@
-// lbq_act.hip -- activation quantisation (Q8_K, Q8_0) and block dequantisation kernels.
+// lbq_act.hip -- activation quantisation (Q8_K, Q8_0, Q8_1) and block dequantisation kernels.
 //
 // Activation quantisation restates candle-core 0.10.2 k_quants.rs
-// BlockQ8K::from_float and BlockQ8_0::from_float, the first step of
+// BlockQ8K::from_float, BlockQ8_0::from_float and BlockQ8_1::from_float, the first step of
 // QMatMul::forward on the reference CPU path.  Every code and scale must be
 // bit-identical to the CPU: the kernels use IEEE division (HIP's default,
 // correctly rounded), roundf (half away from zero, like Rust's f32::round) and
@@ -47,12 +47,15 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0: 8 lanes per 32-value block, 8 blocks per wave.
+// Q8_0 / Q8_1: 8 lanes per 32-value block, 8 blocks per wave.  Q8_1 adds
+// s = f16(f16(sum of the codes) * d) with d the stored f16 scale (candle
+// BlockQ8_1::from_float multiplies two f16 values: widened, multiplied in f32,
+// rounded back).
 // ---------------------------------------------------------------------------
-template <bool GGUF_OUT, bool VEC_IN>
+template <bool GGUF_OUT, bool VEC_IN, bool S>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int64_t nblocks,
                                                     int8_t *__restrict__ xq, float *__restrict__ xd,
-                                                    uint8_t *__restrict__ gguf) {
+                                                    float *__restrict__ xs, uint8_t *__restrict__ gguf) {
     const int tid = blockIdx.x * 256 + threadIdx.x;
     const int64_t blk = (int64_t)tid >> 3;
     const int sub = threadIdx.x & 7;
@@ -61,15 +64,35 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
     if (ok) load4f(x + blk * QK8_0 + sub * 4, VEC_IN, v);
     __half dh;
     const uint32_t packed = q8_0_block8(v, &dh);
+    __half sh = __float2half_rn(0.f);
+    if constexpr (S) {
+        int sum = dot4(packed, 0x01010101u, 0);
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        sh = __float2half_rn(__half2float(__float2half_rn((float)sum)) * __half2float(dh));
+    }
     if (!ok) return;
     if (GGUF_OUT) {
-        uint8_t *b = gguf + blk * 34;
-        if (sub == 0) *reinterpret_cast<unsigned short *>(b) = __half_as_ushort(dh);
-        *reinterpret_cast<unsigned short *>(b + 2 + sub * 4) = (unsigned short)(packed & 0xffffu);
-        *reinterpret_cast<unsigned short *>(b + 4 + sub * 4) = (unsigned short)(packed >> 16);
+        if constexpr (S) {
+            uint8_t *b = gguf + blk * 36;
+            if (sub == 0) {
+                *reinterpret_cast<unsigned short *>(b) = __half_as_ushort(dh);
+                *reinterpret_cast<unsigned short *>(b + 2) = __half_as_ushort(sh);
+            }
+            *reinterpret_cast<uint32_t *>(b + 4 + sub * 4) = packed;
+        } else {
+            uint8_t *b = gguf + blk * 34;
+            if (sub == 0) *reinterpret_cast<unsigned short *>(b) = __half_as_ushort(dh);
+            *reinterpret_cast<unsigned short *>(b + 2 + sub * 4) = (unsigned short)(packed & 0xffffu);
+            *reinterpret_cast<unsigned short *>(b + 4 + sub * 4) = (unsigned short)(packed >> 16);
+        }
     } else {
         *reinterpret_cast<uint32_t *>(xq + blk * QK8_0 + sub * 4) = packed;
-        if (sub == 0) xd[blk] = __half2float(dh);
+        if (sub == 0) {
+            xd[blk] = __half2float(dh);
+            if constexpr (S) xs[blk] = __half2float(sh);
+        }
     }
 }
 
@@ -78,13 +101,27 @@ __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x,
 // ---------------------------------------------------------------------------
 #pragma clang fp contract(off)
 
-// value index e = 16*g + i of a 256-value k-quant block, or of a 32-value Q8_0 block
+// value index e = 16*g + i of a 256-value k-quant block, or of a 32-value block
 template <int TYPE>
 __device__ __forceinline__ void deq_group(const uint8_t *__restrict__ b, int g, float out[16]) {
-    if constexpr (TYPE == TYPE_Q8_0) {
+    if constexpr (TYPE == TYPE_Q8_0 || TYPE == TYPE_Q8_1) {
         const float d = h2f(ld2_a2(b));
-        const uint8_t *qs = b + 2 + 16 * g;
+        const uint8_t *qs = b + (TYPE == TYPE_Q8_0 ? 2 : 4) + 16 * g;
         for (int i = 0; i < 16; i++) out[i] = (float)(int8_t)qs[i] * d;
+    } else if constexpr (is_legacy(TYPE)) {
+        // value 16g + i: nibble g of qs[i]; Q5_* bit 4 from bit 16g + i of qh
+        constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+        constexpr bool FIVE = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1;
+        constexpr int QH = HAS_M ? 4 : 2, QS = (HAS_M ? 4 : 2) + (FIVE ? 4 : 0);
+        const float d = h2f(ld2_a2(b));
+        const float m = HAS_M ? h2f(ld2_a2(b + 2)) : 0.f;
+        const uint32_t qh = FIVE ? (ld2_a2(b + QH) | (ld2_a2(b + QH + 2) << 16)) >> (16 * g) : 0u;
+        const uint8_t *qs = b + QS;
+        for (int i = 0; i < 16; i++) {
+            const int q = (int)((qs[i] >> (4 * g)) & 15u) | (int)(((qh >> i) & 1u) << 4);
+            if constexpr (HAS_M) out[i] = (float)q * d + m;
+            else out[i] = (float)(q - (FIVE ? 16 : 8)) * d;
+        }
     } else if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
         const uint32_t dd = ld_u32(b);
         const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
@@ -122,8 +159,10 @@ __device__ __forceinline__ void deq_group(const uint8_t *__restrict__ b, int g, 
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ blocks, int64_t ngroups,
                                                  float *__restrict__ y) {
-    constexpr int BS = TYPE == TYPE_Q8_0 ? 32 : 256;
-    constexpr int TS = TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 292;
+    constexpr int BS = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q8_1 || is_legacy(TYPE) ? 32 : 256;
+    constexpr int TS = TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q4_1 ? 20 : TYPE == TYPE_Q5_0 ? 22 : TYPE == TYPE_Q5_1 ? 24
+                     : TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q8_1 ? 36 : TYPE == TYPE_Q4_K ? 144
+                     : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 292;
     constexpr int GPB = BS / 16;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= ngroups) return;
@@ -141,7 +180,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ blo
 // launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd, int16_t *xbs,
-                            uint8_t *gguf, hipStream_t st) {
+                            float *xs, uint8_t *gguf, hipStream_t st) {
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);
@@ -153,16 +192,20 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
             if (vec) k_quant_q8k<false, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
             else k_quant_q8k<false, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
         }
-    } else {
+    } else if (act_type == TYPE_Q8_0 || act_type == TYPE_Q8_1) {
         const int64_t nb = m * (k / QK8_0);
         const dim3 grid((unsigned)((nb * 8 + 255) / 256));
+#define LBQ_Q8(G, V)                                                                                   \
+    if (act_type == TYPE_Q8_1) k_quant_q8_0<G, V, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf); \
+    else k_quant_q8_0<G, V, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf);
         if (gguf) {
-            if (vec) k_quant_q8_0<true, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, gguf);
-            else k_quant_q8_0<true, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, gguf);
+            if (vec) { LBQ_Q8(true, true) } else { LBQ_Q8(true, false) }
         } else {
-            if (vec) k_quant_q8_0<false, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, gguf);
-            else k_quant_q8_0<false, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, gguf);
+            if (vec) { LBQ_Q8(false, true) } else { LBQ_Q8(false, false) }
         }
+#undef LBQ_Q8
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -171,7 +214,12 @@ hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float 
     const int64_t ng = nelem / 16;
     const dim3 grid((unsigned)((ng + 255) / 256));
     switch (type) {
+    case TYPE_Q4_0: k_dequant<TYPE_Q4_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q4_1: k_dequant<TYPE_Q4_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q5_0: k_dequant<TYPE_Q5_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q5_1: k_dequant<TYPE_Q5_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q8_0: k_dequant<TYPE_Q8_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q8_1: k_dequant<TYPE_Q8_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q4_K: k_dequant<TYPE_Q4_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q5_K: k_dequant<TYPE_Q5_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q6_K: k_dequant<TYPE_Q6_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;

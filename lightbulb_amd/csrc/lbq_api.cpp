@@ -81,8 +81,10 @@ int hip_fail(hipError_t e, const char *what) {
 }
 
 bool weight_type_ok(uint32_t t) {
-    return t == LBQ_TYPE_Q8_0 || t == LBQ_TYPE_Q4_K || t == LBQ_TYPE_Q5_K || t == LBQ_TYPE_Q6_K;
+    return t == LBQ_TYPE_Q8_0 || lbq::is_kquant((int)t) || lbq::is_legacy((int)t);
 }
+
+bool act_type_ok(uint32_t t) { return t == LBQ_TYPE_Q8_K || t == LBQ_TYPE_Q8_0 || t == LBQ_TYPE_Q8_1; }
 
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
@@ -100,20 +102,26 @@ struct DeviceGuard {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Split activation layout for m rows of length k quantised to act_type.
+// Split activation layout for m rows of length k quantised to act_type: codes,
+// f32 scales, then the Q8_K 16-value sums (int16) or the Q8_1 block sums (f32).
 struct ActLayout {
     size_t q_off, d_off, bs_off, total;
     int nb;
+    int act_type;
 };
 
 ActLayout act_layout(int act_type, int64_t m, int64_t k) {
     ActLayout L;
     const int bs = act_type == LBQ_TYPE_Q8_K ? 256 : 32;
     L.nb = (int)(k / bs);
+    L.act_type = act_type;
     L.q_off = 0;
     L.d_off = align_up((size_t)(m * k), 256);
     L.bs_off = align_up(L.d_off + (size_t)(m * L.nb) * sizeof(float), 256);
-    L.total = align_up(L.bs_off + (act_type == LBQ_TYPE_Q8_K ? (size_t)(m * (k / 16)) * sizeof(int16_t) : 0), 256);
+    size_t tail = 0;
+    if (act_type == LBQ_TYPE_Q8_K) tail = (size_t)(m * (k / 16)) * sizeof(int16_t);
+    else if (act_type == LBQ_TYPE_Q8_1) tail = (size_t)(m * L.nb) * sizeof(float);
+    L.total = align_up(L.bs_off + tail, 256);
     return L;
 }
 
@@ -142,8 +150,16 @@ int ensure_scratch(lbq_ctx *ctx, size_t bytes) {
 }
 
 lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
+    const bool q8k = L.act_type == LBQ_TYPE_Q8_K, q81 = L.act_type == LBQ_TYPE_Q8_1;
     return lbq::ActView{reinterpret_cast<const int8_t *>(base + L.q_off), reinterpret_cast<const float *>(base + L.d_off),
-                        reinterpret_cast<const int16_t *>(base + L.bs_off), k, L.nb};
+                        q8k ? reinterpret_cast<const int16_t *>(base + L.bs_off) : nullptr, k, L.nb,
+                        q81 ? reinterpret_cast<const float *>(base + L.bs_off) : nullptr};
+}
+
+// the activation quantisation into the split layout of av
+hipError_t quant_into(int act_type, const float *d_x, int64_t m, int64_t k, const lbq::ActView &av, hipStream_t st) {
+    return lbq::launch_quant_act(act_type, d_x, m, k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
+                                 const_cast<int16_t *>(av.xbs), const_cast<float *>(av.xs), nullptr, st);
 }
 
 // The dot half of QMatMul::forward: decode GEMV for m <= 8, MFMA GEMM above.
@@ -165,7 +181,7 @@ int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m
 }
 
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
-    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)", type);
     const int bs = lbq_type_block_size(type);
     if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
@@ -211,7 +227,8 @@ const char *lbq_last_error(void) { return g_err.c_str(); }
 
 int lbq_type_block_size(uint32_t t) {
     switch (t) {
-    case LBQ_TYPE_Q8_0: return 32;
+    case LBQ_TYPE_Q4_0: case LBQ_TYPE_Q4_1: case LBQ_TYPE_Q5_0: case LBQ_TYPE_Q5_1: case LBQ_TYPE_Q8_0: case LBQ_TYPE_Q8_1:
+        return 32;
     case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K: return 256;
     default: return 0;
     }
@@ -219,7 +236,12 @@ int lbq_type_block_size(uint32_t t) {
 
 int lbq_type_size(uint32_t t) {
     switch (t) {
+    case LBQ_TYPE_Q4_0: return 18;
+    case LBQ_TYPE_Q4_1: return 20;
+    case LBQ_TYPE_Q5_0: return 22;
+    case LBQ_TYPE_Q5_1: return 24;
     case LBQ_TYPE_Q8_0: return 34;
+    case LBQ_TYPE_Q8_1: return 36;
     case LBQ_TYPE_Q4_K: return 144;
     case LBQ_TYPE_Q5_K: return 176;
     case LBQ_TYPE_Q6_K: return 210;
@@ -321,7 +343,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
         return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
-    const int act_type = w->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    const int act_type = lbq::vec_dot_type(w->type);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -334,7 +356,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
         return LBQ_OK;
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && w->type != LBQ_TYPE_Q8_0 && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
+    if (m > 8 && lbq::is_kquant(w->type) && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
         // batched: the operand pre-pass quantises x itself
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), "GEMM workspace");
         if (s) return s;
@@ -346,8 +368,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
     const lbq::ActView av = view_of(ctx->scratch, L, w->k);
-    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w->k, const_cast<int8_t *>(av.xq),
-                                         const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
+    hipError_t e = quant_into(act_type, d_x, m, w->k, av, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     return run_dot(ctx, w, av, m, d_y, st);
 }
@@ -369,7 +390,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     if (reinterpret_cast<uintptr_t>(d_x) & 3u) return fail(LBQ_ERR_INVALID_ARG, "x must be a 4-byte aligned f32 buffer");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
     const lbq_weight *w0 = ws[0];
-    const int act_type = w0->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    const int act_type = lbq::vec_dot_type(w0->type);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -391,7 +412,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && w0->type != LBQ_TYPE_Q8_0) {
+    if (m > 8 && lbq::is_kquant(w0->type)) {
         // batched: one operand pre-pass (quantising x itself when it can) shared
         // by every weight's GEMM
         size_t wsb = 0;
@@ -406,8 +427,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
             s = ensure_scratch(ctx, L.total);
             if (s) return s;
             const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
-            e = lbq::launch_quant_act(act_type, d_x, m, w0->k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
-                                      const_cast<int16_t *>(av.xbs), nullptr, st);
+            e = quant_into(act_type, d_x, m, w0->k, av, st);
             if (e == hipSuccess) e = lbq::gemm_prepass(w0->type, w0->k, av, nullptr, m, ctx->ws, st);
         }
         if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
@@ -422,8 +442,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
     const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
-    hipError_t e = lbq::launch_quant_act(act_type, d_x, m, w0->k, const_cast<int8_t *>(av.xq),
-                                         const_cast<float *>(av.xd), const_cast<int16_t *>(av.xbs), nullptr, st);
+    hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     for (int i = 0; i < count; i++) {
         s = run_dot(ctx, ws[i], av, m, d_ys[i], st);
@@ -530,7 +549,7 @@ int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int
             rm.end[i] = (int32_t)r;
         }
         rm.n = rows;
-        const int act_type = w0->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+        const int act_type = lbq::vec_dot_type(w0->type);
         const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, act_layout(act_type, 1, w0->k).nb};
         hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, none, d_x, st, d_norm_w, eps);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
@@ -573,8 +592,8 @@ int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const l
 int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_act **out_act) {
     if (!ctx || !out_act) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_act_create");
     *out_act = nullptr;
-    if (act_type != LBQ_TYPE_Q8_K && act_type != LBQ_TYPE_Q8_0)
-        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15) or Q8_0 (8)", act_type);
+    if (!act_type_ok(act_type))
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15), Q8_0 (8) or Q8_1 (9)", act_type);
     const int bs = lbq_type_block_size(act_type);
     if (m <= 0 || k <= 0 || k % bs) return fail(LBQ_ERR_SHAPE, "activation shape (%lld, %lld) invalid for %d-value blocks", (long long)m, (long long)k, bs);
     if (m > (int64_t)1 << 24 || k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "activation shape exceeds the supported maximum");
@@ -604,9 +623,7 @@ int lbq_act_quantize(lbq_act *a, const float *d_x, void *stream) {
     if (reinterpret_cast<uintptr_t>(d_x) & 3u) return fail(LBQ_ERR_INVALID_ARG, "x must be a 4-byte aligned f32 buffer");
     DeviceGuard g(a->ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
-    hipError_t e = lbq::launch_quant_act(a->act_type, d_x, a->m, a->k, const_cast<int8_t *>(a->view.xq),
-                                         const_cast<float *>(a->view.xd), const_cast<int16_t *>(a->view.xbs),
-                                         nullptr, static_cast<hipStream_t>(stream));
+    hipError_t e = quant_into(a->act_type, d_x, a->m, a->k, a->view, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     return LBQ_OK;
 }
@@ -622,7 +639,7 @@ int lbq_act_destroy(lbq_act *a) {
 int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *a, float *d_y, void *stream) {
     if (!ctx || !w || !a || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_qmatmul_act_f32");
     if (reinterpret_cast<uintptr_t>(d_y) & 3u) return fail(LBQ_ERR_INVALID_ARG, "y must be a 4-byte aligned f32 buffer");
-    const int want = w->type == LBQ_TYPE_Q8_0 ? LBQ_TYPE_Q8_0 : LBQ_TYPE_Q8_K;
+    const int want = lbq::vec_dot_type(w->type);
     if (a->act_type != want) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "weight type %d needs activation type %d, got %d", w->type, want, a->act_type);
     if (a->k != w->k) return fail(LBQ_ERR_SHAPE, "activation k = %lld, weight k = %lld", (long long)a->k, (long long)w->k);
     DeviceGuard g(ctx->device);
@@ -643,7 +660,7 @@ int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stre
 
 int lbq_dequantize_blocks_f32(uint32_t type, const void *d_blocks, int64_t nelem, float *d_y, void *stream) {
     if (!d_blocks || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_dequantize_blocks_f32");
-    if (!weight_type_ok(type) && type != LBQ_TYPE_Q8_K) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
+    if (!weight_type_ok(type) && !act_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
     const int bs = lbq_type_block_size(type);
     if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);
     if ((reinterpret_cast<uintptr_t>(d_blocks) & 3u) || (reinterpret_cast<uintptr_t>(d_y) & 15u))
@@ -657,14 +674,14 @@ int lbq_dequantize_blocks_f32(uint32_t type, const void *d_blocks, int64_t nelem
 
 int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, void *d_out_blocks, void *stream) {
     if (!d_x || !d_out_blocks) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_quantize_act");
-    if (act_type != LBQ_TYPE_Q8_K && act_type != LBQ_TYPE_Q8_0)
-        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15) or Q8_0 (8)", act_type);
+    if (!act_type_ok(act_type))
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "activation type %u must be Q8_K (15), Q8_0 (8) or Q8_1 (9)", act_type);
     const int bs = lbq_type_block_size(act_type);
     if (m < 0 || k <= 0 || k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a positive multiple of %d", (long long)k, bs);
     if ((reinterpret_cast<uintptr_t>(d_x) & 3u) || (reinterpret_cast<uintptr_t>(d_out_blocks) & 3u))
         return fail(LBQ_ERR_INVALID_ARG, "x and the output blocks must be 4-byte aligned");
     if (m == 0) return LBQ_OK;
-    hipError_t e = lbq::launch_quant_act((int)act_type, d_x, m, k, nullptr, nullptr, nullptr,
+    hipError_t e = lbq::launch_quant_act((int)act_type, d_x, m, k, nullptr, nullptr, nullptr, nullptr,
                                          static_cast<uint8_t *>(d_out_blocks), static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     return LBQ_OK;

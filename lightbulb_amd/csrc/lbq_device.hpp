@@ -123,6 +123,7 @@ struct ActView {
     const int16_t *xbs;
     int64_t k;  // row length in values
     int nb;     // scale blocks per row (k/256 or k/32)
+    const float *xs = nullptr;  // Q8_1: per-block s = d * sum(codes), widened from f16
 };
 
 struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };

@@ -240,6 +240,105 @@ struct Dec<TYPE_Q8_0> {
     }
 };
 
+// ---- 32-value legacy blocks (Q4_0, Q4_1, Q5_0, Q5_1): piece = one block.  Value
+// j (j < 16) is the low nibble of qs[j], value j + 16 its high nibble; Q5_* take
+// bit 4 of value v from bit v of the u32 qh.  Fields: d f16 | (m f16) | (qh u32) |
+// qs[16]; 18- and 22-byte blocks start 2 bytes into a dword every other block.
+// The products follow candle's vec_dot bodies: Q4_0 ((sumi*d_w)*d_x), Q5_0
+// ((d_w*d_x)*sumi), Q4_1/Q5_1 ((d_w*d_x)*sumi + m_w*s_x) -- with the -8/-16
+// code offsets folded into the int8 weight codes.
+template <int TYPE>
+struct DecLegacy {
+    static constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+    static constexpr bool FIVE = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1;
+    static constexpr int BYTES = 18 + (HAS_M ? 2 : 0) + (FIVE ? 4 : 0);
+    static constexpr bool ODD = BYTES % 4 != 0;  // may start at 2 mod 4
+    static constexpr int NW = FIVE ? 6 : 5;       // aligned dwords covering the block
+    static constexpr int PPB = 1, VALS = 32;
+    struct Raw { uint32_t w[NW]; uint32_t mis; };
+    __device__ static Raw load(const uint8_t *blk, int) {
+        Raw r;
+        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
+        r.mis = ODD ? (uint32_t)(ad & 2u) : 0u;
+        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
+        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
+        r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
+        r.w[4] = *reinterpret_cast<const uint32_t *>(base + 16);
+        if constexpr (NW == 6) r.w[5] = *reinterpret_cast<const uint32_t *>(base + 20);
+        return r;
+    }
+    // 4 bits b0..b3 -> bit 4 of bytes 0..3
+    __device__ static uint32_t spread4(uint32_t b) { return ((b * 0x00204081u) & 0x01010101u) << 4; }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int, const ActView &a, int mrows, float *acc) {
+        // the block's dwords from its own byte 0 (c[i] = bytes 4i..4i+3; the top
+        // half of the last one is not used)
+        constexpr int NC = (BYTES + 3) / 4;
+        uint32_t c[NC];
+#pragma unroll
+        for (int i = 0; i < NC; i++) {
+            if constexpr (ODD) c[i] = __builtin_amdgcn_alignbyte(r.w[i + 1 < NW ? i + 1 : i], r.w[i], r.mis);
+            else c[i] = r.w[i];
+        }
+        const float d = h2f(c[0] & 0xffffu);
+        const float mw = HAS_M ? h2f(c[0] >> 16) : 0.f;
+        // qs dwords: byte offset QS = 2, 4, 6 or 8
+        constexpr int QS = (HAS_M ? 4 : 2) + (FIVE ? 4 : 0);
+        uint32_t qs[4], qh = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if constexpr (QS % 4 == 0) qs[i] = c[QS / 4 + i];
+            else qs[i] = __builtin_amdgcn_alignbyte(c[QS / 4 + i + 1], c[QS / 4 + i], 2);
+        }
+        if constexpr (FIVE) {
+            constexpr int QH = HAS_M ? 4 : 2;
+            if constexpr (QH % 4 == 0) qh = c[QH / 4];
+            else qh = __builtin_amdgcn_alignbyte(c[QH / 4 + 1], c[QH / 4], 2);
+        }
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = qs[i] & 0x0F0F0F0Fu;
+            hi[i] = (qs[i] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (FIVE) {
+                lo[i] |= spread4((qh >> (4 * i)) & 15u);
+                hi[i] |= spread4((qh >> (16 + 4 * i)) & 15u);
+            }
+            if constexpr (!HAS_M) {
+                // code - 8 (Q4_0) / - 16 (Q5_0) per byte as int8, no borrow between bytes
+                constexpr uint32_t OFF = FIVE ? 0x10101010u : 0x08080808u;
+                lo[i] = ((lo[i] | 0x80808080u) - OFF) ^ 0x80808080u;
+                hi[i] = ((hi[i] | 0x80808080u) - OFF) ^ 0x80808080u;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK8_0;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xr);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xr + 16);
+                int s = dot4(lo[0], x0.x, 0);
+                s = dot4(lo[1], x0.y, s);
+                s = dot4(lo[2], x0.z, s);
+                s = dot4(lo[3], x0.w, s);
+                s = dot4(hi[0], x1.x, s);
+                s = dot4(hi[1], x1.y, s);
+                s = dot4(hi[2], x1.z, s);
+                s = dot4(hi[3], x1.w, s);
+                const int64_t xb = (int64_t)m * a.nb + b;
+                const float dx = a.xd[xb];
+                if constexpr (TYPE == TYPE_Q4_0) acc[m] += ((float)s * d) * dx;
+                else if constexpr (TYPE == TYPE_Q5_0) acc[m] += (d * dx) * (float)s;
+                else acc[m] += (d * dx) * (float)s + mw * a.xs[xb];
+            }
+        }
+    }
+};
+template <> struct Dec<TYPE_Q4_0> : DecLegacy<TYPE_Q4_0> {};
+template <> struct Dec<TYPE_Q4_1> : DecLegacy<TYPE_Q4_1> {};
+template <> struct Dec<TYPE_Q5_0> : DecLegacy<TYPE_Q5_0> {};
+template <> struct Dec<TYPE_Q5_1> : DecLegacy<TYPE_Q5_1> {};
+
 // ---------------------------------------------------------------------------
 // Persistent GEMV.  The rows are cut into groups of RPW rows; each wave owns a
 // contiguous range of groups and walks each group's rows in chunks of
@@ -264,7 +363,7 @@ __global__ __launch_bounds__(256) void k_gemv_p(const uint8_t *__restrict__ W, P
     using Raw = typename D::Raw;
     constexpr int LPR = 64 / RPW;
     constexpr int CH = LPR * IT;
-    constexpr bool KQ = TYPE != TYPE_Q8_0;
+    constexpr bool KQ = is_kquant(TYPE);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane / LPR, li = lane % LPR;
     const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
@@ -380,8 +479,6 @@ static int env_int(const char *s, int def) { return s ? atoi(s) : def; }
 static GemvCfg pick_cfg(int type, int64_t n, int pieces, int m, int64_t k) {
     GemvCfg c;
     c.fused = (int64_t)m * k <= 32768;
-    const int ppb = type == TYPE_Q6_K ? 4 : type == TYPE_Q8_0 ? 1 : 8;
-    (void)ppb;
     // rows per wave: enough lanes per row to cover a row in a few chunks
     // must name a pair that run_m compiles for every m
     if (pieces >= 384) { c.rpw = 1; c.it = 7; }
@@ -410,7 +507,7 @@ static hipError_t run_p(const uint8_t *w, const PGeom &g0, const ActView &act, c
     size_t lds = 0;
     if (FUSED) {
         lds = ((size_t)m * act.k + 15) / 16 * 16 + ((size_t)m * act.nb * 4 + 15) / 16 * 16;
-        if (TYPE != TYPE_Q8_0) lds += (size_t)m * (act.k / 16) * 2;
+        if (is_kquant(TYPE)) lds += (size_t)m * (act.k / 16) * 2;
     }
     k_gemv_p<TYPE, M, RPW, IT, FUSED><<<grid, 256, lds, st>>>(w, g, act, x, m, y);
     return hipGetLastError();
@@ -543,9 +640,11 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.row_bytes = row_bytes;
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
-    if (m == 1) {
-        const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
-        if (e != hipErrorNotSupported) return e;
+    if constexpr (!is_legacy(TYPE)) {
+        if (m == 1) {
+            const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
+            if (e != hipErrorNotSupported) return e;
+        }
     }
     if (alpha || map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // m = 1 fast path only
     GemvCfg c = pick_cfg(TYPE, n, g.pieces, m, k);

@@ -6,7 +6,18 @@
 
 namespace lbq {
 
-enum : int { TYPE_Q8_0 = 8, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15 };
+enum : int {
+    TYPE_Q4_0 = 2, TYPE_Q4_1 = 3, TYPE_Q5_0 = 6, TYPE_Q5_1 = 7, TYPE_Q8_0 = 8, TYPE_Q8_1 = 9,
+    TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15
+};
+
+// 32-value weight blocks that pair with Q8_0 / Q8_1 activations.
+constexpr bool is_legacy(int t) { return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1; }
+constexpr bool is_kquant(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K; }
+// activation type of QMatMul's vec_dot for a weight type (candle GgmlType::VecDotType)
+constexpr int vec_dot_type(int t) {
+    return is_kquant(t) ? TYPE_Q8_K : (t == TYPE_Q4_1 || t == TYPE_Q5_1) ? TYPE_Q8_1 : TYPE_Q8_0;
+}
 
 struct ActView;
 
@@ -25,10 +36,11 @@ struct RowMap {
 };
 RowMap single_row_map(const uint8_t *w, int64_t n, float *y);
 
-// Quantise x[m][k] to Q8_K (act_type 15) or Q8_0 (act_type 8).  Writes the split
-// internal layout (xq/xd/xbs) when gguf == nullptr, else GGUF blocks to gguf.
+// Quantise x[m][k] to Q8_K (act_type 15), Q8_0 (8) or Q8_1 (9).  Writes the split
+// internal layout (codes xq, scales xd, Q8_K sub-block sums xbs, Q8_1 block sums
+// xs) when gguf == nullptr, else GGUF blocks to gguf.
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
-                            int16_t *xbs, uint8_t *gguf, hipStream_t st);
+                            int16_t *xbs, float *xs, uint8_t *gguf, hipStream_t st);
 
 // Dequantise nelem values (multiple of the block size) of `type` blocks to f32.
 hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st);

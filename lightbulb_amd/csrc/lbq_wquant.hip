@@ -2,7 +2,8 @@
 //
 // lightbulb's quantize_tensor (/root/reference/src/quantization/mod.rs:257-327)
 // calls ggml-quants 0.1.0, a port of ggml's reference quantisers
-// (quantize_row_q8_0/q4_K/q5_K/q6_K_ref with make_qkx2_quants / make_qx_quants).
+// (quantize_row_q8_0/q4_K/q5_K/q6_K_ref with make_qkx2_quants / make_qx_quants,
+// and the 32-value quantize_row_q4_0/q4_1/q5_0/q5_1_ref).
 // This file restates those published algorithms for the device so multi-GB
 // weight sets can be built in HBM.  Built with -ffp-contract=off: every
 // product and sum is rounded separately, in the source order, so the blocks
@@ -320,9 +321,83 @@ __global__ __launch_bounds__(256) void k_quant_w_q6k(const float *__restrict__ w
     }
 }
 
+// ggml quantize_row_q4_0/q4_1/q5_0/q5_1_ref: one thread per 32-value block.
+//   _0: d = max / -8 (-16), max the signed value of largest |x| (first on ties),
+//       q = min(15 (31), (int8)(x*id + 8.5 (16.5)));
+//   _1: d = (max - min) / 15 (31), m = min, q = (int8)((x - min)*id + 0.5),
+//       clamped to 15 for Q4_1 only;
+// id = 1/d (0 when d = 0); codes are truncated toward zero, as C's cast does.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_quant_w_legacy(const float *__restrict__ w, int64_t nblocks,
+                                                        uint8_t *__restrict__ out) {
+    constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+    constexpr bool FIVE = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1;
+    constexpr int BYTES = 18 + (HAS_M ? 2 : 0) + (FIVE ? 4 : 0);
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= nblocks) return;
+    const float *x = w + blk * 32;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = x[j];
+    float d, mn = 0.f;
+    if constexpr (HAS_M) {
+        float lo = v[0], hi = v[0];
+#pragma unroll
+        for (int j = 1; j < 32; j++) {
+            if (v[j] < lo) lo = v[j];
+            if (v[j] > hi) hi = v[j];
+        }
+        d = (hi - lo) / (FIVE ? 31.f : 15.f);
+        mn = lo;
+    } else {
+        float amax = 0.f, mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++)
+            if (amax < fabsf(v[j])) { amax = fabsf(v[j]); mx = v[j]; }
+        d = mx / (FIVE ? -16.f : -8.f);
+        // An all-zero block has d = 0 / -8 = -0, stored as f16 0x8000.  The
+        // compiler would fold the (power-of-two) quotient and the f16 conversion
+        // into one v_fma_mix with a +0 addend, which turns -0 into +0; keep the
+        // f32 quotient as its own value.
+        asm volatile("" : "+v"(d));
+    }
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    uint32_t qh = 0;
+    uint8_t qs[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        int a, b;
+        if constexpr (HAS_M) {
+            a = (int)((v[j] - mn) * id + 0.5f);
+            b = (int)((v[j + 16] - mn) * id + 0.5f);
+            if constexpr (!FIVE) { a = a < 15 ? a : 15; b = b < 15 ? b : 15; }
+        } else {
+            constexpr float BIAS = FIVE ? 16.5f : 8.5f;
+            constexpr int TOP = FIVE ? 31 : 15;
+            a = (int)(v[j] * id + BIAS);
+            b = (int)(v[j + 16] * id + BIAS);
+            a = a < TOP ? a : TOP;
+            b = b < TOP ? b : TOP;
+        }
+        qs[j] = (uint8_t)((a & 15) | ((b & 15) << 4));
+        if constexpr (FIVE) qh |= ((uint32_t)(a >> 4) & 1u) << j | ((uint32_t)(b >> 4) & 1u) << (j + 16);
+    }
+    // 2-byte stores: 18- and 22-byte blocks sit at even, not always 4-aligned, offsets
+    unsigned short *o = reinterpret_cast<unsigned short *>(out + blk * BYTES);
+    int h = 0;
+    o[h++] = (unsigned short)f2h_bits(d);
+    if constexpr (HAS_M) o[h++] = (unsigned short)f2h_bits(mn);
+    if constexpr (FIVE) {
+        o[h++] = (unsigned short)(qh & 0xffffu);
+        o[h++] = (unsigned short)(qh >> 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[h + j] = (unsigned short)(qs[2 * j] | (qs[2 * j + 1] << 8));
+}
+
 hipError_t launch_quant_weights(int type, const float *w, int64_t nelem, uint8_t *out, hipStream_t st) {
     switch (type) {
-    case TYPE_Q8_0: return launch_quant_act(TYPE_Q8_0, w, 1, nelem, nullptr, nullptr, nullptr, out, st);
+    case TYPE_Q8_0: return launch_quant_act(TYPE_Q8_0, w, 1, nelem, nullptr, nullptr, nullptr, nullptr, out, st);
     case TYPE_Q4_K: {
         const int64_t nb = nelem / QK_K;
         k_quant_w_k45<15><<<dim3((unsigned)((nb * 8 + 255) / 256)), 256, 0, st>>>(w, nb, out);
@@ -336,6 +411,15 @@ hipError_t launch_quant_weights(int type, const float *w, int64_t nelem, uint8_t
     case TYPE_Q6_K: {
         const int64_t nb = nelem / QK_K;
         k_quant_w_q6k<<<dim3((unsigned)((nb * 16 + 255) / 256)), 256, 0, st>>>(w, nb, out);
+        break;
+    }
+    case TYPE_Q4_0: case TYPE_Q4_1: case TYPE_Q5_0: case TYPE_Q5_1: {
+        const int64_t nb = nelem / 32;
+        const dim3 grid((unsigned)((nb + 255) / 256));
+        if (type == TYPE_Q4_0) k_quant_w_legacy<TYPE_Q4_0><<<grid, 256, 0, st>>>(w, nb, out);
+        else if (type == TYPE_Q4_1) k_quant_w_legacy<TYPE_Q4_1><<<grid, 256, 0, st>>>(w, nb, out);
+        else if (type == TYPE_Q5_0) k_quant_w_legacy<TYPE_Q5_0><<<grid, 256, 0, st>>>(w, nb, out);
+        else k_quant_w_legacy<TYPE_Q5_1><<<grid, 256, 0, st>>>(w, nb, out);
         break;
     }
     default: return hipErrorInvalidValue;

@@ -75,7 +75,22 @@ class GgmlDType(IntEnum):
 
 
 #: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE
-SERVED = (GgmlDType.Q8_0, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+SERVED = (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q4K,
+          GgmlDType.Q5K, GgmlDType.Q6K)
+
+#: activation-only block types (the vec-dot partners)
+ACT_TYPES = (GgmlDType.Q8_0, GgmlDType.Q8_1, GgmlDType.Q8K)
+
+
+def vec_dot_type(dtype: GgmlDType) -> GgmlDType:
+    """The activation block type QMatMul::forward quantises x to for a weight type
+    (candle GgmlType::VecDotType): Q8_K for k-quants, Q8_1 for Q4_1/Q5_1, else Q8_0."""
+    dtype = GgmlDType(dtype)
+    if dtype in (GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K):
+        return GgmlDType.Q8K
+    if dtype in (GgmlDType.Q4_1, GgmlDType.Q5_1):
+        return GgmlDType.Q8_1
+    return GgmlDType.Q8_0
 
 
 # ---------------------------------------------------------------------------
@@ -379,7 +394,7 @@ class Mlp:
 
 
 class QActivation:
-    """x [m, k] quantised once (Q8_K for k-quant weights, Q8_0 for Q8_0 weights),
+    """x [m, k] quantised once to the weights' vec-dot type (``vec_dot_type``),
     reusable by every QMatMul that reads the same x -- q/k/v and gate/up."""
 
     def __init__(self, act_type: GgmlDType, m: int, k: int, device="cuda"):
@@ -393,7 +408,7 @@ class QActivation:
 
     @classmethod
     def for_weight(cls, qmatmul: "QMatMul", m: int) -> "QActivation":
-        t = GgmlDType.Q8_0 if qmatmul.qtensor().dtype() == GgmlDType.Q8_0 else GgmlDType.Q8K
+        t = vec_dot_type(qmatmul.qtensor().dtype())
         return cls(t, m, qmatmul.qtensor().shape()[1], qmatmul.qtensor().data.device)
 
     def quantize(self, x: torch.Tensor) -> "QActivation":
@@ -449,7 +464,7 @@ class QuantizableLinear:
 def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> torch.Tensor:
     """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off."""
     dtype = GgmlDType(dtype)
-    if dtype not in SERVED and dtype != GgmlDType.Q8K:
+    if dtype not in SERVED and dtype not in ACT_TYPES:
         raise ValueError(f"Dequantization for {dtype.type_name()} not yet implemented")
     bs, ts = dtype.block_size(), dtype.type_size()
     num_blocks = (elem_count + bs - 1) // bs
@@ -489,10 +504,10 @@ def quantize_tensor(data: torch.Tensor, dtype: GgmlDType, _exact: bool = False) 
 
 
 def quantize_activations(x: torch.Tensor, act_type: GgmlDType) -> torch.Tensor:
-    """The activation step of QMatMul::forward on its own: x f32 [m, k] -> Q8_K / Q8_0 blocks (uint8)."""
+    """The activation step of QMatMul::forward on its own: x f32 [m, k] -> Q8_K / Q8_0 / Q8_1 blocks (uint8)."""
     act_type = GgmlDType(act_type)
-    if act_type not in (GgmlDType.Q8K, GgmlDType.Q8_0):
-        raise ValueError("activations quantise to Q8_K or Q8_0")
+    if act_type not in ACT_TYPES:
+        raise ValueError("activations quantise to Q8_K, Q8_0 or Q8_1")
     x = x.contiguous()
     k = x.shape[-1]
     m = x.numel() // k
