@@ -462,15 +462,16 @@ class QuantizableLinear:
 # dequantize_tensor / quantize_tensor (src/quantization/mod.rs:158-327)
 # ---------------------------------------------------------------------------
 def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> torch.Tensor:
-    """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off."""
+    """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off.
+    Errors name the type as the reference's ``{:?}`` does (the variant: ``Q4K``)."""
     dtype = GgmlDType(dtype)
     if dtype not in SERVED and dtype not in ACT_TYPES:
-        raise ValueError(f"Dequantization for {dtype.type_name()} not yet implemented")
+        raise ValueError(f"Dequantization for {dtype.name} not yet implemented")
     bs, ts = dtype.block_size(), dtype.type_size()
     num_blocks = (elem_count + bs - 1) // bs
     expected = num_blocks * ts
     if data.numel() < expected:
-        raise ValueError(f"Insufficient data for {dtype.type_name()}: got {data.numel()} bytes, "
+        raise ValueError(f"Insufficient data for {dtype.name}: got {data.numel()} bytes, "
                          f"need {expected} bytes")
     out = torch.empty(num_blocks * bs, dtype=torch.float32, device=data.device)
     if num_blocks:
@@ -483,7 +484,7 @@ def quantize_tensor(data: torch.Tensor, dtype: GgmlDType, _exact: bool = False) 
     """f32 device values -> GGUF blocks (uint8); the last block is zero-padded."""
     dtype = GgmlDType(dtype)
     if dtype not in SERVED:
-        raise ValueError(f"Quantization for {dtype.type_name()} not yet implemented")
+        raise ValueError(f"Quantization for {dtype.name} not yet implemented")
     if data.dtype != torch.float32:
         raise ValueError("quantize_tensor expects f32 values")
     flat = data.reshape(-1)

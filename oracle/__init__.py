@@ -21,11 +21,15 @@ this path:
 * dequantize           -- known-answer blocks assembled by an independent Python
                          bit-packer from chosen (d, dmin, sc, m, q) per value, for
                          every scale-unpack branch, nibble, qh bit plane and
-                         Q6_K quarter; plus the reference's own Q8_0 round-trip
-                         bound (|err| < 0.01 on i/256 ramps, mod.rs:99-112).
-* Q8_K / Q8_0 act quant -- closed-form special cases (single non-zero -> -128,
-                         negative max, all-zero, ties, saturation), the bsums
-                         invariant, and |x - d*q| <= |d|/2 on random rows.
+                         Q6_K quarter, the Q2_K/Q3_K 2-bit planes, hmask bits and
+                         6-bit scale layout (packed the way ggml's quantisers
+                         write them), and every code of the 32-value types; plus
+                         the reference's own Q8_0 round-trip bound (|err| < 0.01
+                         on i/256 ramps, mod.rs:99-112).
+* Q8_K / Q8_0 / Q8_1   -- closed-form special cases (single non-zero -> -128,
+  act quant              negative max, all-zero, ties, saturation), the bsums
+                         invariant, |x - d*q| <= |d|/2 on random rows, and Q8_1's
+                         s = f16(f16(sum q) * d) recomputed from its codes.
 * vec_dot / qmatmul    -- float64 brute force over the dequantised weights and
                          dequantised activations (the exact value the integer
                          path computes) on tiny shapes, to ~1e-6 relative.
@@ -46,11 +50,15 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 _BUILD = HERE / "_build"
 
-Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 2, 3, 6, 7, 8, 9, 12, 13, 14, 15
-BLOCK_SIZE = {Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
-TYPE_SIZE = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 = 2, 3, 6, 7, 8, 9
+Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 10, 11, 12, 13, 14, 15
+BLOCK_SIZE = {Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32, Q8_1: 32,
+              Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
+TYPE_SIZE = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 36,
+             Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
 # the activation type each weight type's vec_dot takes (candle GgmlType::VecDotType)
-VEC_DOT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_1: Q8_1, Q5_1: Q8_1, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+VEC_DOT_TYPE = {Q4_0: Q8_0, Q5_0: Q8_0, Q8_0: Q8_0, Q4_1: Q8_1, Q5_1: Q8_1,
+                Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
 
 _libs: dict[str, ctypes.CDLL] = {}
 

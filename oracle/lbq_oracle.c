@@ -19,7 +19,8 @@
  *   - activation quantisation to Q8_K (k-quant weights) or Q8_0 (Q8_0
  *     weights): candle k_quants.rs BlockQ8K::from_float / BlockQ8_0::from_float
  *   - the generic (non-SIMD) integer vec_dot for Q8_0.Q8_0, Q4_K.Q8_K,
- *     Q5_K.Q8_K and Q6_K.Q8_K with its 8-lane partial sums, and for the
+ *     Q5_K.Q8_K, Q6_K.Q8_K and Q3_K.Q8_K with its 8-lane partial sums,
+ *     Q2_K.Q8_K (one integer sum per block, minus dmin * sum(bsum * m)), and for the
  *     32-value legacy blocks Q4_0.Q8_0, Q5_0.Q8_0, Q4_1.Q8_1, Q5_1.Q8_1
  *     (activation quantisation to Q8_1: BlockQ8_1::from_float)
  *   - the k_quants::matmul driver: quantise all M rows, then for each row a
@@ -54,6 +55,8 @@ typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; } b
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; } blk_q5_k;
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_k;
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_k;
+typedef struct { uint8_t scales[QK_K / 16]; uint8_t qs[QK_K / 4]; uint16_t d, dmin; } blk_q2_k;
+typedef struct { uint8_t hmask[QK_K / 8]; uint8_t qs[QK_K / 4]; uint8_t scales[12]; uint16_t d; } blk_q3_k;
 /* 32-value blocks (ggml legacy types) */
 typedef struct { uint16_t d; uint8_t qs[16]; } blk_q4_0;
 typedef struct { uint16_t d, m; uint8_t qs[16]; } blk_q4_1;
@@ -65,6 +68,8 @@ _Static_assert(sizeof(blk_q8_0) == 34, "q8_0 size");
 _Static_assert(sizeof(blk_q4_k) == 144, "q4_k size");
 _Static_assert(sizeof(blk_q5_k) == 176, "q5_k size");
 _Static_assert(sizeof(blk_q6_k) == 210, "q6_k size");
+_Static_assert(sizeof(blk_q2_k) == 84, "q2_k size");
+_Static_assert(sizeof(blk_q3_k) == 110, "q3_k size");
 _Static_assert(sizeof(blk_q8_k) == 292, "q8_k size");
 _Static_assert(sizeof(blk_q4_0) == 18, "q4_0 size");
 _Static_assert(sizeof(blk_q4_1) == 20, "q4_1 size");
@@ -78,7 +83,7 @@ _Static_assert(sizeof(blk_q8_1) == 36, "q8_1 size");
 int oracle_block_size(uint32_t type) {
     switch (type) {
     case ORACLE_Q8_0: case ORACLE_Q4_0: case ORACLE_Q4_1: case ORACLE_Q5_0: case ORACLE_Q5_1: case ORACLE_Q8_1: return 32;
-    case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: case ORACLE_Q8_K: return 256;
+    case ORACLE_Q2_K: case ORACLE_Q3_K: case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: case ORACLE_Q8_K: return 256;
     default: return 0;
     }
 }
@@ -91,6 +96,8 @@ int oracle_type_size(uint32_t type) {
     case ORACLE_Q5_0: return 22;
     case ORACLE_Q5_1: return 24;
     case ORACLE_Q8_1: return 36;
+    case ORACLE_Q2_K: return 84;
+    case ORACLE_Q3_K: return 110;
     case ORACLE_Q4_K: return 144;
     case ORACLE_Q5_K: return 176;
     case ORACLE_Q6_K: return 210;
@@ -257,6 +264,50 @@ static void deq_q8_k(const blk_q8_k *b, float *y) {
     for (int i = 0; i < QK_K; i++) y[i] = b->d * (float)b->qs[i];
 }
 
+/* Q2_K (candle BlockQ2K::to_float): element 128h + 32s + 16t + l (h < 2, s < 4,
+ * t < 2, l < 16) is code (qs[32h + 16t + l] >> 2s) & 3 of sub-block j = 8h + 2s + t,
+ * whose scale byte holds the 4-bit scale (low) and min (high):
+ * y = (d * sc) * q - (dmin * m). */
+static void deq_q2_k(const blk_q2_k *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d), dmin = oracle_f16_to_f32(b->dmin);
+    for (int h = 0; h < 2; h++)
+        for (int s = 0; s < 4; s++)
+            for (int t = 0; t < 2; t++) {
+                const uint8_t sc = b->scales[8 * h + 2 * s + t];
+                const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                for (int l = 0; l < 16; l++) {
+                    const int q = (b->qs[32 * h + 16 * t + l] >> (2 * s)) & 3;
+                    *y++ = dl * (float)q - ml;
+                }
+            }
+}
+
+/* Q3_K 6-bit sub-block scales (ggml's aux rearrangement of the 12 bytes):
+ * scale j = low 4 bits from scales[j % 8] (nibble j / 8) | 2 high bits from
+ * scales[8 + j % 4] (bits 2*(j / 4)), minus 32. */
+static int q3k_scale(const uint8_t sc[12], int j) {
+    const int lo = (sc[j % 8] >> (4 * (j / 8))) & 0xF;
+    const int hi = (sc[8 + j % 4] >> (2 * (j / 4))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+/* Q3_K (candle BlockQ3K::to_float): element 128h + 32s + 16t + l has low bits
+ * (qs[32h + 16t + l] >> 2s) & 3, minus 4 unless bit 4h + s of hmask[16t + l] is
+ * set; sub-block j = 8h + 2s + t: y = (d * scale_j) * q. */
+static void deq_q3_k(const blk_q3_k *b, float *y) {
+    const float d = oracle_f16_to_f32(b->d);
+    for (int h = 0; h < 2; h++)
+        for (int s = 0; s < 4; s++)
+            for (int t = 0; t < 2; t++) {
+                const float dl = d * (float)q3k_scale(b->scales, 8 * h + 2 * s + t);
+                for (int l = 0; l < 16; l++) {
+                    const int lo = (b->qs[32 * h + 16 * t + l] >> (2 * s)) & 3;
+                    const int q = lo - ((b->hmask[16 * t + l] >> (4 * h + s)) & 1 ? 0 : 4);
+                    *y++ = dl * (float)q;
+                }
+            }
+}
+
 /* 32-value blocks (candle k_quants to_float): element j from the low nibble of
  * qs[j], element j + 16 from its high nibble; Q5 fifth bits from the u32 qh,
  * bit j (element j) and bit j + 16 (element j + 16). */
@@ -323,6 +374,8 @@ int oracle_dequantize(uint32_t type, const void *blocks, int64_t nblocks, float 
         case ORACLE_Q5_0: deq_q5_0((const blk_q5_0 *)b, y); break;
         case ORACLE_Q5_1: deq_q5_1((const blk_q5_1 *)b, y); break;
         case ORACLE_Q8_1: deq_q8_1((const blk_q8_1 *)b, y); break;
+        case ORACLE_Q2_K: deq_q2_k((const blk_q2_k *)b, y); break;
+        case ORACLE_Q3_K: deq_q3_k((const blk_q3_k *)b, y); break;
         }
     }
     return 0;
@@ -565,6 +618,80 @@ static float vec_dot_q6_k(int64_t n, const blk_q6_k *xs, const blk_q8_k *ys) {
 }
 
 /* the generic candle/ggml bodies of the 32-block vec_dots */
+/* ggml/candle generic Q2_K.Q8_K: per block an exact integer sum of
+ * sc_j * (codes . x) over the 16 sub-blocks and summs = sum(bsum_j * m_j);
+ * sumf += (y.d * d) * isum - (y.d * dmin) * summs. */
+static float vec_dot_q2_k(int64_t n, const blk_q2_k *xs, const blk_q8_k *ys) {
+    float sumf = 0.f;
+    for (int64_t i = 0; i < n / QK_K; i++) {
+        const blk_q2_k *x = &xs[i];
+        const blk_q8_k *y = &ys[i];
+        int summs = 0;
+        for (int j = 0; j < 16; j++) summs += (int)y->bsums[j] * (int)(x->scales[j] >> 4);
+        const float dall = y->d * oracle_f16_to_f32(x->d);
+        const float dmin = y->d * oracle_f16_to_f32(x->dmin);
+        int isum = 0, is = 0;
+        const uint8_t *q2 = x->qs;
+        const int8_t *q8 = y->qs;
+        for (int h = 0; h < 2; h++) {
+            for (int s = 0; s < 4; s++) {
+                for (int t = 0; t < 2; t++) {
+                    const int d = x->scales[is++] & 0xF;
+                    int isuml = 0;
+                    for (int l = 0; l < 16; l++) isuml += (int)q8[16 * t + l] * ((q2[16 * t + l] >> (2 * s)) & 3);
+                    isum += d * isuml;
+                }
+                q8 += 32;
+            }
+            q2 += 32;
+        }
+        sumf += dall * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+/* ggml/candle generic Q3_K.Q8_K: codes in [-4, 3] expanded to aux8, then the
+ * same 8-lane int32 sums scaled per sub-block as Q6_K. */
+static float vec_dot_q3_k(int64_t n, const blk_q3_k *xs, const blk_q8_k *ys) {
+    int8_t aux8[QK_K];
+    int16_t aux16[8];
+    float sums[8] = {0};
+    int32_t aux32[8];
+    for (int64_t i = 0; i < n / QK_K; i++) {
+        const blk_q3_k *x = &xs[i];
+        const blk_q8_k *y = &ys[i];
+        const uint8_t *q3 = x->qs;
+        int8_t *a = aux8;
+        uint8_t m = 1;
+        for (int h = 0; h < 2; h++) {
+            for (int s = 0; s < 4; s++) {
+                for (int l = 0; l < 32; l++) a[l] = (int8_t)((q3[l] >> (2 * s)) & 3);
+                for (int l = 0; l < 32; l++) a[l] = (int8_t)(a[l] - ((x->hmask[l] & m) ? 0 : 4));
+                a += 32;
+                m = (uint8_t)(m << 1);
+            }
+            q3 += 32;
+        }
+        memset(aux32, 0, sizeof(aux32));
+        const int8_t *q8 = y->qs;
+        a = aux8;
+        for (int j = 0; j < QK_K / 16; j++) {
+            const int32_t scale = q3k_scale(x->scales, j);
+            for (int t = 0; t < 2; t++) {
+                for (int l = 0; l < 8; l++) aux16[l] = (int16_t)(q8[l] * a[l]);
+                for (int l = 0; l < 8; l++) aux32[l] += scale * aux16[l];
+                q8 += 8;
+                a += 8;
+            }
+        }
+        const float d = oracle_f16_to_f32(x->d) * y->d;
+        for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
+    }
+    float s = 0.f;
+    for (int l = 0; l < 8; l++) s += sums[l];
+    return s;
+}
+
 static float vec_dot_q4_0(int64_t n, const blk_q4_0 *xs, const blk_q8_0 *ys) {
     float sumf = 0.f;
     for (int64_t i = 0; i < n / 32; i++) {
@@ -627,7 +754,7 @@ uint32_t oracle_vec_dot_type(uint32_t type) {
     switch (type) {
     case ORACLE_Q8_0: case ORACLE_Q4_0: case ORACLE_Q5_0: return ORACLE_Q8_0;
     case ORACLE_Q4_1: case ORACLE_Q5_1: return ORACLE_Q8_1;
-    case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: return ORACLE_Q8_K;
+    case ORACLE_Q2_K: case ORACLE_Q3_K: case ORACLE_Q4_K: case ORACLE_Q5_K: case ORACLE_Q6_K: return ORACLE_Q8_K;
     default: return 0;
     }
 }
@@ -642,6 +769,8 @@ int oracle_vec_dot(uint32_t type, int64_t k, const void *wrow, const void *xrow,
     case ORACLE_Q4_K: *out = vec_dot_q4_k(k, (const blk_q4_k *)wrow, (const blk_q8_k *)xrow); return 0;
     case ORACLE_Q5_K: *out = vec_dot_q5_k(k, (const blk_q5_k *)wrow, (const blk_q8_k *)xrow); return 0;
     case ORACLE_Q6_K: *out = vec_dot_q6_k(k, (const blk_q6_k *)wrow, (const blk_q8_k *)xrow); return 0;
+    case ORACLE_Q2_K: *out = vec_dot_q2_k(k, (const blk_q2_k *)wrow, (const blk_q8_k *)xrow); return 0;
+    case ORACLE_Q3_K: *out = vec_dot_q3_k(k, (const blk_q3_k *)wrow, (const blk_q8_k *)xrow); return 0;
     default: return -1;
     }
 }

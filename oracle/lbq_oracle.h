@@ -11,7 +11,7 @@ extern "C" {
 /* GGUF type ids, /root/reference/src/quantization/mod.rs:58-75 */
 enum {
     ORACLE_Q4_0 = 2, ORACLE_Q4_1 = 3, ORACLE_Q5_0 = 6, ORACLE_Q5_1 = 7, ORACLE_Q8_0 = 8, ORACLE_Q8_1 = 9,
-    ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14, ORACLE_Q8_K = 15
+    ORACLE_Q2_K = 10, ORACLE_Q3_K = 11, ORACLE_Q4_K = 12, ORACLE_Q5_K = 13, ORACLE_Q6_K = 14, ORACLE_Q8_K = 15
 };
 /* the activation type a weight type's vec_dot takes (0 if none) */
 uint32_t oracle_vec_dot_type(uint32_t type);

@@ -21,6 +21,8 @@ Spec (ggml block layouts, as used by candle-core 0.10.2 / ggml-quants 0.1.0):
         scale index v//16: x = d*scale*q.
   Q8_0: d f16, qs[32] int8: x = d*q.
   Q8_K: d f32, qs[256] int8, bsums[16] int16.
+  Q2_K: scales[16] (scale | min << 4), qs[64], d f16, dmin f16: x = (d*sc)*q - dmin*m.
+  Q3_K: hmask[32], qs[64], scales[12] (6-bit, -32 offset), d f16: x = (d*sc)*q, q in -4..3.
   32-value legacy blocks: value j (j<16) is the low nibble of qs[j], value
   j+16 its high nibble; Q5_* take bit 4 of value v from bit v of the little-
   endian u32 qh.
@@ -106,6 +108,43 @@ def pack_q8k(d: float, q) -> bytes:
     return np.array([d], dtype=np.float32).tobytes() + q.tobytes() + bsums.tobytes()
 
 
+def _k_low2_qs(L) -> bytes:
+    """ggml's Q2_K/Q3_K 2-bit packing: for each 128-value half, value
+    128h + 32s + l goes to bits 2s of qs[32h + l]."""
+    qs = [0] * 64
+    for h in range(2):
+        for l in range(32):
+            qs[32 * h + l] = sum((int(L[128 * h + 32 * s + l]) & 3) << (2 * s) for s in range(4))
+    return bytes(qs)
+
+
+def pack_q2k(d: int, dmin: int, sc, mn, q) -> bytes:
+    """sc, mn: 16 4-bit scales/mins; q: 256 codes 0..3 (ggml quantize_row_q2_K
+    layout: scales[16] = sc | mn << 4, qs[64], d, dmin)."""
+    scales = bytes((int(sc[j]) & 15) | ((int(mn[j]) & 15) << 4) for j in range(16))
+    return scales + _k_low2_qs(q) + d.to_bytes(2, "little") + dmin.to_bytes(2, "little")
+
+
+def pack_q3k(d: int, sc, q) -> bytes:
+    """sc: 16 signed 6-bit scales (-32..31); q: 256 codes -4..3.  ggml
+    quantize_row_q3_K layout: hmask[32] (bit j/32 of hmask[j%32] set when code
+    j >= 0), qs[64] (the low 2 bits of code+4), scales[12], d."""
+    L = [int(v) + 4 for v in q]
+    hmask = [0] * 32
+    for j in range(256):
+        if L[j] > 3:
+            hmask[j % 32] |= 1 << (j // 32)
+    scales = [0] * 12
+    for j in range(16):
+        l = int(sc[j]) + 32
+        if j < 8:
+            scales[j] = l & 0xF
+        else:
+            scales[j - 8] |= (l & 0xF) << 4
+        scales[8 + j % 4] |= (l >> 4) << (2 * (j // 4))
+    return bytes(hmask) + _k_low2_qs(L) + bytes(scales) + d.to_bytes(2, "little")
+
+
 # ---- expected values, straight from the fields (every op rounded to f32) ----
 def expect_q4k(d, dmin, sc, mn, q) -> np.ndarray:
     D, M = f16_val(d), f16_val(dmin)
@@ -124,6 +163,23 @@ def expect_q6k(d, scales, q) -> np.ndarray:
     for v in range(256):
         out[v] = np.float32(np.float32(D * np.float32(scales[v // 16])) * np.float32(q[v]))
     return out
+
+
+def expect_q2k(d, dmin, sc, mn, q) -> np.ndarray:
+    D, M = f16_val(d), f16_val(dmin)
+    out = np.empty(256, dtype=np.float32)
+    for v in range(256):
+        j = v // 16
+        dl = np.float32(D * np.float32(sc[j]))
+        ml = np.float32(M * np.float32(mn[j]))
+        out[v] = np.float32(np.float32(dl * np.float32(q[v])) - ml)
+    return out
+
+
+def expect_q3k(d, sc, q) -> np.ndarray:
+    D = f16_val(d)
+    return np.array([np.float32(np.float32(D * np.float32(sc[v // 16])) * np.float32(q[v])) for v in range(256)],
+                    dtype=np.float32)
 
 
 # ---- unpack Q8_K / Q8_0 blocks produced by the quantisers ----
@@ -196,7 +252,7 @@ def unpack_q8_1(raw: np.ndarray):
 
 def random_blocks(rng: np.random.Generator, t: int, nblocks: int, d_scale: float = 1e-3) -> np.ndarray:
     """Random bytes in every field, with finite, moderate f16 scales."""
-    ts = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 12: 144, 13: 176, 14: 210}[t]
+    ts = {2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210}[t]
     raw = rng.integers(0, 256, size=(nblocks, ts), dtype=np.uint8)
     def f16col(n):
         return (rng.standard_normal(n) * d_scale).astype(np.float16).view(np.uint8).reshape(n, 2)
@@ -205,6 +261,11 @@ def random_blocks(rng: np.random.Generator, t: int, nblocks: int, d_scale: float
         raw[:, 2:4] = f16col(nblocks)
     elif t == 14:
         raw[:, 208:210] = f16col(nblocks)
+    elif t == 10:
+        raw[:, 80:82] = f16col(nblocks)
+        raw[:, 82:84] = f16col(nblocks)
+    elif t == 11:
+        raw[:, 108:110] = f16col(nblocks)
     else:
         raw[:, 0:2] = f16col(nblocks)
     return raw.reshape(-1)

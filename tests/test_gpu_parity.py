@@ -83,7 +83,7 @@ def test_dequant_q8k_and_truncation(oracle, lbq, dev):
     raw = bp.random_blocks(rng, Q4_K, 2)
     got = dequantize_tensor(to_dev(raw, dev), Q4_K, 300).cpu().numpy()
     assert got.shape == (300,) and np.array_equal(got, oracle.dequantize(Q4_K, raw)[:300])
-    with pytest.raises(ValueError, match="Insufficient data for Q4_K"):
+    with pytest.raises(ValueError, match="Insufficient data for Q4K: got 200 bytes, need 288 bytes"):
         dequantize_tensor(to_dev(raw[:200], dev), Q4_K, 512)
 
 

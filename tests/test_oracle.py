@@ -204,13 +204,13 @@ def _brute(oracle, t, w_raw, n, k, x):
     """float64 sum over dequantised weights x dequantised activations: the exact value
     the integer path represents (dequantisation is pinned above)."""
     wd = oracle.dequantize(t, w_raw).astype(np.float64).reshape(n, k)
-    at = Q8_0 if t == Q8_0 else Q8_K
+    at = oracle.VEC_DOT_TYPE[t]
     xq = oracle.quantize_act(at, x)
     xd = oracle.dequantize(at, xq.reshape(-1)).astype(np.float64).reshape(x.shape[0], k)
     return xd @ wd.T
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("t", [Q8_0, 10, 11, Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("k", [256, 512, 768])
 def test_qmatmul_matches_float64_brute_force(oracle, t, k):
     rng = np.random.default_rng(100 + t + k)
@@ -223,7 +223,7 @@ def test_qmatmul_matches_float64_brute_force(oracle, t, k):
     rel = np.abs(y - ref) / (np.abs(ref).max(axis=1, keepdims=True) + 1e-30)
     assert rel.max() < 1e-5
     # the same through vec_dot one element at a time
-    at = Q8_0 if t == Q8_0 else Q8_K
+    at = oracle.VEC_DOT_TYPE[t]
     xq = oracle.quantize_act(at, x)
     rb = k // bs * oracle.type_size(t)
     for r, c in [(0, 0), (2, 47), (1, 13)]:
@@ -348,3 +348,56 @@ def test_legacy_weight_quantisers_valid(oracle):
         assert raw.size == w.size // 32 * oracle.type_size(t)
         rel = np.linalg.norm(oracle.dequantize(t, raw) - w) / np.linalg.norm(w)
         assert rel < tol, (t, rel)
+
+
+# ---------------------------------------------------------------- Q2_K / Q3_K
+def test_dequant_q2k_known_answers(oracle):
+    # every 4-bit scale and min value, every code in every 2-bit plane, through a
+    # packer that follows ggml's quantize_row_q2_K layout
+    rng = np.random.default_rng(240)
+    blobs, want = [], []
+    for rep in range(4):
+        sc = rng.permutation(16)
+        mn = rng.permutation(16)
+        q = rng.integers(0, 4, 256)
+        q[:4] = [0, 1, 2, 3]
+        d = bp.f16_bits(float(rng.uniform(0.01, 1.0)))
+        dmin = bp.f16_bits(float(rng.uniform(0.0, 1.0)) * (-1 if rep == 3 else 1))
+        blobs.append(bp.pack_q2k(d, dmin, sc, mn, q))
+        want.append(bp.expect_q2k(d, dmin, sc, mn, q))
+    got = oracle.dequantize(10, np.frombuffer(b"".join(blobs), dtype=np.uint8))
+    assert np.array_equal(got, np.concatenate(want))
+
+
+def test_dequant_q3k_known_answers(oracle):
+    # all 64 six-bit scales over the blocks (both halves of the high-bit byte
+    # layout), codes -4..3 in every hmask bit plane
+    rng = np.random.default_rng(250)
+    blobs, want = [], []
+    scales = rng.permutation(np.arange(-32, 32))
+    for rep in range(4):
+        sc = scales[16 * rep:16 * rep + 16]
+        q = rng.integers(-4, 4, 256)
+        q[:8] = np.arange(-4, 4)
+        d = bp.f16_bits(float(rng.uniform(0.01, 1.0)) * (-1 if rep == 2 else 1))
+        blobs.append(bp.pack_q3k(d, sc, q))
+        want.append(bp.expect_q3k(d, sc, q))
+    got = oracle.dequantize(11, np.frombuffer(b"".join(blobs), dtype=np.uint8))
+    assert np.array_equal(got, np.concatenate(want))
+
+
+@pytest.mark.parametrize("t", [10, 11])
+def test_k23_integer_sum_closed_form(oracle, t):
+    # one block, x quantised to a single non-zero code: the dot is exactly
+    # d_x * (that value's dequantised weight), so the vec_dot must reproduce
+    # the dequantised weight at each probed position (to f32 rounding)
+    rng = np.random.default_rng(260 + t)
+    raw = bp.random_blocks(rng, t, 1, d_scale=0.05)
+    wd = oracle.dequantize(t, raw).astype(np.float64)
+    for pos in (0, 15, 16, 37, 128, 200, 255):
+        x = np.zeros((1, 256), dtype=np.float32)
+        x[0, pos] = -3.0                                  # code -128, d_x = 3/128
+        xq = oracle.quantize_act(Q8_K, x)
+        got = oracle.vec_dot(t, 256, raw, xq[0])
+        ref = wd[pos] * (-3.0)
+        assert abs(got - ref) <= 1e-6 * max(1.0, abs(ref)), (pos, got, ref)
