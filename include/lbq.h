@@ -60,6 +60,8 @@ enum lbq_ggml_type {
     LBQ_TYPE_Q5_1 = 7, /* 32-value blocks, Q8_1 activations */
     LBQ_TYPE_Q8_0 = 8,
     LBQ_TYPE_Q8_1 = 9, /* activation-only type (vec-dot partner of Q4_1/Q5_1) */
+    LBQ_TYPE_Q2_K = 10,
+    LBQ_TYPE_Q3_K = 11,
     LBQ_TYPE_Q4_K = 12,
     LBQ_TYPE_Q5_K = 13,
     LBQ_TYPE_Q6_K = 14,
@@ -217,7 +219,9 @@ int lbq_gguf_meta_int(const lbq_gguf *g, const char *key, int64_t *out);
 int lbq_gguf_meta_float(const lbq_gguf *g, const char *key, double *out);
 int lbq_gguf_meta_string(const lbq_gguf *g, const char *key, const char **data, size_t *len);
 int lbq_gguf_meta_array(const lbq_gguf *g, const char *key, uint32_t *elem_type, uint64_t *len);
-/* Copy a tensor's bytes into device memory through pinned staging (synchronous). */
+/* Copy a tensor's blocks into device memory through pinned staging (synchronous):
+ * ceil(numel / block_size) * lbq_type_size bytes -- the extent above except for
+ * Q2_K, whose GgmlDType entry (82 bytes) is shorter than its 84-byte block. */
 int lbq_gguf_copy_tensor(const lbq_gguf *g, const char *name, void *d_dst, size_t dst_bytes);
 /* A weight handle straight from the file: the tensor (2-D, ne0 = k, ne1 = n, a
  * served type) goes through pinned staging into device memory the handle owns.

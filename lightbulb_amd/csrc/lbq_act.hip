@@ -108,6 +108,33 @@ __device__ __forceinline__ void deq_group(const uint8_t *__restrict__ b, int g, 
         const float d = h2f(ld2_a2(b));
         const uint8_t *qs = b + (TYPE == TYPE_Q8_0 ? 2 : 4) + 16 * g;
         for (int i = 0; i < 16; i++) out[i] = (float)(int8_t)qs[i] * d;
+    } else if constexpr (TYPE == TYPE_Q2_K || TYPE == TYPE_Q3_K) {
+        // group g = sub-block 8h + 2s + t: values 128h + 32s + 16t + [0,16), low
+        // bits (qs[32h + 16t + i] >> 2s) & 3
+        const int h = g >> 3, s = (g >> 1) & 3, t = g & 1;
+        if constexpr (TYPE == TYPE_Q2_K) {
+            const uint32_t dd = ld_u32(b + 80);
+            const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+            const uint32_t sc = b[g];
+            const float dl = d * (float)(sc & 0xFu);
+            const float ml = dmin * (float)(sc >> 4);
+            const uint8_t *qs = b + 16 + 32 * h + 16 * t;
+            for (int i = 0; i < 16; i++) out[i] = dl * (float)((qs[i] >> (2 * s)) & 3) - ml;
+        } else {
+            // 6-bit scale: low nibble of scales[g % 8] (nibble g / 8), top 2 bits of
+            // scales[8 + g % 4] (bits 2 * (g / 4)); code - 4 unless bit 4h + s of
+            // hmask[16t + i] is set
+            const float d = h2f(ld2_a2(b + 108));
+            const int lo = (b[96 + (g & 7)] >> (4 * (g >> 3))) & 0xF;
+            const int hi = (b[104 + (g & 3)] >> (2 * (g >> 2))) & 3;
+            const float dl = d * (float)((lo | (hi << 4)) - 32);
+            const uint8_t *qs = b + 32 + 32 * h + 16 * t;
+            const uint8_t *hm = b + 16 * t;
+            for (int i = 0; i < 16; i++) {
+                const int q = ((qs[i] >> (2 * s)) & 3) - (((hm[i] >> (4 * h + s)) & 1) ? 0 : 4);
+                out[i] = dl * (float)q;
+            }
+        }
     } else if constexpr (is_legacy(TYPE)) {
         // value 16g + i: nibble g of qs[i]; Q5_* bit 4 from bit 16g + i of qh
         constexpr bool HAS_M = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
@@ -161,7 +188,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ blo
                                                  float *__restrict__ y) {
     constexpr int BS = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q8_1 || is_legacy(TYPE) ? 32 : 256;
     constexpr int TS = TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q4_1 ? 20 : TYPE == TYPE_Q5_0 ? 22 : TYPE == TYPE_Q5_1 ? 24
-                     : TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q8_1 ? 36 : TYPE == TYPE_Q4_K ? 144
+                     : TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q8_1 ? 36 : TYPE == TYPE_Q2_K ? 84
+                     : TYPE == TYPE_Q3_K ? 110 : TYPE == TYPE_Q4_K ? 144
                      : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 292;
     constexpr int GPB = BS / 16;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -220,6 +248,8 @@ hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float 
     case TYPE_Q5_1: k_dequant<TYPE_Q5_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q8_0: k_dequant<TYPE_Q8_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q8_1: k_dequant<TYPE_Q8_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q2_K: k_dequant<TYPE_Q2_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+    case TYPE_Q3_K: k_dequant<TYPE_Q3_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q4_K: k_dequant<TYPE_Q4_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q5_K: k_dequant<TYPE_Q5_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
     case TYPE_Q6_K: k_dequant<TYPE_Q6_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;

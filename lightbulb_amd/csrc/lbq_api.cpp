@@ -181,7 +181,7 @@ int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m
 }
 
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
-    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14)", type);
     const int bs = lbq_type_block_size(type);
     if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
@@ -229,7 +229,8 @@ int lbq_type_block_size(uint32_t t) {
     switch (t) {
     case LBQ_TYPE_Q4_0: case LBQ_TYPE_Q4_1: case LBQ_TYPE_Q5_0: case LBQ_TYPE_Q5_1: case LBQ_TYPE_Q8_0: case LBQ_TYPE_Q8_1:
         return 32;
-    case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K: return 256;
+    case LBQ_TYPE_Q2_K: case LBQ_TYPE_Q3_K: case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K:
+        return 256;
     default: return 0;
     }
 }
@@ -242,6 +243,8 @@ int lbq_type_size(uint32_t t) {
     case LBQ_TYPE_Q5_1: return 24;
     case LBQ_TYPE_Q8_0: return 34;
     case LBQ_TYPE_Q8_1: return 36;
+    case LBQ_TYPE_Q2_K: return 84;
+    case LBQ_TYPE_Q3_K: return 110;
     case LBQ_TYPE_Q4_K: return 144;
     case LBQ_TYPE_Q5_K: return 176;
     case LBQ_TYPE_Q6_K: return 210;
@@ -356,7 +359,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
         return LBQ_OK;
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::is_kquant(w->type) && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
+    if (m > 8 && lbq::has_mfma_gemm(w->type) && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
         // batched: the operand pre-pass quantises x itself
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), "GEMM workspace");
         if (s) return s;
@@ -412,7 +415,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::is_kquant(w0->type)) {
+    if (m > 8 && lbq::has_mfma_gemm(w0->type)) {
         // batched: one operand pre-pass (quantising x itself when it can) shared
         // by every weight's GEMM
         size_t wsb = 0;
@@ -689,7 +692,8 @@ int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, 
 
 int lbq_quantize_weights_f32(uint32_t type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream) {
     if (!d_w || !d_out_blocks) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_quantize_weights_f32");
-    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
+    if (!weight_type_ok(type) || type == LBQ_TYPE_Q2_K || type == LBQ_TYPE_Q3_K)
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "no weight quantiser for ggml type %u", type);
     const int bs = lbq_type_block_size(type);
     if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);
     if ((reinterpret_cast<uintptr_t>(d_w) & 3u) || (reinterpret_cast<uintptr_t>(d_out_blocks) & 3u))

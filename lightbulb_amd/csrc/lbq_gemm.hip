@@ -750,7 +750,7 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
 }  // namespace
 
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
-    if (!is_kquant(type)) return 0;
+    if (!has_mfma_gemm(type)) return 0;
     return ws_layout(plan_for(type, n, k, m), n, k, m).total;
 }
 
@@ -759,7 +759,7 @@ bool gemm_prepass_fuses_quant(int64_t k, const float *x) {
 }
 
 hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st) {
-    if (!ws || !is_kquant(type)) return hipErrorInvalidValue;
+    if (!ws || !has_mfma_gemm(type)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, 1, k, m);  // the operand rows do not depend on n
     const WsLayout L = ws_layout(p, 1, k, m);
     uint8_t *base = static_cast<uint8_t *>(ws);
@@ -776,7 +776,7 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
 
 hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int64_t m, float *y, void *ws,
                      hipStream_t st) {
-    if (!ws || !is_kquant(type)) return hipErrorInvalidValue;
+    if (!ws || !has_mfma_gemm(type)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, n, k, m);
     const WsLayout L = ws_layout(p, n, k, m);
     uint8_t *base = static_cast<uint8_t *>(ws);
@@ -799,14 +799,13 @@ hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t r
 
 hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                        const float *x, int64_t m, float *y, void *ws, hipStream_t st) {
-    if (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K) {
+    if (has_mfma_gemm(type)) {
         hipError_t e = gemm_prepass(type, k, act, x, m, ws, st);
         if (e != hipSuccess) return e;
         return gemm_main(type, w, n, k, row_bytes, m, y, ws, st);
     }
-    if (x) return hipErrorInvalidValue;  // 32-value types take quantised activations
-    // Q8_0 and the legacy types (activation scale every 32 values): the decode
-    // GEMV over row chunks of 8
+    if (x) return hipErrorInvalidValue;  // the GEMV over row chunks takes quantised activations
+    // Q8_0, the legacy types, Q2_K and Q3_K: the decode GEMV over row chunks of 8
     for (int64_t m0 = 0; m0 < m; m0 += 8) {
         const int mc = (int)(m - m0 < 8 ? m - m0 : 8);
         ActView a = act;

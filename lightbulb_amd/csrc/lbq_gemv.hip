@@ -9,6 +9,8 @@ hipError_t gemv_q6k(const RowMap &, int64_t, int64_t, const ActView &, const flo
 hipError_t gemv_q8_0(const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float, hipStream_t);
 hipError_t gemv_legacy(int, const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float,
                        hipStream_t);
+hipError_t gemv_k23(int, const RowMap &, int64_t, int64_t, const ActView &, const float *, int, int, const float *, float,
+                    hipStream_t);
 
 bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     (void)n;
@@ -54,6 +56,7 @@ static hipError_t dispatch(int type, const RowMap &rm, int64_t k, int64_t row_by
     case TYPE_Q8_0: return gemv_q8_0(rm, k, row_bytes, act, x, m, map, alpha, eps, st);
     case TYPE_Q4_0: case TYPE_Q4_1: case TYPE_Q5_0: case TYPE_Q5_1:
         return gemv_legacy(type, rm, k, row_bytes, act, x, m, map, alpha, eps, st);
+    case TYPE_Q2_K: case TYPE_Q3_K: return gemv_k23(type, rm, k, row_bytes, act, x, m, map, alpha, eps, st);
     default: return hipErrorInvalidValue;
     }
 }

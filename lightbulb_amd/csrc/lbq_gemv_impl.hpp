@@ -240,6 +240,122 @@ struct Dec<TYPE_Q8_0> {
     }
 };
 
+// ---- Q2_K / Q3_K: piece p (0..3) = qs[16p .. 16p+16) (h = p/2, t = p%2).  Its
+// byte i holds the 2-bit codes of values 128h + 32s + 16t + i for s = 0..3 (bits
+// 2s), sub-block j = 8h + 2s + t.  Codes go through sdot4 unsigned (Q2_K 0..3,
+// Q3_K 0..7 with the hmask bit as bit 2); Q3_K's -4 offset is restored with the
+// Q8_K block sums, sum (u-4)*x = sum u*x - 4*bsum_j.
+//   Q2_K (candle vec_dot): d_x*d*sum_j sc_j*(q.x)_j - d_x*dmin*sum_j m_j*bsum_j
+//   Q3_K (ggml generic): d*d_x * sum_j (scale_j - 32)*(q.x)_j
+template <>
+struct Dec<TYPE_Q2_K> {
+    static constexpr int BYTES = 84, PPB = 4, VALS = 256;
+    struct Raw { uint32_t qs[4], sc0, sc1, dd; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        const int h = p >> 1;
+        Raw r;
+        const u32x4a4 q = *reinterpret_cast<const u32x4a4 *>(blk + 16 + 16 * p);
+        r.qs[0] = q.x; r.qs[1] = q.y; r.qs[2] = q.z; r.qs[3] = q.w;
+        r.sc0 = ld_u32(blk + 8 * h);  // scale bytes 8h .. 8h+7 (j = 8h + 2s + t)
+        r.sc1 = ld_u32(blk + 8 * h + 4);
+        r.dd = ld_u32(blk + 80);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int p, const ActView &a, int mrows, float *acc) {
+        const int h = p >> 1, t = p & 1;
+        const float d = h2f(r.dd & 0xffffu), dmin = h2f(r.dd >> 16);
+        int sc[4], mn[4];
+        uint32_t v[4][4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const uint32_t byte = ((s < 2 ? r.sc0 : r.sc1) >> (8 * ((2 * s + t) & 3))) & 0xffu;
+            sc[s] = (int)(byte & 0xFu);
+            mn[s] = (int)(byte >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[s][i] = (r.qs[i] >> (2 * s)) & 0x03030303u;
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK_K + 128 * h + 16 * t;
+                const int64_t sb = (int64_t)m * a.nb + b;
+                const uint4 bs = *reinterpret_cast<const uint4 *>(a.xbs + sb * 16 + 8 * h);
+                const uint32_t bsw[4] = {bs.x, bs.y, bs.z, bs.w};
+                int isum = 0, summs = 0;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + 32 * s);
+                    int q = dot4(v[s][0], xv.x, 0);
+                    q = dot4(v[s][1], xv.y, q);
+                    q = dot4(v[s][2], xv.z, q);
+                    q = dot4(v[s][3], xv.w, q);
+                    isum += sc[s] * q;
+                    summs += mn[s] * (int)(int16_t)(bsw[s] >> (16 * t));
+                }
+                const float dx = a.xd[sb];
+                acc[m] += (dx * d) * (float)isum - (dx * dmin) * (float)summs;
+            }
+        }
+    }
+};
+
+// Q3_K blocks are 110 bytes (2-byte aligned).  The 14-byte tail (scales[12], d)
+// is read as the 16 bytes from block byte 94, so no dword past the block is read.
+template <>
+struct Dec<TYPE_Q3_K> {
+    static constexpr int BYTES = 110, PPB = 4, VALS = 256;
+    struct Raw { uint32_t hm[4], qs[4], tl[4]; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        Raw r;
+        ld16_a2(blk + 16 * (p & 1), r.hm);  // hmask[16t .. 16t+16)
+        ld16_a2(blk + 32 + 16 * p, r.qs);
+        ld16_a2(blk + 94, r.tl);
+        return r;
+    }
+    template <int M>
+    __device__ static void dot(const Raw &r, int64_t b, int p, const ActView &a, int mrows, float *acc) {
+        const int h = p >> 1, t = p & 1;
+        // scales bytes 0..3, 4..7, 8..11 and d (bytes 14, 15 of the tail)
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(r.tl[1], r.tl[0], 2);
+        const uint32_t s1 = __builtin_amdgcn_alignbyte(r.tl[2], r.tl[1], 2);
+        const uint32_t s2 = __builtin_amdgcn_alignbyte(r.tl[3], r.tl[2], 2);
+        const float d = h2f(r.tl[3] >> 16);
+        int sc[4];
+        uint32_t v[4][4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int jm = 2 * s + t;  // j % 8 for j = 8h + 2s + t
+            const int lo = (int)(((jm < 4 ? s0 : s1) >> (8 * (jm & 3) + 4 * h)) & 0xFu);
+            const int hi = (int)((s2 >> (8 * (jm & 3) + 2 * (2 * h + (jm >> 2)))) & 3u);
+            sc[s] = (lo | (hi << 4)) - 32;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[s][i] = ((r.qs[i] >> (2 * s)) & 0x03030303u) | (((r.hm[i] >> (4 * h + s)) & 0x01010101u) << 2);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (m < mrows) {
+                const int8_t *xr = a.xq + m * a.k + b * QK_K + 128 * h + 16 * t;
+                const int64_t sb = (int64_t)m * a.nb + b;
+                const uint4 bs = *reinterpret_cast<const uint4 *>(a.xbs + sb * 16 + 8 * h);
+                const uint32_t bsw[4] = {bs.x, bs.y, bs.z, bs.w};
+                int isum = 0;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + 32 * s);
+                    int q = dot4(v[s][0], xv.x, 0);
+                    q = dot4(v[s][1], xv.y, q);
+                    q = dot4(v[s][2], xv.z, q);
+                    q = dot4(v[s][3], xv.w, q);
+                    isum += sc[s] * (q - 4 * (int)(int16_t)(bsw[s] >> (16 * t)));
+                }
+                acc[m] += (d * a.xd[sb]) * (float)isum;
+            }
+        }
+    }
+};
+
 // ---- 32-value legacy blocks (Q4_0, Q4_1, Q5_0, Q5_1): piece = one block.  Value
 // j (j < 16) is the low nibble of qs[j], value j + 16 its high nibble; Q5_* take
 // bit 4 of value v from bit v of the u32 qh.  Fields: d f16 | (m f16) | (qh u32) |
@@ -640,7 +756,7 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.row_bytes = row_bytes;
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
-    if constexpr (!is_legacy(TYPE)) {
+    if constexpr (has_mfma_gemm(TYPE) || TYPE == TYPE_Q8_0) {  // the types with a Fast<> decoder
         if (m == 1) {
             const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
             if (e != hipErrorNotSupported) return e;

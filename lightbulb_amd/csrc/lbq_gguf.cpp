@@ -243,13 +243,19 @@ const Meta *meta_of(const lbq_gguf *g, const char *key) {
 }
 
 // extract_tensor_bytes: the tensor's exact extent, bounds-checked
-int tensor_span(const lbq_gguf *g, const char *name, const Tensor **t_out, uint64_t *start, uint64_t *nbytes) {
+// The tensor's byte extent as extract_tensor_bytes computes it: ceil(numel / bs) *
+// type_size from the GgmlDType table.  With `blocks`, type_size is instead the size
+// of the block the kernels read (lbq_type_size): the two differ for Q2_K only,
+// whose table entry (82) is shorter than its 84-byte block.
+int tensor_span(const lbq_gguf *g, const char *name, const Tensor **t_out, uint64_t *start, uint64_t *nbytes,
+                bool blocks_layout = false) {
     auto it = g->tensor_at.find(name);
     if (it == g->tensor_at.end()) return gfail(LBQ_ERR_NOT_FOUND, "Tensor not found: %s", name);
     const Tensor &t = g->tensors[it->second];
     uint64_t bs, ts;
     ggml_layout(t.type, &bs, &ts);
     if (!bs) return gfail(LBQ_ERR_UNSUPPORTED_TYPE, "Unknown quantization type: %u", t.type);
+    if (blocks_layout && lbq_type_size(t.type) > 0) ts = (uint64_t)lbq_type_size(t.type);
     uint64_t numel = 1;
     for (uint64_t d : t.dims) {
         if (d && numel > UINT64_MAX / d) return gfail(LBQ_ERR_FORMAT, "tensor '%s' is too large", name);
@@ -472,7 +478,7 @@ int lbq_gguf_copy_tensor(const lbq_gguf *g, const char *name, void *d_dst, size_
     if (!g || !name || !d_dst) return gfail(LBQ_ERR_INVALID_ARG, "null argument to lbq_gguf_copy_tensor");
     const Tensor *t;
     uint64_t st, sz;
-    int s = tensor_span(g, name, &t, &st, &sz);
+    int s = tensor_span(g, name, &t, &st, &sz, true);
     if (s) return s;
     if (dst_bytes < sz)
         return gfail(LBQ_ERR_SHAPE, "destination holds %zu bytes, tensor %s needs %llu", dst_bytes, name, (unsigned long long)sz);
@@ -484,7 +490,7 @@ int lbq_weight_from_gguf(lbq_ctx *ctx, const lbq_gguf *g, const char *name, lbq_
     *out_w = nullptr;
     const Tensor *t;
     uint64_t st, sz;
-    int s = tensor_span(g, name, &t, &st, &sz);
+    int s = tensor_span(g, name, &t, &st, &sz, true);
     if (s) return s;
     if (t->dims.size() != 2)
         return gfail(LBQ_ERR_SHAPE, "tensor %s has %zu dimensions; a weight has 2 (ne0 = k, ne1 = n)", name, t->dims.size());

@@ -8,12 +8,17 @@ namespace lbq {
 
 enum : int {
     TYPE_Q4_0 = 2, TYPE_Q4_1 = 3, TYPE_Q5_0 = 6, TYPE_Q5_1 = 7, TYPE_Q8_0 = 8, TYPE_Q8_1 = 9,
-    TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15
+    TYPE_Q2_K = 10, TYPE_Q3_K = 11, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15
 };
 
 // 32-value weight blocks that pair with Q8_0 / Q8_1 activations.
 constexpr bool is_legacy(int t) { return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1; }
-constexpr bool is_kquant(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K; }
+// 256-value weight blocks that pair with Q8_K activations.
+constexpr bool is_kquant(int t) {
+    return t == TYPE_Q2_K || t == TYPE_Q3_K || t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K;
+}
+// weight types the MFMA GEMM serves at m > 8 (the others run the GEMV over row chunks)
+constexpr bool has_mfma_gemm(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K; }
 // activation type of QMatMul's vec_dot for a weight type (candle GgmlType::VecDotType)
 constexpr int vec_dot_type(int t) {
     return is_kquant(t) ? TYPE_Q8_K : (t == TYPE_Q4_1 || t == TYPE_Q5_1) ? TYPE_Q8_1 : TYPE_Q8_0;

@@ -105,12 +105,14 @@ class Content:
             raise ValueError(f"Tensor '{name}' not found in GGUF file")
         if len(info.dimensions) != 2:
             raise ValueError(f"tensor {name} has {len(info.dimensions)} dimensions, a weight has 2")
-        nbytes = self.get_tensor_data(name).size
+        dt = GgmlDType(info.tensor_type)
+        numel = int(np.prod(info.dimensions, dtype=np.uint64))
+        nbytes = -(-numel // dt.block_size()) * dt.block_bytes()  # the blocks lbq_gguf_copy_tensor copies
         data = torch.empty(nbytes, dtype=torch.uint8, device=device)
         if nbytes:
             _lib.check(_lib.lib().lbq_gguf_copy_tensor(self._h, name.encode(), data.data_ptr(), nbytes))
         k, n = info.dimensions
-        return QTensor(data, GgmlDType(info.tensor_type), (n, k))
+        return QTensor(data, dt, (n, k))
 
     def close(self):
         h = getattr(self, "_h", None)

@@ -66,6 +66,12 @@ class GgmlDType(IntEnum):
             GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292,
         }[self]
 
+    def block_bytes(self) -> int:
+        """Bytes of one block as the kernels (and candle) lay it out.  Equal to
+        ``type_size`` except for Q2_K: the reference's table gives 82, the block
+        (scales[16], qs[64], d, dmin) is 84."""
+        return 84 if self == GgmlDType.Q2K else self.type_size()
+
     def type_name(self) -> str:
         """Human-readable name as the reference prints it (``GgmlDType::name``)."""
         return {
@@ -75,8 +81,11 @@ class GgmlDType(IntEnum):
 
 
 #: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE
-SERVED = (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q4K,
-          GgmlDType.Q5K, GgmlDType.Q6K)
+SERVED = (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q2K,
+          GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+
+#: weight types quantize_tensor can produce (no Q2_K / Q3_K quantiser)
+QUANTIZABLE = tuple(t for t in SERVED if t not in (GgmlDType.Q2K, GgmlDType.Q3K))
 
 #: activation-only block types (the vec-dot partners)
 ACT_TYPES = (GgmlDType.Q8_0, GgmlDType.Q8_1, GgmlDType.Q8K)
@@ -86,7 +95,7 @@ def vec_dot_type(dtype: GgmlDType) -> GgmlDType:
     """The activation block type QMatMul::forward quantises x to for a weight type
     (candle GgmlType::VecDotType): Q8_K for k-quants, Q8_1 for Q4_1/Q5_1, else Q8_0."""
     dtype = GgmlDType(dtype)
-    if dtype in (GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K):
+    if dtype in (GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K):
         return GgmlDType.Q8K
     if dtype in (GgmlDType.Q4_1, GgmlDType.Q5_1):
         return GgmlDType.Q8_1
@@ -139,7 +148,7 @@ class QTensor:
             raise ValueError("QTensor data must be a contiguous 1-D uint8 tensor")
         if k % dtype.block_size():
             raise ValueError(f"{dtype.type_name()}: k = {k} is not a multiple of {dtype.block_size()}")
-        need = n * (k // dtype.block_size()) * dtype.type_size()
+        need = n * (k // dtype.block_size()) * dtype.block_bytes()
         if data.numel() != need:
             raise ValueError(f"{dtype.type_name()}: {data.numel()} bytes for shape ({n}, {k}), expected {need}")
         self.data = data
@@ -467,7 +476,7 @@ def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> 
     dtype = GgmlDType(dtype)
     if dtype not in SERVED and dtype not in ACT_TYPES:
         raise ValueError(f"Dequantization for {dtype.name} not yet implemented")
-    bs, ts = dtype.block_size(), dtype.type_size()
+    bs, ts = dtype.block_size(), dtype.block_bytes()
     num_blocks = (elem_count + bs - 1) // bs
     expected = num_blocks * ts
     if data.numel() < expected:
@@ -483,7 +492,7 @@ def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> 
 def quantize_tensor(data: torch.Tensor, dtype: GgmlDType, _exact: bool = False) -> torch.Tensor:
     """f32 device values -> GGUF blocks (uint8); the last block is zero-padded."""
     dtype = GgmlDType(dtype)
-    if dtype not in SERVED:
+    if dtype not in QUANTIZABLE:
         raise ValueError(f"Quantization for {dtype.name} not yet implemented")
     if data.dtype != torch.float32:
         raise ValueError("quantize_tensor expects f32 values")
@@ -497,7 +506,7 @@ def quantize_tensor(data: torch.Tensor, dtype: GgmlDType, _exact: bool = False) 
         padded[:flat.numel()] = flat
         flat = padded
     flat = flat.contiguous()
-    out = torch.empty(num_blocks * dtype.type_size(), dtype=torch.uint8, device=flat.device)
+    out = torch.empty(num_blocks * dtype.block_bytes(), dtype=torch.uint8, device=flat.device)
     if num_blocks:
         _lib.check(_lib.lib().lbq_quantize_weights_f32(int(dtype), flat.data_ptr(), flat.numel(), out.data_ptr(),
                                                        _stream(flat.device)))

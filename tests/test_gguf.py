@@ -76,6 +76,20 @@ def test_header_metadata_tensors(tmp_path):
             c.meta_int("missing")
 
 
+def test_q2k_extent_follows_the_reference_table(tmp_path):
+    # extract_tensor_bytes sizes a Q2_K tensor with GgmlDType::type_size = 82
+    # (quantization/mod.rs:118); the block itself is 84 bytes, which is what
+    # lbq_gguf_copy_tensor and the weight upload take
+    from lightbulb_amd.gguf import Content
+    from lightbulb_amd.quantized import GgmlDType
+    rng = np.random.default_rng(3)
+    q2 = rng.integers(0, 256, 4 * 84, dtype=np.uint8).tobytes()  # 2 rows x 512
+    blob, _, _ = gw.build(KVS, [("w2", [512, 2], 10, q2)])
+    with Content.read(write(tmp_path, blob)) as c:
+        assert c.get_tensor_data("w2").tobytes() == q2[:4 * 82]
+    assert GgmlDType.Q2K.type_size() == 82 and GgmlDType.Q2K.block_bytes() == 84
+
+
 def test_alignment_rule(tmp_path):
     # parser.rs:374-380: align(0)=0, align(1)=32, align(31)=32, align(32)=32,
     # align(33)=64 -- here as header ends at 64 + r for r in 0, 1, 31, 32, 33

@@ -1,5 +1,6 @@
-"""GPU parity for the 32-value legacy weight types (Q4_0, Q4_1, Q5_0, Q5_1) and
-their Q8_0 / Q8_1 activations, through the C ABI, against the CPU oracle.
+"""GPU parity for the remaining GGUF block types -- the 32-value legacy weights
+(Q4_0, Q4_1, Q5_0, Q5_1) with their Q8_0 / Q8_1 activations, and Q2_K / Q3_K
+with Q8_K activations -- through the C ABI, against the CPU oracle.
 
 Bars as for the other types: dequantisation, activation and weight
 quantisation bit-exact; QMatMul::forward per-row relative L2 <= 2e-3 and max
@@ -17,7 +18,7 @@ from test_gpu_parity import _special_rows, assert_rows_close, gpu_qmatmul, gpu_q
 
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 = 2, 3, 6, 7, 8, 9
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K = 2, 3, 6, 7, 8, 9, 10, 11
 LEGACY = [Q4_0, Q4_1, Q5_0, Q5_1]
 
 
@@ -125,3 +126,54 @@ def test_legacy_activation_type_mismatch(oracle, lbq, dev):
     act = QActivation(Q8_0, 1, 64, dev).quantize(to_dev(rng.standard_normal((1, 64)).astype(np.float32), dev))
     with pytest.raises(_lib.LbqError, match="needs activation type 9"):
         qm.forward_quantized(act)
+
+
+# ---------------------------------------------------------------- Q2_K / Q3_K
+@pytest.mark.parametrize("t", [Q2_K, Q3_K])
+def test_k23_dequant_bit_exact(oracle, lbq, dev, t):
+    from lightbulb_amd.quantized import dequantize_tensor
+    rng = np.random.default_rng(370 + t)
+    nb = 333  # odd: 110-byte Q3_K blocks alternate between 4-aligned and 2 mod 4
+    raw = bp.random_blocks(rng, t, nb, d_scale=0.5)
+    got = dequantize_tensor(to_dev(raw, dev), t, nb * 256).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), oracle.dequantize(t, raw).view(np.uint32))
+
+
+K23_SHAPES = [(48, 256), (100, 512), (257, 256 * 5), (1024, 1024)]
+
+
+@pytest.mark.parametrize("t", [Q2_K, Q3_K])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 17])
+def test_k23_qmatmul(oracle, lbq, dev, t, m):
+    rng = np.random.default_rng(1000 * t + m + 9)
+    for n, k in K23_SHAPES:
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-2)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+        assert_rows_close(gpu_qmatmul(t, w_raw, n, k, x, dev), ref)
+
+
+@pytest.mark.parametrize("t", [Q2_K, Q3_K])
+def test_k23_llama_rows(oracle, lbq, dev, t):
+    # Llama-3 row lengths, x with outliers, ragged n; the activation handle gives
+    # the same bits as forward()
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    rng = np.random.default_rng(380 + t)
+    for n, k in ((300, 4096), (77, 14336)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+        for m in (1, 4, 12):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            x[rng.random(x.shape) < 0.01] *= 20
+            xd = to_dev(x, dev)
+            y = qm.forward(xd)
+            y2 = qm.forward_quantized(QActivation.for_weight(qm, m).quantize(xd))
+            torch.cuda.synchronize()
+            assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64))
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+
+
+def test_k23_has_no_weight_quantiser(lbq, dev):
+    from lightbulb_amd.quantized import quantize_tensor
+    with pytest.raises(ValueError, match="Quantization for Q2K not yet implemented"):
+        quantize_tensor(torch.zeros(256, device=dev), Q2_K)

@@ -326,7 +326,7 @@ def test_gguf_to_qmatmul(oracle, lbq, dev, tmp_path):
     from lightbulb_amd.quantized import QMatMul, context
     rng = np.random.default_rng(150)
     w = {t: (bp.random_blocks(rng, t, n * k // oracle.block_size(t)), n, k)
-         for t, n, k in ((Q4_K, 300, 512), (Q6_K, 64, 1024), (Q8_0, 33, 256), (2, 41, 96), (7, 17, 160))}
+         for t, n, k in ((Q4_K, 300, 512), (Q6_K, 64, 1024), (Q8_0, 33, 256), (2, 41, 96), (7, 17, 160), (10, 23, 512), (11, 19, 512))}
     tensors = [("token_norm", [512], 0, rng.standard_normal(512).astype(np.float32).tobytes())]
     tensors += [(f"blk.0.w{t}", [k, n], t, raw.tobytes()) for t, (raw, n, k) in w.items()]
     blob, _, _ = gw.build([("general.architecture", gw.STR, "llama"), ("general.alignment", gw.U32, 64)], tensors,
@@ -477,7 +477,7 @@ def test_c_abi_error_paths(lbq, dev):
     ctx = context(dev)
     h = ctypes.c_void_p()
     buf = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
-    assert lbq.lbq_weight_wrap_device(ctx, 10, 4, 256, buf.data_ptr(), 84 * 4, ctypes.byref(h)) == -2  # Q2_K
+    assert lbq.lbq_weight_wrap_device(ctx, 1, 4, 256, buf.data_ptr(), 2 * 4 * 256, ctypes.byref(h)) == -2  # F16
     assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 255, buf.data_ptr(), buf.numel(), ctypes.byref(h)) == -3
     assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 256, buf.data_ptr(), buf.numel() - 1, ctypes.byref(h)) == -3
     assert lbq.lbq_weight_wrap_device(ctx, Q4_K, 4, 256, buf.data_ptr() + 4, 144 * 4, ctypes.byref(h)) == -1
