@@ -54,6 +54,8 @@ enum lbq_status {
 
 /* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
 enum lbq_ggml_type {
+    LBQ_TYPE_F32 = 0,  /* dense; dequantisation (a copy) only */
+    LBQ_TYPE_F16 = 1,  /* dense; dequantisation (exact widening) only */
     LBQ_TYPE_Q4_0 = 2, /* 32-value blocks, Q8_0 activations */
     LBQ_TYPE_Q4_1 = 3, /* 32-value blocks, Q8_1 activations */
     LBQ_TYPE_Q5_0 = 6, /* 32-value blocks, Q8_0 activations */
@@ -168,10 +170,21 @@ int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *act, f
 int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream);
 
 /* Dequantise nelem values of raw device blocks -- dequantize_tensor
- * (/root/reference/src/quantization/mod.rs:158-247), extended to Q5_K/Q6_K/Q8_K and
- * the remaining 32-value types (Q4_1, Q5_0, Q5_1, Q8_1).
+ * (/root/reference/src/quantization/mod.rs:158-247), extended to every block type
+ * above, and F32 / F16 tensors (QTensor::dequantize of the norm weights,
+ * custom_transformer_block.rs:229-231, which GGUF files store as F32).
  * nelem must be a multiple of the block size. */
 int lbq_dequantize_blocks_f32(uint32_t ggml_type, const void *d_blocks, int64_t nelem, float *d_y, void *stream);
+
+/* Embedding lookup without the dense table: d_out[i][:] = row d_ids[i] of the
+ * dequantised weight (f32 [count][k], bit-exact with QTensor::dequantize followed
+ * by Embedding::forward's index_select -- custom_transformer.rs:321-323, the
+ * token embedding, which the reference dequantises whole at load).  d_ids holds
+ * count int32 ids; an id outside [0, n) yields a row of NaN (the reference's
+ * index_select raises; the device cannot, so the row is poisoned instead).
+ * k must be a multiple of 16; d_out 16-byte aligned. */
+int lbq_embedding_f32(lbq_ctx *ctx, const lbq_weight *w, const int32_t *d_ids, int64_t count, float *d_out,
+                      void *stream);
 
 /* Quantise activations x[m][k] to GGUF blocks of `act_type` (LBQ_TYPE_Q8_K:
  * 292-byte blocks; LBQ_TYPE_Q8_0: 34-byte blocks; LBQ_TYPE_Q8_1: 36-byte

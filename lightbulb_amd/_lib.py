@@ -50,6 +50,7 @@ SIGNATURES = {
     "lbq_qmatmul_act_f32": (_c.c_int, [_VP, _VP, _VP, _VP, _VP]),
     "lbq_dequantize_f32": (_c.c_int, [_VP, _VP, _VP, _VP]),
     "lbq_dequantize_blocks_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
+    "lbq_embedding_f32": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
     "lbq_quantize_act": (_c.c_int, [_U32, _VP, _I64, _I64, _VP, _VP]),
     "lbq_quantize_weights_f32": (_c.c_int, [_U32, _VP, _I64, _VP, _VP]),
     "lbq_gguf_open": (_c.c_int, [_c.c_char_p, _c.POINTER(_VP)]),

@@ -184,22 +184,59 @@ __device__ __forceinline__ void deq_group(const uint8_t *__restrict__ b, int g, 
 }
 
 template <int TYPE>
+constexpr int type_bs() { return TYPE == TYPE_Q8_0 || TYPE == TYPE_Q8_1 || is_legacy(TYPE) ? 32 : 256; }
+template <int TYPE>
+constexpr int type_ts() {
+    return TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q4_1 ? 20 : TYPE == TYPE_Q5_0 ? 22 : TYPE == TYPE_Q5_1 ? 24
+         : TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q8_1 ? 36 : TYPE == TYPE_Q2_K ? 84 : TYPE == TYPE_Q3_K ? 110
+         : TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 292;
+}
+
+__device__ __forceinline__ void store16(float *dst, const float out[16]) {
+    float4 *d4 = reinterpret_cast<float4 *>(dst);
+    for (int i = 0; i < 4; i++) d4[i] = make_float4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+}
+
+template <int TYPE>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ blocks, int64_t ngroups,
                                                  float *__restrict__ y) {
-    constexpr int BS = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q8_1 || is_legacy(TYPE) ? 32 : 256;
-    constexpr int TS = TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q4_1 ? 20 : TYPE == TYPE_Q5_0 ? 22 : TYPE == TYPE_Q5_1 ? 24
-                     : TYPE == TYPE_Q8_0 ? 34 : TYPE == TYPE_Q8_1 ? 36 : TYPE == TYPE_Q2_K ? 84
-                     : TYPE == TYPE_Q3_K ? 110 : TYPE == TYPE_Q4_K ? 144
-                     : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 292;
-    constexpr int GPB = BS / 16;
+    constexpr int GPB = type_bs<TYPE>() / 16;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= ngroups) return;
     const int64_t blk = t / GPB;
     const int g = (int)(t % GPB);
     float out[16];
-    deq_group<TYPE>(blocks + blk * TS, g, out);
-    float4 *dst = reinterpret_cast<float4 *>(y + t * 16);
-    for (int i = 0; i < 4; i++) dst[i] = make_float4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+    deq_group<TYPE>(blocks + blk * type_ts<TYPE>(), g, out);
+    store16(y + t * 16, out);
+}
+
+// Embedding rows: thread t handles group g = t % gpr (16 values) of output row
+// i = t / gpr, read from weight row ids[i].
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_embed_rows(const uint8_t *__restrict__ w, int64_t n, int64_t row_bytes,
+                                                    const int32_t *__restrict__ ids, int64_t count, int64_t gpr,
+                                                    float *__restrict__ y) {
+    constexpr int GPB = type_bs<TYPE>() / 16;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= count * gpr) return;
+    const int64_t i = t / gpr, g = t % gpr;
+    const int64_t id = ids[i];
+    float out[16];
+    if (id < 0 || id >= n) {
+        for (int j = 0; j < 16; j++) out[j] = __int_as_float(0x7fc00000);
+    } else {
+        deq_group<TYPE>(w + id * row_bytes + (g / GPB) * type_ts<TYPE>(), (int)(g % GPB), out);
+    }
+    store16(y + t * 16, out);
+}
+
+// F32 / F16 tensors: y[i] = x[i] (bits) / the exact f16 -> f32 widening
+template <bool F16>
+__global__ __launch_bounds__(256) void k_dense_f32(const uint8_t *__restrict__ x, int64_t n, float *__restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    if constexpr (F16) y[i] = h2f(reinterpret_cast<const unsigned short *>(x)[i]);
+    else y[i] = reinterpret_cast<const float *>(x)[i];
 }
 
 #pragma clang fp contract(on)
@@ -238,22 +275,38 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
     return hipGetLastError();
 }
 
+#define LBQ_BLOCK_TYPES(X) \
+    X(TYPE_Q4_0) X(TYPE_Q4_1) X(TYPE_Q5_0) X(TYPE_Q5_1) X(TYPE_Q8_0) X(TYPE_Q8_1) X(TYPE_Q2_K) X(TYPE_Q3_K) \
+    X(TYPE_Q4_K) X(TYPE_Q5_K) X(TYPE_Q6_K) X(TYPE_Q8_K)
+
 hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st) {
+    if (type == TYPE_F32 || type == TYPE_F16) {
+        const dim3 grid((unsigned)((nelem + 255) / 256));
+        if (type == TYPE_F16) k_dense_f32<true><<<grid, 256, 0, st>>>(blocks, nelem, y);
+        else k_dense_f32<false><<<grid, 256, 0, st>>>(blocks, nelem, y);
+        return hipGetLastError();
+    }
     const int64_t ng = nelem / 16;
     const dim3 grid((unsigned)((ng + 255) / 256));
     switch (type) {
-    case TYPE_Q4_0: k_dequant<TYPE_Q4_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q4_1: k_dequant<TYPE_Q4_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q5_0: k_dequant<TYPE_Q5_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q5_1: k_dequant<TYPE_Q5_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q8_0: k_dequant<TYPE_Q8_0><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q8_1: k_dequant<TYPE_Q8_1><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q2_K: k_dequant<TYPE_Q2_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q3_K: k_dequant<TYPE_Q3_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q4_K: k_dequant<TYPE_Q4_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q5_K: k_dequant<TYPE_Q5_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q6_K: k_dequant<TYPE_Q6_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
-    case TYPE_Q8_K: k_dequant<TYPE_Q8_K><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+#define LBQ_DEQ(T) \
+    case T: k_dequant<T><<<grid, 256, 0, st>>>(blocks, ng, y); break;
+        LBQ_BLOCK_TYPES(LBQ_DEQ)
+#undef LBQ_DEQ
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const int32_t *ids,
+                            int64_t count, float *y, hipStream_t st) {
+    const int64_t gpr = k / 16;
+    const dim3 grid((unsigned)((count * gpr + 255) / 256));
+    switch (type) {
+#define LBQ_EMB(T) \
+    case T: k_embed_rows<T><<<grid, 256, 0, st>>>(w, n, row_bytes, ids, count, gpr, y); break;
+        LBQ_BLOCK_TYPES(LBQ_EMB)
+#undef LBQ_EMB
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

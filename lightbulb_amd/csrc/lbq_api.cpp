@@ -227,6 +227,7 @@ const char *lbq_last_error(void) { return g_err.c_str(); }
 
 int lbq_type_block_size(uint32_t t) {
     switch (t) {
+    case LBQ_TYPE_F32: case LBQ_TYPE_F16: return 1;
     case LBQ_TYPE_Q4_0: case LBQ_TYPE_Q4_1: case LBQ_TYPE_Q5_0: case LBQ_TYPE_Q5_1: case LBQ_TYPE_Q8_0: case LBQ_TYPE_Q8_1:
         return 32;
     case LBQ_TYPE_Q2_K: case LBQ_TYPE_Q3_K: case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K:
@@ -237,6 +238,8 @@ int lbq_type_block_size(uint32_t t) {
 
 int lbq_type_size(uint32_t t) {
     switch (t) {
+    case LBQ_TYPE_F32: return 4;
+    case LBQ_TYPE_F16: return 2;
     case LBQ_TYPE_Q4_0: return 18;
     case LBQ_TYPE_Q4_1: return 20;
     case LBQ_TYPE_Q5_0: return 22;
@@ -663,7 +666,8 @@ int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stre
 
 int lbq_dequantize_blocks_f32(uint32_t type, const void *d_blocks, int64_t nelem, float *d_y, void *stream) {
     if (!d_blocks || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_dequantize_blocks_f32");
-    if (!weight_type_ok(type) && !act_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
+    if (!weight_type_ok(type) && !act_type_ok(type) && type != LBQ_TYPE_F32 && type != LBQ_TYPE_F16)
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served", type);
     const int bs = lbq_type_block_size(type);
     if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);
     if ((reinterpret_cast<uintptr_t>(d_blocks) & 3u) || (reinterpret_cast<uintptr_t>(d_y) & 15u))
@@ -673,6 +677,23 @@ int lbq_dequantize_blocks_f32(uint32_t type, const void *d_blocks, int64_t nelem
                                        static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
     return LBQ_OK;
+}
+
+int lbq_embedding_f32(lbq_ctx *ctx, const lbq_weight *w, const int32_t *d_ids, int64_t count, float *d_out,
+                      void *stream) {
+    if (!ctx || !w) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_embedding_f32");
+    if (count < 0) return fail(LBQ_ERR_INVALID_ARG, "count = %lld is negative", (long long)count);
+    if (w->k % 16) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of 16", (long long)w->k);
+    if (count == 0) return LBQ_OK;
+    if (!d_ids || !d_out) return fail(LBQ_ERR_INVALID_ARG, "null ids or output pointer");
+    if ((reinterpret_cast<uintptr_t>(d_ids) & 3u) || (reinterpret_cast<uintptr_t>(d_out) & 15u))
+        return fail(LBQ_ERR_INVALID_ARG, "ids must be 4-byte and the output 16-byte aligned");
+    if (count > ((int64_t)1 << 40) / w->k) return fail(LBQ_ERR_LIMIT, "count = %lld exceeds the supported maximum", (long long)count);
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = lbq::launch_embedding(w->type, w->d_blocks, w->n, w->k, w->row_bytes, d_ids, count, d_out,
+                                         static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? LBQ_OK : hip_fail(e, "embedding launch");
 }
 
 int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, void *d_out_blocks, void *stream) {

@@ -7,6 +7,7 @@
 namespace lbq {
 
 enum : int {
+    TYPE_F32 = 0, TYPE_F16 = 1,
     TYPE_Q4_0 = 2, TYPE_Q4_1 = 3, TYPE_Q5_0 = 6, TYPE_Q5_1 = 7, TYPE_Q8_0 = 8, TYPE_Q8_1 = 9,
     TYPE_Q2_K = 10, TYPE_Q3_K = 11, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15
 };
@@ -47,8 +48,14 @@ RowMap single_row_map(const uint8_t *w, int64_t n, float *y);
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
                             int16_t *xbs, float *xs, uint8_t *gguf, hipStream_t st);
 
-// Dequantise nelem values (multiple of the block size) of `type` blocks to f32.
+// Dequantise nelem values (multiple of the block size) of `type` blocks to f32
+// (F32 / F16: any nelem, a copy / an exact widening).
 hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st);
+
+// y[i][:] = the dequantised row ids[i] of an [n][k] weight (rows row_bytes apart),
+// i < count; an id outside [0, n) gives a row of NaN.  k is a multiple of 16.
+hipError_t launch_embedding(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const int32_t *ids,
+                            int64_t count, float *y, hipStream_t st);
 
 // y[m][n] += nothing: y is overwritten.  Weight rows are row_bytes apart.
 // Requires m <= 8 (decode GEMV) -- the kernels keep one accumulator per row of x.

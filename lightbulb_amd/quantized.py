@@ -437,6 +437,30 @@ class QActivation:
 
 
 # ---------------------------------------------------------------------------
+# token embedding straight from the quantized table
+# ---------------------------------------------------------------------------
+class QEmbedding:
+    """``Embedding::new(qtensor.dequantize(), hidden)`` then ``forward(ids)``
+    (/root/reference/src/model/custom_transformer.rs:321-323) without the dense
+    table: each call dequantises only the rows it gathers, bit-identical to
+    index_select on the dequantised weight.  Ids outside [0, n) give NaN rows."""
+
+    def __init__(self, qtensor: QTensor):
+        self._qmatmul = QMatMul.from_qtensor(qtensor)
+        self.num_embeddings, self.hidden_size = qtensor.shape()
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        dev = self._qmatmul.qtensor().data.device
+        flat = ids.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+        out = torch.empty(flat.numel(), self.hidden_size, dtype=torch.float32, device=dev)
+        _lib.check(_lib.lib().lbq_embedding_f32(context(dev), self._qmatmul._handle, flat.data_ptr(), flat.numel(),
+                                                out.data_ptr(), _stream(dev)))
+        return out.reshape(*ids.shape, self.hidden_size)
+
+    __call__ = forward
+
+
+# ---------------------------------------------------------------------------
 # QuantizableLinear (src/model/quantizable_linear.rs)
 # ---------------------------------------------------------------------------
 class QuantizableLinear:
@@ -474,7 +498,7 @@ def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> 
     """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off.
     Errors name the type as the reference's ``{:?}`` does (the variant: ``Q4K``)."""
     dtype = GgmlDType(dtype)
-    if dtype not in SERVED and dtype not in ACT_TYPES:
+    if dtype not in SERVED and dtype not in ACT_TYPES and dtype not in (GgmlDType.F32, GgmlDType.F16):
         raise ValueError(f"Dequantization for {dtype.name} not yet implemented")
     bs, ts = dtype.block_size(), dtype.block_bytes()
     num_blocks = (elem_count + bs - 1) // bs

@@ -24,11 +24,10 @@ def test_every_declared_symbol_is_exported_and_bound(lbq):
 
 def test_type_table_matches_reference(lbq):
     # GgmlDType::block_size / type_size, /root/reference/src/quantization/mod.rs:99-126
-    for t, bs, ts in [(2, 32, 18), (3, 32, 20), (6, 32, 22), (7, 32, 24), (8, 32, 34), (9, 32, 36),
+    for t, bs, ts in [(0, 1, 4), (1, 1, 2), (2, 32, 18), (3, 32, 20), (6, 32, 22), (7, 32, 24), (8, 32, 34), (9, 32, 36),
                       (10, 256, 84), (11, 256, 110), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 292)]:
         assert lbq.lbq_type_block_size(t) == bs and lbq.lbq_type_size(t) == ts
-    # F32 and F16 are not block types of this path
-    for t in (0, 1, 16, 999):
+    for t in (4, 5, 16, 999):
         assert lbq.lbq_type_block_size(t) == 0 and lbq.lbq_type_size(t) == 0
 
 
@@ -38,7 +37,8 @@ def test_argument_errors_without_device(lbq):
     assert lbq.lbq_quantize_act(12, dummy, 1, 256, dummy, None) == -2
     assert lbq.lbq_quantize_act(15, dummy, 1, 255, dummy, None) == -3
     assert lbq.lbq_quantize_act(15, None, 1, 256, dummy, None) == -1
-    assert lbq.lbq_dequantize_blocks_f32(1, dummy, 256, dummy, None) == -2
+    assert lbq.lbq_dequantize_blocks_f32(4, dummy, 256, dummy, None) == -2
+    assert lbq.lbq_embedding_f32(None, None, dummy, 1, dummy, None) == -1
     assert lbq.lbq_dequantize_blocks_f32(11, dummy, 300, dummy, None) == -3
     assert lbq.lbq_quantize_weights_f32(10, dummy, 256, dummy, None) == -2  # no Q2_K quantiser
     assert lbq.lbq_dequantize_blocks_f32(2, dummy, 48, dummy, None) == -3

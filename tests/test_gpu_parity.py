@@ -87,6 +87,40 @@ def test_dequant_q8k_and_truncation(oracle, lbq, dev):
         dequantize_tensor(to_dev(raw[:200], dev), Q4_K, 512)
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0, 2, 7, 11])
+def test_embedding_rows_bit_exact(oracle, lbq, dev, t):
+    # QEmbedding gathers dequantised rows without the dense table: equal to the
+    # oracle's dequantised rows (repeats, first/last row, odd row starts), NaN
+    # rows for ids outside [0, n)
+    from lightbulb_amd.quantized import QEmbedding, QTensor
+    rng = np.random.default_rng(160 + t)
+    n, k = 333, 512 if t != 7 else 160
+    raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=0.5)
+    dense = oracle.dequantize(t, raw).reshape(n, k)
+    emb = QEmbedding(QTensor(to_dev(raw, dev), t, (n, k)))
+    ids = np.array([[0, 5, 5, 332], [17, 1, 200, 0]], dtype=np.int64)
+    got = emb.forward(torch.from_numpy(ids).to(dev)).cpu().numpy()
+    assert got.shape == (2, 4, k)
+    assert np.array_equal(got.view(np.uint32), dense[ids].view(np.uint32))
+    bad = emb.forward(torch.tensor([3, -1, 333, 4], device=dev)).cpu().numpy()
+    assert np.isnan(bad[1]).all() and np.isnan(bad[2]).all()
+    assert np.array_equal(bad[[0, 3]], dense[[3, 4]])
+    assert emb.forward(torch.zeros(0, dtype=torch.int32, device=dev)).shape == (0, k)
+
+
+def test_dense_f32_f16_dequantize(lbq, dev):
+    # norm weights are stored as F32 (a copy) or F16 (an exact widening)
+    from lightbulb_amd.quantized import dequantize_tensor
+    rng = np.random.default_rng(170)
+    h = rng.standard_normal(4099).astype(np.float16)
+    h[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    got = dequantize_tensor(to_dev(h.view(np.uint8), dev), 1, h.size).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), h.astype(np.float32).view(np.uint32))
+    f = rng.standard_normal(1001).astype(np.float32)
+    got = dequantize_tensor(to_dev(f.view(np.uint8), dev), 0, f.size).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), f.view(np.uint32))
+
+
 # ---------------------------------------------------------------- activation quantisation
 def _special_rows(k: int) -> np.ndarray:
     rows = np.zeros((7, k), dtype=np.float32)
