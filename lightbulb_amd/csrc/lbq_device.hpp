@@ -29,6 +29,11 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// quad_perm broadcast with every lane active (no old value to preserve)
+template <int CTRL>
+__device__ __forceinline__ uint32_t qperm(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
 // every lane of each 16-lane row gets the row's max / min / sum
 __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
     v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]

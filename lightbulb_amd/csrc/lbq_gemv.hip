@@ -20,12 +20,12 @@ bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     // quantisation launch (4096 x 14336 Q4_K: fused 10.3 us, quantise + GEMV 11.7).
     if (getenv("LBQ_GEMV1_NOFUSE")) return false;  // tuning switch: always quantise separately
     const int nb = (int)(k / (type == TYPE_Q8_0 ? QK8_0 : QK_K));
-    int rpw, it;
+    int ppb, rpw, it;
     switch (type) {
-    case TYPE_Q4_K: return fast_shape<TYPE_Q4_K>(nb, &rpw, &it);
-    case TYPE_Q5_K: return fast_shape<TYPE_Q5_K>(nb, &rpw, &it);
-    case TYPE_Q6_K: return fast_shape<TYPE_Q6_K>(nb, &rpw, &it);
-    case TYPE_Q8_0: return fast_shape<TYPE_Q8_0>(nb, &rpw, &it);
+    case TYPE_Q4_K: return fast_shape<TYPE_Q4_K>(nb, &ppb, &rpw, &it);
+    case TYPE_Q5_K: return fast_shape<TYPE_Q5_K>(nb, &ppb, &rpw, &it);
+    case TYPE_Q6_K: return fast_shape<TYPE_Q6_K>(nb, &ppb, &rpw, &it);
+    case TYPE_Q8_0: return fast_shape<TYPE_Q8_0>(nb, &ppb, &rpw, &it);
     default: return false;
     }
 }

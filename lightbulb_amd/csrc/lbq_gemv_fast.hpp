@@ -76,7 +76,7 @@ constexpr int XS_0 = 48;
 // per-type register traits.  A piece is the unit a lane decodes (see the
 // general GEMV); XW is the number of activation dwords a lane keeps per block.
 // ---------------------------------------------------------------------------
-template <int TYPE>
+template <int TYPE, int PPB>
 struct Fast;
 
 __device__ __forceinline__ uint32_t pack_halves(uint32_t lo_word, uint32_t hi_word, int h) {
@@ -84,16 +84,91 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t lo_word, uint32_t hi_wo
     return a | (b << 16);
 }
 
+// Q4_K / Q5_K: piece p (0..3) of a block is its 32-byte qs chunk c = p: the low
+// nibbles of qs[32c + l] are values 64c + l (sub-block 2c), the high nibbles values
+// 64c + 32 + l (sub-block 2c + 1), l < 32.  The four lanes of a block form a DPP
+// quad; lane p loads header dword p and the quad shares the four through quad
+// broadcasts.  Sixty-four weights per lane and piece keep the per-piece work (header
+// broadcast, scale unpack, float combine) to one instance per two sub-blocks.
+template <int TYPE>
+struct FastK45 {  // Q4_K and Q5_K
+    static constexpr int PPB = 4, VALS = 256, XW = 19;
+    static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
+    static constexpr int NBUF = 3;  // three-buffer ring allowed (see k_gemv1)
+    struct Raw { uint32_t hw; uint4 qh0, qh1, qs0, qs1; };
+    __device__ static Raw load(const uint8_t *blk, int p) {
+        Raw r;
+        r.hw = *reinterpret_cast<const uint32_t *>(blk + 4 * p);
+        if (TYPE == TYPE_Q5_K) {
+            r.qh0 = ld_u4(blk + 16);
+            r.qh1 = ld_u4(blk + 32);
+        }
+        const uint8_t *qs = blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 32 * p;
+        r.qs0 = ld_u4(qs);
+        r.qs1 = ld_u4(qs + 16);
+        return r;
+    }
+    // activation registers for piece p: codes 64p .. 64p + 63 (xr[0..15]), the
+    // bsums of its four 16-value runs (xr[16], xr[17]) and the block's d (xr[18])
+    __device__ static void xload_lds(const uint8_t *xb, int p, uint32_t *xr) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(xb + 64 * p + 16 * j);
+            xr[4 * j] = a.x; xr[4 * j + 1] = a.y; xr[4 * j + 2] = a.z; xr[4 * j + 3] = a.w;
+        }
+        const uint2 s = *reinterpret_cast<const uint2 *>(xb + 256 + 8 * p);
+        xr[16] = s.x;
+        xr[17] = s.y;
+        xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
+    }
+    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+        // Header dword i sits in lane i of every quad.  The 6-bit scales and mins of
+        // sub-blocks 2p, 2p + 1 (get_scale_min_k4): for p < 2, sc = scales[j] & 63 and
+        // m = scales[j + 4] & 63 (bytes 2p, 2p + 1 of dwords 1 and 2); for p >= 2,
+        // sc = (scales[j + 4] & 15) | (scales[j - 4] >> 6) << 4 and
+        // m = (scales[j + 4] >> 4) | (scales[j] >> 6) << 4 (dword 3 with the top bits
+        // of dwords 1 and 2).  X and Y deliver dword 1 / 2 to lanes 0, 1 of the quad
+        // and dword 3 to lanes 2, 3; shifts and masks depend on p only.
+        const uint32_t h0 = qperm<0x00>(r.hw), s0 = qperm<0x55>(r.hw), s1 = qperm<0xAA>(r.hw);
+        const uint32_t X = qperm<0xF5>(r.hw), Y = qperm<0xFA>(r.hw);
+        const bool upper = p >= 2;
+        const uint32_t bsh = 16u * (uint32_t)(p & 1);
+        const uint32_t MA = upper ? 0x0f0fu : 0x3f3fu, MB = upper ? 0x3030u : 0u;
+        const uint32_t sc2 = ((X >> bsh) & MA) | ((s0 >> (bsh + 2)) & MB);
+        const uint32_t m2 = ((Y >> (bsh + (upper ? 4u : 0u))) & MA) | ((s1 >> (bsh + 2)) & MB);
+        const uint32_t q[8] = {r.qs0.x, r.qs0.y, r.qs0.z, r.qs0.w, r.qs1.x, r.qs1.y, r.qs1.z, r.qs1.w};
+        int sl = 0, sh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            if (TYPE == TYPE_Q5_K) {
+                const uint32_t qh = i < 4 ? (i == 0 ? r.qh0.x : i == 1 ? r.qh0.y : i == 2 ? r.qh0.z : r.qh0.w)
+                                          : (i == 4 ? r.qh1.x : i == 5 ? r.qh1.y : i == 6 ? r.qh1.z : r.qh1.w);
+                lo |= ((qh >> (2 * p)) & 0x01010101u) << 4;
+                hi |= ((qh >> (2 * p + 1)) & 0x01010101u) << 4;
+            }
+            sl = dot4(lo, xr[i], sl);
+            sh = dot4(hi, xr[8 + i], sh);
+        }
+        // bsums of the two sub-blocks: runs (4p, 4p + 1) and (4p + 2, 4p + 3)
+        const int bl = (int)(int16_t)(xr[16] & 0xffffu) + ((int)xr[16] >> 16);
+        const int bh = (int)(int16_t)(xr[17] & 0xffffu) + ((int)xr[17] >> 16);
+        const int isum = __mul24((int)(sc2 & 0xffu), sl) + __mul24((int)(sc2 >> 8), sh);
+        const int msum = __mul24((int)(m2 & 0xffu), bl) + __mul24((int)(m2 >> 8), bh);
+        const float dx = __uint_as_float(xr[18]);
+        return (h2f(h0 & 0xffffu) * dx) * (float)isum - (h2f(h0 >> 16) * dx) * (float)msum;
+    }
+};
 // Q4_K / Q5_K: piece p (0..7) of a block is qs bytes 16p..16p+15, i.e. values
 // 64c + 16h + [0,16) (low nibbles) and 64c + 32 + 16h + [0,16) (high) with c = p/2,
 // h = p%2.  The eight lanes of a block each load one dword of its 16-byte header
 // (dword p%4) and share the four through DPP quad broadcasts, instead of each
 // holding the whole header.
 template <int TYPE>
-struct FastK45 {  // Q4_K and Q5_K
+struct FastK45T {  // Q4_K and Q5_K, eight lanes per block
     static constexpr int PPB = 8, VALS = 256, XW = 10;
     static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
-    static constexpr int NBUF = 3;  // three-buffer ring allowed (see k_gemv1)
+    static constexpr int NBUF = 3;
     struct Raw { uint32_t hw; uint4 qh, qs; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         Raw r;
@@ -113,23 +188,11 @@ struct FastK45 {  // Q4_K and Q5_K
         xr[8] = pack_halves(s.x, s.y, h);
         xr[9] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
-    // ... or from the split global layout (pre-quantised activations)
-    __device__ static void xload_glb(const ActView &a, int64_t blk, int p, uint32_t *xr) {
-        const int c = p >> 1, h = p & 1;
-        const int8_t *q = a.xq + blk * 256;
-        const uint4 u = *reinterpret_cast<const uint4 *>(q + 64 * c + 16 * h);
-        const uint4 v = *reinterpret_cast<const uint4 *>(q + 64 * c + 32 + 16 * h);
-        const uint2 s = *reinterpret_cast<const uint2 *>(a.xbs + blk * 16 + 4 * c);
-        xr[0] = u.x; xr[1] = u.y; xr[2] = u.z; xr[3] = u.w;
-        xr[4] = v.x; xr[5] = v.y; xr[6] = v.z; xr[7] = v.w;
-        xr[8] = pack_halves(s.x, s.y, h);
-        xr[9] = __float_as_uint(a.xd[blk]);
-    }
     __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
         const int c = p >> 1;
         // header dword i sits in lane i of every quad (quad_perm [i,i,i,i])
-        const uint32_t h0 = dpp_u32<0x00>(r.hw), s0 = dpp_u32<0x55>(r.hw);
-        const uint32_t s1 = dpp_u32<0xAA>(r.hw), s2 = dpp_u32<0xFF>(r.hw);
+        const uint32_t h0 = qperm<0x00>(r.hw), s0 = qperm<0x55>(r.hw);
+        const uint32_t s1 = qperm<0xAA>(r.hw), s2 = qperm<0xFF>(r.hw);
         uint32_t sc2, m2;
         k4_scale_pair(s0, s1, s2, c, &sc2, &m2);
         const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
@@ -163,12 +226,14 @@ struct FastK45 {  // Q4_K and Q5_K
         return (h2f(h0 & 0xffffu) * dx) * (float)isum - (h2f(h0 >> 16) * dx) * (float)msum;
     }
 };
-template <> struct Fast<TYPE_Q4_K> : FastK45<TYPE_Q4_K> {};
-template <> struct Fast<TYPE_Q5_K> : FastK45<TYPE_Q5_K> {};
+template <> struct Fast<TYPE_Q4_K, 4> : FastK45<TYPE_Q4_K> {};
+template <> struct Fast<TYPE_Q5_K, 4> : FastK45<TYPE_Q5_K> {};
+template <> struct Fast<TYPE_Q4_K, 8> : FastK45T<TYPE_Q4_K> {};
+template <> struct Fast<TYPE_Q5_K, 8> : FastK45T<TYPE_Q5_K> {};
 
 // Q6_K piece p = (n, h) covers runs 128n+16h+32j (j < 4) with int8 scales 8n+h+2j.
 template <>
-struct Fast<TYPE_Q6_K> {
+struct Fast<TYPE_Q6_K, 4> {
     static constexpr int PPB = 4, VALS = 256, XW = 19, BYTES = 210;
     static constexpr int NBUF = 2;
     struct Raw { uint32_t qa[4], qb[4], qh[4], s0, s1, dbits; };
@@ -196,19 +261,6 @@ struct Fast<TYPE_Q6_K> {
         xr[17] = pack_halves(s.z, s.w, h);
         xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
-    __device__ static void xload_glb(const ActView &a, int64_t blk, int p, uint32_t *xr) {
-        const int n = p >> 1, h = p & 1;
-        const int8_t *q = a.xq + blk * 256;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint4 u = *reinterpret_cast<const uint4 *>(q + 128 * n + 16 * h + 32 * j);
-            xr[4 * j] = u.x; xr[4 * j + 1] = u.y; xr[4 * j + 2] = u.z; xr[4 * j + 3] = u.w;
-        }
-        const uint4 s = *reinterpret_cast<const uint4 *>(a.xbs + blk * 16 + 8 * n);
-        xr[16] = pack_halves(s.x, s.y, h);
-        xr[17] = pack_halves(s.z, s.w, h);
-        xr[18] = __float_as_uint(a.xd[blk]);
-    }
     __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
         const int h = p & 1;
         const int sh = 8 * h;
@@ -235,7 +287,7 @@ struct Fast<TYPE_Q6_K> {
 
 // Q8_0: one 34-byte block (32 values) per piece.
 template <>
-struct Fast<TYPE_Q8_0> {
+struct Fast<TYPE_Q8_0, 1> {
     static constexpr int PPB = 1, VALS = 32, XW = 9, BYTES = 34;
     static constexpr int NBUF = 2;
     struct Raw { uint32_t w[9]; uint32_t mis; };
@@ -257,14 +309,6 @@ struct Fast<TYPE_Q8_0> {
         xr[0] = a.x; xr[1] = a.y; xr[2] = a.z; xr[3] = a.w;
         xr[4] = b.x; xr[5] = b.y; xr[6] = b.z; xr[7] = b.w;
         xr[8] = *reinterpret_cast<const uint32_t *>(xb + 32);
-    }
-    __device__ static void xload_glb(const ActView &a, int64_t blk, int, uint32_t *xr) {
-        const int8_t *q = a.xq + blk * 32;
-        const uint4 u = *reinterpret_cast<const uint4 *>(q);
-        const uint4 v = *reinterpret_cast<const uint4 *>(q + 16);
-        xr[0] = u.x; xr[1] = u.y; xr[2] = u.z; xr[3] = u.w;
-        xr[4] = v.x; xr[5] = v.y; xr[6] = v.z; xr[7] = v.w;
-        xr[8] = __float_as_uint(a.xd[blk]);
     }
     __device__ static float dot(const Raw &r, int, const uint32_t *xr) {
         const bool odd = r.mis != 0;
@@ -488,7 +532,7 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
-template <int TYPE, int RPW, int IT, bool FUSED, int MAP, bool NORM = false>
+template <int TYPE, int PPB, int RPW, int IT, bool FUSED, int MAP, bool NORM = false>
 __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                ActView act, const float *__restrict__ alpha, float eps) {
     static_assert(!NORM || (FUSED && TYPE != TYPE_Q8_0), "the RMS norm runs in the quantising prologue");
@@ -502,14 +546,14 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     // silu pairs: up row i is (w1 - w0) past gate row i (arithmetic, not a select
     // between fields, which the compiler would turn into an indexed copy)
     const uint64_t wdiff = rs.w1 - rs.w0;
-    using F = Fast<TYPE>;
+    using F = Fast<TYPE, PPB>;
     using Raw = typename F::Raw;
     constexpr int LPR = 64 / RPW;
     constexpr int BPI = LPR / F::PPB;
     static_assert(BPI >= 1, "a row needs at least one whole block per sweep");
-    // row maps: the wave index as a scalar, so row-group indices (and row lookups) are scalar
-    const int lane = threadIdx.x & 63,
-              wave = MAP != MAP_ONE ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
+    // the wave index as a scalar, so row-group indices, row addresses and row-map
+    // lookups run on the scalar unit
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane / LPR, li = lane % LPR;
     const int p = li % F::PPB, bs0 = li / F::PPB;
     // silu pairs are never split between waves: ranges are counted in pairs
@@ -554,11 +598,12 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
         } else {
             wr = W + min(g * RPW + r, n - 1) * row_bytes;
         }
+        // blocks of sweeps before the last are in range (the host launches the
+        // smallest IT with nb <= BPI * IT); only the last sweep's block is clamped
+        const uint8_t *lb = wr + bs0 * F::BYTES;
 #pragma unroll
-        for (int i = 0; i < IT; i++) {
-            const int b = min(bs0 + BPI * i, nb - 1);
-            buf[i] = F::load(wr + (int64_t)b * F::BYTES, p);
-        }
+        for (int i = 0; i < IT - 1; i++) buf[i] = F::load(lb + i * BPI * F::BYTES, p);
+        buf[IT - 1] = F::load(wr + (int64_t)min(bs0 + BPI * (IT - 1), nb - 1) * F::BYTES, p);
     };
 
     // group indices are clamped into the wave's range (a wave without groups
@@ -585,15 +630,29 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     if constexpr (FUSED) quantise_x_lds<TYPE, NORM>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE>(act, nb, sx, issue_ring);
 
+    // A lane decodes the same piece slots in every row, so when they fit its
+    // activation registers are read from LDS once and kept for the whole row loop.
+    constexpr bool XREG = IT * F::XW <= 80;
+    uint32_t xk[XREG ? IT : 1][F::XW];
+    if constexpr (XREG) {
+#pragma unroll
+        for (int i = 0; i < IT; i++) F::xload_lds(sx + min(bs0 + BPI * i, nb - 1) * XS, p, xk[i]);
+    }
+
     float pend = 0.f;  // silu pairs: the gate sum waiting for its up sum (wave-uniform)
     auto compute_group = [&](int64_t g, const Raw *buf, bool store) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < IT; i++) {
             const int b = bs0 + BPI * i;
-            uint32_t xr[F::XW];
-            F::xload_lds(sx + min(b, nb - 1) * XS, p, xr);
-            const float v = F::dot(buf[i], p, xr);
+            float v;
+            if constexpr (XREG) {
+                v = F::dot(buf[i], p, xk[i]);
+            } else {
+                uint32_t xr[F::XW];
+                F::xload_lds(sx + min(b, nb - 1) * XS, p, xr);
+                v = F::dot(buf[i], p, xr);
+            }
             acc += b < nb ? v : 0.f;
         }
         acc = row_sum_f32(acc);

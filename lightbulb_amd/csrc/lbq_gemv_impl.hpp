@@ -645,43 +645,43 @@ static hipError_t run_m(const GemvCfg &c, const uint8_t *w, const PGeom &g, cons
 // ---------------------------------------------------------------------------
 // m = 1: the register-activation kernel (lbq_gemv_fast.hpp)
 // ---------------------------------------------------------------------------
+// Launch shape of the m = 1 kernel for nb blocks per row: lanes per block (ppb:
+// 4 = 64-weight pieces, 8 = 32-weight pieces for Q4_K / Q5_K), rows per wave
+// group and sweeps.  Measured on Q4_K at Llama-3-8B shapes: 64-weight pieces with
+// one row per group for k = 4096; at k = 14336 (56 blocks) 32-weight pieces fill
+// seven sweeps of eight blocks exactly, where 64-weight pieces would leave an
+// eighth of the lanes idle.
 template <int TYPE>
-static bool fast_shape(int nb, int *rpw, int *it) {
-    constexpr int PPB = Fast<TYPE>::PPB;
-    if (const char *e = getenv("LBQ_GEMV1_CFG")) {  // tuning override "rpw,it"
-        int r = 0, i = 0;
-        if (sscanf(e, "%d,%d", &r, &i) == 2 && r >= 1 && i >= 1 && (64 / r / PPB) * i >= nb) {
-            *rpw = r; *it = i;
-            return true;
-        }
+static bool fast_shape(int nb, int *ppb, int *rpw, int *it) {
+    int q = 0, r = 0;
+    if (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
+        if (nb <= 4) { q = 4; r = 4; }
+        else if (nb <= 8) { q = 4; r = 2; }
+        else if (nb <= 64 && (nb > 56 || nb <= 48)) { q = 4; r = 1; }
+        else if (nb <= 56) { q = 8; r = 1; }
+    } else if (TYPE == TYPE_Q6_K) {
+        if (nb <= 16) { q = 4; r = 2; }
+        else if (nb <= 64) { q = 4; r = 1; }
+    } else if (nb <= 512) {  // Q8_0: nb counts 32-value blocks
+        q = 1; r = 1;
     }
-    if (PPB == 8) {  // Q4_K, Q5_K
-        if (nb <= 4) { *rpw = 2; *it = 1; return true; }
-        if (nb <= 8) { *rpw = 2; *it = 2; return true; }
-        if (nb <= 16) { *rpw = 1; *it = 2; return true; }
-        if (nb <= 32) { *rpw = 1; *it = 4; return true; }
-        if (nb <= 56) { *rpw = 1; *it = 7; return true; }
-        if (nb <= 64) { *rpw = 1; *it = 8; return true; }
-    } else if (PPB == 4) {  // Q6_K
-        if (nb <= 8) { *rpw = 2; *it = 1; return true; }
-        if (nb <= 16) { *rpw = 2; *it = 2; return true; }
-        if (nb <= 32) { *rpw = 1; *it = 2; return true; }
-        if (nb <= 64) { *rpw = 1; *it = 4; return true; }
-    } else {  // Q8_0: nb counts 32-value blocks
-        if (nb <= 64) { *rpw = 1; *it = 1; return true; }
-        if (nb <= 128) { *rpw = 1; *it = 2; return true; }
-        if (nb <= 256) { *rpw = 1; *it = 4; return true; }
-        if (nb <= 448) { *rpw = 1; *it = 7; return true; }
-        if (nb <= 512) { *rpw = 1; *it = 8; return true; }
-    }
-    return false;
+    if (const char *e = getenv("LBQ_GEMV1_CFG")) sscanf(e, "%d,%d", &q, &r);  // tuning override "ppb,rpw"
+    if (q <= 0 || r <= 0 || 64 % (q * r) != 0) return false;
+    const int bpi = 64 / (q * r);
+    *ppb = q;
+    *rpw = r;
+    *it = (nb + bpi - 1) / bpi;  // the smallest sweep count covering the row (the kernel relies on it)
+    return true;
 }
 
-template <int TYPE, int RPW, int IT>
+template <int TYPE, int PPB, int RPW, int IT>
 static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
                               const float *alpha, float eps, hipStream_t st) {
     const int64_t n = rm.n;
     const int64_t ng = (n + RPW - 1) / RPW;
+    // the kernel clamps only the last sweep's block: IT must be the smallest that covers nb
+    constexpr int BPI = 64 / RPW / PPB;
+    if (!(BPI * (IT - 1) < nb && nb <= BPI * IT)) return hipErrorNotSupported;
     // Waves per CU.  With the fused prologue every workgroup quantises all of x,
     // so for fewer rows (less weight per CU to hide it behind) one workgroup per
     // CU does better; measured on Q4_K: 4096 x 4096 5.3 us at 4 vs 5.8 at 8,
@@ -694,17 +694,17 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     const size_t lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
     // row maps take the fused quantisation only (the caller runs the rest weight by
     // weight); the RMS norm (alpha != nullptr) only k-quant row maps with k <= 8192
-    constexpr bool NORM_OK = TYPE != TYPE_Q8_0 && (64 / RPW / Fast<TYPE>::PPB) * IT <= 32;
+    constexpr bool NORM_OK = TYPE != TYPE_Q8_0 && BPI * IT <= 32;
     if (alpha && (!NORM_OK || nb > 32 || !x || map == MAP_ONE)) return hipErrorNotSupported;
     if (map == MAP_SILU_PAIRS) {
         if constexpr (RPW <= 2) {
             if (!x || (n & 1)) return hipErrorNotSupported;
             if constexpr (NORM_OK)
                 if (alpha) {
-                    k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                    k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
                     return hipGetLastError();
                 }
-            k_gemv1<TYPE, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+            k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
         } else {
             return hipErrorNotSupported;
         }
@@ -712,14 +712,14 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
         if (!x) return hipErrorNotSupported;
         if constexpr (NORM_OK)
             if (alpha) {
-                k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
                 return hipGetLastError();
             }
-        k_gemv1<TYPE, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else if (x) {
-        k_gemv1<TYPE, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else {
-        k_gemv1<TYPE, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     }
     return hipGetLastError();
 }
@@ -727,16 +727,18 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
 template <int TYPE>
 static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
                            const float *alpha, float eps, hipStream_t st) {
-    int rpw, it;
-    if (!fast_shape<TYPE>(nb, &rpw, &it)) return hipErrorNotSupported;
-#define LBQ_FAST(R, I) \
-    if (rpw == R && it == I) return launch_fast<TYPE, R, I>(rm, row_bytes, nb, x, act, map, alpha, eps, st);
-    if constexpr (Fast<TYPE>::PPB == 8) {
-        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(2, 4) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
-    } else if constexpr (Fast<TYPE>::PPB == 4) {
-        LBQ_FAST(2, 1) LBQ_FAST(2, 2) LBQ_FAST(1, 2) LBQ_FAST(1, 4)
+    int ppb, rpw, it;
+    if (!fast_shape<TYPE>(nb, &ppb, &rpw, &it)) return hipErrorNotSupported;
+#define LBQ_FAST(Q, R, I) \
+    if (ppb == Q && rpw == R && it == I) return launch_fast<TYPE, Q, R, I>(rm, row_bytes, nb, x, act, map, alpha, eps, st);
+    if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
+        LBQ_FAST(4, 4, 1) LBQ_FAST(4, 2, 1) LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
+        LBQ_FAST(8, 1, 7)
+    } else if constexpr (TYPE == TYPE_Q6_K) {
+        LBQ_FAST(4, 2, 1) LBQ_FAST(4, 2, 2) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
     } else {
-        LBQ_FAST(1, 1) LBQ_FAST(1, 2) LBQ_FAST(1, 4) LBQ_FAST(1, 7) LBQ_FAST(1, 8)
+        LBQ_FAST(1, 1, 1) LBQ_FAST(1, 1, 2) LBQ_FAST(1, 1, 3) LBQ_FAST(1, 1, 4) LBQ_FAST(1, 1, 5) LBQ_FAST(1, 1, 6)
+        LBQ_FAST(1, 1, 7) LBQ_FAST(1, 1, 8)
     }
 #undef LBQ_FAST
     return hipErrorNotSupported;
