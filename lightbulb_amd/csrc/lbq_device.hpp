@@ -143,15 +143,31 @@ __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { return *reinterpr
 
 __device__ __forceinline__ uint4 ld_u4(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
+// Weight blocks live in global memory.  Aligned dwords around a 2-byte aligned
+// field are addressed through an explicit global pointer built from the integer
+// address: a generic pointer rebuilt from an integer would make flat loads, and
+// rounding the pointer itself (__builtin_align_down) lets the compiler assume the
+// field is 4-byte aligned and merge neighbouring byte loads into the wrong dword.
+typedef const __attribute__((address_space(1))) uint8_t *gbytes_c;
+__device__ __forceinline__ gbytes_c align4_global(uintptr_t a) { return (gbytes_c)(a & ~(uintptr_t)3); }
+typedef uint32_t u32x4v4 __attribute__((ext_vector_type(4), aligned(4)));  // 16 bytes, 4-byte aligned
+__device__ __forceinline__ u32x4a4 gld16(gbytes_c p) {
+    const u32x4v4 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4v4 *>(p);
+    return u32x4a4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ uint32_t gld4(gbytes_c p) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t *>(p);
+}
+
 // 16 bytes starting at a 2-byte aligned address p.  Reads only aligned dwords that
 // hold at least one byte of [p, p+16), so it never touches a dword outside the
 // caller's buffer.
 __device__ __forceinline__ void ld16_a2(const uint8_t *p, uint32_t out[4]) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     const uint32_t mis = (uint32_t)(a & 3u);
-    const uint8_t *base = reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3);
-    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(base);
-    const uint32_t t = *reinterpret_cast<const uint32_t *>(base + (mis ? 16 : 12));
+    const gbytes_c base = align4_global(a);
+    const u32x4a4 v = gld16(base);
+    const uint32_t t = gld4(base + (mis ? 16 : 12));
     out[0] = __builtin_amdgcn_alignbyte(v.y, v.x, mis);
     out[1] = __builtin_amdgcn_alignbyte(v.z, v.y, mis);
     out[2] = __builtin_amdgcn_alignbyte(v.w, v.z, mis);
@@ -162,16 +178,16 @@ __device__ __forceinline__ void ld16_a2(const uint8_t *p, uint32_t out[4]) {
 __device__ __forceinline__ uint32_t ld4_a2(const uint8_t *p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     const uint32_t mis = (uint32_t)(a & 3u);
-    const uint8_t *base = reinterpret_cast<const uint8_t *>(a & ~(uintptr_t)3);
-    const uint32_t lo = *reinterpret_cast<const uint32_t *>(base);
-    const uint32_t hi = *reinterpret_cast<const uint32_t *>(base + (mis ? 4 : 0));
+    const gbytes_c base = align4_global(a);
+    const uint32_t lo = gld4(base);
+    const uint32_t hi = gld4(base + (mis ? 4 : 0));
     return __builtin_amdgcn_alignbyte(hi, lo, mis);
 }
 
 // 2 bytes (f16 bits) at a 2-byte aligned address.
 __device__ __forceinline__ uint32_t ld2_a2(const uint8_t *p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+    const uint32_t w = gld4(align4_global(a));
     return (a & 2u) ? (w >> 16) : (w & 0xffffu);
 }
 

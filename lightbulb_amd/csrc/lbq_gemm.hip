@@ -257,18 +257,17 @@ struct GB<TYPE_Q6_K> {
     static constexpr int NL = 12;
     struct Raw { u32x4a4 ql[4], qh[2]; uint32_t qlt, qht, sc[3], dw; };
     struct Prep { float d1[8], c1[8]; uint32_t l[16], qh[8]; };
-    __device__ static const uint8_t *al4(const uint8_t *p) {
-        return reinterpret_cast<const uint8_t *>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
-    }
+    // aligned dwords of the block's fields, through global pointers (align4_global)
+    __device__ static gbytes_c al4(const uint8_t *p) { return align4_global(reinterpret_cast<uintptr_t>(p)); }
     __device__ static void load_part(const uint8_t *blk, int h, Raw &r, int i) {
         const bool mis = (reinterpret_cast<uintptr_t>(blk) & 3u) != 0;
-        const uint8_t *ql = al4(blk + 64 * h), *qh = al4(blk + 128 + 32 * h), *sc = al4(blk + 192 + 8 * h);
-        if (i < 4) r.ql[i] = *reinterpret_cast<const u32x4a4 *>(ql + 16 * i);
-        else if (i < 6) r.qh[i - 4] = *reinterpret_cast<const u32x4a4 *>(qh + 16 * (i - 4));
-        else if (i == 6) r.qlt = *reinterpret_cast<const uint32_t *>(ql + (mis ? 64 : 60));
-        else if (i == 7) r.qht = *reinterpret_cast<const uint32_t *>(qh + (mis ? 32 : 28));
-        else if (i < 10) r.sc[i - 8] = *reinterpret_cast<const uint32_t *>(sc + 4 * (i - 8));
-        else if (i == 10) r.sc[2] = *reinterpret_cast<const uint32_t *>(sc + (mis ? 8 : 4));
+        const gbytes_c ql = al4(blk + 64 * h), qh = al4(blk + 128 + 32 * h), sc = al4(blk + 192 + 8 * h);
+        if (i < 4) r.ql[i] = gld16(ql + 16 * i);
+        else if (i < 6) r.qh[i - 4] = gld16(qh + 16 * (i - 4));
+        else if (i == 6) r.qlt = gld4(ql + (mis ? 64 : 60));
+        else if (i == 7) r.qht = gld4(qh + (mis ? 32 : 28));
+        else if (i < 10) r.sc[i - 8] = gld4(sc + 4 * (i - 8));
+        else if (i == 10) r.sc[2] = gld4(sc + (mis ? 8 : 4));
         else r.dw = ld2_a2(blk + 208);
     }
     // mis: byte misalignment of the block (0 or 2)

@@ -95,6 +95,7 @@ struct FastK45 {  // Q4_K and Q5_K
     static constexpr int PPB = 4, VALS = 256, XW = 19;
     static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
     static constexpr int NBUF = 3;  // three-buffer ring allowed (see k_gemv1)
+    static constexpr int RAW = TYPE == TYPE_Q4_K ? 9 : 17;  // registers a loaded piece occupies
     struct Raw { uint32_t hw; uint4 qh0, qh1, qs0, qs1; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         Raw r;
@@ -121,7 +122,11 @@ struct FastK45 {  // Q4_K and Q5_K
         xr[17] = s.y;
         xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
-    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+    // Piece p of one weight block against MR activation rows: the weight codes are
+    // unpacked once; xl(m, xr) fills row m's activation registers; valid masks the
+    // contribution of a clamped (duplicate) block.
+    template <int MR, class XL>
+    __device__ static void dotm(const Raw &r, int p, XL xl, float *acc, bool valid) {
         // Header dword i sits in lane i of every quad.  The 6-bit scales and mins of
         // sub-blocks 2p, 2p + 1 (get_scale_min_k4): for p < 2, sc = scales[j] & 63 and
         // m = scales[j + 4] & 63 (bytes 2p, 2p + 1 of dwords 1 and 2); for p >= 2,
@@ -137,26 +142,39 @@ struct FastK45 {  // Q4_K and Q5_K
         const uint32_t sc2 = ((X >> bsh) & MA) | ((s0 >> (bsh + 2)) & MB);
         const uint32_t m2 = ((Y >> (bsh + (upper ? 4u : 0u))) & MA) | ((s1 >> (bsh + 2)) & MB);
         const uint32_t q[8] = {r.qs0.x, r.qs0.y, r.qs0.z, r.qs0.w, r.qs1.x, r.qs1.y, r.qs1.z, r.qs1.w};
-        int sl = 0, sh = 0;
+        uint32_t lo[8], hi[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            uint32_t lo = q[i] & 0x0f0f0f0fu, hi = (q[i] >> 4) & 0x0f0f0f0fu;
+            lo[i] = q[i] & 0x0f0f0f0fu;
+            hi[i] = (q[i] >> 4) & 0x0f0f0f0fu;
             if (TYPE == TYPE_Q5_K) {
                 const uint32_t qh = i < 4 ? (i == 0 ? r.qh0.x : i == 1 ? r.qh0.y : i == 2 ? r.qh0.z : r.qh0.w)
                                           : (i == 4 ? r.qh1.x : i == 5 ? r.qh1.y : i == 6 ? r.qh1.z : r.qh1.w);
-                lo |= ((qh >> (2 * p)) & 0x01010101u) << 4;
-                hi |= ((qh >> (2 * p + 1)) & 0x01010101u) << 4;
+                lo[i] |= ((qh >> (2 * p)) & 0x01010101u) << 4;
+                hi[i] |= ((qh >> (2 * p + 1)) & 0x01010101u) << 4;
             }
-            sl = dot4(lo, xr[i], sl);
-            sh = dot4(hi, xr[8 + i], sh);
         }
-        // bsums of the two sub-blocks: runs (4p, 4p + 1) and (4p + 2, 4p + 3)
-        const int bl = (int)(int16_t)(xr[16] & 0xffffu) + ((int)xr[16] >> 16);
-        const int bh = (int)(int16_t)(xr[17] & 0xffffu) + ((int)xr[17] >> 16);
-        const int isum = __mul24((int)(sc2 & 0xffu), sl) + __mul24((int)(sc2 >> 8), sh);
-        const int msum = __mul24((int)(m2 & 0xffu), bl) + __mul24((int)(m2 >> 8), bh);
-        const float dx = __uint_as_float(xr[18]);
-        return (h2f(h0 & 0xffffu) * dx) * (float)isum - (h2f(h0 >> 16) * dx) * (float)msum;
+        const float dw = h2f(h0 & 0xffffu), dmw = h2f(h0 >> 16);
+        const int scl = (int)(sc2 & 0xffu), sch = (int)(sc2 >> 8), ml = (int)(m2 & 0xffu), mh = (int)(m2 >> 8);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            uint32_t xr[XW];
+            xl(m, xr);
+            int sl = 0, sh = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                sl = dot4(lo[i], xr[i], sl);
+                sh = dot4(hi[i], xr[8 + i], sh);
+            }
+            // bsums of the two sub-blocks: runs (4p, 4p + 1) and (4p + 2, 4p + 3)
+            const int bl = (int)(int16_t)(xr[16] & 0xffffu) + ((int)xr[16] >> 16);
+            const int bh = (int)(int16_t)(xr[17] & 0xffffu) + ((int)xr[17] >> 16);
+            const int isum = __mul24(scl, sl) + __mul24(sch, sh);
+            const int msum = __mul24(ml, bl) + __mul24(mh, bh);
+            const float dx = __uint_as_float(xr[18]);
+            const float v = (dw * dx) * (float)isum - (dmw * dx) * (float)msum;
+            acc[m] += valid ? v : 0.f;
+        }
     }
 };
 // Q4_K / Q5_K: piece p (0..7) of a block is qs bytes 16p..16p+15, i.e. values
@@ -169,6 +187,7 @@ struct FastK45T {  // Q4_K and Q5_K, eight lanes per block
     static constexpr int PPB = 8, VALS = 256, XW = 10;
     static constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
     static constexpr int NBUF = 3;
+    static constexpr int RAW = TYPE == TYPE_Q4_K ? 5 : 9;
     struct Raw { uint32_t hw; uint4 qh, qs; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         Raw r;
@@ -188,7 +207,8 @@ struct FastK45T {  // Q4_K and Q5_K, eight lanes per block
         xr[8] = pack_halves(s.x, s.y, h);
         xr[9] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
-    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+    template <int MR, class XL>
+    __device__ static void dotm(const Raw &r, int p, XL xl, float *acc, bool valid) {
         const int c = p >> 1;
         // header dword i sits in lane i of every quad (quad_perm [i,i,i,i])
         const uint32_t h0 = qperm<0x00>(r.hw), s0 = qperm<0x55>(r.hw);
@@ -211,19 +231,24 @@ struct FastK45T {  // Q4_K and Q5_K, eight lanes per block
                 hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
             }
         }
-        int sl = dot4(lo[0], xr[0], 0);
-        sl = dot4(lo[1], xr[1], sl);
-        sl = dot4(lo[2], xr[2], sl);
-        sl = dot4(lo[3], xr[3], sl);
-        int sh = dot4(hi[0], xr[4], 0);
-        sh = dot4(hi[1], xr[5], sh);
-        sh = dot4(hi[2], xr[6], sh);
-        sh = dot4(hi[3], xr[7], sh);
-        const int isum = __mul24((int)(sc2 & 0xffu), sl) + __mul24((int)(sc2 >> 8), sh);
-        const int msum = __mul24((int)(m2 & 0xffu), (int)(int16_t)(xr[8] & 0xffffu)) +
-                         __mul24((int)(m2 >> 8), (int)(int16_t)(xr[8] >> 16));
-        const float dx = __uint_as_float(xr[9]);
-        return (h2f(h0 & 0xffffu) * dx) * (float)isum - (h2f(h0 >> 16) * dx) * (float)msum;
+        const float dw = h2f(h0 & 0xffffu), dmw = h2f(h0 >> 16);
+        const int scl = (int)(sc2 & 0xffu), sch = (int)(sc2 >> 8), ml = (int)(m2 & 0xffu), mh = (int)(m2 >> 8);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            uint32_t xr[XW];
+            xl(m, xr);
+            int sl = 0, sh = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sl = dot4(lo[i], xr[i], sl);
+                sh = dot4(hi[i], xr[4 + i], sh);
+            }
+            const int isum = __mul24(scl, sl) + __mul24(sch, sh);
+            const int msum = __mul24(ml, (int)(int16_t)(xr[8] & 0xffffu)) + __mul24(mh, (int)(int16_t)(xr[8] >> 16));
+            const float dx = __uint_as_float(xr[9]);
+            const float v = (dw * dx) * (float)isum - (dmw * dx) * (float)msum;
+            acc[m] += valid ? v : 0.f;
+        }
     }
 };
 template <> struct Fast<TYPE_Q4_K, 4> : FastK45<TYPE_Q4_K> {};
@@ -235,7 +260,7 @@ template <> struct Fast<TYPE_Q5_K, 8> : FastK45T<TYPE_Q5_K> {};
 template <>
 struct Fast<TYPE_Q6_K, 4> {
     static constexpr int PPB = 4, VALS = 256, XW = 19, BYTES = 210;
-    static constexpr int NBUF = 2;
+    static constexpr int NBUF = 2, RAW = 15;
     struct Raw { uint32_t qa[4], qb[4], qh[4], s0, s1, dbits; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         const int n = p >> 1, h = p & 1;
@@ -261,27 +286,38 @@ struct Fast<TYPE_Q6_K, 4> {
         xr[17] = pack_halves(s.z, s.w, h);
         xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
-    __device__ static float dot(const Raw &r, int p, const uint32_t *xr) {
+    template <int MR, class XL>
+    __device__ static void dotm(const Raw &r, int p, XL xl, float *acc, bool valid) {
         const int h = p & 1;
         const int sh = 8 * h;
         const int sc[4] = {(int)(int8_t)(r.s0 >> sh), (int)(int8_t)(r.s0 >> (sh + 16)), (int)(int8_t)(r.s1 >> sh),
                            (int)(int8_t)(r.s1 >> (sh + 16))};
-        const int bs[4] = {(int)(int16_t)(xr[16] & 0xffffu), (int)(int16_t)(xr[16] >> 16),
-                           (int)(int16_t)(xr[17] & 0xffffu), (int)(int16_t)(xr[17] >> 16)};
-        int isum = 0;
+        uint32_t v[4][4];  // 6-bit codes (0..63) of run j, four per dword
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t *qs = (j & 1) ? r.qb : r.qa;
             const int shq = (j >> 1) * 4, shh = 2 * j;
-            int s = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t v = ((qs[i] >> shq) & 0x0f0f0f0fu) | (((r.qh[i] >> shh) & 0x03030303u) << 4);
-                s = dot4(v, xr[4 * j + i], s);
-            }
-            isum += sc[j] * (s - 32 * bs[j]);
+            for (int i = 0; i < 4; i++) v[j][i] = ((qs[i] >> shq) & 0x0f0f0f0fu) | (((r.qh[i] >> shh) & 0x03030303u) << 4);
         }
-        return (h2f(r.dbits) * __uint_as_float(xr[18])) * (float)isum;
+        const float dw = h2f(r.dbits);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            uint32_t xr[XW];
+            xl(m, xr);
+            const int bs[4] = {(int)(int16_t)(xr[16] & 0xffffu), (int)(int16_t)(xr[16] >> 16),
+                               (int)(int16_t)(xr[17] & 0xffffu), (int)(int16_t)(xr[17] >> 16)};
+            int isum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) s = dot4(v[j][i], xr[4 * j + i], s);
+                isum += sc[j] * (s - 32 * bs[j]);
+            }
+            const float val = (dw * __uint_as_float(xr[18])) * (float)isum;
+            acc[m] += valid ? val : 0.f;
+        }
     }
 };
 
@@ -289,18 +325,17 @@ struct Fast<TYPE_Q6_K, 4> {
 template <>
 struct Fast<TYPE_Q8_0, 1> {
     static constexpr int PPB = 1, VALS = 32, XW = 9, BYTES = 34;
-    static constexpr int NBUF = 2;
+    static constexpr int NBUF = 2, RAW = 10;
     struct Raw { uint32_t w[9]; uint32_t mis; };
     __device__ static Raw load(const uint8_t *blk, int) {
         Raw r;
-        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
-        r.mis = (uint32_t)(ad & 3u);
-        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
-        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
-        const u32x4a4 a1 = *reinterpret_cast<const u32x4a4 *>(base + 16);
+        r.mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const gbytes_c base = align4_global(reinterpret_cast<uintptr_t>(blk));
+        const u32x4a4 a0 = gld16(base);
+        const u32x4a4 a1 = gld16(base + 16);
         r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
         r.w[4] = a1.x; r.w[5] = a1.y; r.w[6] = a1.z; r.w[7] = a1.w;
-        r.w[8] = *reinterpret_cast<const uint32_t *>(base + 32);
+        r.w[8] = gld4(base + 32);
         return r;
     }
     __device__ static void xload_lds(const uint8_t *xb, int, uint32_t *xr) {
@@ -310,16 +345,23 @@ struct Fast<TYPE_Q8_0, 1> {
         xr[4] = b.x; xr[5] = b.y; xr[6] = b.z; xr[7] = b.w;
         xr[8] = *reinterpret_cast<const uint32_t *>(xb + 32);
     }
-    __device__ static float dot(const Raw &r, int, const uint32_t *xr) {
+    template <int MR, class XL>
+    __device__ static void dotm(const Raw &r, int, XL xl, float *acc, bool valid) {
         const bool odd = r.mis != 0;
         const float d = h2f(odd ? (r.w[0] >> 16) : (r.w[0] & 0xffffu));
-        int s = 0;
+        uint32_t q[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t q = odd ? r.w[i + 1] : __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
-            s = dot4(q, xr[i], s);
+        for (int i = 0; i < 8; i++) q[i] = odd ? r.w[i + 1] : __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            uint32_t xr[XW];
+            xl(m, xr);
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) s = dot4(q[i], xr[i], s);
+            const float v = ((float)s * d) * __uint_as_float(xr[8]);
+            acc[m] += valid ? v : 0.f;
         }
-        return ((float)s * d) * __uint_as_float(xr[8]);
     }
 };
 
@@ -437,7 +479,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
 // before any store, with indices clamped into range instead of branches;
 // `between` as for quantise_x_lds.
 template <int TYPE, class Between>
-__device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx, Between between) {
+__device__ __forceinline__ void copy_x_row_lds(const ActView &a, int nbx, uint8_t *sx, Between between) {
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
     constexpr int CPB = TYPE == TYPE_Q8_0 ? 2 : 16;  // 16-byte code chunks per block
     constexpr int NC = TYPE == TYPE_Q8_0 ? 4 : 4;    // code chunks per thread (<= 1024 total)
@@ -465,6 +507,22 @@ __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *s
     }
     *reinterpret_cast<float *>(sx + min(t, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d0;
     *reinterpret_cast<float *>(sx + min(t + 256, nbx - 1) * XS + (TYPE == TYPE_Q8_0 ? 32 : 288)) = d1;
+}
+
+// MR pre-quantised activation rows -> MR consecutive LDS row images of nbx
+// blocks each; `between` runs once, inside the first row's copy.
+template <int TYPE, int MR, class Between>
+__device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx, Between between) {
+    constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
+    copy_x_row_lds<TYPE>(a, nbx, sx, between);
+#pragma unroll 1
+    for (int m = 1; m < MR; m++) {
+        ActView r = a;
+        r.xq = a.xq + (int64_t)m * a.k;
+        r.xd = a.xd + (int64_t)m * a.nb;
+        if constexpr (TYPE != TYPE_Q8_0) r.xbs = a.xbs + (int64_t)m * (a.k / 16);
+        copy_x_row_lds<TYPE>(r, nbx, sx + (int64_t)m * nbx * XS, [] {});
+    }
     __syncthreads();
 }
 
@@ -532,10 +590,11 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
-template <int TYPE, int PPB, int RPW, int IT, bool FUSED, int MAP, bool NORM = false>
+template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false>
 __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                ActView act, const float *__restrict__ alpha, float eps) {
     static_assert(!NORM || (FUSED && TYPE != TYPE_Q8_0), "the RMS norm runs in the quantising prologue");
+    static_assert(MR == 1 || (!FUSED && MAP == MAP_ONE), "several activation rows: pre-quantised, one weight");
     constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
     static_assert(!PAIRED || RPW <= 2, "a silu pair spans two row groups or one");
     const int64_t n = rm.n;
@@ -618,7 +677,7 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     // wave's whole stream up front, leave every wave waiting for its first rows
     // while the whole matrix is in flight, and bunch the compute at the end.
     // Deep rows (IT > 4) keep two buffers (registers).
-    constexpr int NBUF = (F::NBUF == 3 && IT <= 4) ? 3 : 2;
+    constexpr int NBUF = (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
     Raw ring[NBUF][IT];
     auto issue_ring = [&] {
 #pragma unroll
@@ -628,33 +687,68 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
     if constexpr (FUSED) quantise_x_lds<TYPE, NORM>(x, nb, sx, issue_ring, alpha, eps);
-    else copy_x_lds<TYPE>(act, nb, sx, issue_ring);
+    else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its
     // activation registers are read from LDS once and kept for the whole row loop.
-    constexpr bool XREG = IT * F::XW <= 80;
-    uint32_t xk[XREG ? IT : 1][F::XW];
+    constexpr bool XREG = MR * IT * F::XW <= (MR == 1 ? 80 : 160) && NBUF * IT * F::RAW + MR * IT * F::XW <= 190;
+    uint32_t xk[XREG ? MR : 1][XREG ? IT : 1][F::XW];
     if constexpr (XREG) {
 #pragma unroll
-        for (int i = 0; i < IT; i++) F::xload_lds(sx + min(bs0 + BPI * i, nb - 1) * XS, p, xk[i]);
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int i = 0; i < IT; i++) F::xload_lds(sx + (m * nb + min(bs0 + BPI * i, nb - 1)) * XS, p, xk[m][i]);
     }
 
     float pend = 0.f;  // silu pairs: the gate sum waiting for its up sum (wave-uniform)
     auto compute_group = [&](int64_t g, const Raw *buf, bool store) {
-        float acc = 0.f;
+        float accm[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) accm[m] = 0.f;
 #pragma unroll
         for (int i = 0; i < IT; i++) {
             const int b = bs0 + BPI * i;
-            float v;
-            if constexpr (XREG) {
-                v = F::dot(buf[i], p, xk[i]);
-            } else {
-                uint32_t xr[F::XW];
-                F::xload_lds(sx + min(b, nb - 1) * XS, p, xr);
-                v = F::dot(buf[i], p, xr);
-            }
-            acc += b < nb ? v : 0.f;
+            auto xl = [&](int m, uint32_t *xr) {
+                if constexpr (XREG) {
+#pragma unroll
+                    for (int w = 0; w < F::XW; w++) xr[w] = xk[m][i][w];
+                } else {
+                    // The LDS image does not change inside the row loop, so without this
+                    // barrier the compiler hoists every row's and sweep's reads out of it
+                    // and holds them all in registers (spilling): read them where used.
+                    if constexpr (MR > 1) asm volatile("" ::: "memory");
+                    F::xload_lds(sx + (m * nb + min(b, nb - 1)) * XS, p, xr);
+                }
+            };
+            F::template dotm<MR>(buf[i], p, xl, accm, b < nb);
+            // several rows: one piece's unpacked codes live at a time
+            if constexpr (MR > 1) __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (MR > 1) {
+            // several activation rows (one weight, MAP_ONE): row q of the group,
+            // activation row m goes to y[m][row]
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const float a = row_sum_f32(accm[m]);
+#pragma unroll
+                for (int q = 0; q < RPW; q++) {
+                    float s;
+                    if constexpr (LPR == 64) {
+                        s = __int_as_float(rl(__float_as_uint(a), 0)) + __int_as_float(rl(__float_as_uint(a), 16)) +
+                            __int_as_float(rl(__float_as_uint(a), 32)) + __int_as_float(rl(__float_as_uint(a), 48));
+                    } else if constexpr (LPR == 32) {
+                        s = __int_as_float(rl(__float_as_uint(a), 32 * q)) +
+                            __int_as_float(rl(__float_as_uint(a), 32 * q + 16));
+                    } else {
+                        s = __int_as_float(rl(__float_as_uint(a), 16 * q));
+                    }
+                    const int64_t rq = g * RPW + q;
+                    if (store && lane == LPR * q && rq < n) y[(int64_t)m * n + rq] = s;
+                }
+            }
+            return;
+        }
+        float acc = accm[0];
         acc = row_sum_f32(acc);
         // row group q of this wave spans 16-lane rows LPR/16*q .. ; lane LPR*q writes it
 #pragma unroll

@@ -203,14 +203,13 @@ struct Dec<TYPE_Q8_0> {
     struct Raw { uint32_t w[9]; uint32_t mis; };
     __device__ static Raw load(const uint8_t *blk, int) {
         Raw r;
-        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
-        r.mis = (uint32_t)(ad & 3u);
-        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
-        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
-        const u32x4a4 a1 = *reinterpret_cast<const u32x4a4 *>(base + 16);
+        r.mis = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u);
+        const gbytes_c base = align4_global(reinterpret_cast<uintptr_t>(blk));
+        const u32x4a4 a0 = gld16(base);
+        const u32x4a4 a1 = gld16(base + 16);
         r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
         r.w[4] = a1.x; r.w[5] = a1.y; r.w[6] = a1.z; r.w[7] = a1.w;
-        r.w[8] = *reinterpret_cast<const uint32_t *>(base + 32);
+        r.w[8] = gld4(base + 32);
         return r;
     }
     template <int M>
@@ -374,13 +373,12 @@ struct DecLegacy {
     struct Raw { uint32_t w[NW]; uint32_t mis; };
     __device__ static Raw load(const uint8_t *blk, int) {
         Raw r;
-        const uintptr_t ad = reinterpret_cast<uintptr_t>(blk);
-        r.mis = ODD ? (uint32_t)(ad & 2u) : 0u;
-        const uint8_t *base = reinterpret_cast<const uint8_t *>(ad & ~(uintptr_t)3);
-        const u32x4a4 a0 = *reinterpret_cast<const u32x4a4 *>(base);
+        r.mis = ODD ? (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 2u) : 0u;
+        const gbytes_c base = align4_global(reinterpret_cast<uintptr_t>(blk));
+        const u32x4a4 a0 = gld16(base);
         r.w[0] = a0.x; r.w[1] = a0.y; r.w[2] = a0.z; r.w[3] = a0.w;
-        r.w[4] = *reinterpret_cast<const uint32_t *>(base + 16);
-        if constexpr (NW == 6) r.w[5] = *reinterpret_cast<const uint32_t *>(base + 20);
+        r.w[4] = gld4(base + 16);
+        if constexpr (NW == 6) r.w[5] = gld4(base + 20);
         return r;
     }
     // 4 bits b0..b3 -> bit 4 of bytes 0..3
@@ -652,16 +650,18 @@ static hipError_t run_m(const GemvCfg &c, const uint8_t *w, const PGeom &g, cons
 // seven sweeps of eight blocks exactly, where 64-weight pieces would leave an
 // eighth of the lanes idle.
 template <int TYPE>
-static bool fast_shape(int nb, int *ppb, int *rpw, int *it) {
+static bool fast_shape(int nb, int *ppb, int *rpw, int *it, int mr = 1) {
     int q = 0, r = 0;
     if (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
+        // several activation rows: 64-weight pieces throughout (the seven sweeps
+        // of 32-weight pieces leave no registers for more than one row)
         if (nb <= 4) { q = 4; r = 4; }
         else if (nb <= 8) { q = 4; r = 2; }
-        else if (nb <= 64 && (nb > 56 || nb <= 48)) { q = 4; r = 1; }
+        else if (nb <= 64 && (nb > 56 || nb <= 48 || mr > 1)) { q = 4; r = 1; }
         else if (nb <= 56) { q = 8; r = 1; }
     } else if (TYPE == TYPE_Q6_K) {
-        if (nb <= 16) { q = 4; r = 2; }
-        else if (nb <= 64) { q = 4; r = 1; }
+        if (nb <= 16 && mr == 1) { q = 4; r = 2; }
+        else if (nb <= 64) { q = 4; r = 1; }  // several rows: one sweep per row at k <= 4096
     } else if (nb <= 512) {  // Q8_0: nb counts 32-value blocks
         q = 1; r = 1;
     }
@@ -701,10 +701,10 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
             if (!x || (n & 1)) return hipErrorNotSupported;
             if constexpr (NORM_OK)
                 if (alpha) {
-                    k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                    k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
                     return hipGetLastError();
                 }
-            k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+            k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
         } else {
             return hipErrorNotSupported;
         }
@@ -712,16 +712,99 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
         if (!x) return hipErrorNotSupported;
         if constexpr (NORM_OK)
             if (alpha) {
-                k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
                 return hipGetLastError();
             }
-        k_gemv1<TYPE, PPB, RPW, IT, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else if (x) {
-        k_gemv1<TYPE, PPB, RPW, IT, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     } else {
-        k_gemv1<TYPE, PPB, RPW, IT, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        k_gemv1<TYPE, PPB, RPW, IT, 1, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     }
     return hipGetLastError();
+}
+
+// MR pre-quantised activation rows (m = MR) against one weight: the weight is
+// streamed once for all MR rows, the activation rows sit in LDS (or registers).
+template <int TYPE, int PPB, int RPW, int IT, int MR>
+static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, hipStream_t st) {
+    const int64_t n = rm.n;
+    const int64_t ng = (n + RPW - 1) / RPW;
+    constexpr int BPI = 64 / RPW / PPB;
+    if (!(BPI * (IT - 1) < nb && nb <= BPI * IT)) return hipErrorNotSupported;
+    const size_t lds = (size_t)MR * nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
+    auto kern = k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE>;
+    if (lds > 65536) {
+        static const hipError_t attr =
+            hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+        if (attr != hipSuccess) return attr;
+    }
+    // two workgroups per CU while both fit the CU's 160 KB of LDS
+    int wpc = lds <= 80 * 1024 ? 8 : 4;
+    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
+    int64_t waves = (int64_t)num_cus() * wpc;
+    if (waves > ng) waves = ng;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    kern<<<grid, 256, lds, st>>>(rm, row_bytes, nb, nullptr, act, nullptr, 0.f);
+    return hipGetLastError();
+}
+
+template <int TYPE, int MR>
+static hipError_t run_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, hipStream_t st) {
+    int ppb, rpw, it;
+    // every chunk of a multi-row call (its single-row remainder too) uses the multi-row shape
+    if (!fast_shape<TYPE>(nb, &ppb, &rpw, &it, 2)) return hipErrorNotSupported;
+    // only the (shape, rows) pairs fast_rows_max admits are compiled
+#define LBQ_FAST(Q, R, I)                                                                                   \
+    if constexpr (MR <= (I <= 1 ? 8 : I == 2 ? 4 : 1))                                                     \
+        if (ppb == Q && rpw == R && it == I) return launch_fast_rows<TYPE, Q, R, I, MR>(rm, row_bytes, nb, act, st);
+    if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
+        LBQ_FAST(4, 4, 1) LBQ_FAST(4, 2, 1) LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
+    } else if constexpr (TYPE == TYPE_Q6_K) {
+        LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
+    } else {
+        LBQ_FAST(1, 1, 1) LBQ_FAST(1, 1, 2) LBQ_FAST(1, 1, 3) LBQ_FAST(1, 1, 4) LBQ_FAST(1, 1, 5) LBQ_FAST(1, 1, 6)
+        LBQ_FAST(1, 1, 7) LBQ_FAST(1, 1, 8)
+    }
+#undef LBQ_FAST
+    return hipErrorNotSupported;
+}
+
+// Rows of x one launch can take: their activation registers must fit beside the
+// weight ring (8 rows for one sweep per row, 4 for two; beyond, one).
+template <int TYPE>
+static int fast_rows_max(int nb) {
+    int ppb, rpw, it;
+    if (!fast_shape<TYPE>(nb, &ppb, &rpw, &it, 2)) return 0;
+    return it <= 1 ? 8 : it == 2 ? 4 : 1;
+}
+
+// m = 2..8 pre-quantised rows: chunks of 8, 4, 2 and 1 rows, each chunk one launch
+// (the largest chunk within fast_rows_max whose activation image fits 80 KB of LDS).
+template <int TYPE>
+static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const ActView &act, int m, hipStream_t st) {
+    const size_t row_lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
+    const int mr_max = fast_rows_max<TYPE>(nb);
+    for (int m0 = 0; m0 < m;) {
+        int mr = 8;
+        while (mr > 1 && (mr > m - m0 || mr > mr_max || (size_t)mr * row_lds > 80 * 1024)) mr >>= 1;
+        RowMap rm = rm0;
+        rm.y[0] = rm0.y[0] + (int64_t)m0 * rm0.n;
+        ActView a = act;
+        a.xq = act.xq + (int64_t)m0 * act.k;
+        a.xd = act.xd + (int64_t)m0 * act.nb;
+        if (act.xbs) a.xbs = act.xbs + (int64_t)m0 * (act.k / 16);
+        hipError_t e;
+        switch (mr) {
+        case 8: e = run_fast_rows<TYPE, 8>(rm, row_bytes, nb, a, st); break;
+        case 4: e = run_fast_rows<TYPE, 4>(rm, row_bytes, nb, a, st); break;
+        case 2: e = run_fast_rows<TYPE, 2>(rm, row_bytes, nb, a, st); break;
+        default: e = run_fast_rows<TYPE, 1>(rm, row_bytes, nb, a, st); break;
+        }
+        if (e != hipSuccess) return e;
+        m0 += mr;
+    }
+    return hipSuccess;
 }
 
 template <int TYPE>
@@ -762,6 +845,10 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
         if (m == 1) {
             const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
             if (e != hipErrorNotSupported) return e;
+        } else if (m <= 8 && !x && !alpha && map == MAP_ONE && rm.end[0] == n && !getenv("LBQ_GEMV_ROWS_OFF")) {
+            // one launch per chunk of rows, each streaming the weight once: worth it
+            // while a chunk holds at least half the rows (one or two sweeps per row)
+            if (fast_rows_max<TYPE>(g.nb) >= 4) return run_fast_m<TYPE>(rm, row_bytes, g.nb, act, m, st);
         }
     }
     if (alpha || map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // m = 1 fast path only
