@@ -56,6 +56,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-gemm", action="store_true", help="skip the M = 512 MFMA measurement")
+    p.add_argument("--no-configs", action="store_true",
+                   help="skip configs 1, 3 and 4 (Q8_0 GEMV, Q6_K head / Q5_K batch 1-8, M crossover)")
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a 256 MiB device copy 4 times (reference kernel of known size for "
                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -325,6 +327,10 @@ def main():
     if not args.no_gemm:
         result["prefill_gemm"] = gemm_bench(torch, qz, gen, dev, stream, reps)
 
+    # ---------------------------------------------------------------- configs 1, 3, 4: other shapes
+    if not args.no_configs:
+        result["configs"] = configs_bench(torch, qz, gen, dev, stream)
+
     # ---------------------------------------------------------------- config 5: 32-layer stack
     if not args.no_stack:
         result["stack"] = stack_bench(torch, qz, gen, dev, stream)
@@ -358,6 +364,69 @@ def gemm_bench(torch, qz, gen, dev, stream, reps):
         log(f"gemm {name} M={M}: forward {ms_f * 1e3:.1f} us, dot {ms_d * 1e3:.1f} us "
             f"({fl / (ms_d * 1e-3) / 1e12:.0f} TFLOP/s)")
         del g_f, g_d, qm, x, y, act
+    return out
+
+
+def configs_bench(torch, qz, gen, dev, stream):
+    """BASELINE configs[0] (Q8_0 4096x4096 GEMV, m = 1), configs[2] (Q6_K LM head 128256x4096 and
+    Q5_K gate/up 14336x4096 at batch 1, 4, 8; x ~ N(0, 1) with 1 % of entries x20) and configs[3]
+    (Q4_K gate 14336x4096 / down 4096x14336 at M = 16, 64, 512, 2048): QMatMul::forward per launch,
+    HIP-graph replay, enough weight copies rotated that the working set exceeds the 256 MB MALL."""
+    out = {}
+
+    def timed_rot(qms, x, reps):
+        y = torch.empty(x.shape[0], qms[0].qtensor().shape()[0], device=dev)
+        g = capture(torch, lambda: [qm.forward(x) for qm in qms])
+        timed_graph(torch, g, 2, stream)
+        us = timed_graph(torch, g, reps, stream) / len(qms) * 1e3
+        del g, y
+        return us
+
+    def x_outliers(b, k):
+        x = torch.randn(b, k, generator=gen, device=dev)
+        mask = torch.rand(b, k, generator=gen, device=dev) < 0.01
+        return torch.where(mask, x * 20.0, x)
+
+    # configs[0]: Q8_0 GEMV (17.8 MB per copy, 16 copies)
+    q8 = [make_weights(torch, qz, qz.GgmlDType.Q8_0, 4096, 4096, gen, dev) for _ in range(16)]
+    wb = q8[0].qtensor().storage_size_in_bytes()
+    us = timed_rot(q8, torch.randn(1, 4096, generator=gen, device=dev), 20)
+    out["q8_0_4096x4096_m1"] = {"us": round(us, 2), "weight_GB/s": round(wb / us / 1e3, 1),
+                                "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del q8
+    torch.cuda.empty_cache()
+
+    # configs[2]: Q6_K LM head (431 MB, one copy exceeds the MALL) and Q5_K gate/up (8 copies)
+    head = [make_weights(torch, qz, qz.GgmlDType.Q6K, VOCAB, 4096, gen, dev)]
+    q5 = [make_weights(torch, qz, qz.GgmlDType.Q5K, 14336, 4096, gen, dev) for _ in range(8)]
+    hb, q5b = head[0].qtensor().storage_size_in_bytes(), q5[0].qtensor().storage_size_in_bytes()
+    for B in (1, 4, 8):
+        x = x_outliers(B, 4096)
+        for name, qms, nbytes in (("q6_k_head_128256x4096", head, hb), ("q5_k_gate_up_14336x4096", q5, q5b)):
+            us = timed_rot(qms, x, 10 if qms is head else 20)
+            out[f"{name}_b{B}"] = {"us": round(us, 2), "weight_GB/s": round(nbytes / us / 1e3, 1),
+                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"configs[2] batch {B}: head {out[f'q6_k_head_128256x4096_b{B}']['us']} us, "
+            f"q5_k {out[f'q5_k_gate_up_14336x4096_b{B}']['us']} us")
+    del head, q5
+    torch.cuda.empty_cache()
+
+    # configs[3]: Q4_K gate / down at M = 16, 64, 512, 2048 (8 copies of each: 264 MB)
+    for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
+        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(8)]
+        nbytes = qms[0].qtensor().storage_size_in_bytes()
+        for M in (16, 64, 512, 2048):
+            x = torch.randn(M, k, generator=gen, device=dev)
+            us = timed_rot(qms if M <= 64 else qms[:2], x, 10 if M <= 64 else 4)
+            fl = 2.0 * M * n * k
+            out[f"q4_k_{name}_{n}x{k}_m{M}"] = {
+                "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                "weight_GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                "bound": "hbm" if M <= 64 else "mfma"}
+            log(f"configs[3] {name} M={M}: {us:.1f} us")
+        del qms
+        torch.cuda.empty_cache()
     return out
 
 

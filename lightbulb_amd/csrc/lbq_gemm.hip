@@ -75,6 +75,16 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint
     *hi = __builtin_bit_cast(uint32_t, rb);
 }
 
+// Where the pre-pass puts the 8 operand values at k-order position 8*p8 of block
+// b of row m (p8 = 16h + s: lane half h, k-step s).  Row-major ([m][k], the
+// tiled kernels stage it through LDS) or, for the skinny kernel (m <= 32),
+// operand-major: the 64 lanes' operands of one (block, k-step) are 1 KB in a
+// row, so each k-step's A operand is a single contiguous load.
+__device__ __forceinline__ int64_t op_pos(bool opmajor, int64_t m, int64_t b, int p8, int64_t K) {
+    if (opmajor) return ((b * 16 + (p8 & 15)) * 64 + (p8 >> 4) * 32 + m) * 8;
+    return m * K + b * KB + 8 * p8;
+}
+
 // ---------------------------------------------------------------------------
 // Pre-pass: Q8_K rows (codes + block scales) -> fp16 operand rows in the GEMM's k
 // order, and the row exponent e_m.  One 256-thread workgroup per row; every
@@ -82,7 +92,7 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint
 // workgroup), takes their maximum, and converts 16-code chunks.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
-                                                 int *__restrict__ erow) {
+                                                 int *__restrict__ erow, bool opmajor) {
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x;
     const int nb = act.nb;
@@ -94,7 +104,6 @@ __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float1
     const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;
     if (t == 0) erow[m] = e;
     const int8_t *q = act.xq + m * act.k;
-    _Float16 *a = A + m * act.k;
     for (int64_t c = 16 * t; c < act.k; c += 16 * 256) {
         const uint4 w = *reinterpret_cast<const uint4 *>(q + c);
         const float sx = __builtin_amdgcn_ldexpf(xd[c / KB], -e);
@@ -104,9 +113,10 @@ __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float1
         codes_to_f16(w.y, sx, cc, &v[2], &v[3]);
         codes_to_f16(w.z, sx, cc, &v[4], &v[5]);
         codes_to_f16(w.w, sx, cc, &v[6], &v[7]);
-        uint4 *dst = reinterpret_cast<uint4 *>(a + c);
-        dst[0] = make_uint4(v[0], v[1], v[2], v[3]);
-        dst[1] = make_uint4(v[4], v[5], v[6], v[7]);
+        const int64_t b = c / KB;
+        const int p8 = (int)(c % KB) / 8;
+        *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, p8, act.k)) = make_uint4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, p8 + 1, act.k)) = make_uint4(v[4], v[5], v[6], v[7]);
     }
 }
 
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float1
 // converts with the same arithmetic as k_act_f16 -- one launch instead of two,
 // bit-identical operands.
 __global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
-                                                   int *__restrict__ erow) {
+                                                   int *__restrict__ erow, bool opmajor) {
     constexpr int MAXP = 4;  // passes of 16 blocks
     __shared__ float ds[16 * MAXP];
     const int64_t m = blockIdx.x;
@@ -154,7 +164,6 @@ __global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, 
     for (int b = 0; b < nbx; b++) mx = fmaxf(mx, fabsf(ds[b]));
     const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;  // as k_act_f16
     if (t == 0) erow[m] = e;
-    _Float16 *a = A + m * K;
 #pragma unroll
     for (int j = 0; j < MAXP; j++) {
         const int b = 16 * j + (t >> 4);
@@ -166,9 +175,8 @@ __global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, 
             codes_to_f16(codes[j].y, sx, cc, &w8[2], &w8[3]);
             codes_to_f16(codes[j].z, sx, cc, &w8[4], &w8[5]);
             codes_to_f16(codes[j].w, sx, cc, &w8[6], &w8[7]);
-            uint4 *dst = reinterpret_cast<uint4 *>(a + (int64_t)b * KB + 16 * sub);
-            dst[0] = make_uint4(w8[0], w8[1], w8[2], w8[3]);
-            dst[1] = make_uint4(w8[4], w8[5], w8[6], w8[7]);
+            *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, 2 * sub, K)) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+            *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, 2 * sub + 1, K)) = make_uint4(w8[4], w8[5], w8[6], w8[7]);
         }
     }
 }
@@ -322,6 +330,9 @@ struct GemmGrid {
 // resident workgroups per CU the register budget allows
 template <int TYPE, int MT>
 constexpr int gemm_occupancy() { return (MT == 4 || TYPE == TYPE_Q6_K || (TYPE == TYPE_Q5_K && MT == 2)) ? 1 : 2; }
+// weight bytes loaded two blocks ahead (where the registers allow: Q4_K, 32-row tiles)
+template <int TYPE, int MT>
+constexpr bool gemm_deep() { return TYPE == TYPE_Q4_K && MT == 1; }
 
 // Pipeline.  The MFMAs of a block run as 16 k-steps of 2*MT MFMAs; each MFMA sits
 // in its own scheduling region (sched_barrier) together with a share of the
@@ -376,15 +387,21 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
     const _Float16 *abase = A + (m0 + pr) * K + pc * 8;
     if (t < BM) Es[t] = erow[min(m0 + t, M - 1)];
 
-    typename B::Raw raw[2];
+    // Raw weight bytes: with DEEP, two sets, so the loads for block b + 2 go out
+    // while block b + 1's bytes wait in the other set (a short block's MFMA work
+    // does not cover a memory latency); the set roles swap with the LDS buffer.
+    constexpr bool DEEP = gemm_deep<TYPE, MT>();
+    typename B::Raw raw[DEEP ? 2 : 1][2];
     typename B::Prep p[2];
     uint4 ra[ALOADS];
     auto a_load = [&](int b, int i) { ra[i] = *reinterpret_cast<const uint4 *>(abase + 8 * i * K + (int64_t)b * KB); };
     auto a_store = [&](int buf, int i) {
         *reinterpret_cast<uint4 *>(&As[buf][8 * i + pr][8 * pc]) = make_uint4(ra[i].x, ra[i].y, ra[i].z, ra[i].w);
     };
-    auto w_load = [&](int b, int q) { B::load_part(wrow[q / B::NL] + (int64_t)b * B::BYTES, h, raw[q / B::NL], q % B::NL); };
-    auto w_prep = [&](int b, int j) { gb_prep<TYPE>(raw[j], h, wrow[j] + (int64_t)b * B::BYTES, p[j]); };
+    auto w_load = [&](int b, int q, int set) {
+        B::load_part(wrow[q / B::NL] + (int64_t)b * B::BYTES, h, raw[DEEP ? set : 0][q / B::NL], q % B::NL);
+    };
+    auto w_prep = [&](int b, int j, int set) { gb_prep<TYPE>(raw[DEEP ? set : 0][j], h, wrow[j] + (int64_t)b * B::BYTES, p[j]); };
 
     floatx16 acc[MT][2];
 #pragma unroll
@@ -394,16 +411,21 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
-    // prologue: block b0 into LDS buffer 0, its scales and first operands
+    // prologue: block b0 into LDS buffer 0, its scales and first operands (and
+    // with DEEP block b0 + 1's bytes into set 0, which the first block preps)
 #pragma unroll
     for (int i = 0; i < ALOADS; i++) a_load(b0, i);
 #pragma unroll
-    for (int q = 0; q < WL; q++) w_load(b0, q);
+    for (int q = 0; q < WL; q++) w_load(b0, q, 1);
+    if constexpr (DEEP) {
+#pragma unroll
+        for (int q = 0; q < WL; q++) w_load(min(b0 + 1, b1 - 1), q, 0);
+    }
 #pragma unroll
     for (int i = 0; i < ALOADS; i++) a_store(0, i);
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 2; j++) w_prep(b0, j);
+    for (int j = 0; j < 2; j++) w_prep(b0, j, 1);
     const _Float16 *al0 = &As[0][lr][128 * h], *al1 = &As[1][lr][128 * h];
     half8 acur[MT];
     uint32_t bcur[2][4];
@@ -414,6 +436,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 
     auto block = [&](int b, int buf) {
         const int bn = min(b + 1, b1 - 1);  // clamped: the last block re-stages itself, harmlessly
+        const int bl = DEEP ? min(b + 2, b1 - 1) : bn;  // the block whose weight bytes this block loads
         const _Float16 *al = buf ? al1 : al0, *aln = buf ? al0 : al1;
         half8 ablk[MT];
         uint32_t bblk[2][4];
@@ -437,7 +460,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
                     if (s >= 1 && s <= 3) {
 #pragma unroll
                         for (int w = ((s - 1) * NG + rg) * WPR; w < ((s - 1) * NG + rg + 1) * WPR; w++)
-                            if (w < WL) w_load(bn, w);
+                            if (w < WL) w_load(bl, w, buf ^ 1);
                     }
                     if (s == 4 && rg == 0) __syncthreads();
                     if (s == 8) { a_store(buf ^ 1, 2 * rg); a_store(buf ^ 1, 2 * rg + 1); }
@@ -446,7 +469,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
                     if (s == 15) {
                         if (rg == 0) {
 #pragma unroll
-                            for (int jj = 0; jj < 2; jj++) w_prep(bn, jj);
+                            for (int jj = 0; jj < 2; jj++) w_prep(bn, jj, buf);
                         }
                         if (NG == 1 || rg > 0) {
                             const int r0 = NG == 1 ? 0 : (rg - 1) * NPR;
@@ -681,6 +704,107 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny tiles for m <= 32: the weight stream, not the MFMA work, sets the time,
+// so waves stream independently instead of sharing an LDS activation tile.  A
+// workgroup owns 32 columns (one 32x32 MFMA tile of y) and 4*KC consecutive
+// blocks of k; wave w takes blocks KC*w .. KC*w + KC - 1 of them, with the raw
+// weight bytes of the next two blocks in flight (three-slot ring) and the fp16
+// activation operands of the next block in a 16-slot ring (slot s = k-step s,
+// read straight from the operand rows in L2).  The four waves' tiles are added
+// through LDS in a fixed order at the end; a grid of several k-slices writes
+// partial sums that k_split_sum adds.  Lane (lr, h) serves weight row n0 + lr and
+// half h of every block (the GB operand builders, as in k_gemm).
+// ---------------------------------------------------------------------------
+constexpr int SKB = 32;  // columns per skinny workgroup
+
+template <int TYPE>
+__global__ __launch_bounds__(256, 2) void k_gemm_s(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
+                                                   const _Float16 *__restrict__ A, const int *__restrict__ erow,
+                                                   int64_t K, int64_t M, float *__restrict__ out, int kc, int slices,
+                                                   int64_t split_stride) {
+    using B = GB<TYPE>;
+    __shared__ float red[3][64][17];  // waves 1..3's tiles for the reduction (padded)
+    const int tn = (int)blockIdx.x / slices, z = (int)blockIdx.x % slices;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
+    const int nb = (int)(K / KB);
+    const int wb0 = (z * 4 + wave) * kc, wb1 = min(nb, wb0 + kc);  // this wave's blocks (may be empty)
+    const int64_t n0 = (int64_t)tn * SKB;
+    const uint8_t *wrow = W + min(n0 + lr, N - 1) * row_bytes;
+    // operand-major activations: (block, k-step) -> 64 lanes x 8 halfs; rows past
+    // M hold garbage, their outputs are dropped
+    const _Float16 *aop = A + lane * 8;
+
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.f;
+
+    if (wb0 < wb1) {
+        typename B::Raw raw[3];
+        typename B::Prep p;
+        half8 ar[16];
+        auto w_load = [&](int b, int slot) {
+            const uint8_t *blk = wrow + (int64_t)min(b, wb1 - 1) * B::BYTES;  // clamped: re-reads the last block
+#pragma unroll
+            for (int i = 0; i < B::NL; i++) B::load_part(blk, h, raw[slot], i);
+        };
+        auto a_load = [&](int b, int s) {
+            ar[s] = *reinterpret_cast<const half8 *>(aop + ((int64_t)min(b, wb1 - 1) * 16 + s) * 512);
+        };
+        // prologue: blocks wb0 .. wb0 + 2 in flight, block wb0's operands
+        w_load(wb0, 0);
+#pragma unroll
+        for (int s = 0; s < 16; s++) a_load(wb0, s);
+        w_load(wb0 + 1, 1);
+        w_load(wb0 + 2, 2);
+        gb_prep<TYPE>(raw[0], h, wrow + (int64_t)wb0 * B::BYTES, p);
+
+        // block b in ring slot `slot`: 16 k-steps; the A slot of each step is
+        // refilled with the next block's step; at the end the next block's
+        // scales are prepared and block b + 3's bytes go into this slot
+        auto block = [&](int b, int slot) {
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                uint32_t bw[4];
+#pragma unroll
+                for (int d = 0; d < 4; d++) bw[d] = B::dw(p, s, d);
+                const half8 bo = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ar[s], bo, acc, 0, 0, 0);
+                a_load(b + 1, s);
+            }
+            const int nslot = slot == 2 ? 0 : slot + 1;
+            gb_prep<TYPE>(raw[nslot], h, wrow + (int64_t)min(b + 1, wb1 - 1) * B::BYTES, p);
+            w_load(b + 3, slot);
+        };
+        for (int b = wb0; b < wb1; b += 3) {
+            block(b, 0);
+            if (b + 1 < wb1) block(b + 1, 1);
+            if (b + 2 < wb1) block(b + 2, 2);
+        }
+    }
+
+    // fixed-order reduction of the four waves' tiles: waves 1..3 park theirs in LDS
+    if (wave > 0) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) red[wave - 1][lane][v] = acc[v];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < 3; w++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[v] += red[w][lane][v];
+        float *y = out + (int64_t)z * split_stride;
+        const int64_t n = n0 + lr;
+        // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[v], erow[r]);
+        }
+    }
+}
+
 // y = sum over s < S of part[s] (fixed order), count values.
 __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int S, int64_t count,
                                                    float *__restrict__ y) {
@@ -694,12 +818,28 @@ __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ par
 namespace {
 
 struct Plan {
-    int mt, tiles_m, tiles_n, splits, bps;
+    int mt, tiles_m, tiles_n, splits, bps;  // mt = 0: skinny (m <= 32; bps = blocks per wave)
 };
 
 // mt = 8 selects the tall kernel (256 x 128 tiles) for m >= 256
 Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     Plan p;
+    // Q6_K's skinny variant measured slower than its 32-row tiles (register-heavy raw blocks)
+    if (m <= 32 && type != TYPE_Q6_K && !getenv("LBQ_GEMM_NO_SKINNY")) {
+        // skinny: 32-column workgroups of four waves, each wave kc blocks; about
+        // 2048 waves over the chip (eight per CU), slices of 4*kc blocks
+        p.mt = 0;
+        p.tiles_m = 1;
+        p.tiles_n = (int)((n + SKB - 1) / SKB);
+        const int nb = (int)(k / KB);
+        const int64_t work = (int64_t)p.tiles_n * nb;  // (column tile, block) units
+        int kc = (int)std::max<int64_t>(1, (work + 2047) / 2048);
+        kc = std::min(kc, (nb + 3) / 4);
+        if (const char *e = getenv("LBQ_GEMM_KC")) kc = std::max(1, atoi(e));  // tuning override
+        p.bps = kc;
+        p.splits = (nb + 4 * kc - 1) / (4 * kc);
+        return p;
+    }
     if (m >= 256 && !getenv("LBQ_GEMM_NO_TALL")) p.mt = 8;
     else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
     p.tiles_m = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
@@ -710,6 +850,7 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     const int64_t slots = (int64_t)num_cus() * occ;
     int s = 1;
     if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
+    if (const char *e = getenv("LBQ_GEMM_SPLITS")) s = std::max(1, std::min(atoi(e), nb));  // tuning override
     p.bps = (nb + s - 1) / s;
     p.splits = (nb + p.bps - 1) / p.bps;
     return p;
@@ -720,6 +861,13 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
                         const int *erow, int64_t k, int64_t m, float *out, int64_t split_stride, hipStream_t st) {
     const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
+    if (p.mt == 0) {
+        if constexpr (TYPE != TYPE_Q6_K) {
+            k_gemm_s<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, p.bps, p.splits, split_stride);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
     switch (p.mt) {
     case 8: k_gemm_t<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
@@ -740,7 +888,7 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     WsLayout L;
     L.a_off = 0;
-    L.e_off = up((size_t)p.tiles_m * 32 * p.mt * (size_t)k * sizeof(_Float16));  // whole row tiles
+    L.e_off = up((size_t)p.tiles_m * 32 * (p.mt ? p.mt : 1) * (size_t)k * sizeof(_Float16));  // whole row tiles
     L.part_off = L.e_off + up((size_t)m * sizeof(int));
     L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
     return L;
@@ -766,9 +914,9 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     int *erow = reinterpret_cast<int *>(base + L.e_off);
     if (x) {
         if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
-        k_quant_f16<<<(unsigned)m, 256, 0, st>>>(x, k, a, erow);
+        k_quant_f16<<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, p.mt == 0);
     } else {
-        k_act_f16<<<(unsigned)m, 256, 0, st>>>(act, m, a, erow);
+        k_act_f16<<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, p.mt == 0);
     }
     return hipGetLastError();
 }
