@@ -684,9 +684,11 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     if (!(BPI * (IT - 1) < nb && nb <= BPI * IT)) return hipErrorNotSupported;
     // Waves per CU.  With the fused prologue every workgroup quantises all of x,
     // so for fewer rows (less weight per CU to hide it behind) one workgroup per
-    // CU does better; measured on Q4_K: 4096 x 4096 5.3 us at 4 vs 5.8 at 8,
-    // 14336 x 4096 9.1 us at 8 vs 9.8 at 4.
-    int wpc = (x && n < 8192) ? 4 : 8;
+    // CU does better, and so it does for k = 14336 and for Q6_K throughout.
+    // Measured (fused / pre-quantised x): Q4_K 4096 x 4096 5.0 / 4.5 us at 4 vs
+    // 5.7 / 4.6 at 8; 14336 x 4096 9.3 / 8.8 at 4 vs 9.1 / 8.4 at 8; 4096 x 14336
+    // 10.1 / 8.2 at 4 vs 11.2 / 9.0 at 8; Q6_K 14336 x 4096 14.4 at 4 vs 16.1 at 8.
+    int wpc = (TYPE == TYPE_Q6_K || (n < 8192 && (x || nb > 32))) ? 4 : 8;
     if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
