@@ -468,6 +468,34 @@ def test_qmatmul_group_errors(oracle, lbq, dev):
     assert L.lbq_gate_up_silu_f32(a._ctx, a._handle, None, x.data_ptr(), 1, y.data_ptr(), None) == -1
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+def test_batch_decode_row_chunks(oracle, lbq, dev, t):
+    # m = 2..8 at k = 4096 takes the multi-row decode kernel: activation rows in
+    # chunks of at most 4 or 8 (m = 5 and 7 leave a ragged last chunk), ragged n
+    rng = np.random.default_rng(90 + t)
+    k = 4096
+    for n in (1, 257, 1000):
+        w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
+        for m in (2, 5, 7, 8):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+            assert_rows_close(gpu_qmatmul(t, w_raw, n, k, x, dev), ref, tight_bound(t, m))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_skinny_tiles_split_k(oracle, lbq, dev, t, k):
+    # 9 <= m <= 32 takes the 32-row MFMA tiles with k split over waves and
+    # workgroups: ragged m and n, both Llama-3 row lengths
+    rng = np.random.default_rng(95 + t + k)
+    for n in (40, 1000):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        for m in (9, 23, 32):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+            assert_rows_close(gpu_qmatmul(t, w_raw, n, k, x, dev), ref, tight_bound(t, m))
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
     # m >= 256 takes the 256 x 128 tile kernel: ragged m and n, odd and even block counts
