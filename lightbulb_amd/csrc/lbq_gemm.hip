@@ -576,9 +576,21 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     // direct-to-LDS staging: instruction j of a wave fills stage rows
     // 64 wave + 4j + [0, 4); lane l writes row 64 wave + 4j + l/16, slot l%16,
     // so it fetches logical chunk (l%16) ^ (row & 15), whose pattern repeats
-    // every 4 instructions: a scalar base plus one of four 32-bit lane offsets.
+    // every 4 instructions: a scalar offset plus one of four 32-bit lane offsets.
     // Rows past M exist in the operand buffer (whole tiles), so no clamping.
-    const char *dma_base = reinterpret_cast<const char *>(A + (m0 + 64 * wave) * K);
+    // Buffer loads, not global ones: the compiler counts a pending global
+    // load-to-LDS against the LDS-read counter as well and then drains every
+    // LDS read (lgkmcnt(0)) at each A-operand use until the stage's loads land;
+    // a buffer load is counted as a vector-memory load only, so the A reads keep
+    // their read-ahead.  The resource spans the tile's 256 operand rows
+    // (the host keeps 256 * K * 2 bytes below 2^31).
+    // (the base passes through readfirstlane so the resource is known to be
+    // scalar: otherwise each load becomes a waterfall loop)
+    const uint64_t abase = reinterpret_cast<uint64_t>(A + m0 * K);
+    const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
+                             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane((int)(TBM * K * 2)), 0x00020000);
     uint32_t voff[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -586,9 +598,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
         voff[q] = (uint32_t)(((lane >> 4) * (int)K + 128 * (c >> 3) + 8 * (c & 7)) * 2);
     }
     auto a_dma = [&](int u, int buf, int j) {
-        const char *src = dma_base + ((int64_t)j * 4 * K + (int64_t)(u >> 1) * KB + 64 * (u & 1)) * 2 + voff[j & 3];
+        const int soff = ((64 * wave + 4 * j) * (int)K + (u >> 1) * KB + 64 * (u & 1)) * 2;
         uint8_t *dst = (buf ? As1 : As0) + (64 * wave + 4 * j) * TROW;
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)dst, 16, voff[j & 3],
+                                                 soff, 0, 0);
     };
     // A-operand read addresses: row lr (+32 i, an immediate offset), chunk 8h + j
     // in slot (8h + j) ^ (lr & 15); one register per k-step and buffer
@@ -694,6 +707,169 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
 
 #pragma unroll
     for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int64_t m = m0 + r;
+            const int64_t n = n0 + 32 * wave + lr;
+            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wide tiles for m >= 128: eight waves (two per SIMD), workgroup tile 128 x 256;
+// wave w owns columns 32w..32w+31 for all 128 rows (4 MFMA tiles), so each
+// weight byte is dequantised once per workgroup.  One wave per SIMD cannot keep
+// the matrix core busy -- even back-to-back independent 32x32x16 MFMAs from a
+// single wave issue at about two thirds of the peak rate, and the LDS reads and
+// dequantisation VALU between them add to that -- while two waves per SIMD
+// overlap one wave's VALU and LDS work with the other's MFMAs.  The activation
+// stage is the tall kernel's layout at 128 rows (32 KB per buffer, XOR-swizzled
+// chunks, filled by buffer loads to LDS), and the per-stage protocol is the same:
+//   k-step 0    : barrier, then the next stage's loads into the other buffer
+//                 (4 per wave);
+//   k-step 6    : wait for this wave's loads, barrier;
+//   k-steps 6-7 : in stage 0, the next block's weight loads;
+//   k-step 7    : in stage 1, the next block's scales and first B operand.
+// ---------------------------------------------------------------------------
+constexpr int WBM = 128, WBN = 256;
+
+template <int TYPE>
+__global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
+                                                   const _Float16 *__restrict__ A, const int *__restrict__ erow,
+                                                   int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
+    using B = GB<TYPE>;
+    __shared__ __align__(1024) uint8_t As0[WBM * TROW];
+    __shared__ __align__(1024) uint8_t As1[WBM * TROW];
+    __shared__ int Es[WBM];
+
+    const int G = (int)gridDim.x, L = (int)blockIdx.x;
+    const int T = (G & 7) == 0 ? (L & 7) * (G >> 3) + (L >> 3) : L;
+    const int tm = T % g.tiles_m, tn = (T / g.tiles_m) % g.tiles_n, z = T / (g.tiles_m * g.tiles_n);
+    const int nb = (int)(K / KB);
+    const int b0 = z * g.bps, b1 = min(nb, b0 + g.bps);
+    const int64_t m0 = (int64_t)tm * WBM, n0 = (int64_t)tn * WBN;
+    float *y = out + (int64_t)z * g.split_stride;
+
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
+              lr = lane & 31;
+    const uint8_t *wrow = W + min(n0 + 32 * wave + lr, N - 1) * row_bytes;
+    if (t < WBM) Es[t] = erow[min(m0 + t, M - 1)];
+
+    // staging: instruction j (0..3) of wave w fills stage rows 16w + 4j + [0, 4);
+    // lane l writes row 16w + 4j + l/16, slot l%16, holding logical chunk
+    // (l%16) ^ (row & 15) = (l%16) ^ ((4j + l/16) & 15)
+    const uint64_t abase = reinterpret_cast<uint64_t>(A + m0 * K);
+    const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
+                             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane((int)(WBM * K * 2)), 0x00020000);
+    uint32_t voff[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int c = (lane & 15) ^ ((4 * q + (lane >> 4)) & 15);
+        voff[q] = (uint32_t)(((lane >> 4) * (int)K + 128 * (c >> 3) + 8 * (c & 7)) * 2);
+    }
+    auto a_dma = [&](int u, int buf, int j) {
+        const int soff = ((16 * wave + 4 * j) * (int)K + (u >> 1) * KB + 64 * (u & 1)) * 2;
+        uint8_t *dst = (buf ? As1 : As0) + (16 * wave + 4 * j) * TROW;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)dst, 16, voff[j],
+                                                 soff, 0, 0);
+    };
+    // A operand of MFMA tile i at k-step j: row lr + 32i, chunk 8h + j in slot
+    // (8h + j) ^ (lr & 15)
+    const uint8_t *rb[2][8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        int o0 = lr * TROW + 16 * ((8 * h + j) ^ (lr & 15)), o1 = o0;
+        asm volatile("" : "+v"(o0), "+v"(o1));
+        rb[0][j] = As0 + o0;
+        rb[1][j] = As1 + o1;
+    }
+    auto a_read = [&](int buf, int j, int i) -> half8 {
+        return *reinterpret_cast<const half8 *>(rb[buf][j] + 32 * i * TROW);
+    };
+
+    typename B::Raw raw;
+    typename B::Prep p;
+    auto w_load = [&](int b, int q) { B::load_part(wrow + (int64_t)b * B::BYTES, h, raw, q); };
+    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, p); };
+
+    floatx16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
+
+#pragma unroll
+    for (int j = 0; j < 4; j++) a_dma(2 * b0, 0, j);
+#pragma unroll
+    for (int q = 0; q < B::NL; q++) w_load(b0, q);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    w_prep(b0);
+    constexpr int AH = 2;
+    half8 ar[AH][4];
+    uint32_t bcur[4];
+#pragma unroll
+    for (int j = 0; j < AH; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) ar[j][i] = a_read(0, j, i);
+#pragma unroll
+    for (int d = 0; d < 4; d++) bcur[d] = B::dw(p, 0, d);
+
+    const int u_end = 2 * b1;
+    auto stage = [&](int u, int buf) {
+        const int ts = u & 1;
+        const int un = min(u + 1, u_end - 1);  // clamped: the last stage re-stages itself
+        const int bn = min((u >> 1) + 1, b1 - 1);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const int s = 8 * ts + ks;
+            half8 an[4];
+            uint32_t bnxt[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (ks == 0 && i == 0) __syncthreads();  // every wave is done with the other buffer
+                if (ks == 6 && i == 0) {
+                    __builtin_amdgcn_s_waitcnt(0);  // this wave's stage loads (the weight loads come after)
+                    __syncthreads();
+                }
+                const half8 bo = __builtin_bit_cast(half8, make_uint4(bcur[0], bcur[1], bcur[2], bcur[3]));
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ar[0][i], bo, acc[i], 0, 0, 0);
+                if (ks + AH < 8) an[i] = a_read(buf, ks + AH, i);
+                else an[i] = a_read(buf ^ 1, ks + AH - 8, i);
+                if (s < 15) {
+                    if (i == 0 || i == 2) { bnxt[i] = B::dw(p, s + 1, i); bnxt[i + 1] = B::dw(p, s + 1, i + 1); }
+                } else {
+                    if (i == 0) w_prep(bn);
+                    else if (i == 1 || i == 3) { bnxt[i - 1] = B::dw(p, 0, i - 1); bnxt[i] = B::dw(p, 0, i); }
+                }
+                if (ks == 0) a_dma(un, buf ^ 1, i);
+                if (ts == 0 && (ks == 6 || ks == 7)) {
+#pragma unroll
+                    for (int q = 4 * (ks - 6) + i; q < B::NL; q += 8) w_load(bn, q);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int j = 0; j + 1 < AH; j++) ar[j][i] = ar[j + 1][i];
+                ar[AH - 1][i] = an[i];
+            }
+#pragma unroll
+            for (int d = 0; d < 4; d++) bcur[d] = bnxt[d];
+        }
+    };
+    for (int u = 2 * b0; u < u_end; u += 2) {
+        stage(u, 0);
+        stage(u + 1, 1);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
@@ -821,7 +997,10 @@ struct Plan {
     int mt, tiles_m, tiles_n, splits, bps;  // mt = 0: skinny (m <= 32; bps = blocks per wave)
 };
 
-// mt = 8 selects the tall kernel (256 x 128 tiles) for m >= 256
+// mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256)
+constexpr int MT_WIDE = 16;
+int tile_rows(int mt) { return mt == 0 ? 32 : mt == 8 ? TBM : mt == MT_WIDE ? WBM : 32 * mt; }
+
 Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     Plan p;
     // Q6_K's skinny variant measured slower than its 32-row tiles (register-heavy raw blocks)
@@ -840,10 +1019,20 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
         p.splits = (nb + 4 * kc - 1) / (4 * kc);
         return p;
     }
-    if (m >= 256 && !getenv("LBQ_GEMM_NO_TALL")) p.mt = 8;
+    // the wide and tall kernels address a tile's operand rows through a buffer
+    // resource of 256 * k * 2 bytes or less, which must stay below 2^31
+    const bool big_ok = k * 2 * TBM < (int64_t(1) << 31) && !getenv("LBQ_GEMM_NO_TALL");
+    // wide tiles (two waves per SIMD, dequantisation per 128 rows) below 256 rows,
+    // and for Q4_K (the cheapest dequantisation) up to 512; tall tiles (one wave
+    // per SIMD, dequantisation per 256 rows) where the dequantisation VALU per
+    // MFMA decides (measured per type and m: 128, 256, 512, 2048)
+    bool wide = m < 256 || (type == TYPE_Q4_K && m <= 512);
+    if (const char *e = getenv("LBQ_GEMM_BIG")) wide = e[0] != 't' || m < 256;  // tuning override: "wide" or "tall"
+    if (m >= 128 && big_ok) p.mt = wide ? MT_WIDE : 8;
     else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
-    p.tiles_m = (int)((m + 32 * p.mt - 1) / (32 * p.mt));
-    p.tiles_n = (int)((n + (p.mt == 8 ? TBN : BN) - 1) / (p.mt == 8 ? TBN : BN));
+    const int rows = tile_rows(p.mt), cols = p.mt == 8 ? TBN : BN;
+    p.tiles_m = (int)((m + rows - 1) / rows);
+    p.tiles_n = (int)((n + cols - 1) / cols);
     const int nb = (int)(k / KB);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     const int occ = (p.mt >= 4 || type == TYPE_Q6_K || (type == TYPE_Q5_K && p.mt == 2)) ? 1 : 2;  // gemm_occupancy
@@ -870,6 +1059,7 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
     }
     switch (p.mt) {
     case 8: k_gemm_t<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+    case MT_WIDE: k_gemm_w<TYPE><<<grid, 512, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 2: k_gemm<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     default:
@@ -888,7 +1078,7 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     WsLayout L;
     L.a_off = 0;
-    L.e_off = up((size_t)p.tiles_m * 32 * (p.mt ? p.mt : 1) * (size_t)k * sizeof(_Float16));  // whole row tiles
+    L.e_off = up((size_t)p.tiles_m * tile_rows(p.mt) * (size_t)k * sizeof(_Float16));  // whole row tiles
     L.part_off = L.e_off + up((size_t)m * sizeof(int));
     L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
     return L;

@@ -497,10 +497,25 @@ def test_skinny_tiles_split_k(oracle, lbq, dev, t, k):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_qmatmul_wide_tiles(oracle, lbq, dev, t):
+    # 128 <= m < 256 (and Q4_K up to 512) takes the 128 x 256 eight-wave tiles:
+    # ragged m and n, odd block counts, split-k over 12 one-block slices
+    rng = np.random.default_rng(85 + t)
+    for (m, n, k) in ((128, 256, 256), (200, 77, 256 * 3), (255, 300, 256 * 12), (400, 290, 256 * 2)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        rows = np.r_[0:4, m // 2:m // 2 + 4, m - 4:m]
+        y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y[rows], ref, tight_bound(t, m))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
-    # m >= 256 takes the 256 x 128 tile kernel: ragged m and n, odd and even block counts
+    # Q5_K / Q6_K at m >= 256 and Q4_K above 512 take the 256 x 128 tiles: ragged
+    # m and n, odd and even block counts (Q4_K at m = 256, 300: the wide tiles)
     rng = np.random.default_rng(80 + t)
-    for (m, n, k) in ((256, 128, 256), (300, 200, 256 * 3), (520, 390, 256 * 4)):
+    for (m, n, k) in ((256, 128, 256), (300, 200, 256 * 3), (520, 390, 256 * 4), (640, 130, 256 * 5)):
         w_raw = bp.random_blocks(rng, t, n * k // 256)
         x = rng.standard_normal((m, k)).astype(np.float32)
         rows = np.r_[0:4, m // 2:m // 2 + 4, m - 4:m]
