@@ -87,24 +87,33 @@ __device__ __forceinline__ int64_t op_pos(bool opmajor, int64_t m, int64_t b, in
 
 // ---------------------------------------------------------------------------
 // Pre-pass: Q8_K rows (codes + block scales) -> fp16 operand rows in the GEMM's k
-// order, and the row exponent e_m.  One 256-thread workgroup per row; every
-// thread reads the row's block scales (the same few addresses across the
-// workgroup), takes their maximum, and converts 16-code chunks.
+// order, and the row exponent e_m.  One workgroup of T threads per row (T = 1024
+// for few rows, so the row's chunks are converted in one pass): the threads
+// share the maximum of the row's block scales through LDS, then convert
+// 16-code chunks.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
-                                                 int *__restrict__ erow, bool opmajor) {
+template <int T>
+__global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
+                                               int *__restrict__ erow, bool opmajor) {
+    __shared__ float wmax[T / 64];
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x;
     const int nb = act.nb;
     const float *xd = act.xd + m * nb;
     float mx = 0.f;
-    for (int b = 0; b < nb; b++) mx = fmaxf(mx, fabsf(xd[b]));
+    for (int b = t; b < nb; b += T) mx = fmaxf(mx, fabsf(xd[b]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < T / 64; w++) mx = fmaxf(mx, wmax[w]);
     // max |d_x| = f*2^E, f in [0.5, 1): |q8*d_x| < 128*2^E, so e = E - 8 keeps the
     // row's values below 2^15 and its largest at or above 2^14
     const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;
     if (t == 0) erow[m] = e;
     const int8_t *q = act.xq + m * act.k;
-    for (int64_t c = 16 * t; c < act.k; c += 16 * 256) {
+    for (int64_t c = 16 * t; c < act.k; c += 16 * T) {
         const uint4 w = *reinterpret_cast<const uint4 *>(q + c);
         const float sx = __builtin_amdgcn_ldexpf(xd[c / KB], -e);
         const float cc = -1152.f * sx;
@@ -125,18 +134,19 @@ __global__ __launch_bounds__(256) void k_act_f16(ActView act, int64_t M, _Float1
 // quantiser), shares the block scales through LDS for the row exponent, and
 // converts with the same arithmetic as k_act_f16 -- one launch instead of two,
 // bit-identical operands.
-__global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
-                                                   int *__restrict__ erow, bool opmajor) {
-    constexpr int MAXP = 4;  // passes of 16 blocks
-    __shared__ float ds[16 * MAXP];
+template <int T>
+__global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
+                                                 int *__restrict__ erow, bool opmajor) {
+    constexpr int BPP = T / 16, MAXP = 64 / BPP;  // passes of BPP blocks, 64 blocks at most
+    __shared__ float ds[64];
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x, sub = t & 15;
-    const int nbx = (int)(K / KB), np = (nbx + 15) >> 4;
+    const int nbx = (int)(K / KB), np = (nbx + BPP - 1) / BPP;
     const float *xr = x + m * K;
     float v[MAXP][16];
 #pragma unroll
     for (int j = 0; j < MAXP; j++) {
-        const int b = min(16 * j + (t >> 4), nbx - 1);
+        const int b = min(BPP * j + (t >> 4), nbx - 1);
         const float4 *src = reinterpret_cast<const float4 *>(xr + (int64_t)b * KB + 16 * sub);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -155,7 +165,7 @@ __global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, 
             int sum;
             q8k_lane16(v[j], sub, packed, &sum, &dj[j]);
             codes[j] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-            const int b = 16 * j + (t >> 4);
+            const int b = BPP * j + (t >> 4);
             if (sub == 0 && b < nbx) ds[b] = dj[j];
         }
     }
@@ -166,7 +176,7 @@ __global__ __launch_bounds__(256) void k_quant_f16(const float *__restrict__ x, 
     if (t == 0) erow[m] = e;
 #pragma unroll
     for (int j = 0; j < MAXP; j++) {
-        const int b = 16 * j + (t >> 4);
+        const int b = BPP * j + (t >> 4);
         if (j < np && b < nbx) {
             const float sx = __builtin_amdgcn_ldexpf(dj[j], -e);
             const float cc = -1152.f * sx;
@@ -325,6 +335,7 @@ __device__ __forceinline__ void gb_prep(const typename GB<TYPE>::Raw &r, int h, 
 struct GemmGrid {
     int tiles_m, tiles_n, bps;  // bps: blocks of k per split
     int64_t split_stride;       // floats between the partial outputs of two splits (0: no split)
+    int splits;
 };
 
 // resident workgroups per CU the register budget allows
@@ -981,6 +992,100 @@ __global__ __launch_bounds__(256, 2) void k_gemm_s(const uint8_t *__restrict__ W
     }
 }
 
+// ---------------------------------------------------------------------------
+// K-sliced tiles for m <= 32.  A workgroup owns 128 columns (32 per wave) and a
+// slice of S consecutive blocks of k that its four waves share.  The slice's
+// activation operands (16 KB per block, operand-major) go into LDS by buffer
+// loads issued first; then every weight load of the slice is issued at once.
+// Memory loads complete in order, so with the activations ahead of the weights
+// no wait ever holds a wave for a weight block it does not need yet, and each
+// wave has its whole slice of weight bytes in flight (the stream's latency is
+// paid once per workgroup, not once per block).  Slices write partial sums that
+// k_split_sum adds in a fixed order.
+// ---------------------------------------------------------------------------
+constexpr int KSN = 128;  // columns per k-sliced workgroup
+
+template <int TYPE>
+constexpr int ks_blocks() { return 4; }  // longest slice: 4 x 16 KB of LDS, two workgroups per CU
+
+template <int TYPE, int S>
+__global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N, int64_t row_bytes,
+                                                    const _Float16 *__restrict__ A, const int *__restrict__ erow,
+                                                    int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
+    const int slices = g.splits;
+    const int64_t split_stride = g.split_stride;
+    using B = GB<TYPE>;
+    static_assert(S >= 1 && S <= ks_blocks<TYPE>(), "slice length");
+    __shared__ __align__(1024) uint8_t As[S * 16384];
+    const int tn = (int)blockIdx.x / slices, z = (int)blockIdx.x % slices;
+    const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
+              lr = lane & 31;
+    const int nb = (int)(K / KB);
+    const int b0 = z * S, cnt = min(S, nb - b0);  // cnt >= 1
+    const int64_t n0 = (int64_t)tn * KSN + 32 * wave;
+    const uint8_t *wrow = W + min(n0 + lr, N - 1) * row_bytes + (int64_t)b0 * B::BYTES;
+
+    // the slice's operands: block b, k-step s, lane l at byte ((16 b + s) 64 + l) 16;
+    // 1 KB per wave instruction, chunk 4i + wave; chunks past the slice's last
+    // block read as zero (outside the buffer resource) and are never used
+    const uint64_t abase = reinterpret_cast<uint64_t>(A + (int64_t)b0 * 16 * 512);
+    const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
+                             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
+    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane(cnt * 16384), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4 * S; i++) {
+        const int chunk = 4 * i + wave;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)(As + chunk * 1024),
+                                                 16, (uint32_t)lane * 16, chunk * 1024, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // weight loads block by block, in order (each block's wait then covers only
+    // the blocks before it)
+    typename B::Raw raw[S];
+#pragma unroll
+    for (int b = 0; b < S; b++) {
+#pragma unroll
+        for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b], q);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the activation loads are the oldest in flight: wait for them alone
+    constexpr int VM = S * B::NL;
+    static_assert(VM < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+    __syncthreads();
+
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.f;
+    const uint8_t *arow = As + lane * 16;
+#pragma unroll
+    for (int b = 0; b < S; b++) {
+        if (b < cnt) {
+            typename B::Prep p;
+            gb_prep<TYPE>(raw[b], h, wrow + (int64_t)b * B::BYTES, p);
+#pragma unroll
+            for (int s = 0; s < 16; s++) {
+                const half8 a = *reinterpret_cast<const half8 *>(arow + (b * 16 + s) * 1024);
+                uint32_t bw[4];
+#pragma unroll
+                for (int d = 0; d < 4; d++) bw[d] = B::dw(p, s, d);
+                const half8 bo = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc, 0, 0, 0);
+            }
+        }
+    }
+
+    float *y = out + (int64_t)z * split_stride;
+    const int64_t n = n0 + lr;
+    // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int r = 8 * (v >> 2) + 4 * h + (v & 3);
+        if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[v], erow[r]);
+    }
+}
+
 // y = sum over s < S of part[s] (fixed order), count values.
 __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int S, int64_t count,
                                                    float *__restrict__ y) {
@@ -998,11 +1103,30 @@ struct Plan {
 };
 
 // mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256)
-constexpr int MT_WIDE = 16;
-int tile_rows(int mt) { return mt == 0 ? 32 : mt == 8 ? TBM : mt == MT_WIDE ? WBM : 32 * mt; }
+constexpr int MT_WIDE = 16, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 32)
+int tile_rows(int mt) { return mt == 0 || mt == MT_KS ? 32 : mt == 8 ? TBM : mt == MT_WIDE ? WBM : 32 * mt; }
+bool operand_major(int mt) { return mt == 0 || mt == MT_KS; }
+int ks_blocks_for(int type) {
+    return type == TYPE_Q4_K ? ks_blocks<TYPE_Q4_K>() : type == TYPE_Q5_K ? ks_blocks<TYPE_Q5_K>() : ks_blocks<TYPE_Q6_K>();
+}
 
 Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     Plan p;
+    if (m <= 32 && !getenv("LBQ_GEMM_NO_KS")) {
+        // k-sliced: 128-column workgroups, each a slice of S blocks
+        p.mt = MT_KS;
+        p.tiles_m = 1;
+        p.tiles_n = (int)((n + KSN - 1) / KSN);
+        // blocks per slice: 4, fewer (down to 2) until the grid has a workgroup
+        // per CU (measured at m = 16 on the Llama-3 shapes, 1 to 4 blocks)
+        const int nb = (int)(k / KB);
+        int bps = ks_blocks_for(type);
+        while (bps > 2 && (int64_t)p.tiles_n * ((nb + bps - 1) / bps) < (int64_t)num_cus()) bps--;
+        if (const char *e = getenv("LBQ_GEMM_KS")) bps = std::max(1, std::min(atoi(e), ks_blocks_for(type)));  // tuning
+        p.bps = bps;
+        p.splits = (nb + bps - 1) / bps;
+        return p;
+    }
     // Q6_K's skinny variant measured slower than its 32-row tiles (register-heavy raw blocks)
     if (m <= 32 && type != TYPE_Q6_K && !getenv("LBQ_GEMM_NO_SKINNY")) {
         // skinny: 32-column workgroups of four waves, each wave kc blocks; about
@@ -1048,8 +1172,21 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
 template <int TYPE>
 hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_bytes, const _Float16 *a,
                         const int *erow, int64_t k, int64_t m, float *out, int64_t split_stride, hipStream_t st) {
-    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride};
+    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
+    if (p.mt == MT_KS) {
+        switch (p.bps) {  // slice length (within the type's register budget)
+        case 1: k_gemm_ks<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+        case 2: k_gemm_ks<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+        case 3:
+            if constexpr (ks_blocks<TYPE>() >= 3) k_gemm_ks<TYPE, 3><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+            break;
+        default:
+            if constexpr (ks_blocks<TYPE>() >= 4) k_gemm_ks<TYPE, 4><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+            break;
+        }
+        return hipGetLastError();
+    }
     if (p.mt == 0) {
         if constexpr (TYPE != TYPE_Q6_K) {
             k_gemm_s<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, p.bps, p.splits, split_stride);
@@ -1078,7 +1215,7 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     WsLayout L;
     L.a_off = 0;
-    L.e_off = up((size_t)p.tiles_m * tile_rows(p.mt) * (size_t)k * sizeof(_Float16));  // whole row tiles
+    L.e_off = L.a_off + up((size_t)p.tiles_m * tile_rows(p.mt) * (size_t)k * sizeof(_Float16));  // whole row tiles
     L.part_off = L.e_off + up((size_t)m * sizeof(int));
     L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
     return L;
@@ -1104,9 +1241,12 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     int *erow = reinterpret_cast<int *>(base + L.e_off);
     if (x) {
         if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
-        k_quant_f16<<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, p.mt == 0);
+        // few rows: one pass of 1024 threads per row; many rows: 256-thread workgroups
+        if (m <= 64) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p.mt));
+        else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, operand_major(p.mt));
     } else {
-        k_act_f16<<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, p.mt == 0);
+        if (m <= 64) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p.mt));
+        else k_act_f16<256><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, operand_major(p.mt));
     }
     return hipGetLastError();
 }

@@ -511,6 +511,23 @@ def test_qmatmul_wide_tiles(oracle, lbq, dev, t):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_split_k_shapes_deterministic(oracle, lbq, dev, t):
+    # shapes that split k (k-sliced m <= 32, 32-row tiles, wide, tall): partial
+    # sums are added in slice order, so repeated calls give the same bits
+    rng = np.random.default_rng(88 + t)
+    for (m, n, k) in ((16, 300, 256 * 16), (32, 1000, 256 * 56), (48, 300, 256 * 8), (130, 300, 256 * 12),
+                      (300, 100, 256 * 16)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y1 = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        y2 = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), (m, n, k)
+        rows = np.r_[0:2, m - 2:m]
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y1[rows], ref, tight_bound(t, m))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
     # Q5_K / Q6_K at m >= 256 and Q4_K above 512 take the 256 x 128 tiles: ragged
     # m and n, odd and even block counts (Q4_K at m = 256, 300: the wide tiles)
