@@ -1086,14 +1086,34 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     }
 }
 
-// y = sum over s < S of part[s] (fixed order), count values.
+// y = sum over s < S of part[s] (fixed order: ((p0 + p1) + p2) + ...), count
+// values.  Four values per thread, the partials' loads issued eight slices at a
+// time (a runtime trip count would otherwise serialise them).
 __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ part, int S, int64_t count,
                                                    float *__restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= count) return;
-    float s = part[i];
-    for (int z = 1; z < S; z++) s += part[(int64_t)z * count + i];
-    y[i] = s;
+    if (i + 4 <= count && (reinterpret_cast<uintptr_t>(y) & 15u) == 0 && (count & 3) == 0) {
+        const float4 *pp = reinterpret_cast<const float4 *>(part + i);
+        const int64_t st = count / 4;
+        float4 acc = pp[0];
+        for (int z0 = 1; z0 < S; z0 += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (z0 + j < S) v[j] = pp[(int64_t)(z0 + j) * st];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (z0 + j < S) { acc.x += v[j].x; acc.y += v[j].y; acc.z += v[j].z; acc.w += v[j].w; }
+        }
+        *reinterpret_cast<float4 *>(y + i) = acc;
+        return;
+    }
+    for (int64_t e = i; e < min(i + 4, count); e++) {
+        float a = part[e];
+        for (int z = 1; z < S; z++) a += part[(int64_t)z * count + e];
+        y[e] = a;
+    }
 }
 
 namespace {
@@ -1270,7 +1290,7 @@ hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t r
     }
     if (e != hipSuccess || p.splits == 1) return e;
     const int64_t count = m * n;
-    k_split_sum<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(part, p.splits, count, y);
+    k_split_sum<<<(unsigned)((count + 1023) / 1024), 256, 0, st>>>(part, p.splits, count, y);
     return hipGetLastError();
 }
 
