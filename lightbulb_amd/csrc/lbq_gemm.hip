@@ -80,8 +80,10 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint
 // tiled kernels stage it through LDS) or, for the skinny kernel (m <= 32),
 // operand-major: the 64 lanes' operands of one (block, k-step) are 1 KB in a
 // row, so each k-step's A operand is a single contiguous load.
-__device__ __forceinline__ int64_t op_pos(bool opmajor, int64_t m, int64_t b, int p8, int64_t K) {
-    if (opmajor) return ((b * 16 + (p8 & 15)) * 64 + (p8 >> 4) * 32 + m) * 8;
+__device__ __forceinline__ int64_t op_pos(int opmajor, int64_t m, int64_t b, int p8, int64_t K) {
+    // opmajor = number of 32-row tiles (0: row-major); operand-major order is
+    // block, row tile, k-step, lane
+    if (opmajor) return (((b * opmajor + (m >> 5)) * 16 + (p8 & 15)) * 64 + (p8 >> 4) * 32 + (m & 31)) * 8;
     return m * K + b * KB + 8 * p8;
 }
 
@@ -94,7 +96,7 @@ __device__ __forceinline__ int64_t op_pos(bool opmajor, int64_t m, int64_t b, in
 // ---------------------------------------------------------------------------
 template <int T>
 __global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
-                                               int *__restrict__ erow, bool opmajor) {
+                                               int *__restrict__ erow, int opmajor) {
     __shared__ float wmax[T / 64];
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x;
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 
 // bit-identical operands.
 template <int T>
 __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
-                                                 int *__restrict__ erow, bool opmajor) {
+                                                 int *__restrict__ erow, int opmajor) {
     constexpr int BPP = T / 16, MAXP = 64 / BPP;  // passes of BPP blocks, 64 blocks at most
     __shared__ float ds[64];
     const int64_t m = blockIdx.x;
@@ -1008,15 +1010,15 @@ constexpr int KSN = 128;  // columns per k-sliced workgroup
 template <int TYPE>
 constexpr int ks_blocks() { return 4; }  // longest slice: 4 x 16 KB of LDS, two workgroups per CU
 
-template <int TYPE, int S>
+template <int TYPE, int S, int T>
 __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N, int64_t row_bytes,
                                                     const _Float16 *__restrict__ A, const int *__restrict__ erow,
                                                     int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
     const int slices = g.splits;
     const int64_t split_stride = g.split_stride;
     using B = GB<TYPE>;
-    static_assert(S >= 1 && S <= ks_blocks<TYPE>(), "slice length");
-    __shared__ __align__(1024) uint8_t As[S * 16384];
+    static_assert(S >= 1 && S <= ks_blocks<TYPE>() && (T == 1 || T == 2), "slice length, row tiles");
+    __shared__ __align__(1024) uint8_t As[S * T * 16384];
     const int tn = (int)blockIdx.x / slices, z = (int)blockIdx.x % slices;
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
               lr = lane & 31;
@@ -1025,16 +1027,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     const int64_t n0 = (int64_t)tn * KSN + 32 * wave;
     const uint8_t *wrow = W + min(n0 + lr, N - 1) * row_bytes + (int64_t)b0 * B::BYTES;
 
-    // the slice's operands: block b, k-step s, lane l at byte ((16 b + s) 64 + l) 16;
-    // 1 KB per wave instruction, chunk 4i + wave; chunks past the slice's last
-    // block read as zero (outside the buffer resource) and are never used
-    const uint64_t abase = reinterpret_cast<uint64_t>(A + (int64_t)b0 * 16 * 512);
+    // the slice's operands: block b, row tile u, k-step s, lane l at byte
+    // (((T b + u) 16 + s) 64 + l) 16; 1 KB per wave instruction, chunk 4i + wave;
+    // chunks past the slice's last block read as zero (outside the buffer
+    // resource) and are never used
+    const uint64_t abase = reinterpret_cast<uint64_t>(A + (int64_t)b0 * T * 16 * 512);
     const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
                              ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
     const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane(cnt * 16384), 0x00020000);
+        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane(cnt * T * 16384), 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 4 * S; i++) {
+    for (int i = 0; i < 4 * S * T; i++) {
         const int chunk = 4 * i + wave;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)(As + chunk * 1024),
                                                  16, (uint32_t)lane * 16, chunk * 1024, 0, 0);
@@ -1055,9 +1058,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
     __syncthreads();
 
-    floatx16 acc;
+    floatx16 acc[T];
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.f;
+    for (int u = 0; u < T; u++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[u][v] = 0.f;
     const uint8_t *arow = As + lane * 16;
 #pragma unroll
     for (int b = 0; b < S; b++) {
@@ -1066,12 +1071,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
             gb_prep<TYPE>(raw[b], h, wrow + (int64_t)b * B::BYTES, p);
 #pragma unroll
             for (int s = 0; s < 16; s++) {
-                const half8 a = *reinterpret_cast<const half8 *>(arow + (b * 16 + s) * 1024);
                 uint32_t bw[4];
 #pragma unroll
                 for (int d = 0; d < 4; d++) bw[d] = B::dw(p, s, d);
                 const half8 bo = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc, 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < T; u++) {
+                    const half8 a = *reinterpret_cast<const half8 *>(arow + ((b * T + u) * 16 + s) * 1024);
+                    acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc[u], 0, 0, 0);
+                }
             }
         }
     }
@@ -1080,10 +1088,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     const int64_t n = n0 + lr;
     // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int r = 8 * (v >> 2) + 4 * h + (v & 3);
-        if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[v], erow[r]);
-    }
+    for (int u = 0; u < T; u++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], erow[r]);
+        }
 }
 
 // y = sum over s < S of part[s] (fixed order: ((p0 + p1) + p2) + ...), count
@@ -1120,29 +1130,43 @@ namespace {
 
 struct Plan {
     int mt, tiles_m, tiles_n, splits, bps;  // mt = 0: skinny (m <= 32; bps = blocks per wave)
+    int rt = 1;                             // k-sliced kernel: 32-row tiles per workgroup
 };
 
 // mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256)
-constexpr int MT_WIDE = 16, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 32)
-int tile_rows(int mt) { return mt == 0 || mt == MT_KS ? 32 : mt == 8 ? TBM : mt == MT_WIDE ? WBM : 32 * mt; }
-bool operand_major(int mt) { return mt == 0 || mt == MT_KS; }
+constexpr int MT_WIDE = 16, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 64)
+int tile_rows(const Plan &p) {
+    return p.mt == 0 ? 32 : p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TBM : p.mt == MT_WIDE ? WBM : 32 * p.mt;
+}
+// the pre-pass layout: 32-row tiles of operand-major rows, or 0 (row-major)
+int operand_major(const Plan &p) { return p.mt == 0 ? 1 : p.mt == MT_KS ? p.rt : 0; }
 int ks_blocks_for(int type) {
     return type == TYPE_Q4_K ? ks_blocks<TYPE_Q4_K>() : type == TYPE_Q5_K ? ks_blocks<TYPE_Q5_K>() : ks_blocks<TYPE_Q6_K>();
 }
 
+// mt, rt and tile_rows depend on (type, k, m) only -- the pre-pass plans with n = 1
 Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     Plan p;
-    if (m <= 32 && !getenv("LBQ_GEMM_NO_KS")) {
-        // k-sliced: 128-column workgroups, each a slice of S blocks
+    // two row tiles (m <= 64) for Q6_K (3-19 % faster than its 64-row tiles at
+    // m = 48, 64; for Q4_K / Q5_K the 64-row tiles win on the large matrices).
+    // The choice -- and so the operand layout -- must not depend on n: a grouped
+    // call runs one pre-pass for weights of different n.
+    const bool ks2 = type == TYPE_Q6_K || getenv("LBQ_GEMM_KS64");
+    if (m <= (ks2 ? 64 : 32) && !getenv("LBQ_GEMM_NO_KS")) {
+        // k-sliced: 128-column workgroups of one or two 32-row tiles, each a
+        // slice of S blocks
         p.mt = MT_KS;
+        p.rt = m <= 32 ? 1 : 2;
         p.tiles_m = 1;
         p.tiles_n = (int)((n + KSN - 1) / KSN);
         // blocks per slice: 4, fewer (down to 2) until the grid has a workgroup
-        // per CU (measured at m = 16 on the Llama-3 shapes, 1 to 4 blocks)
+        // per CU (measured at m = 16 on the Llama-3 shapes, 1 to 4 blocks); two
+        // row tiles: 2 (the activation slice is 32 KB per block)
         const int nb = (int)(k / KB);
-        int bps = ks_blocks_for(type);
+        const int smax = p.rt == 1 ? ks_blocks_for(type) : 2;
+        int bps = smax;
         while (bps > 2 && (int64_t)p.tiles_n * ((nb + bps - 1) / bps) < (int64_t)num_cus()) bps--;
-        if (const char *e = getenv("LBQ_GEMM_KS")) bps = std::max(1, std::min(atoi(e), ks_blocks_for(type)));  // tuning
+        if (const char *e = getenv("LBQ_GEMM_KS")) bps = std::max(1, std::min(atoi(e), smax));  // tuning
         p.bps = bps;
         p.splits = (nb + bps - 1) / bps;
         return p;
@@ -1174,7 +1198,7 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     if (const char *e = getenv("LBQ_GEMM_BIG")) wide = e[0] != 't' || m < 256;  // tuning override: "wide" or "tall"
     if (m >= 128 && big_ok) p.mt = wide ? MT_WIDE : 8;
     else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
-    const int rows = tile_rows(p.mt), cols = p.mt == 8 ? TBN : BN;
+    const int rows = tile_rows(p), cols = p.mt == 8 ? TBN : BN;
     p.tiles_m = (int)((m + rows - 1) / rows);
     p.tiles_n = (int)((n + cols - 1) / cols);
     const int nb = (int)(k / KB);
@@ -1195,15 +1219,16 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
     const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
     if (p.mt == MT_KS) {
-        switch (p.bps) {  // slice length (within the type's register budget)
-        case 1: k_gemm_ks<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
-        case 2: k_gemm_ks<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
-        case 3:
-            if constexpr (ks_blocks<TYPE>() >= 3) k_gemm_ks<TYPE, 3><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
-            break;
-        default:
-            if constexpr (ks_blocks<TYPE>() >= 4) k_gemm_ks<TYPE, 4><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
-            break;
+        if (p.rt == 2) {  // two row tiles: slices of 1 or 2 blocks
+            if (p.bps == 1) k_gemm_ks<TYPE, 1, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+            else k_gemm_ks<TYPE, 2, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+            return hipGetLastError();
+        }
+        switch (p.bps) {  // slice length
+        case 1: k_gemm_ks<TYPE, 1, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+        case 2: k_gemm_ks<TYPE, 2, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+        case 3: k_gemm_ks<TYPE, 3, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+        default: k_gemm_ks<TYPE, 4, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
         }
         return hipGetLastError();
     }
@@ -1235,7 +1260,7 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
     auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     WsLayout L;
     L.a_off = 0;
-    L.e_off = L.a_off + up((size_t)p.tiles_m * tile_rows(p.mt) * (size_t)k * sizeof(_Float16));  // whole row tiles
+    L.e_off = L.a_off + up((size_t)p.tiles_m * tile_rows(p) * (size_t)k * sizeof(_Float16));  // whole row tiles
     L.part_off = L.e_off + up((size_t)m * sizeof(int));
     L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
     return L;
@@ -1262,11 +1287,11 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     if (x) {
         if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
         // few rows: one pass of 1024 threads per row; many rows: 256-thread workgroups
-        if (m <= 64) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p.mt));
-        else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, operand_major(p.mt));
+        if (m <= 64) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p));
+        else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, operand_major(p));
     } else {
-        if (m <= 64) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p.mt));
-        else k_act_f16<256><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, operand_major(p.mt));
+        if (m <= 64) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p));
+        else k_act_f16<256><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, operand_major(p));
     }
     return hipGetLastError();
 }

@@ -295,7 +295,7 @@ def test_qmatmul_group_matches_separate_calls(oracle, lbq, dev, t):
     for k, ns in ((4096, (512, 128, 128)), (1024, (300, 77)), (14336, (64, 33, 96, 5))):
         raws = [bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3) for n in ns]
         qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
-        for m in (1, 3, 20):
+        for m in (1, 3, 20, 48):
             x = rng.standard_normal((m, k)).astype(np.float32)
             for shift in ((0, 1) if m == 1 else (0,)):
                 buf = to_dev(np.concatenate([np.zeros(shift, np.float32), x.ravel()]), dev)
@@ -308,6 +308,10 @@ def test_qmatmul_group_matches_separate_calls(oracle, lbq, dev, t):
             if m == 1:
                 for y, r, n in zip(ys, raws, ns):
                     assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, x, nthreads=8).astype(np.float64))
+            if m == 48:  # the shared pre-pass's operand layout matches every member's GEMM
+                for y, r, n in zip(ys, raws, ns):
+                    assert_rows_close(y.cpu().numpy()[::7], oracle.qmatmul(t, r, n, k, x[::7], nthreads=8).astype(np.float64),
+                                      tight_bound(t, m))
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
@@ -323,7 +327,7 @@ def test_gate_up_silu(oracle, lbq, dev, t):
         u_raw = bp.random_blocks(rng, t, n * k // bs, d_scale=1e-3)
         qg = QMatMul.from_qtensor(QTensor(to_dev(g_raw, dev), t, (n, k)))
         qu = QMatMul.from_qtensor(QTensor(to_dev(u_raw, dev), t, (n, k)))
-        for m in (1, 3, 20):
+        for m in (1, 3, 20, 48):
             x = rng.standard_normal((m, k)).astype(np.float32)
             for shift in ((0, 1) if m == 1 else (0,)):
                 buf = to_dev(np.concatenate([np.zeros(shift, np.float32), x.ravel()]), dev)
