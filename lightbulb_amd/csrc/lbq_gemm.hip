@@ -1196,15 +1196,18 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     // MFMA decides (measured per type and m: 128, 256, 512, 2048)
     bool wide = m < 256 || (type == TYPE_Q4_K && m <= 512);
     if (const char *e = getenv("LBQ_GEMM_BIG")) wide = e[0] != 't' || m < 256;  // tuning override: "wide" or "tall"
-    if (m >= 128 && big_ok) p.mt = wide ? MT_WIDE : 8;
+    // (Q6_K from 65 rows: its 64-row tiles took 66 us at m = 100 where the wide
+    // tiles take 50 at m = 128, 14336 x 4096)
+    if ((m >= 128 || (type == TYPE_Q6_K && m > 64)) && big_ok) p.mt = wide ? MT_WIDE : 8;
     else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
     const int rows = tile_rows(p), cols = p.mt == 8 ? TBN : BN;
     p.tiles_m = (int)((m + rows - 1) / rows);
     p.tiles_n = (int)((n + cols - 1) / cols);
     const int nb = (int)(k / KB);
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-    const int occ = (p.mt >= 4 || type == TYPE_Q6_K || (type == TYPE_Q5_K && p.mt == 2)) ? 1 : 2;  // gemm_occupancy
-    const int64_t slots = (int64_t)num_cus() * occ;
+    // split k until the grid has about one workgroup per CU (also where two fit:
+    // measured at m = 64, more splits only add partial-sum traffic)
+    const int64_t slots = (int64_t)num_cus();
     int s = 1;
     if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
     if (const char *e = getenv("LBQ_GEMM_SPLITS")) s = std::max(1, std::min(atoi(e), nb));  // tuning override
