@@ -77,9 +77,9 @@ __device__ __forceinline__ void codes_to_f16(uint32_t w, float sx, float c, uint
 
 // Where the pre-pass puts the 8 operand values at k-order position 8*p8 of block
 // b of row m (p8 = 16h + s: lane half h, k-step s).  Row-major ([m][k], the
-// tiled kernels stage it through LDS) or, for the skinny kernel (m <= 32),
-// operand-major: the 64 lanes' operands of one (block, k-step) are 1 KB in a
-// row, so each k-step's A operand is a single contiguous load.
+// tiled kernels stage it through LDS) or, for the k-sliced kernel (m <= 64),
+// operand-major: the 64 lanes' operands of one (block, 32-row tile, k-step) are
+// 1 KB in a row, so each k-step's A operand is a single contiguous read.
 __device__ __forceinline__ int64_t op_pos(int opmajor, int64_t m, int64_t b, int p8, int64_t K) {
     // opmajor = number of 32-row tiles (0: row-major); operand-major order is
     // block, row tile, k-step, lane
@@ -894,107 +894,6 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
 }
 
 // ---------------------------------------------------------------------------
-// Skinny tiles for m <= 32: the weight stream, not the MFMA work, sets the time,
-// so waves stream independently instead of sharing an LDS activation tile.  A
-// workgroup owns 32 columns (one 32x32 MFMA tile of y) and 4*KC consecutive
-// blocks of k; wave w takes blocks KC*w .. KC*w + KC - 1 of them, with the raw
-// weight bytes of the next two blocks in flight (three-slot ring) and the fp16
-// activation operands of the next block in a 16-slot ring (slot s = k-step s,
-// read straight from the operand rows in L2).  The four waves' tiles are added
-// through LDS in a fixed order at the end; a grid of several k-slices writes
-// partial sums that k_split_sum adds.  Lane (lr, h) serves weight row n0 + lr and
-// half h of every block (the GB operand builders, as in k_gemm).
-// ---------------------------------------------------------------------------
-constexpr int SKB = 32;  // columns per skinny workgroup
-
-template <int TYPE>
-__global__ __launch_bounds__(256, 2) void k_gemm_s(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
-                                                   const _Float16 *__restrict__ A, const int *__restrict__ erow,
-                                                   int64_t K, int64_t M, float *__restrict__ out, int kc, int slices,
-                                                   int64_t split_stride) {
-    using B = GB<TYPE>;
-    __shared__ float red[3][64][17];  // waves 1..3's tiles for the reduction (padded)
-    const int tn = (int)blockIdx.x / slices, z = (int)blockIdx.x % slices;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
-    const int nb = (int)(K / KB);
-    const int wb0 = (z * 4 + wave) * kc, wb1 = min(nb, wb0 + kc);  // this wave's blocks (may be empty)
-    const int64_t n0 = (int64_t)tn * SKB;
-    const uint8_t *wrow = W + min(n0 + lr, N - 1) * row_bytes;
-    // operand-major activations: (block, k-step) -> 64 lanes x 8 halfs; rows past
-    // M hold garbage, their outputs are dropped
-    const _Float16 *aop = A + lane * 8;
-
-    floatx16 acc;
-#pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.f;
-
-    if (wb0 < wb1) {
-        typename B::Raw raw[3];
-        typename B::Prep p;
-        half8 ar[16];
-        auto w_load = [&](int b, int slot) {
-            const uint8_t *blk = wrow + (int64_t)min(b, wb1 - 1) * B::BYTES;  // clamped: re-reads the last block
-#pragma unroll
-            for (int i = 0; i < B::NL; i++) B::load_part(blk, h, raw[slot], i);
-        };
-        auto a_load = [&](int b, int s) {
-            ar[s] = *reinterpret_cast<const half8 *>(aop + ((int64_t)min(b, wb1 - 1) * 16 + s) * 512);
-        };
-        // prologue: blocks wb0 .. wb0 + 2 in flight, block wb0's operands
-        w_load(wb0, 0);
-#pragma unroll
-        for (int s = 0; s < 16; s++) a_load(wb0, s);
-        w_load(wb0 + 1, 1);
-        w_load(wb0 + 2, 2);
-        gb_prep<TYPE>(raw[0], h, wrow + (int64_t)wb0 * B::BYTES, p);
-
-        // block b in ring slot `slot`: 16 k-steps; the A slot of each step is
-        // refilled with the next block's step; at the end the next block's
-        // scales are prepared and block b + 3's bytes go into this slot
-        auto block = [&](int b, int slot) {
-#pragma unroll
-            for (int s = 0; s < 16; s++) {
-                uint32_t bw[4];
-#pragma unroll
-                for (int d = 0; d < 4; d++) bw[d] = B::dw(p, s, d);
-                const half8 bo = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ar[s], bo, acc, 0, 0, 0);
-                a_load(b + 1, s);
-            }
-            const int nslot = slot == 2 ? 0 : slot + 1;
-            gb_prep<TYPE>(raw[nslot], h, wrow + (int64_t)min(b + 1, wb1 - 1) * B::BYTES, p);
-            w_load(b + 3, slot);
-        };
-        for (int b = wb0; b < wb1; b += 3) {
-            block(b, 0);
-            if (b + 1 < wb1) block(b + 1, 1);
-            if (b + 2 < wb1) block(b + 2, 2);
-        }
-    }
-
-    // fixed-order reduction of the four waves' tiles: waves 1..3 park theirs in LDS
-    if (wave > 0) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) red[wave - 1][lane][v] = acc[v];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int w = 0; w < 3; w++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[v] += red[w][lane][v];
-        float *y = out + (int64_t)z * split_stride;
-        const int64_t n = n0 + lr;
-        // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int r = 8 * (v >> 2) + 4 * h + (v & 3);
-            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[v], erow[r]);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // K-sliced tiles for m <= 32.  A workgroup owns 128 columns (32 per wave) and a
 // slice of S consecutive blocks of k that its four waves share.  The slice's
 // activation operands (16 KB per block, operand-major) go into LDS by buffer
@@ -1129,17 +1028,15 @@ __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ par
 namespace {
 
 struct Plan {
-    int mt, tiles_m, tiles_n, splits, bps;  // mt = 0: skinny (m <= 32; bps = blocks per wave)
+    int mt, tiles_m, tiles_n, splits, bps;  // bps: blocks of k per split
     int rt = 1;                             // k-sliced kernel: 32-row tiles per workgroup
 };
 
 // mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256)
 constexpr int MT_WIDE = 16, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 64)
-int tile_rows(const Plan &p) {
-    return p.mt == 0 ? 32 : p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TBM : p.mt == MT_WIDE ? WBM : 32 * p.mt;
-}
+int tile_rows(const Plan &p) { return p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TBM : p.mt == MT_WIDE ? WBM : 32 * p.mt; }
 // the pre-pass layout: 32-row tiles of operand-major rows, or 0 (row-major)
-int operand_major(const Plan &p) { return p.mt == 0 ? 1 : p.mt == MT_KS ? p.rt : 0; }
+int operand_major(const Plan &p) { return p.mt == MT_KS ? p.rt : 0; }
 int ks_blocks_for(int type) {
     return type == TYPE_Q4_K ? ks_blocks<TYPE_Q4_K>() : type == TYPE_Q5_K ? ks_blocks<TYPE_Q5_K>() : ks_blocks<TYPE_Q6_K>();
 }
@@ -1169,22 +1066,6 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
         if (const char *e = getenv("LBQ_GEMM_KS")) bps = std::max(1, std::min(atoi(e), smax));  // tuning
         p.bps = bps;
         p.splits = (nb + bps - 1) / bps;
-        return p;
-    }
-    // Q6_K's skinny variant measured slower than its 32-row tiles (register-heavy raw blocks)
-    if (m <= 32 && type != TYPE_Q6_K && !getenv("LBQ_GEMM_NO_SKINNY")) {
-        // skinny: 32-column workgroups of four waves, each wave kc blocks; about
-        // 2048 waves over the chip (eight per CU), slices of 4*kc blocks
-        p.mt = 0;
-        p.tiles_m = 1;
-        p.tiles_n = (int)((n + SKB - 1) / SKB);
-        const int nb = (int)(k / KB);
-        const int64_t work = (int64_t)p.tiles_n * nb;  // (column tile, block) units
-        int kc = (int)std::max<int64_t>(1, (work + 2047) / 2048);
-        kc = std::min(kc, (nb + 3) / 4);
-        if (const char *e = getenv("LBQ_GEMM_KC")) kc = std::max(1, atoi(e));  // tuning override
-        p.bps = kc;
-        p.splits = (nb + 4 * kc - 1) / (4 * kc);
         return p;
     }
     // the wide and tall kernels address a tile's operand rows through a buffer
@@ -1234,13 +1115,6 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
         default: k_gemm_ks<TYPE, 4, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
         }
         return hipGetLastError();
-    }
-    if (p.mt == 0) {
-        if constexpr (TYPE != TYPE_Q6_K) {
-            k_gemm_s<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, p.bps, p.splits, split_stride);
-            return hipGetLastError();
-        }
-        return hipErrorInvalidValue;
     }
     switch (p.mt) {
     case 8: k_gemm_t<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;

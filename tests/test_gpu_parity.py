@@ -532,6 +532,29 @@ def test_split_k_shapes_deterministic(oracle, lbq, dev, t):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_gemm_routing_overrides(oracle, lbq, dev, t, monkeypatch):
+    # the kernels a shape reaches only through the tuning overrides stay correct:
+    # 32-row tiles at m <= 32, k-sliced two-row tiles for Q4_K / Q5_K, wide tiles
+    # where tall ones are chosen and the reverse, explicit slice and split counts
+    rng = np.random.default_rng(97 + t)
+    n, k = 300, 256 * 6
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    cases = [({"LBQ_GEMM_NO_KS": "1"}, 20), ({"LBQ_GEMM_KS64": "1"}, 50), ({"LBQ_GEMM_KS": "1"}, 24),
+             ({"LBQ_GEMM_BIG": "tall"}, 300), ({"LBQ_GEMM_BIG": "wide"}, 600), ({"LBQ_GEMM_SPLITS": "3"}, 70),
+             ({"LBQ_GEMM_NO_TALL": "1"}, 260)]
+    for env, m in cases:
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        for key, val in env.items():
+            monkeypatch.setenv(key, val)
+        y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        for key in env:
+            monkeypatch.delenv(key)
+        rows = np.r_[0:2, m // 2, m - 2:m]
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y[rows], ref, tight_bound(t, m))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_qmatmul_tall_tiles(oracle, lbq, dev, t):
     # Q5_K / Q6_K at m >= 256 and Q4_K above 512 take the 256 x 128 tiles: ragged
     # m and n, odd and even block counts (Q4_K at m = 256, 300: the wide tiles)
