@@ -375,7 +375,7 @@ struct Fast<TYPE_Q8_0, 1> {
 // NORM (k-quants, nbx <= 32): x is first RMS-normalised as candle's RmsNorm does
 // in f32 -- x / sqrt(sum(x^2) / k + eps) * alpha -- with the sum of squares taken
 // over the whole workgroup (every workgroup holds all of x).
-template <int TYPE, bool NORM, class Between>
+template <int TYPE, bool NORM, int XJ, class Between>
 __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between,
                                                const float *__restrict__ alpha, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -447,8 +447,11 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             }
         }
     } else {
-        // 8 lanes per 32-value block; thread t handles blocks t/8 + 32j (nbx <= 512: one pass)
-        constexpr int MAXJ = 16;
+        // 8 lanes per 32-value block; thread t handles blocks t/8 + 32j, j < XJ
+        // (XJ = ceil(blocks / 32) for the kernel's largest row: every load is
+        // issued, so no more than the row needs)
+        constexpr int MAXJ = XJ;
+        static_assert(MAXJ >= 1 && MAXJ <= 16, "x passes");
         const int sub = threadIdx.x & 7, bt = threadIdx.x >> 3;
         float v[MAXJ][4];
 #pragma unroll
@@ -686,7 +689,8 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
 
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
-    if constexpr (FUSED) quantise_x_lds<TYPE, NORM>(x, nb, sx, issue_ring, alpha, eps);
+    // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 32 per pass
+    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (2 * IT < 16 ? 2 * IT : 16)>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its
