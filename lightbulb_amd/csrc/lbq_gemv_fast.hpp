@@ -447,30 +447,44 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             }
         }
     } else {
-        // 8 lanes per 32-value block; thread t handles blocks t/8 + 32j, j < XJ
-        // (XJ = ceil(blocks / 32) for the kernel's largest row: every load is
-        // issued, so no more than the row needs)
+        // 2 lanes per 32-value block, 16 consecutive values each; thread t handles
+        // blocks t/2 + 128j, j < XJ (XJ = ceil(blocks / 128) for the kernel's
+        // largest row: every load is issued, so no more than the row needs).  The
+        // block maximum is order-free and each code depends on its value and the
+        // block's scale only, so any lane split gives the same bytes.
         constexpr int MAXJ = XJ;
-        static_assert(MAXJ >= 1 && MAXJ <= 16, "x passes");
-        const int sub = threadIdx.x & 7, bt = threadIdx.x >> 3;
-        float v[MAXJ][4];
+        static_assert(MAXJ >= 1 && MAXJ <= 4, "x passes");
+        const int sub = threadIdx.x & 1, bt = threadIdx.x >> 1;
+        float v[MAXJ][16];
 #pragma unroll
         for (int j = 0; j < MAXJ; j++) {
-            const int b = min(bt + 32 * j, nbx - 1);
-            load4f(x + (int64_t)b * QK8_0 + sub * 4, vec, v[j]);
+            const int b = min(bt + 128 * j, nbx - 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) load4f(x + (int64_t)b * QK8_0 + sub * 16 + 4 * i, vec, &v[j][4 * i]);
         }
         __builtin_amdgcn_sched_barrier(0);
         between();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < MAXJ; j++) {
-            if (32 * j < nbx) {  // uniform across the workgroup: shuffles stay convergent
-                __half dh;
-                const uint32_t packed = q8_0_block8(v[j], &dh);
-                const int b = min(bt + 32 * j, nbx - 1);  // clamped duplicates rewrite equal data
+            if (128 * j < nbx) {  // uniform across the workgroup: the shuffle stays convergent
+                float amax = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[j][i]));
+                amax = fmaxf(amax, __shfl_xor(amax, 1));
+                const float d = amax / 127.f;
+                const float id = d != 0.f ? 1.f / d : 0.f;
+                uint32_t packed[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float r = roundf(v[j][i] * id);
+                    const int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.f), 127.f);
+                    packed[i >> 2] |= ((uint32_t)q & 0xffu) << (8 * (i & 3));
+                }
+                const int b = min(bt + 128 * j, nbx - 1);  // clamped duplicates rewrite equal data
                 uint8_t *xb = sx + b * XS_0;
-                *reinterpret_cast<uint32_t *>(xb + sub * 4) = packed;
-                if (sub == 0) *reinterpret_cast<float *>(xb + 32) = __half2float(dh);
+                *reinterpret_cast<uint4 *>(xb + sub * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                if (sub == 0) *reinterpret_cast<float *>(xb + 32) = __half2float(__float2half_rn(d));
             }
         }
     }
@@ -689,8 +703,8 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
 
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
-    // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 32 per pass
-    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (2 * IT < 16 ? 2 * IT : 16)>(x, nb, sx, issue_ring, alpha, eps);
+    // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 128 per pass
+    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, ((IT + 1) / 2 < 4 ? (IT + 1) / 2 : 4)>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its
