@@ -375,22 +375,23 @@ struct Fast<TYPE_Q8_0, 1> {
 // NORM (k-quants, nbx <= 32): x is first RMS-normalised as candle's RmsNorm does
 // in f32 -- x / sqrt(sum(x^2) / k + eps) * alpha -- with the sum of squares taken
 // over the whole workgroup (every workgroup holds all of x).
-template <int TYPE, bool NORM, int XJ, class Between>
+template <int TYPE, bool NORM, int XJ, int WPG, class Between>
 __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between,
                                                const float *__restrict__ alpha, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
     if constexpr (TYPE != TYPE_Q8_0) {
         // 16 lanes per 256-value block, 16 consecutive values per lane
-        // (q8k_lane16), so the workgroup quantises 16 blocks per pass (nbx <= 64:
-        // at most 4 passes); a lane's 16 codes are exactly one bsums entry.
-        constexpr int MAXP = NORM ? 2 : 4;
+        // (q8k_lane16), so a workgroup of WPG waves quantises BPP = 4 WPG blocks
+        // per pass (nbx <= 64, 32 with the norm); a lane's 16 codes are exactly
+        // one bsums entry.
+        constexpr int BPP = 4 * WPG, MAXP = (NORM ? 32 : 64) / BPP;
         const int t = threadIdx.x, sub = t & 15;
-        const int np = (nbx + 15) >> 4;  // workgroup-uniform
+        const int np = (nbx + BPP - 1) / BPP;  // workgroup-uniform
         float v[MAXP][16], al[NORM ? MAXP : 1][16];
 #pragma unroll
         for (int j = 0; j < MAXP; j++) {
-            const int b = min(16 * j + (t >> 4), nbx - 1);
+            const int b = min(BPP * j + (t >> 4), nbx - 1);
             const float4 *src = reinterpret_cast<const float4 *>(x + (int64_t)b * QK_K + 16 * sub);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -410,11 +411,11 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
         between();
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (NORM) {
-            __shared__ float red[4];
+            __shared__ float red[WPG];
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < MAXP; j++) {
-                if (j < np && 16 * j + (t >> 4) < nbx) {  // clamped duplicates do not count
+                if (j < np && BPP * j + (t >> 4) < nbx) {  // clamped duplicates do not count
 #pragma unroll
                     for (int i = 0; i < 16; i++) ss += v[j][i] * v[j][i];
                 }
@@ -424,7 +425,10 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
                  __int_as_float(rl(__float_as_uint(ss), 32)) + __int_as_float(rl(__float_as_uint(ss), 48));
             if (lane == 0) red[wave] = ss;
             __syncthreads();
-            const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)(nbx * QK_K) + eps);
+            float tot = red[0];
+#pragma unroll
+            for (int w = 1; w < WPG; w++) tot += red[w];
+            const float rms = sqrtf(tot / (float)(nbx * QK_K) + eps);
 #pragma unroll
             for (int j = 0; j < MAXP; j++)
 #pragma unroll
@@ -437,7 +441,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
                 int sum;
                 float d;
                 q8k_lane16(v[j], sub, packed, &sum, &d);
-                const int b = 16 * j + (t >> 4);
+                const int b = BPP * j + (t >> 4);
                 if (b < nbx) {
                     uint8_t *xb = sx + b * XS_K;
                     *reinterpret_cast<uint4 *>(xb + 16 * sub) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
@@ -448,7 +452,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
         }
     } else {
         // 2 lanes per 32-value block, 16 consecutive values each; thread t handles
-        // blocks t/2 + 128j, j < XJ (XJ = ceil(blocks / 128) for the kernel's
+        // blocks t/2 + 32 WPG j, j < XJ (XJ = ceil(blocks / (32 WPG)) for the kernel's
         // largest row: every load is issued, so no more than the row needs).  The
         // block maximum is order-free and each code depends on its value and the
         // block's scale only, so any lane split gives the same bytes.
@@ -458,7 +462,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
         float v[MAXJ][16];
 #pragma unroll
         for (int j = 0; j < MAXJ; j++) {
-            const int b = min(bt + 128 * j, nbx - 1);
+            const int b = min(bt + 32 * WPG * j, nbx - 1);
 #pragma unroll
             for (int i = 0; i < 4; i++) load4f(x + (int64_t)b * QK8_0 + sub * 16 + 4 * i, vec, &v[j][4 * i]);
         }
@@ -467,7 +471,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < MAXJ; j++) {
-            if (128 * j < nbx) {  // uniform across the workgroup: the shuffle stays convergent
+            if (32 * WPG * j < nbx) {  // uniform across the workgroup: the shuffle stays convergent
                 float amax = 0.f;
 #pragma unroll
                 for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[j][i]));
@@ -481,7 +485,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
                     const int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.f), 127.f);
                     packed[i >> 2] |= ((uint32_t)q & 0xffu) << (8 * (i & 3));
                 }
-                const int b = min(bt + 128 * j, nbx - 1);  // clamped duplicates rewrite equal data
+                const int b = min(bt + 32 * WPG * j, nbx - 1);  // clamped duplicates rewrite equal data
                 uint8_t *xb = sx + b * XS_0;
                 *reinterpret_cast<uint4 *>(xb + sub * 16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
                 if (sub == 0) *reinterpret_cast<float *>(xb + 32) = __half2float(__float2half_rn(d));
@@ -607,9 +611,10 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
-template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false>
-__global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
-                                               ActView act, const float *__restrict__ alpha, float eps) {
+template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4>
+__global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
+                                                    ActView act, const float *__restrict__ alpha, float eps) {
+    static_assert(WPG == 4 || (FUSED && WPG == 8), "waves per workgroup: 4, or 8 for the fused prologue");
     static_assert(!NORM || (FUSED && TYPE != TYPE_Q8_0), "the RMS norm runs in the quantising prologue");
     static_assert(MR == 1 || (!FUSED && MAP == MAP_ONE), "several activation rows: pre-quantised, one weight");
     constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
@@ -635,7 +640,7 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
     // silu pairs are never split between waves: ranges are counted in pairs
     constexpr int GPU_ = PAIRED ? 2 / RPW : 1;  // row groups per unit
     const int64_t ng = PAIRED ? n / 2 : (n + RPW - 1) / RPW;
-    const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
+    const int64_t gw = (int64_t)blockIdx.x * WPG + wave, nw = (int64_t)gridDim.x * WPG;
     const int64_t per = ng / nw, rem = ng % nw;
     const int64_t g0 = (gw * per + (gw < rem ? gw : rem)) * GPU_, g1 = g0 + (per + (gw < rem ? 1 : 0)) * GPU_;
 
@@ -703,8 +708,9 @@ __global__ __launch_bounds__(256) void k_gemv1(RowMap rm, int64_t row_bytes, int
 
     extern __shared__ __align__(16) uint8_t sx[];
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
-    // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 128 per pass
-    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, ((IT + 1) / 2 < 4 ? (IT + 1) / 2 : 4)>(x, nb, sx, issue_ring, alpha, eps);
+    // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 32 WPG per pass
+    constexpr int XJ = (64 * IT + 32 * WPG - 1) / (32 * WPG);
+    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (XJ < 4 ? XJ : 4), WPG>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its

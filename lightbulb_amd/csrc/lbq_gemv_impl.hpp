@@ -698,15 +698,30 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // weight); the RMS norm (alpha != nullptr) only k-quant row maps with k <= 8192
     constexpr bool NORM_OK = TYPE != TYPE_Q8_0 && BPI * IT <= 32;
     if (alpha && (!NORM_OK || nb > 32 || !x || map == MAP_ONE)) return hipErrorNotSupported;
+    // Fused launches of Q4_K / Q5_K that run eight waves per CU anyway (n >= 8192)
+    // take eight-wave workgroups: one x prologue per CU instead of two, spread
+    // over 512 threads (gate/up 14336 x 4096: 9.1 -> 8.7 us; where one four-wave
+    // workgroup per CU was chosen, eight waves measured slower).
+    constexpr bool W8_OK = TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K;
+    bool w8 = W8_OK && wpc == 8;
+    if (const char *e = getenv("LBQ_GEMV1_WPG")) w8 = W8_OK && atoi(e) == 8;
+    const unsigned grid8 = (unsigned)((waves + 7) / 8);
+    auto fused = [&](auto k4, auto k8, const float *al, float ep) {
+        if (w8) k8<<<grid8, 512, lds, st>>>(rm, row_bytes, nb, x, act, al, ep);
+        else k4<<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, al, ep);
+    };
+    constexpr int W8 = W8_OK ? 8 : 4;  // (no eight-wave instantiations for the other types)
     if (map == MAP_SILU_PAIRS) {
         if constexpr (RPW <= 2) {
             if (!x || (n & 1)) return hipErrorNotSupported;
             if constexpr (NORM_OK)
                 if (alpha) {
-                    k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                    fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS, true>,
+                          k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS, true, W8>, alpha, eps);
                     return hipGetLastError();
                 }
-            k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+            fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS>,
+                  k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SILU_PAIRS, false, W8>, nullptr, 0.f);
         } else {
             return hipErrorNotSupported;
         }
@@ -714,12 +729,15 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
         if (!x) return hipErrorNotSupported;
         if constexpr (NORM_OK)
             if (alpha) {
-                k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, true><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, alpha, eps);
+                fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, true>,
+                      k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, true, W8>, alpha, eps);
                 return hipGetLastError();
             }
-        k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS>,
+              k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, false, W8>, nullptr, 0.f);
     } else if (x) {
-        k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
+        fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE>, k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, W8>,
+              nullptr, 0.f);
     } else {
         k_gemv1<TYPE, PPB, RPW, IT, 1, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     }
