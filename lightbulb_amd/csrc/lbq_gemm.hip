@@ -1163,11 +1163,12 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     int *erow = reinterpret_cast<int *>(base + L.e_off);
     if (x) {
         if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
-        // few rows: one pass of 1024 threads per row; many rows: 256-thread workgroups
-        if (m <= 64) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p));
+        // few rows, or long rows up to 1024 of them: one pass of 1024 threads per
+        // row; otherwise 256-thread workgroups (measured at m = 512 and 2048)
+        if (m <= 64 || (k > 8192 && m <= 1024)) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p));
         else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, operand_major(p));
     } else {
-        if (m <= 64) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p));
+        if (m <= 64 || (k > 8192 && m <= 1024)) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p));
         else k_act_f16<256><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, operand_major(p));
     }
     return hipGetLastError();
