@@ -283,7 +283,8 @@ def main():
             "frac": round(full_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
             "kernel": "k_gemv1<Q4_K, fused> (quantise x + dequant/int-dot GEMV, one launch per projection: "
-                      "4 lanes per block at k = 4096, 8 at k = 14336); algorithmic bytes per launch = "
+                      "4 lanes per block at k = 4096, 8 at k = 14336; eight-wave workgroups for gate/up); "
+                      "algorithmic bytes per launch = "
                       "N*K/256*144 + 4K + 4N, averaged over the 7 launches",
             "us_per_launch": round(ms_full * 1e3 / len(LAYER), 3),
             "algorithmic_bytes_per_launch": round((layer_bytes + io_bytes) / len(LAYER)),
