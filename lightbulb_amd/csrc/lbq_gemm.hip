@@ -13,6 +13,12 @@
 // So the products differ from the reference's by two fp16 roundings (relative
 // <= 2^-11 each) and the sum by f32 summation order: about 4e-4 relative on a row.
 //
+// Kernels by m (plan_for): k_gemm_ks, k-sliced 32- or 64-row tiles, for m <= 32
+// (Q6_K: 64); k_gemm<MT>, 32*MT-row tiles, up to 127 rows (Q6_K: 64); k_gemm_w,
+// eight-wave 128 x 256 tiles, from 128 rows (Q6_K: 65) below 256 (Q4_K: up to
+// 512); k_gemm_t, 256 x 128 tiles, above.  Each has its own description below;
+// the work split of k_gemm<MT>, on which the others build, follows.
+//
 // Work split.  A 256-thread workgroup owns BM = 32*MT rows of y and BN = 256
 // columns; wave w owns columns 64w..64w+63 (two 32-column MFMA tiles) for all BM
 // rows (MT 32-row tiles).  Lane l serves weight rows 32j + l%32 (j = 0, 1) and the

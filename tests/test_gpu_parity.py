@@ -488,9 +488,9 @@ def test_batch_decode_row_chunks(oracle, lbq, dev, t):
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
 @pytest.mark.parametrize("k", [4096, 14336])
-def test_skinny_tiles_split_k(oracle, lbq, dev, t, k):
-    # 9 <= m <= 32 takes the 32-row MFMA tiles with k split over waves and
-    # workgroups: ragged m and n, both Llama-3 row lengths
+def test_ksliced_tiles_split_k(oracle, lbq, dev, t, k):
+    # 9 <= m <= 32 takes the k-sliced tiles (32 rows x 128 columns, k split over
+    # workgroups): ragged m and n, both Llama-3 row lengths
     rng = np.random.default_rng(95 + t + k)
     for n in (40, 1000):
         w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
