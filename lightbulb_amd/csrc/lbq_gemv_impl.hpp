@@ -688,7 +688,8 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // Measured (fused / pre-quantised x): Q4_K 4096 x 4096 5.0 / 4.5 us at 4 vs
     // 5.7 / 4.6 at 8; 14336 x 4096 9.3 / 8.8 at 4 vs 9.1 / 8.4 at 8; 4096 x 14336
     // 10.1 / 8.2 at 4 vs 11.2 / 9.0 at 8; Q6_K 14336 x 4096 14.4 at 4 vs 16.1 at 8.
-    int wpc = (TYPE == TYPE_Q6_K || (n < 8192 && (x || nb > 32))) ? 4 : 8;
+    // Q8_0 takes eight everywhere (4096 x 4096 fused: 6.2 us at 4, 5.7 at 8).
+    int wpc = (TYPE == TYPE_Q6_K || (TYPE != TYPE_Q8_0 && n < 8192 && (x || nb > 32))) ? 4 : 8;
     if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
