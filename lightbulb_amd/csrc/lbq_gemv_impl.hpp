@@ -704,7 +704,10 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // over 512 threads (gate/up 14336 x 4096: 9.1 -> 8.7 us; where one four-wave
     // workgroup per CU was chosen, eight waves measured slower).
     constexpr bool W8_OK = TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K;
-    bool w8 = W8_OK && wpc == 8;
+    // So does the grouped q|k|v launch (6144 rows at k = 4096: grouped step 37.6 -> 37.2 us;
+    // at 4096 rows the four-wave workgroups stay ahead).
+    bool w8 = W8_OK && (wpc == 8 || (n > 4096 && nb <= 32));
+    if (w8 && wpc < 8) waves = std::min<int64_t>((int64_t)num_cus() * 8, ng);
     if (const char *e = getenv("LBQ_GEMV1_WPG")) w8 = W8_OK && atoi(e) == 8;
     const unsigned grid8 = (unsigned)((waves + 7) / 8);
     auto fused = [&](auto k4, auto k8, const float *al, float ep) {
