@@ -441,6 +441,47 @@ def test_rmsnorm_fused_projections(oracle, lbq, dev, t):
             assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, 2e-3)
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+def test_eight_wave_fused_launches(oracle, lbq, dev, t):
+    # fused m = 1 launches on eight-wave workgroups: grouped q|k|v at Llama-3
+    # sizes (6144 rows), gate/up pairs past 8192 rows and both with the RMS norm
+    # in the prologue; grouped outputs bit-identical to the separate (four-wave)
+    # calls, all against the oracle
+    from lightbulb_amd.quantized import (QMatMul, QTensor, gate_up_silu, qmatmul_group, rmsnorm_gate_up_silu,
+                                         rmsnorm_qmatmul_group)
+    rng = np.random.default_rng(180 + t)
+    k, ns = 4096, (4096, 1024, 1024)
+    raws = [bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3) for n in ns]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    xd = to_dev(x, dev)
+    ys = qmatmul_group(qms, xd)
+    singles = [q.forward(xd) for q in qms]
+    torch.cuda.synchronize()
+    for y, y1, r, n in zip(ys, singles, raws, ns):
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), y1.cpu().numpy().view(np.uint32))
+        assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, x, nthreads=8).astype(np.float64))
+    w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    wd = to_dev(w, dev)
+    xn = _rms_norm_ref(x, w, 1e-5)
+    ys = rmsnorm_qmatmul_group(qms, xd, wd, 1e-5)
+    torch.cuda.synchronize()
+    for y, r, n in zip(ys, raws, ns):
+        assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, xn, nthreads=8).astype(np.float64), 2e-3)
+    n2 = 4200  # 8400 interleaved rows
+    g_raw = bp.random_blocks(rng, t, n2 * k // 256, d_scale=1e-3)
+    u_raw = bp.random_blocks(rng, t, n2 * k // 256, d_scale=1e-3)
+    qg = QMatMul.from_qtensor(QTensor(to_dev(g_raw, dev), t, (n2, k)))
+    qu = QMatMul.from_qtensor(QTensor(to_dev(u_raw, dev), t, (n2, k)))
+    for fn, xin, xr, tol in ((lambda: gate_up_silu(qg, qu, xd), x, x, 1e-4),
+                             (lambda: rmsnorm_gate_up_silu(qg, qu, xd, wd, 1e-5), x, xn, 2e-3)):
+        out = fn()
+        torch.cuda.synchronize()
+        gr = oracle.qmatmul(t, g_raw, n2, k, xr, nthreads=8).astype(np.float64)
+        ur = oracle.qmatmul(t, u_raw, n2, k, xr, nthreads=8).astype(np.float64)
+        assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, tol)
+
+
 def test_qmatmul_group_errors(oracle, lbq, dev):
     from lightbulb_amd import _lib
     from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
