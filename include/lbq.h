@@ -54,8 +54,8 @@ enum lbq_status {
 
 /* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
 enum lbq_ggml_type {
-    LBQ_TYPE_F32 = 0,  /* dense; dequantisation (a copy) only */
-    LBQ_TYPE_F16 = 1,  /* dense; dequantisation (exact widening) only */
+    LBQ_TYPE_F32 = 0,  /* dense: an f32 matmul (candle's dense QMatMul variant), k % 8 == 0 */
+    LBQ_TYPE_F16 = 1,  /* dense: widened exactly to f32, then as F32 */
     LBQ_TYPE_Q4_0 = 2, /* 32-value blocks, Q8_0 activations */
     LBQ_TYPE_Q4_1 = 3, /* 32-value blocks, Q8_1 activations */
     LBQ_TYPE_Q5_0 = 6, /* 32-value blocks, Q8_0 activations */
@@ -74,9 +74,18 @@ enum lbq_ggml_type {
 const char *lbq_last_error(void);
 
 /* GgmlDType::block_size / type_size (/root/reference/src/quantization/mod.rs:99-126)
- * for the types above; 0 for any other id. */
+ * for the types above; 0 for any other id.  lbq_type_size returns the table's
+ * value, so GGUF extents computed from it agree with the reference's
+ * extract_tensor_bytes (src/quantization/gguf_ops.rs:19-59); for Q2_K that is 82. */
 int lbq_type_block_size(uint32_t ggml_type);
 int lbq_type_size(uint32_t ggml_type);
+
+/* Bytes of one block as it sits in device memory and as the kernels read it
+ * (candle's BlockQ2K: scales[16], qs[64], d, dmin): equal to lbq_type_size except
+ * for Q2_K, whose block is 84 bytes.  Weight handles take
+ * n * (k / block_size) * lbq_type_block_bytes bytes.  No counterpart in the
+ * reference, whose table (mod.rs:118) is 2 bytes short for Q2_K. */
+int lbq_type_block_bytes(uint32_t ggml_type);
 
 /* Open a context on HIP device `device`.  Replaces the device selection at
  * /root/reference/src/model/parallel_model_manager.rs:239-248. */
@@ -88,7 +97,7 @@ int lbq_ctx_destroy(lbq_ctx *ctx);
  * (called at /root/reference/src/model/custom_attention.rs:195-206,
  * mlp_wrapper.rs:127-135, custom_transformer.rs:360-363) together with the
  * upload done by Content::tensor (src/gguf/mod.rs:274-282).
- * nbytes must equal n * (k / block_size) * type_size. */
+ * nbytes must equal n * (k / block_size) * lbq_type_block_bytes. */
 int lbq_weight_create(lbq_ctx *ctx, uint32_t ggml_type, int64_t n, int64_t k, const void *host_blocks,
                       size_t nbytes, lbq_weight **out_w);
 
@@ -106,11 +115,13 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * reached through /root/reference/src/model/quantizable_linear.rs:67).
  * x and y are contiguous f32 device buffers; any leading dims of the
  * reference's [.., k] tensor are flattened into m.  The activation is
- * quantised to Q8_K (k-quant weights) or Q8_0 (Q8_0 weights) exactly as the
- * reference CPU path does.  For m <= 8 (and Q8_0) each output is formed from
- * integer sub-block dot products as in the reference; for k-quant weights at
- * m > 8 the products run on MFMA from fp16 roundings of the same activation
- * and weight values (about 4e-4 relative on a row).  m == 0 is a no-op. */
+ * quantised to Q8_K (k-quant weights), Q8_1 (Q4_1/Q5_1) or Q8_0 (the other
+ * 32-value types) exactly as the reference CPU path does.  For m <= 8 each
+ * output is formed from integer sub-block dot products as in the reference;
+ * for Q4_K/Q5_K/Q6_K/Q8_0 weights at m > 8 (Q8_0: k % 256 == 0) the products
+ * run on MFMA from fp16 roundings of the same activation and weight values
+ * (about 4e-4 relative on a row).  Dense F32/F16 weights are candle's dense
+ * variant: no quantisation, an f32 matmul.  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
 /* Several weights applied to one x: ys[i][m][n_i] = x . W_i^T, exactly as
@@ -233,8 +244,8 @@ int lbq_gguf_meta_float(const lbq_gguf *g, const char *key, double *out);
 int lbq_gguf_meta_string(const lbq_gguf *g, const char *key, const char **data, size_t *len);
 int lbq_gguf_meta_array(const lbq_gguf *g, const char *key, uint32_t *elem_type, uint64_t *len);
 /* Copy a tensor's blocks into device memory through pinned staging (synchronous):
- * ceil(numel / block_size) * lbq_type_size bytes -- the extent above except for
- * Q2_K, whose GgmlDType entry (82 bytes) is shorter than its 84-byte block. */
+ * ceil(numel / block_size) * lbq_type_block_bytes bytes -- the extent above except
+ * for Q2_K, whose GgmlDType entry (82 bytes) is shorter than its 84-byte block. */
 int lbq_gguf_copy_tensor(const lbq_gguf *g, const char *name, void *d_dst, size_t dst_bytes);
 /* A weight handle straight from the file: the tensor (2-D, ne0 = k, ne1 = n, a
  * served type) goes through pinned staging into device memory the handle owns.

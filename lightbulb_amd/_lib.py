@@ -31,6 +31,7 @@ SIGNATURES = {
     "lbq_last_error": (_c.c_char_p, []),
     "lbq_type_block_size": (_c.c_int, [_U32]),
     "lbq_type_size": (_c.c_int, [_U32]),
+    "lbq_type_block_bytes": (_c.c_int, [_U32]),
     "lbq_init": (_c.c_int, [_c.c_int, _c.POINTER(_VP)]),
     "lbq_ctx_destroy": (_c.c_int, [_VP]),
     "lbq_weight_create": (_c.c_int, [_VP, _U32, _I64, _I64, _VP, _SZ, _c.POINTER(_VP)]),

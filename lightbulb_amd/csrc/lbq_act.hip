@@ -239,6 +239,29 @@ __global__ __launch_bounds__(256) void k_dense_f32(const uint8_t *__restrict__ x
     else y[i] = reinterpret_cast<const float *>(x)[i];
 }
 
+// Embedding rows of an F32 / F16 table (16 values per thread, widened exactly);
+// ids outside [0, n) give NaN rows, as k_embed_rows.
+template <bool F16>
+__global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__ w, int64_t n, int64_t k,
+                                                     const int32_t *__restrict__ ids, int64_t count, int64_t gpr,
+                                                     float *__restrict__ y) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= count * gpr) return;
+    const int64_t i = t / gpr, g = t % gpr;
+    const int64_t id = ids[i];
+    float out[16];
+    if (id < 0 || id >= n) {
+        for (int j = 0; j < 16; j++) out[j] = __int_as_float(0x7fc00000);
+    } else if constexpr (F16) {
+        const unsigned short *src = reinterpret_cast<const unsigned short *>(w) + id * k + 16 * g;
+        for (int j = 0; j < 16; j++) out[j] = h2f(src[j]);
+    } else {
+        const float *src = reinterpret_cast<const float *>(w) + id * k + 16 * g;
+        for (int j = 0; j < 16; j++) out[j] = src[j];
+    }
+    store16(y + t * 16, out);
+}
+
 #pragma clang fp contract(on)
 
 // ---------------------------------------------------------------------------
@@ -303,6 +326,8 @@ hipError_t launch_embedding(int type, const uint8_t *w, int64_t n, int64_t k, in
     const int64_t gpr = k / 16;
     const dim3 grid((unsigned)((count * gpr + 255) / 256));
     switch (type) {
+    case TYPE_F16: k_embed_dense<true><<<grid, 256, 0, st>>>(w, n, k, ids, count, gpr, y); break;
+    case TYPE_F32: k_embed_dense<false><<<grid, 256, 0, st>>>(w, n, k, ids, count, gpr, y); break;
 #define LBQ_EMB(T) \
     case T: k_embed_rows<T><<<grid, 256, 0, st>>>(w, n, row_bytes, ids, count, gpr, y); break;
         LBQ_BLOCK_TYPES(LBQ_EMB)

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -22,6 +23,7 @@ static_assert(LBQ_GROUP_MAX == lbq::GROUP_MAX, "one group limit for the ABI and 
 
 struct lbq_ctx {
     int device;
+    lbq::Tuning tune;     // launch-plan overrides, read from the environment at lbq_init
     std::mutex mu;        // guards scratch growth
     uint8_t *scratch;     // quantised activations (split layout)
     size_t scratch_bytes;
@@ -39,6 +41,7 @@ struct lbq_weight {
     size_t nbytes;
     const uint8_t *d_blocks;
     bool owned;
+    int8_t *d_rexp;  // per-row operand exponents of the MFMA GEMM (types it serves), else null
 };
 
 struct lbq_act {
@@ -50,6 +53,43 @@ struct lbq_act {
 };
 
 namespace lbq {
+namespace {
+thread_local const Tuning *t_tuning = nullptr;
+const Tuning k_default_tuning{};
+int env_int(const char *name) {
+    const char *e = getenv(name);
+    return e ? atoi(e) : 0;
+}
+}  // namespace
+
+Tuning tuning_from_env() {
+    Tuning t;
+    t.gemm_ks64 = getenv("LBQ_GEMM_KS64") != nullptr;
+    t.gemm_no_ks = getenv("LBQ_GEMM_NO_KS") != nullptr;
+    t.gemm_no_tall = getenv("LBQ_GEMM_NO_TALL") != nullptr;
+    t.gemm_ks = std::max(0, env_int("LBQ_GEMM_KS"));
+    if (const char *e = getenv("LBQ_GEMM_BIG")) t.gemm_big = e[0] == 't' ? 2 : 1;
+    t.gemm_splits = std::max(0, env_int("LBQ_GEMM_SPLITS"));
+    t.gemv1_nofuse = getenv("LBQ_GEMV1_NOFUSE") != nullptr;
+    t.gemv_rows_off = getenv("LBQ_GEMV_ROWS_OFF") != nullptr;
+    if (const char *e = getenv("LBQ_GEMV1_CFG")) {
+        int q = 0, r = 0;
+        if (sscanf(e, "%d,%d", &q, &r) == 2 && q > 0 && r > 0) { t.gemv1_ppb = q; t.gemv1_rpw = r; }
+    }
+    t.gemv1_wpc = std::max(0, env_int("LBQ_GEMV1_WPC"));
+    t.gemv1_wpg = std::max(0, env_int("LBQ_GEMV1_WPG"));
+    if (const char *e = getenv("LBQ_GEMV")) {
+        int v[4] = {0, 0, 0, 0};
+        if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)
+            for (int i = 0; i < 4; i++) t.gemv_cfg[i] = v[i];
+    }
+    return t;
+}
+
+const Tuning &tuning() { return t_tuning ? *t_tuning : k_default_tuning; }
+TuningScope::TuningScope(const Tuning *t) : prev(t_tuning) { t_tuning = t; }
+TuningScope::~TuningScope() { t_tuning = prev; }
+
 int num_cus() {
     static int cus = 0;
     if (!cus) {
@@ -81,7 +121,7 @@ int hip_fail(hipError_t e, const char *what) {
 }
 
 bool weight_type_ok(uint32_t t) {
-    return t == LBQ_TYPE_Q8_0 || lbq::is_kquant((int)t) || lbq::is_legacy((int)t);
+    return t == LBQ_TYPE_Q8_0 || lbq::is_kquant((int)t) || lbq::is_legacy((int)t) || lbq::is_dense((int)t);
 }
 
 bool act_type_ok(uint32_t t) { return t == LBQ_TYPE_Q8_K || t == LBQ_TYPE_Q8_0 || t == LBQ_TYPE_Q8_1; }
@@ -174,22 +214,25 @@ int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m
             int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
             if (s) return s;
         }
-        e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ctx->ws, st);
+        e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ctx->ws, st);
     }
     if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
 }
 
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
-    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14)", type);
     const int bs = lbq_type_block_size(type);
     if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
+    if (lbq::is_dense((int)type) && k % 8)
+        return fail(LBQ_ERR_SHAPE, "k = %lld: dense weights need k to be a multiple of 8", (long long)k);
     if (k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "k = %lld exceeds the supported maximum", (long long)k);
     if (n > lbq::MAX_ROWS) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)n);
-    const size_t want = (size_t)n * (size_t)(k / bs) * (size_t)lbq_type_size(type);
+    const size_t want = (size_t)n * (size_t)(k / bs) * (size_t)lbq_type_block_bytes(type);
     if (nbytes != want)
-        return fail(LBQ_ERR_SHAPE, "byte count %zu does not match n*(k/%d)*%d = %zu", nbytes, bs, lbq_type_size(type), want);
+        return fail(LBQ_ERR_SHAPE, "byte count %zu does not match n*(k/%d)*%d = %zu", nbytes, bs, lbq_type_block_bytes(type),
+                    want);
     return LBQ_OK;
 }
 
@@ -201,10 +244,27 @@ int make_weight(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const uint8_t
     w->type = (int)type;
     w->n = n;
     w->k = k;
-    w->row_bytes = (k / lbq_type_block_size(type)) * lbq_type_size(type);
+    w->row_bytes = (k / lbq_type_block_size(type)) * lbq_type_block_bytes(type);
     w->nbytes = nbytes;
     w->d_blocks = dev;
     w->owned = owned;
+    w->d_rexp = nullptr;
+    if (lbq::gemm_serves((int)type, k)) {
+        // the batched GEMM's per-row operand exponents, once per weight (load time):
+        // wait for whatever wrote the blocks on any stream, then one small launch
+        DeviceGuard g(ctx->device);
+        hipError_t e = g.err != hipSuccess ? g.err : hipDeviceSynchronize();
+        void *p = nullptr;
+        if (e == hipSuccess) e = hipMalloc(&p, (size_t)n);
+        if (e == hipSuccess) e = lbq::launch_row_exponents((int)type, dev, n, k, w->row_bytes, static_cast<int8_t *>(p), nullptr);
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) {
+            if (p) (void)hipFree(p);
+            delete w;
+            return hip_fail(e, "per-row exponents of the weight");
+        }
+        w->d_rexp = static_cast<int8_t *>(p);
+    }
     *out = w;
     return LBQ_OK;
 }
@@ -246,7 +306,7 @@ int lbq_type_size(uint32_t t) {
     case LBQ_TYPE_Q5_1: return 24;
     case LBQ_TYPE_Q8_0: return 34;
     case LBQ_TYPE_Q8_1: return 36;
-    case LBQ_TYPE_Q2_K: return 84;
+    case LBQ_TYPE_Q2_K: return 82;  // as GgmlDType::type_size; the block itself is 84 bytes
     case LBQ_TYPE_Q3_K: return 110;
     case LBQ_TYPE_Q4_K: return 144;
     case LBQ_TYPE_Q5_K: return 176;
@@ -255,6 +315,8 @@ int lbq_type_size(uint32_t t) {
     default: return 0;
     }
 }
+
+int lbq_type_block_bytes(uint32_t t) { return t == LBQ_TYPE_Q2_K ? 84 : lbq_type_size(t); }
 
 int lbq_init(int device, lbq_ctx **out_ctx) {
     if (!out_ctx) return fail(LBQ_ERR_INVALID_ARG, "out_ctx is null");
@@ -268,6 +330,7 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
     lbq_ctx *c = new (std::nothrow) lbq_ctx;
     if (!c) return fail(LBQ_ERR_OOM, "host allocation failed");
     c->device = device;
+    c->tune = lbq::tuning_from_env();
     c->scratch = nullptr;
     c->scratch_bytes = 0;
     c->ws = nullptr;
@@ -299,6 +362,7 @@ int lbq_weight_create(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, const v
     if (s) return s;
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     void *d = nullptr;
     hipError_t e = hipMalloc(&d, nbytes);
     if (e != hipSuccess) return fail(LBQ_ERR_OOM, "hipMalloc(%zu) for weight blocks: %s", nbytes, hipGetErrorString(e));
@@ -325,9 +389,10 @@ int lbq_weight_wrap_device(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, co
 
 int lbq_weight_destroy(lbq_weight *w) {
     if (!w) return LBQ_OK;
-    if (w->owned) {
+    if (w->owned || w->d_rexp) {
         DeviceGuard g(w->ctx->device);
-        (void)hipFree(const_cast<uint8_t *>(w->d_blocks));
+        if (w->owned) (void)hipFree(const_cast<uint8_t *>(w->d_blocks));
+        if (w->d_rexp) (void)hipFree(w->d_rexp);
     }
     delete w;
     return LBQ_OK;
@@ -352,7 +417,13 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     const int act_type = lbq::vec_dot_type(w->type);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (lbq::is_dense(w->type)) {
+        // candle's dense variant: an f32 matmul, no activation quantisation
+        hipError_t e = lbq::launch_dense(w->type, w->d_blocks, w->n, w->k, d_x, m, d_y, st);
+        return e == hipSuccess ? LBQ_OK : hip_fail(e, "dense matmul launch");
+    }
     const ActLayout L = act_layout(act_type, m, w->k);
     if (m <= 8 && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
         // decode: the GEMV quantises x in its own prologue -- one launch, no scratch
@@ -362,12 +433,13 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
         return LBQ_OK;
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::has_mfma_gemm(w->type) && lbq::gemm_prepass_fuses_quant(w->k, d_x)) {
+    if (m > 8 && lbq::gemm_prepass_fuses_quant(w->type, w->k, d_x)) {
         // batched: the operand pre-pass quantises x itself
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), "GEMM workspace");
         if (s) return s;
         const lbq::ActView none{nullptr, nullptr, nullptr, w->k, L.nb};
-        hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->n, w->k, w->row_bytes, none, d_x, m, d_y, ctx->ws, st);
+        hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, none, d_x, m, d_y,
+                                        ctx->ws, st);
         if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
         return LBQ_OK;
     }
@@ -399,7 +471,15 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     const int act_type = lbq::vec_dot_type(w0->type);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (lbq::is_dense(w0->type)) {
+        for (int i = 0; i < count; i++) {
+            hipError_t e = lbq::launch_dense(ws[i]->type, ws[i]->d_blocks, ws[i]->n, ws[i]->k, d_x, m, d_ys[i], st);
+            if (e != hipSuccess) return hip_fail(e, "dense matmul launch");
+        }
+        return LBQ_OK;
+    }
     const ActLayout L = act_layout(act_type, m, w0->k);
     // m = 1: every weight's rows in one launch (one row space)
     lbq::RowMap rm = lbq::single_row_map(w0->d_blocks, w0->n, d_ys[0]);
@@ -418,7 +498,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::has_mfma_gemm(w0->type)) {
+    if (m > 8 && lbq::gemm_serves(w0->type, w0->k)) {
         // batched: one operand pre-pass (quantising x itself when it can) shared
         // by every weight's GEMM
         size_t wsb = 0;
@@ -426,7 +506,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
         if (s) return s;
         hipError_t e;
-        if (lbq::gemm_prepass_fuses_quant(w0->k, d_x)) {
+        if (lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x)) {
             const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, L.nb};
             e = lbq::gemm_prepass(w0->type, w0->k, none, d_x, m, ctx->ws, st);
         } else {
@@ -438,7 +518,8 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         }
         if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
         for (int i = 0; i < count; i++) {
-            e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i], ctx->ws, st);
+            e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->d_rexp, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i],
+                               ctx->ws, st);
             if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
         }
         return LBQ_OK;
@@ -472,6 +553,7 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
     if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (m == 1 && lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
         // one launch: both weights' rows interleaved, the product in the epilogue
@@ -540,6 +622,7 @@ int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int
     const lbq_weight *w0 = ws[0];
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
     int64_t rows = 0;
     for (int i = 0; i < count; i++) rows += ws[i]->n;
@@ -580,6 +663,7 @@ int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const l
     if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (m == 1 && !((reinterpret_cast<uintptr_t>(d_norm_w)) & 15u) &&
         lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
@@ -605,6 +689,7 @@ int lbq_act_create(lbq_ctx *ctx, uint32_t act_type, int64_t m, int64_t k, lbq_ac
     if (m > (int64_t)1 << 24 || k / bs > (1 << 24)) return fail(LBQ_ERR_LIMIT, "activation shape exceeds the supported maximum");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     const ActLayout L = act_layout((int)act_type, m, k);
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, L.total);
@@ -645,11 +730,14 @@ int lbq_act_destroy(lbq_act *a) {
 int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *a, float *d_y, void *stream) {
     if (!ctx || !w || !a || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_qmatmul_act_f32");
     if (reinterpret_cast<uintptr_t>(d_y) & 3u) return fail(LBQ_ERR_INVALID_ARG, "y must be a 4-byte aligned f32 buffer");
+    if (lbq::is_dense(w->type))
+        return fail(LBQ_ERR_UNSUPPORTED_TYPE, "dense weight (type %d) takes f32 activations: use lbq_qmatmul_f32", w->type);
     const int want = lbq::vec_dot_type(w->type);
     if (a->act_type != want) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "weight type %d needs activation type %d, got %d", w->type, want, a->act_type);
     if (a->k != w->k) return fail(LBQ_ERR_SHAPE, "activation k = %lld, weight k = %lld", (long long)a->k, (long long)w->k);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     std::lock_guard<std::mutex> lock(ctx->mu);
     return run_dot(ctx, w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
 }
@@ -659,6 +747,7 @@ int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stre
     if (reinterpret_cast<uintptr_t>(d_y) & 15u) return fail(LBQ_ERR_INVALID_ARG, "output must be 16-byte aligned");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipError_t e = lbq::launch_dequant(w->type, w->d_blocks, w->n * w->k, d_y, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
     return LBQ_OK;
@@ -691,6 +780,7 @@ int lbq_embedding_f32(lbq_ctx *ctx, const lbq_weight *w, const int32_t *d_ids, i
     if (count > ((int64_t)1 << 40) / w->k) return fail(LBQ_ERR_LIMIT, "count = %lld exceeds the supported maximum", (long long)count);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
     hipError_t e = lbq::launch_embedding(w->type, w->d_blocks, w->n, w->k, w->row_bytes, d_ids, count, d_out,
                                          static_cast<hipStream_t>(stream));
     return e == hipSuccess ? LBQ_OK : hip_fail(e, "embedding launch");
@@ -713,7 +803,7 @@ int lbq_quantize_act(uint32_t act_type, const float *d_x, int64_t m, int64_t k, 
 
 int lbq_quantize_weights_f32(uint32_t type, const float *d_w, int64_t nelem, void *d_out_blocks, void *stream) {
     if (!d_w || !d_out_blocks) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_quantize_weights_f32");
-    if (!weight_type_ok(type) || type == LBQ_TYPE_Q2_K || type == LBQ_TYPE_Q3_K)
+    if (!weight_type_ok(type) || type == LBQ_TYPE_Q2_K || type == LBQ_TYPE_Q3_K || lbq::is_dense((int)type))
         return fail(LBQ_ERR_UNSUPPORTED_TYPE, "no weight quantiser for ggml type %u", type);
     const int bs = lbq_type_block_size(type);
     if (nelem < 0 || nelem % bs) return fail(LBQ_ERR_SHAPE, "nelem = %lld is not a multiple of %d", (long long)nelem, bs);

@@ -1,0 +1,199 @@
+// lbq_dense.hip -- QMatMul over dense F32 / F16 weights.
+//
+// candle's QMatMul::from_qtensor does not keep F32 / F16 / BF16 tensors
+// quantised: it dequantises them (F16 widened exactly to f32) and forward is a
+// plain f32 matmul, y = x . W^T (the dense variant; the reference reaches it for
+// whatever type output.weight or a projection has, custom_transformer.rs:360-363,
+// custom_attention.rs:195-206, mlp_wrapper.rs:127-135).  Here the weight stays
+// in its file layout ([n][k], f16 or f32) and is widened on the fly:
+//   m <= 8  k_dense_gemv: one wave per weight row at a time, 16-byte weight
+//           loads, f32 FMA against up to 8 activation rows, DPP row sums --
+//           HBM-bound like the quantised decode GEMV;
+//   m > 8   k_dense_gemm: 64 x 128 output tiles on v_mfma_f32_32x32x2_f32
+//           (f32 operands, f32 accumulation), operands staged through LDS.
+// Both compute in f32 throughout; only the summation order differs from
+// candle's, so results agree to f32 rounding (~1e-6 relative on a row).
+#include <algorithm>
+
+#include "lbq_device.hpp"
+#include "lbq_internal.hpp"
+
+namespace lbq {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// 8 consecutive weights of row `row` at column c (c % 8 == 0) widened to f32
+template <bool F16>
+__device__ __forceinline__ void load_w8(const uint8_t *row, int64_t c, float w[8]) {
+    if constexpr (F16) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(row + 2 * c);
+        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w[2 * i] = h2f(d[i] & 0xffffu);
+            w[2 * i + 1] = h2f(d[i] >> 16);
+        }
+    } else {
+        const float4 a = *reinterpret_cast<const float4 *>(row + 4 * c);
+        const float4 b = *reinterpret_cast<const float4 *>(row + 4 * c + 16);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// m <= 8.  Waves take rows gw, gw + nw, ...; a lane covers 8 consecutive
+// columns per 512-column step (k % 8 == 0; a partial last step is masked), UN
+// steps in flight.  x rows are read through the caches (every wave reads all
+// of them).
+// ---------------------------------------------------------------------------
+// 8 consecutive values of x at c (vec: 16-byte aligned, else four-byte loads)
+__device__ __forceinline__ void load_x8(const float *p, bool vec, float v[8]) {
+    load4f(p, vec, v);
+    load4f(p + 4, vec, v + 4);
+}
+
+template <bool F16, int MR>
+__global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ W, int64_t N, int64_t K,
+                                                    const float *__restrict__ x, int m, float *__restrict__ y) {
+    const bool xv = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;  // K % 8 == 0: every row likewise
+    constexpr int UN = 4;
+    constexpr int64_t WB = F16 ? 2 : 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), nw = (int64_t)gridDim.x * 4;
+    for (int64_t r = gw; r < N; r += nw) {
+        const uint8_t *row = W + r * K * WB;
+        float acc[MR];
+#pragma unroll
+        for (int i = 0; i < MR; i++) acc[i] = 0.f;
+        for (int64_t c0 = 0; c0 < K; c0 += 512 * UN) {
+            float w[UN][8];
+#pragma unroll
+            for (int u = 0; u < UN; u++) {
+                const int64_t c = c0 + 512 * u + 8 * lane;
+                if (c < K) load_w8<F16>(row, c, w[u]);
+                else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) w[u][e] = 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UN; u++) {
+                const int64_t c = c0 + 512 * u + 8 * lane;
+                if (c < K) {
+#pragma unroll
+                    for (int i = 0; i < MR; i++) {
+                        if (i < m) {
+                            float xv8[8];
+                            load_x8(x + (int64_t)i * K + c, xv, xv8);
+#pragma unroll
+                            for (int e = 0; e < 8; e++) acc[i] = fmaf(w[u][e], xv8[e], acc[i]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MR; i++) {
+            if (i < m) {
+                const float s = row_sum_f32(acc[i]);
+                const float t = __int_as_float(rl(__float_as_uint(s), 0)) + __int_as_float(rl(__float_as_uint(s), 16)) +
+                                __int_as_float(rl(__float_as_uint(s), 32)) + __int_as_float(rl(__float_as_uint(s), 48));
+                if (lane == 0) y[(int64_t)i * N + r] = t;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// m > 8.  Workgroup tile 64 (m) x 128 (n), four waves; wave w owns columns
+// 32w..32w+31 for all 64 rows (two 32 x 32 MFMA tiles that share the B operand).
+// k advances in stages of 32: x [64][32] and W [128][32] are loaded (f16 widened)
+// and stored k-major into LDS (row stride padded), then 16 k-steps of
+// v_mfma_f32_32x32x2_f32: lane l supplies A[row l%32][k 2s + l/32] and
+// B[k 2s + l/32][column l%32].  Out-of-range rows, columns and k read as zero.
+// ---------------------------------------------------------------------------
+constexpr int DBM = 64, DBN = 128, DBK = 32;
+
+template <bool F16>
+__global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ W, int64_t N, int64_t K,
+                                                    const float *__restrict__ x, int64_t M, float *__restrict__ y) {
+    __shared__ float As[DBK][DBM + 4];
+    __shared__ float Bs[DBK][DBN + 4];
+    constexpr int64_t WB = F16 ? 2 : 4;
+    const bool xv = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.y * DBM, n0 = (int64_t)blockIdx.x * DBN;
+    floatx16 acc[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
+    // staging: x tile 64 x 32 as 512 float4 (2 per thread: row t/8 + 32j, k 4(t%8));
+    // W tile 128 x 32 as 512 runs of 8 (2 per thread: row t/4 + 64j, k 8(t%4))
+    for (int64_t k0 = 0; k0 < K; k0 += DBK) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = (t >> 3) + 32 * j, kk = 4 * (t & 7);
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (m0 + r < M && k0 + kk < K) load4f(x + (m0 + r) * K + k0 + kk, xv, v);
+            As[kk][r] = v[0]; As[kk + 1][r] = v[1]; As[kk + 2][r] = v[2]; As[kk + 3][r] = v[3];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = (t >> 2) + 64 * j, kk = 8 * (t & 3);
+            float w[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (n0 + r < N && k0 + kk < K) load_w8<F16>(W + (n0 + r) * K * WB, k0 + kk, w);
+#pragma unroll
+            for (int e = 0; e < 8; e++) Bs[kk + e][r] = w[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < DBK / 2; s++) {
+            const float b = Bs[2 * s + h][32 * wave + lr];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const float a = As[2 * s + h][32 * i + lr];
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // D layout of a 32 x 32 tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
+    const int64_t n = n0 + 32 * wave + lr;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int64_t m = m0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m < M && n < N) y[m * N + n] = acc[i][v];
+        }
+}
+
+template <bool F16>
+static hipError_t dense_typed(const uint8_t *w, int64_t n, int64_t k, const float *x, int64_t m, float *y,
+                              hipStream_t st) {
+    if (m <= 8) {
+        const int64_t waves = std::min<int64_t>(n, (int64_t)num_cus() * 8);
+        const unsigned grid = (unsigned)((waves + 3) / 4);
+        const int mi = (int)m;
+        if (m == 1) k_dense_gemv<F16, 1><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
+        else if (m <= 2) k_dense_gemv<F16, 2><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
+        else if (m <= 4) k_dense_gemv<F16, 4><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
+        else k_dense_gemv<F16, 8><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)((n + DBN - 1) / DBN), (unsigned)((m + DBM - 1) / DBM));
+    k_dense_gemm<F16><<<grid, 256, 0, st>>>(w, n, k, x, m, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_dense(int type, const uint8_t *w, int64_t n, int64_t k, const float *x, int64_t m, float *y,
+                        hipStream_t st) {
+    if (k % 8 || m > 65535LL * DBM) return hipErrorInvalidValue;
+    if (type == TYPE_F16) return dense_typed<true>(w, n, k, x, m, y, st);
+    if (type == TYPE_F32) return dense_typed<false>(w, n, k, x, m, y, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace lbq

@@ -1,15 +1,19 @@
 // lbq_gemm.hip -- batched path (m > 8): k-quant weights dequantised in registers
 // straight into MFMA operands, activation codes staged through LDS.
 //
-// y[m][n] = 2^e_m * sum_k a[m][k] * w[n][k]   (v_mfma_f32_32x32x16_f16, f32 accumulation)
+// y[m][n] = 2^(e_m + e_n) * sum_k a[m][k] * w[n][k]   (v_mfma_f32_32x32x16_f16, f32 accumulation)
 //   a[m][k] = f16(q8[m][k] * d_x[m][b] * 2^-e_m): the Q8_K activation value as the
 //             reference quantises it (codes q8, block scale d_x), rounded once to
 //             fp16 after a power-of-two row normalisation e_m chosen so that the
 //             row's largest |value| lies in [2^14, 2^15) -- no overflow, and
 //             every block within 2^14 of the row's largest keeps full precision;
-//   w[n][k] = the weight value the reference's integer path implies,
-//             (d*sc)*q - dmin*m (Q4_K/Q5_K) or (d*sc)*(q-32) (Q6_K), formed at f32
-//             precision and rounded once to fp16.
+//   w[n][k] = 2^-e_n times the weight value the reference's integer path
+//             implies, (d*sc)*q - dmin*m (Q4_K/Q5_K), (d*sc)*(q-32) (Q6_K) or d*q
+//             (Q8_0), formed at f32 precision and rounded once to fp16.  The
+//             per-row exponent e_n (computed once per weight, row_exponents)
+//             puts the largest value a row's blocks can produce just below 2^15,
+//             so small block scales never fall into the fp16 subnormal range;
+//   y[m][n] = 2^(e_m + e_n) * sum_k a[m][k] * w[n][k].
 // So the products differ from the reference's by two fp16 roundings (relative
 // <= 2^-11 each) and the sum by f32 summation order: about 4e-4 relative on a row.
 //
@@ -38,8 +42,6 @@
 // Shapes with few output tiles split k over S workgroups (split-K) that write
 // partial sums to the workspace; a second kernel adds them in a fixed order, so
 // results do not depend on scheduling.
-#include <stdlib.h>
-
 #include <algorithm>
 
 #include "lbq_device.hpp"
@@ -100,7 +102,8 @@ __device__ __forceinline__ int64_t op_pos(int opmajor, int64_t m, int64_t b, int
 // share the maximum of the row's block scales through LDS, then convert
 // 16-code chunks.
 // ---------------------------------------------------------------------------
-template <int T>
+// QB: values per activation scale block (256: Q8_K, 32: Q8_0)
+template <int T, int QB>
 __global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 *__restrict__ A,
                                                int *__restrict__ erow, int opmajor) {
     __shared__ float wmax[T / 64];
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 
     const int8_t *q = act.xq + m * act.k;
     for (int64_t c = 16 * t; c < act.k; c += 16 * T) {
         const uint4 w = *reinterpret_cast<const uint4 *>(q + c);
-        const float sx = __builtin_amdgcn_ldexpf(xd[c / KB], -e);
+        const float sx = __builtin_amdgcn_ldexpf(xd[c / QB], -e);
         const float cc = -1152.f * sx;
         uint32_t v[8];
         codes_to_f16(w.x, sx, cc, &v[0], &v[1]);
@@ -199,6 +202,82 @@ __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, in
     }
 }
 
+// The operand rows for Q8_0 weights straight from f32 x (k <= 16384): the
+// workgroup quantises its row to Q8_0 as candle's BlockQ8_0::from_float does
+// (two lanes per 32-value block, the decode prologue's arithmetic), shares the
+// stored f16 scales through LDS for the row exponent, and converts with
+// k_act_f16's arithmetic -- bit-identical operands, one launch.
+template <int T>
+__global__ __launch_bounds__(T) void k_quant_f16_q80(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
+                                                     int *__restrict__ erow, int opmajor) {
+    constexpr int BPP = T / 2, MAXP = 512 / BPP;  // passes of BPP blocks, 512 blocks at most
+    __shared__ float wmax[T / 64];
+    const int64_t m = blockIdx.x;
+    const int t = threadIdx.x, sub = t & 1;
+    const int nbx = (int)(K / 32), np = (nbx + BPP - 1) / BPP;
+    const float *xr = x + m * K;
+    float v[MAXP][16];
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        const int b = min(BPP * j + (t >> 1), nbx - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(xr + (int64_t)b * 32 + 16 * sub);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = src[i];
+            v[j][4 * i] = f.x; v[j][4 * i + 1] = f.y; v[j][4 * i + 2] = f.z; v[j][4 * i + 3] = f.w;
+        }
+    }
+    uint32_t codes[MAXP][4];
+    float dj[MAXP];
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        codes[j][0] = codes[j][1] = codes[j][2] = codes[j][3] = 0u;
+        dj[j] = 0.f;
+        if (j < np) {  // workgroup-uniform: the shuffle stays convergent
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[j][i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1));
+            const float d = amax / 127.f;
+            const float id = d != 0.f ? 1.f / d : 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float r = roundf(v[j][i] * id);
+                const int q = (r != r) ? 0 : (int)fminf(fmaxf(r, -128.f), 127.f);
+                codes[j][i >> 2] |= ((uint32_t)q & 0xffu) << (8 * (i & 3));
+            }
+            dj[j] = __half2float(__float2half_rn(d));  // the stored scale
+            if (BPP * j + (t >> 1) < nbx) mx = fmaxf(mx, fabsf(dj[j]));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < T / 64; w++) mx = fmaxf(mx, wmax[w]);
+    const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;  // as k_act_f16
+    if (t == 0) erow[m] = e;
+#pragma unroll
+    for (int j = 0; j < MAXP; j++) {
+        const int b = BPP * j + (t >> 1);
+        if (j < np && b < nbx) {
+            const float sx = __builtin_amdgcn_ldexpf(dj[j], -e);
+            const float cc = -1152.f * sx;
+            uint32_t w8[8];
+            codes_to_f16(codes[j][0], sx, cc, &w8[0], &w8[1]);
+            codes_to_f16(codes[j][1], sx, cc, &w8[2], &w8[3]);
+            codes_to_f16(codes[j][2], sx, cc, &w8[4], &w8[5]);
+            codes_to_f16(codes[j][3], sx, cc, &w8[6], &w8[7]);
+            const int64_t c = (int64_t)b * 32 + 16 * sub;  // first value of the lane's 16
+            const int p8 = (int)(c % KB) / 8;
+            *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, c / KB, p8, K)) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+            *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, c / KB, p8 + 1, K)) = make_uint4(w8[4], w8[5], w8[6], w8[7]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // B-operand sources.  A lane's raw bytes of one block come in NL loads
 // (load_part(i), so the kernel can spread them over its MFMA stream); prep()
@@ -224,9 +303,10 @@ struct GBK45 {
     }
     // lane sub-block j (0..3) is block sub-block 4h + j: low nibbles for even j,
     // high nibbles (read as 16u) for odd j
-    __device__ static void prep(const Raw &r, int h, Prep &p) {
+    // wsc = 2^-e_n, the row's power-of-two scale (exact in f32)
+    __device__ static void prep(const Raw &r, int h, float wsc, Prep &p) {
         const uint4 hdr = r.v[0];
-        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+        const float d = h2f(hdr.x & 0xffffu) * wsc, dmin = h2f(hdr.x >> 16) * wsc;
 #pragma unroll
         for (int cl = 0; cl < 2; cl++) {
             uint32_t sc2, m2;
@@ -297,7 +377,7 @@ struct GB<TYPE_Q6_K> {
         else r.dw = ld2_a2(blk + 208);
     }
     // mis: byte misalignment of the block (0 or 2)
-    __device__ static void prep(const Raw &r, uint32_t mis, Prep &p) {
+    __device__ static void prep(const Raw &r, uint32_t mis, float wsc, Prep &p) {
         uint32_t w[17], x[9];
 #pragma unroll
         for (int i = 0; i < 4; i++) { w[4 * i] = r.ql[i].x; w[4 * i + 1] = r.ql[i].y; w[4 * i + 2] = r.ql[i].z; w[4 * i + 3] = r.ql[i].w; }
@@ -310,7 +390,7 @@ struct GB<TYPE_Q6_K> {
 #pragma unroll
         for (int i = 0; i < 8; i++) p.qh[i] = __builtin_amdgcn_alignbyte(x[i + 1], x[i], mis);
         const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc[1], r.sc[0], mis), s1 = __builtin_amdgcn_alignbyte(r.sc[2], r.sc[1], mis);
-        const float d = h2f(r.dw);
+        const float d = h2f(r.dw) * wsc;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             // scale i covers quarter q = i/2 of the half: high nibbles (read as 16u) for i >= 4
@@ -331,11 +411,64 @@ struct GB<TYPE_Q6_K> {
     }
 };
 
+// Q8_0: a 256-value super-block of the k loop is 8 consecutive 34-byte blocks
+// (272 bytes; rows of k % 256 == 0 keep every super-block 16-byte aligned).
+// Lane half h holds blocks 4h..4h+3 (bytes 136h..136h+135, 8-byte aligned):
+// block j's f16 d at byte 34j of that range, its 32 codes from byte 34j + 2.
+// The weight value is d*q (q int8); each code becomes (1152 + q) in the f16
+// mantissa and (1152 + q)*sx - 1152*sx with sx = d * 2^-e_n is formed at f32
+// precision and rounded once (as the activation operands are built).
+template <>
+struct GB<TYPE_Q8_0> {
+    static constexpr int BYTES = 272;
+    static constexpr int NL = 9;
+    struct Raw { u32x4a4 v[8]; uint2 t; };
+    struct Prep { float sx[4], c[4]; uint32_t q[32]; };
+    __device__ static void load_part(const uint8_t *blk, int h, Raw &r, int i) {
+        const uint8_t *base = blk + 136 * h;
+        if (i < 8) r.v[i] = gld16(align4_global(reinterpret_cast<uintptr_t>(base + 16 * i)));
+        else r.t = *reinterpret_cast<const uint2 *>(base + 128);
+    }
+    __device__ static void prep(const Raw &r, float wsc, Prep &p) {
+        uint32_t w[34];
+#pragma unroll
+        for (int i = 0; i < 8; i++) { w[4 * i] = r.v[i].x; w[4 * i + 1] = r.v[i].y; w[4 * i + 2] = r.v[i].z; w[4 * i + 3] = r.v[i].w; }
+        w[32] = r.t.x;
+        w[33] = r.t.y;
+        // block j: d at byte 34j, codes at 34j + 2 (dword-aligned for odd j)
+        const uint32_t dbits[4] = {w[0] & 0xffffu, w[8] >> 16, w[17] & 0xffffu, w[25] >> 16};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            p.sx[j] = h2f(dbits[j]) * wsc;
+            p.c[j] = -1152.f * p.sx[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            p.q[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+            p.q[8 + i] = w[9 + i];
+            p.q[16 + i] = __builtin_amdgcn_alignbyte(w[18 + i], w[17 + i], 2);
+            p.q[24 + i] = w[26 + i];
+        }
+    }
+    // k-step s takes codes 8(s%4)..8(s%4)+7 of block s/4; dword d holds values
+    // (0, 2), (1, 3), (4, 6), (5, 7) of those eight
+    __device__ static uint32_t dw(const Prep &p, int s, int d) {
+        const int j = s >> 2;
+        const uint32_t u = p.q[8 * j + 2 * (s & 3) + (d >> 1)] ^ 0x80808080u;
+        const half2v a = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, u, (d & 1) ? 0x04030401u : 0x04020400u));
+        const half2v r2 = {(_Float16)fmaf((float)a.x, p.sx[j], p.c[j]), (_Float16)fmaf((float)a.y, p.sx[j], p.c[j])};
+        return __builtin_bit_cast(uint32_t, r2);
+    }
+};
+
 template <int TYPE>
-__device__ __forceinline__ void gb_prep(const typename GB<TYPE>::Raw &r, int h, const uint8_t *blk, typename GB<TYPE>::Prep &p) {
-    if constexpr (TYPE == TYPE_Q6_K) GB<TYPE>::prep(r, (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u), p);
-    else { (void)blk; GB<TYPE>::prep(r, h, p); }
+__device__ __forceinline__ void gb_prep(const typename GB<TYPE>::Raw &r, int h, const uint8_t *blk, float wsc,
+                                        typename GB<TYPE>::Prep &p) {
+    if constexpr (TYPE == TYPE_Q6_K) GB<TYPE>::prep(r, (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3u), wsc, p);
+    else if constexpr (TYPE == TYPE_Q8_0) { (void)blk; (void)h; GB<TYPE>::prep(r, wsc, p); }
+    else { (void)blk; GB<TYPE>::prep(r, h, wsc, p); }
 }
+
 
 // ---------------------------------------------------------------------------
 // the kernel
@@ -344,11 +477,14 @@ struct GemmGrid {
     int tiles_m, tiles_n, bps;  // bps: blocks of k per split
     int64_t split_stride;       // floats between the partial outputs of two splits (0: no split)
     int splits;
+    const int8_t *rexp;         // per weight row: e_n (w operands carry 2^-e_n)
 };
 
 // resident workgroups per CU the register budget allows
 template <int TYPE, int MT>
-constexpr int gemm_occupancy() { return (MT == 4 || TYPE == TYPE_Q6_K || (TYPE == TYPE_Q5_K && MT == 2)) ? 1 : 2; }
+constexpr int gemm_occupancy() {
+    return (MT == 4 || TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0 || (TYPE == TYPE_Q5_K && MT == 2)) ? 1 : 2;
+}
 // weight bytes loaded two blocks ahead (where the registers allow: Q4_K, 32-row tiles)
 template <int TYPE, int MT>
 constexpr bool gemm_deep() { return TYPE == TYPE_Q4_K && MT == 1; }
@@ -396,8 +532,15 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, h = lane >> 5, lr = lane & 31;
     const uint8_t *wrow[2];
+    int en[2];
+    float wsc[2];
 #pragma unroll
-    for (int j = 0; j < 2; j++) wrow[j] = W + min(n0 + 64 * wave + 32 * j + lr, N - 1) * row_bytes;
+    for (int j = 0; j < 2; j++) {
+        const int64_t row = min(n0 + 64 * wave + 32 * j + lr, N - 1);
+        wrow[j] = W + row * row_bytes;
+        en[j] = g.rexp[row];
+        wsc[j] = __builtin_amdgcn_ldexpf(1.f, -en[j]);
+    }
     // activation staging: a block row is 256 halfs = 32 16-byte pieces; load i of
     // thread t moves piece t%32 of tile row 8i + t/32, so every load instruction
     // reads two whole 512-byte rows.  The operand buffer holds whole tiles of rows
@@ -420,7 +563,9 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
     auto w_load = [&](int b, int q, int set) {
         B::load_part(wrow[q / B::NL] + (int64_t)b * B::BYTES, h, raw[DEEP ? set : 0][q / B::NL], q % B::NL);
     };
-    auto w_prep = [&](int b, int j, int set) { gb_prep<TYPE>(raw[DEEP ? set : 0][j], h, wrow[j] + (int64_t)b * B::BYTES, p[j]); };
+    auto w_prep = [&](int b, int j, int set) {
+        gb_prep<TYPE>(raw[DEEP ? set : 0][j], h, wrow[j] + (int64_t)b * B::BYTES, wsc[j], p[j]);
+    };
 
     floatx16 acc[MT][2];
 #pragma unroll
@@ -531,7 +676,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int64_t n = n0 + 64 * wave + 32 * j + lr;
-                if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][v], e);
+                if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][v], e + en[j]);
             }
         }
     }
@@ -589,7 +734,10 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     // scalar too (the direct-to-LDS target goes through M0)
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
               lr = lane & 31;
-    const uint8_t *wrow = W + min(n0 + 32 * wave + lr, N - 1) * row_bytes;
+    const int64_t wr = min(n0 + 32 * wave + lr, N - 1);
+    const uint8_t *wrow = W + wr * row_bytes;
+    const int en = g.rexp[wr];
+    const float wsc = __builtin_amdgcn_ldexpf(1.f, -en);
     Es[t] = erow[min(m0 + t, M - 1)];
 
     // direct-to-LDS staging: instruction j of a wave fills stage rows
@@ -643,7 +791,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     typename B::Raw raw;
     typename B::Prep p;
     auto w_load = [&](int b, int q) { B::load_part(wrow + (int64_t)b * B::BYTES, h, raw, q); };
-    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, p); };
+    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, wsc, p); };
 
     floatx16 acc[8];
 #pragma unroll
@@ -661,7 +809,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
     // A operands are read AH k-steps ahead (ar[j] holds k-step ks + j): with one
     // wave per SIMD, 8 KB of reads per k-step need that depth to keep the LDS
     // busy.  Q6_K's larger weight state leaves registers for one step only.
-    constexpr int AH = TYPE == TYPE_Q6_K ? 1 : 2;
+    constexpr int AH = (TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0) ? 1 : 2;
     half8 ar[AH][8];
     uint32_t bcur[4];
 #pragma unroll
@@ -731,7 +879,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
             const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
             const int64_t m = m0 + r;
             const int64_t n = n0 + 32 * wave + lr;
-            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r]);
+            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r] + en);
         }
     }
 }
@@ -773,7 +921,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
 
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
               lr = lane & 31;
-    const uint8_t *wrow = W + min(n0 + 32 * wave + lr, N - 1) * row_bytes;
+    const int64_t wr = min(n0 + 32 * wave + lr, N - 1);
+    const uint8_t *wrow = W + wr * row_bytes;
+    const int en = g.rexp[wr];
+    const float wsc = __builtin_amdgcn_ldexpf(1.f, -en);
     if (t < WBM) Es[t] = erow[min(m0 + t, M - 1)];
 
     // staging: instruction j (0..3) of wave w fills stage rows 16w + 4j + [0, 4);
@@ -813,7 +964,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
     typename B::Raw raw;
     typename B::Prep p;
     auto w_load = [&](int b, int q) { B::load_part(wrow + (int64_t)b * B::BYTES, h, raw, q); };
-    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, p); };
+    auto w_prep = [&](int b) { gb_prep<TYPE>(raw, h, wrow + (int64_t)b * B::BYTES, wsc, p); };
 
     floatx16 acc[4];
 #pragma unroll
@@ -894,7 +1045,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
             const int r = 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
             const int64_t m = m0 + r;
             const int64_t n = n0 + 32 * wave + lr;
-            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r]);
+            if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][v], Es[r] + en);
         }
     }
 }
@@ -930,7 +1081,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     const int nb = (int)(K / KB);
     const int b0 = z * S, cnt = min(S, nb - b0);  // cnt >= 1
     const int64_t n0 = (int64_t)tn * KSN + 32 * wave;
-    const uint8_t *wrow = W + min(n0 + lr, N - 1) * row_bytes + (int64_t)b0 * B::BYTES;
+    const int64_t wr = min(n0 + lr, N - 1);
+    const uint8_t *wrow = W + wr * row_bytes + (int64_t)b0 * B::BYTES;
+    const int en = g.rexp[wr];
+    const float wsc = __builtin_amdgcn_ldexpf(1.f, -en);
 
     // the slice's operands: block b, row tile u, k-step s, lane l at byte
     // (((T b + u) 16 + s) 64 + l) 16; 1 KB per wave instruction, chunk 4i + wave;
@@ -957,10 +1111,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
         for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b], q);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // the activation loads are the oldest in flight: wait for them alone
-    constexpr int VM = S * B::NL;
-    static_assert(VM < 64, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+    // The activation loads are the oldest in flight.  The compiler tracks loads
+    // to LDS and, before the barrier, waits for exactly those (vmcnt = the number
+    // of weight load instructions issued after them, as it emitted them -- it may
+    // merge neighbouring loads, so a count written here could be too high).
     __syncthreads();
 
     floatx16 acc[T];
@@ -973,7 +1127,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     for (int b = 0; b < S; b++) {
         if (b < cnt) {
             typename B::Prep p;
-            gb_prep<TYPE>(raw[b], h, wrow + (int64_t)b * B::BYTES, p);
+            gb_prep<TYPE>(raw[b], h, wrow + (int64_t)b * B::BYTES, wsc, p);
 #pragma unroll
             for (int s = 0; s < 16; s++) {
                 uint32_t bw[4];
@@ -997,7 +1151,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], erow[r]);
+            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], erow[r] + en);
         }
 }
 
@@ -1031,6 +1185,62 @@ __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ par
     }
 }
 
+// ---------------------------------------------------------------------------
+// Per-row operand exponents, once per weight: e_n such that the largest value
+// any block of row n can produce, B_n, satisfies B_n * 2^-e_n < 2^15.  The
+// bound is the largest |d|, |dmin| of the row's blocks times the largest code
+// and scale products of the format: Q4_K 63*15 |d| + 63 |dmin|, Q5_K
+// 63*31 |d| + 63 |dmin|, Q6_K 128*32 |d|, Q8_0 128 |d|.  Non-finite scales are
+// left out (their blocks produce non-finite values whatever the exponent); a
+// row of zero scales gets e_n = 0.  One thread per row.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_row_exponents(const uint8_t *__restrict__ W, int64_t N, int nb,
+                                                        int64_t row_bytes, int8_t *__restrict__ rexp) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    const uint8_t *row = W + n * row_bytes;
+    constexpr int SB = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 34;
+    float dm = 0.f, mm = 0.f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *blk = row + (int64_t)b * SB;
+        float d, dmin = 0.f;
+        if constexpr (TYPE == TYPE_Q6_K) {
+            d = h2f(ld2_a2(blk + 208));
+        } else if constexpr (TYPE == TYPE_Q8_0) {
+            d = h2f(ld2_a2(blk));
+        } else {
+            const uint32_t hdr = ld_u32(blk);
+            d = h2f(hdr & 0xffffu);
+            dmin = h2f(hdr >> 16);
+        }
+        d = fabsf(d);
+        dmin = fabsf(dmin);
+        if (d <= 3.4e38f) dm = fmaxf(dm, d);  // false for NaN and Inf
+        if (dmin <= 3.4e38f) mm = fmaxf(mm, dmin);
+    }
+    const float bound = TYPE == TYPE_Q4_K   ? 945.f * dm + 63.f * mm
+                        : TYPE == TYPE_Q5_K ? 1953.f * dm + 63.f * mm
+                        : TYPE == TYPE_Q6_K ? 4096.f * dm
+                                            : 128.f * dm;
+    // bound = f * 2^E, f in [0.5, 1): bound * 2^-(E - 15) = f * 2^15 < 2^15
+    rexp[n] = (int8_t)(bound > 0.f ? __builtin_amdgcn_frexp_expf(bound) - 15 : 0);
+}
+
+hipError_t launch_row_exponents(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int8_t *rexp,
+                                hipStream_t st) {
+    if (!gemm_serves(type, k)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    const int nb = (int)(k / (type == TYPE_Q8_0 ? 32 : KB));
+    switch (type) {
+    case TYPE_Q4_K: k_row_exponents<TYPE_Q4_K><<<grid, 256, 0, st>>>(w, n, nb, row_bytes, rexp); break;
+    case TYPE_Q5_K: k_row_exponents<TYPE_Q5_K><<<grid, 256, 0, st>>>(w, n, nb, row_bytes, rexp); break;
+    case TYPE_Q6_K: k_row_exponents<TYPE_Q6_K><<<grid, 256, 0, st>>>(w, n, nb, row_bytes, rexp); break;
+    default: k_row_exponents<TYPE_Q8_0><<<grid, 256, 0, st>>>(w, n, nb, row_bytes, rexp); break;
+    }
+    return hipGetLastError();
+}
+
 namespace {
 
 struct Plan {
@@ -1044,7 +1254,10 @@ int tile_rows(const Plan &p) { return p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TB
 // the pre-pass layout: 32-row tiles of operand-major rows, or 0 (row-major)
 int operand_major(const Plan &p) { return p.mt == MT_KS ? p.rt : 0; }
 int ks_blocks_for(int type) {
-    return type == TYPE_Q4_K ? ks_blocks<TYPE_Q4_K>() : type == TYPE_Q5_K ? ks_blocks<TYPE_Q5_K>() : ks_blocks<TYPE_Q6_K>();
+    return type == TYPE_Q4_K   ? ks_blocks<TYPE_Q4_K>()
+           : type == TYPE_Q5_K ? ks_blocks<TYPE_Q5_K>()
+           : type == TYPE_Q6_K ? ks_blocks<TYPE_Q6_K>()
+                               : ks_blocks<TYPE_Q8_0>();
 }
 
 // mt, rt and tile_rows depend on (type, k, m) only -- the pre-pass plans with n = 1
@@ -1054,8 +1267,11 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     // m = 48, 64; for Q4_K / Q5_K the 64-row tiles win on the large matrices).
     // The choice -- and so the operand layout -- must not depend on n: a grouped
     // call runs one pre-pass for weights of different n.
-    const bool ks2 = type == TYPE_Q6_K || getenv("LBQ_GEMM_KS64");
-    if (m <= (ks2 ? 64 : 32) && !getenv("LBQ_GEMM_NO_KS")) {
+    const Tuning &tu = tuning();
+    // (Q8_0, whose raw super-blocks are the largest, plans as Q6_K)
+    const bool heavy = type == TYPE_Q6_K || type == TYPE_Q8_0;
+    const bool ks2 = heavy || tu.gemm_ks64;
+    if (m <= (ks2 ? 64 : 32) && !tu.gemm_no_ks) {
         // k-sliced: 128-column workgroups of one or two 32-row tiles, each a
         // slice of S blocks
         p.mt = MT_KS;
@@ -1069,24 +1285,24 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
         const int smax = p.rt == 1 ? ks_blocks_for(type) : 2;
         int bps = smax;
         while (bps > 2 && (int64_t)p.tiles_n * ((nb + bps - 1) / bps) < (int64_t)num_cus()) bps--;
-        if (const char *e = getenv("LBQ_GEMM_KS")) bps = std::max(1, std::min(atoi(e), smax));  // tuning
+        if (tu.gemm_ks) bps = std::max(1, std::min(tu.gemm_ks, smax));  // tuning
         p.bps = bps;
         p.splits = (nb + bps - 1) / bps;
         return p;
     }
     // the wide and tall kernels address a tile's operand rows through a buffer
     // resource of 256 * k * 2 bytes or less, which must stay below 2^31
-    const bool big_ok = k * 2 * TBM < (int64_t(1) << 31) && !getenv("LBQ_GEMM_NO_TALL");
+    const bool big_ok = k * 2 * TBM < (int64_t(1) << 31) && !tu.gemm_no_tall;
     // wide tiles (two waves per SIMD, dequantisation per 128 rows) below 256 rows,
     // and for Q4_K (the cheapest dequantisation) up to 512; tall tiles (one wave
     // per SIMD, dequantisation per 256 rows) where the dequantisation VALU per
     // MFMA decides (measured per type and m: 128, 256, 512, 2048)
     bool wide = m < 256 || (type == TYPE_Q4_K && m <= 512);
-    if (const char *e = getenv("LBQ_GEMM_BIG")) wide = e[0] != 't' || m < 256;  // tuning override: "wide" or "tall"
+    if (tu.gemm_big) wide = tu.gemm_big == 1 || m < 256;  // tuning override: wide or tall
     // (Q6_K from 65 rows: its 64-row tiles took 66 us at m = 100 where the wide
     // tiles take 50 at m = 128, 14336 x 4096)
-    if ((m >= 128 || (type == TYPE_Q6_K && m > 64)) && big_ok) p.mt = wide ? MT_WIDE : 8;
-    else p.mt = m <= 32 ? 1 : (m <= 64 || type == TYPE_Q6_K) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
+    if ((m >= 128 || (heavy && m > 64)) && big_ok) p.mt = wide ? MT_WIDE : 8;
+    else p.mt = m <= 32 ? 1 : (m <= 64 || heavy) ? 2 : 4;  // Q6_K's raw blocks leave no room for MT = 4
     const int rows = tile_rows(p), cols = p.mt == 8 ? TBN : BN;
     p.tiles_m = (int)((m + rows - 1) / rows);
     p.tiles_n = (int)((n + cols - 1) / cols);
@@ -1097,16 +1313,17 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     const int64_t slots = (int64_t)num_cus();
     int s = 1;
     if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
-    if (const char *e = getenv("LBQ_GEMM_SPLITS")) s = std::max(1, std::min(atoi(e), nb));  // tuning override
+    if (tu.gemm_splits) s = std::max(1, std::min(tu.gemm_splits, nb));  // tuning override
     p.bps = (nb + s - 1) / s;
     p.splits = (nb + p.bps - 1) / p.bps;
     return p;
 }
 
 template <int TYPE>
-hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_bytes, const _Float16 *a,
-                        const int *erow, int64_t k, int64_t m, float *out, int64_t split_stride, hipStream_t st) {
-    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits};
+hipError_t launch_typed(const Plan &p, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t row_bytes,
+                        const _Float16 *a, const int *erow, int64_t k, int64_t m, float *out, int64_t split_stride,
+                        hipStream_t st) {
+    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits, rexp};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
     if (p.mt == MT_KS) {
         if (p.rt == 2) {  // two row tiles: slices of 1 or 2 blocks
@@ -1128,7 +1345,8 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, int64_t n, int64_t row_
     case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 2: k_gemm<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     default:
-        if constexpr (TYPE != TYPE_Q6_K) k_gemm<TYPE, 4><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
+        if constexpr (TYPE != TYPE_Q6_K && TYPE != TYPE_Q8_0)
+            k_gemm<TYPE, 4><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);
         break;
     }
     return hipGetLastError();
@@ -1152,37 +1370,47 @@ WsLayout ws_layout(const Plan &p, int64_t n, int64_t k, int64_t m) {
 }  // namespace
 
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m) {
-    if (!has_mfma_gemm(type)) return 0;
+    if (!gemm_serves(type, k)) return 0;
     return ws_layout(plan_for(type, n, k, m), n, k, m).total;
 }
 
-bool gemm_prepass_fuses_quant(int64_t k, const float *x) {
-    return x && k % KB == 0 && k / KB <= 64 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+bool gemm_prepass_fuses_quant(int type, int64_t k, const float *x) {
+    return x && gemm_serves(type, k) && k / KB <= 64 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st) {
-    if (!ws || !has_mfma_gemm(type)) return hipErrorInvalidValue;
+    if (!ws || !gemm_serves(type, k)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, 1, k, m);  // the operand rows do not depend on n
     const WsLayout L = ws_layout(p, 1, k, m);
     uint8_t *base = static_cast<uint8_t *>(ws);
     _Float16 *a = reinterpret_cast<_Float16 *>(base + L.a_off);
     int *erow = reinterpret_cast<int *>(base + L.e_off);
+    // few rows, or long rows up to 1024 of them: one pass of 1024 threads per
+    // row; otherwise 256-thread workgroups (measured at m = 512 and 2048)
+    const bool wide_wg = m <= 64 || (k > 8192 && m <= 1024);
+    const int om = operand_major(p);
     if (x) {
-        if (!gemm_prepass_fuses_quant(k, x)) return hipErrorInvalidValue;
-        // few rows, or long rows up to 1024 of them: one pass of 1024 threads per
-        // row; otherwise 256-thread workgroups (measured at m = 512 and 2048)
-        if (m <= 64 || (k > 8192 && m <= 1024)) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, operand_major(p));
-        else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, operand_major(p));
+        if (!gemm_prepass_fuses_quant(type, k, x)) return hipErrorInvalidValue;
+        if (type == TYPE_Q8_0) {
+            if (wide_wg) k_quant_f16_q80<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, om);
+            else k_quant_f16_q80<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, om);
+        } else {
+            if (wide_wg) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, om);
+            else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, om);
+        }
+    } else if (type == TYPE_Q8_0) {
+        if (wide_wg) k_act_f16<1024, 32><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, om);
+        else k_act_f16<256, 32><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, om);
     } else {
-        if (m <= 64 || (k > 8192 && m <= 1024)) k_act_f16<1024><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, operand_major(p));
-        else k_act_f16<256><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, operand_major(p));
+        if (wide_wg) k_act_f16<1024, KB><<<(unsigned)m, 1024, 0, st>>>(act, m, a, erow, om);
+        else k_act_f16<256, KB><<<(unsigned)m, 256, 0, st>>>(act, m, a, erow, om);
     }
     return hipGetLastError();
 }
 
-hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int64_t m, float *y, void *ws,
-                     hipStream_t st) {
-    if (!ws || !has_mfma_gemm(type)) return hipErrorInvalidValue;
+hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
+                     float *y, void *ws, hipStream_t st) {
+    if (!ws || !rexp || !gemm_serves(type, k)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, n, k, m);
     const WsLayout L = ws_layout(p, n, k, m);
     uint8_t *base = static_cast<uint8_t *>(ws);
@@ -1193,9 +1421,10 @@ hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t r
     const int64_t stride = p.splits > 1 ? m * n : 0;
     hipError_t e;
     switch (type) {
-    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
-    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
-    default: e = launch_typed<TYPE_Q6_K>(p, w, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, rexp, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, rexp, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    case TYPE_Q6_K: e = launch_typed<TYPE_Q6_K>(p, w, rexp, n, row_bytes, a, erow, k, m, out, stride, st); break;
+    default: e = launch_typed<TYPE_Q8_0>(p, w, rexp, n, row_bytes, a, erow, k, m, out, stride, st); break;
     }
     if (e != hipSuccess || p.splits == 1) return e;
     const int64_t count = m * n;
@@ -1203,12 +1432,12 @@ hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t r
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       const float *x, int64_t m, float *y, void *ws, hipStream_t st) {
-    if (has_mfma_gemm(type)) {
+hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes,
+                       const ActView &act, const float *x, int64_t m, float *y, void *ws, hipStream_t st) {
+    if (gemm_serves(type, k)) {
         hipError_t e = gemm_prepass(type, k, act, x, m, ws, st);
         if (e != hipSuccess) return e;
-        return gemm_main(type, w, n, k, row_bytes, m, y, ws, st);
+        return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, st);
     }
     if (x) return hipErrorInvalidValue;  // the GEMV over row chunks takes quantised activations
     // Q8_0, the legacy types, Q2_K and Q3_K: the decode GEMV over row chunks of 8

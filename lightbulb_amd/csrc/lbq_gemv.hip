@@ -18,7 +18,7 @@ bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     // Every workgroup quantises all of x before its first dot, so the prologue
     // grows with k, but even at k = 14336 it costs less than a separate
     // quantisation launch (4096 x 14336 Q4_K: fused 10.3 us, quantise + GEMV 11.7).
-    if (getenv("LBQ_GEMV1_NOFUSE")) return false;  // tuning switch: always quantise separately
+    if (tuning().gemv1_nofuse) return false;  // tuning switch: always quantise separately
     const int nb = (int)(k / (type == TYPE_Q8_0 ? QK8_0 : QK_K));
     int ppb, rpw, it;
     switch (type) {

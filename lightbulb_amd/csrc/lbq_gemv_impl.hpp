@@ -587,8 +587,6 @@ struct GemvCfg {
     bool fused;
 };
 
-static int env_int(const char *s, int def) { return s ? atoi(s) : def; }
-
 // LBQ_GEMV="rpw,it,wpc,fused" overrides the choice (tuning; any value is correct).
 static GemvCfg pick_cfg(int type, int64_t n, int pieces, int m, int64_t k) {
     GemvCfg c;
@@ -599,9 +597,7 @@ static GemvCfg pick_cfg(int type, int64_t n, int pieces, int m, int64_t k) {
     else if (pieces >= 128) { c.rpw = 2; c.it = 4; }
     else { c.rpw = 4; c.it = 4; }
     c.wpc = 8;
-    if (const char *e = getenv("LBQ_GEMV")) {
-        int v[4] = {c.rpw, c.it, c.wpc, c.fused ? 1 : 0};
-        sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]);
+    if (const int *v = tuning().gemv_cfg; v[0] > 0) {
         c.rpw = v[0]; c.it = v[1]; c.wpc = v[2]; c.fused = v[3] != 0 && (int64_t)m * k <= 65536;
     }
     (void)n;
@@ -665,7 +661,7 @@ static bool fast_shape(int nb, int *ppb, int *rpw, int *it, int mr = 1) {
     } else if (nb <= 512) {  // Q8_0: nb counts 32-value blocks
         q = 1; r = 1;
     }
-    if (const char *e = getenv("LBQ_GEMV1_CFG")) sscanf(e, "%d,%d", &q, &r);  // tuning override "ppb,rpw"
+    if (tuning().gemv1_ppb > 0) { q = tuning().gemv1_ppb; r = tuning().gemv1_rpw; }  // tuning override
     if (q <= 0 || r <= 0 || 64 % (q * r) != 0) return false;
     const int bpi = 64 / (q * r);
     *ppb = q;
@@ -690,7 +686,7 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // 10.1 / 8.2 at 4 vs 11.2 / 9.0 at 8; Q6_K 14336 x 4096 14.4 at 4 vs 16.1 at 8.
     // Q8_0 takes eight everywhere (4096 x 4096 fused: 6.2 us at 4, 5.7 at 8).
     int wpc = (TYPE == TYPE_Q6_K || (TYPE != TYPE_Q8_0 && n < 8192 && (x || nb > 32))) ? 4 : 8;
-    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
+    if (tuning().gemv1_wpc > 0) wpc = tuning().gemv1_wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
@@ -708,7 +704,7 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // at 4096 rows the four-wave workgroups stay ahead).
     bool w8 = W8_OK && (wpc == 8 || (n > 4096 && nb <= 32));
     if (w8 && wpc < 8) waves = std::min<int64_t>((int64_t)num_cus() * 8, ng);
-    if (const char *e = getenv("LBQ_GEMV1_WPG")) w8 = W8_OK && atoi(e) == 8;
+    if (tuning().gemv1_wpg > 0) w8 = W8_OK && tuning().gemv1_wpg == 8;
     const unsigned grid8 = (unsigned)((waves + 7) / 8);
     auto fused = [&](auto k4, auto k8, const float *al, float ep) {
         if (w8) k8<<<grid8, 512, lds, st>>>(rm, row_bytes, nb, x, act, al, ep);
@@ -765,7 +761,7 @@ static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, 
     }
     // two workgroups per CU while both fit the CU's 160 KB of LDS
     int wpc = lds <= 80 * 1024 ? 8 : 4;
-    if (const char *e = getenv("LBQ_GEMV1_WPC")) wpc = atoi(e) > 0 ? atoi(e) : wpc;
+    if (tuning().gemv1_wpc > 0) wpc = tuning().gemv1_wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
@@ -865,11 +861,11 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.row_bytes = row_bytes;
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
-    if constexpr (has_mfma_gemm(TYPE) || TYPE == TYPE_Q8_0) {  // the types with a Fast<> decoder
+    if constexpr (has_mfma_gemm(TYPE)) {  // the types with a Fast<> decoder
         if (m == 1) {
             const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
             if (e != hipErrorNotSupported) return e;
-        } else if (m <= 8 && !x && !alpha && map == MAP_ONE && rm.end[0] == n && !getenv("LBQ_GEMV_ROWS_OFF")) {
+        } else if (m <= 8 && !x && !alpha && map == MAP_ONE && rm.end[0] == n && !tuning().gemv_rows_off) {
             // one launch per chunk of rows, each streaming the weight once: worth it
             // while a chunk holds at least half the rows (one or two sweeps per row)
             if (fast_rows_max<TYPE>(g.nb) >= 4) return run_fast_m<TYPE>(rm, row_bytes, g.nb, act, m, st);

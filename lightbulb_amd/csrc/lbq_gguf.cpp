@@ -245,7 +245,7 @@ const Meta *meta_of(const lbq_gguf *g, const char *key) {
 // extract_tensor_bytes: the tensor's exact extent, bounds-checked
 // The tensor's byte extent as extract_tensor_bytes computes it: ceil(numel / bs) *
 // type_size from the GgmlDType table.  With `blocks`, type_size is instead the size
-// of the block the kernels read (lbq_type_size): the two differ for Q2_K only,
+// of the block the kernels read (lbq_type_block_bytes): the two differ for Q2_K only,
 // whose table entry (82) is shorter than its 84-byte block.
 int tensor_span(const lbq_gguf *g, const char *name, const Tensor **t_out, uint64_t *start, uint64_t *nbytes,
                 bool blocks_layout = false) {
@@ -255,7 +255,7 @@ int tensor_span(const lbq_gguf *g, const char *name, const Tensor **t_out, uint6
     uint64_t bs, ts;
     ggml_layout(t.type, &bs, &ts);
     if (!bs) return gfail(LBQ_ERR_UNSUPPORTED_TYPE, "Unknown quantization type: %u", t.type);
-    if (blocks_layout && lbq_type_size(t.type) > 0) ts = (uint64_t)lbq_type_size(t.type);
+    if (blocks_layout && lbq_type_block_bytes(t.type) > 0) ts = (uint64_t)lbq_type_block_bytes(t.type);
     uint64_t numel = 1;
     for (uint64_t d : t.dims) {
         if (d && numel > UINT64_MAX / d) return gfail(LBQ_ERR_FORMAT, "tensor '%s' is too large", name);

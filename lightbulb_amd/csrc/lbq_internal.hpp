@@ -19,13 +19,44 @@ constexpr bool is_kquant(int t) {
     return t == TYPE_Q2_K || t == TYPE_Q3_K || t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K;
 }
 // weight types the MFMA GEMM serves at m > 8 (the others run the GEMV over row chunks)
-constexpr bool has_mfma_gemm(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K; }
+constexpr bool has_mfma_gemm(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+// ... at this k: the GEMM steps through k in 256-value super-blocks (Q8_0: 8 blocks)
+constexpr bool gemm_serves(int t, int64_t k) { return has_mfma_gemm(t) && k % 256 == 0; }
 // activation type of QMatMul's vec_dot for a weight type (candle GgmlType::VecDotType)
 constexpr int vec_dot_type(int t) {
     return is_kquant(t) ? TYPE_Q8_K : (t == TYPE_Q4_1 || t == TYPE_Q5_1) ? TYPE_Q8_1 : TYPE_Q8_0;
 }
 
 struct ActView;
+
+// Launch-plan overrides for tuning runs, read from the environment once, when a
+// context is created (lbq_init), never on a forward call.  Any setting computes
+// the same result; only the kernel shape changes.  Zero / false: the measured
+// default plan.
+//   LBQ_GEMM_KS64, LBQ_GEMM_NO_KS, LBQ_GEMM_KS=<blocks>, LBQ_GEMM_NO_TALL,
+//   LBQ_GEMM_BIG=wide|tall, LBQ_GEMM_SPLITS=<n>     batched GEMM plan
+//   LBQ_GEMV1_NOFUSE, LBQ_GEMV1_CFG=<ppb>,<rpw>, LBQ_GEMV1_WPC=<waves per CU>,
+//   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
+//   LBQ_GEMV_ROWS_OFF                               decode GEMV plan
+struct Tuning {
+    bool gemm_ks64 = false, gemm_no_ks = false, gemm_no_tall = false;
+    int gemm_ks = 0;      // k-sliced tiles: blocks per slice (0: planned)
+    int gemm_big = 0;     // 1: wide tiles, 2: tall tiles (0: planned)
+    int gemm_splits = 0;  // split-k count (0: planned)
+    bool gemv1_nofuse = false, gemv_rows_off = false;
+    int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
+    int gemv1_wpc = 0, gemv1_wpg = 0;
+    int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
+};
+Tuning tuning_from_env();
+// The plan overrides of the context the calling thread is inside (set by the C
+// ABI entry points for the duration of a call), or the defaults.
+const Tuning &tuning();
+struct TuningScope {
+    explicit TuningScope(const Tuning *t);
+    ~TuningScope();
+    const Tuning *prev;
+};
 
 // The rows of up to GROUP_MAX weights of one type and k, seen as one row space
 // (weights applied to the same x: q|k|v, gate|up).  Segment s holds rows
@@ -98,12 +129,25 @@ hipError_t launch_silu_mul(const float *g, const float *u, int64_t count, float 
 // and the GEMM proper, which weights of one type, k and m can share a pre-pass
 // for (the operand rows do not depend on n).
 size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
-bool gemm_prepass_fuses_quant(int64_t k, const float *x);
+bool gemm_prepass_fuses_quant(int type, int64_t k, const float *x);
 hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st);
-hipError_t gemm_main(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int64_t m, float *y, void *ws,
-                     hipStream_t st);
-hipError_t launch_gemm(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
-                       const float *x, int64_t m, float *y, void *ws, hipStream_t st);
+// rexp: the weight's per-row operand exponents (launch_row_exponents).
+hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
+                     float *y, void *ws, hipStream_t st);
+hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes,
+                       const ActView &act, const float *x, int64_t m, float *y, void *ws, hipStream_t st);
+// Per-row operand exponents of a weight the MFMA GEMM serves (gemm_serves):
+// rexp[i] = e such that every value row i's blocks can produce is below
+// 2^(15 + e), so the GEMM's fp16 weight operands, scaled by 2^-e, stay clear
+// of the fp16 subnormal range.  n bytes at rexp.
+hipError_t launch_row_exponents(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, int8_t *rexp,
+                                hipStream_t st);
+
+// Dense F32 / F16 weights (candle's dense QMatMul variant): y[m][n] = x . W^T in
+// f32, W [n][k] in its file layout widened on the fly; k % 8 == 0.
+constexpr bool is_dense(int t) { return t == TYPE_F32 || t == TYPE_F16; }
+hipError_t launch_dense(int type, const uint8_t *w, int64_t n, int64_t k, const float *x, int64_t m, float *y,
+                        hipStream_t st);
 
 // Compute units of the current device (cached after the first call).
 int num_cus();

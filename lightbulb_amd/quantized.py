@@ -80,12 +80,13 @@ class GgmlDType(IntEnum):
         }.get(self, self.name)
 
 
-#: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE
-SERVED = (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q2K,
-          GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
+#: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE.
+#: F32 / F16 are candle's dense QMatMul variant (an f32 matmul, no activation quantisation).
+SERVED = (GgmlDType.F32, GgmlDType.F16, GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1,
+          GgmlDType.Q8_0, GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
 
-#: weight types quantize_tensor can produce (no Q2_K / Q3_K quantiser)
-QUANTIZABLE = tuple(t for t in SERVED if t not in (GgmlDType.Q2K, GgmlDType.Q3K))
+#: weight types quantize_tensor can produce (no Q2_K / Q3_K quantiser; dense types are not quantised)
+QUANTIZABLE = tuple(t for t in SERVED if t not in (GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.F32, GgmlDType.F16))
 
 #: activation-only block types (the vec-dot partners)
 ACT_TYPES = (GgmlDType.Q8_0, GgmlDType.Q8_1, GgmlDType.Q8K)

@@ -24,11 +24,13 @@ def test_every_declared_symbol_is_exported_and_bound(lbq):
 
 def test_type_table_matches_reference(lbq):
     # GgmlDType::block_size / type_size, /root/reference/src/quantization/mod.rs:99-126
+    # (Q2_K: the table's 82); lbq_type_block_bytes is the block in memory (Q2_K: 84)
     for t, bs, ts in [(0, 1, 4), (1, 1, 2), (2, 32, 18), (3, 32, 20), (6, 32, 22), (7, 32, 24), (8, 32, 34), (9, 32, 36),
-                      (10, 256, 84), (11, 256, 110), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 292)]:
+                      (10, 256, 82), (11, 256, 110), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 292)]:
         assert lbq.lbq_type_block_size(t) == bs and lbq.lbq_type_size(t) == ts
+        assert lbq.lbq_type_block_bytes(t) == (84 if t == 10 else ts)
     for t in (4, 5, 16, 999):
-        assert lbq.lbq_type_block_size(t) == 0 and lbq.lbq_type_size(t) == 0
+        assert lbq.lbq_type_block_size(t) == 0 and lbq.lbq_type_size(t) == 0 and lbq.lbq_type_block_bytes(t) == 0
 
 
 def test_argument_errors_without_device(lbq):
