@@ -202,22 +202,108 @@ hipError_t quant_into(int act_type, const float *d_x, int64_t m, int64_t k, cons
                                  const_cast<int16_t *>(av.xbs), const_cast<float *>(av.xs), nullptr, st);
 }
 
+// Device memory of one forward call: the quantised activations, then the batched
+// GEMM's workspace.  Either the context's buffers, grown on demand (the caller
+// holds ctx->mu), or one fixed region (the allocation-free entry point): the
+// activations at its start, the workspace after them, both checked against its
+// size before any launch.
+struct Scratch {
+    lbq_ctx *ctx = nullptr;
+    uint8_t *fixed = nullptr;
+    size_t fixed_bytes = 0;
+    size_t act_used = 0;  // fixed region: bytes taken by the activations
+
+    int limit(size_t need) const {
+        return fail(LBQ_ERR_LIMIT,
+                    "the call needs %zu bytes of scratch; the allocation-free entry point has %zu per device", need,
+                    fixed_bytes);
+    }
+    int act(size_t bytes, uint8_t **out) {
+        if (!fixed) {
+            const int s = ensure_scratch(ctx, bytes);
+            *out = ctx->scratch;
+            return s;
+        }
+        if (bytes > fixed_bytes) return limit(bytes);
+        act_used = align_up(bytes, 256);
+        *out = fixed;
+        return LBQ_OK;
+    }
+    int ws(size_t bytes, uint8_t **out) {
+        if (!fixed) {
+            const int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, bytes, "GEMM workspace");
+            *out = ctx->ws;
+            return s;
+        }
+        if (act_used + bytes > fixed_bytes) return limit(act_used + bytes);
+        *out = fixed + act_used;
+        return LBQ_OK;
+    }
+};
+
 // The dot half of QMatMul::forward: decode GEMV for m <= 8, MFMA GEMM above.
-// Caller holds ctx->mu (the GEMM's split-k workspace lives in the context).
-int run_dot(lbq_ctx *ctx, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
+int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
     hipError_t e;
     if (m <= 8) {
         e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
     } else {
         const size_t wsb = lbq::gemm_workspace_bytes(w->type, w->n, w->k, m);
+        uint8_t *ws = nullptr;
         if (wsb) {
-            int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
+            int s = sc.ws(wsb, &ws);
             if (s) return s;
         }
-        e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ctx->ws, st);
+        e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ws, st);
     }
     if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
+}
+
+// QMatMul::forward after the argument checks, on the caller's device; `mu`
+// (the context's lock, null for the fixed region) is taken before any buffer is
+// touched.
+int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, hipStream_t st, Scratch &sc,
+            std::mutex *mu) {
+    const int act_type = lbq::vec_dot_type(w->type);
+    if (lbq::is_dense(w->type)) {
+        // candle's dense variant: an f32 matmul, no activation quantisation
+        hipError_t e = lbq::launch_dense(w->type, w->d_blocks, w->n, w->k, d_x, m, d_y, st);
+        return e == hipSuccess ? LBQ_OK : hip_fail(e, "dense matmul launch");
+    }
+    const ActLayout L = act_layout(act_type, m, w->k);
+    if (m <= 8 && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
+        // decode: the GEMV quantises x in its own prologue -- one launch, no scratch
+        const lbq::ActView av{nullptr, nullptr, nullptr, w->k, L.nb};
+        hipError_t e = lbq::launch_gemv_x(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, d_x, (int)m, d_y, st);
+        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+        return LBQ_OK;
+    }
+    std::unique_lock<std::mutex> lock;
+    if (mu) lock = std::unique_lock<std::mutex>(*mu);
+    (void)ctx;
+    if (m > 8 && lbq::gemm_prepass_fuses_quant(w->type, w->k, d_x)) {
+        // batched: the operand pre-pass quantises x itself
+        uint8_t *ws = nullptr;
+        int s = sc.ws(lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), &ws);
+        if (s) return s;
+        const lbq::ActView none{nullptr, nullptr, nullptr, w->k, L.nb};
+        hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, none, d_x, m, d_y, ws,
+                                        st);
+        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
+        return LBQ_OK;
+    }
+    uint8_t *abuf = nullptr;
+    int s = sc.act(L.total, &abuf);
+    if (s) return s;
+    if (m > 8) {  // reserve the GEMM workspace too before anything is launched
+        uint8_t *ws = nullptr;
+        const size_t wsb = lbq::gemm_workspace_bytes(w->type, w->n, w->k, m);
+        if (wsb && (s = sc.ws(wsb, &ws))) return s;
+    }
+    const lbq::ActView av = view_of(abuf, L, w->k);
+    hipError_t e = quant_into(act_type, d_x, m, w->k, av, st);
+    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    return run_dot(sc, w, av, m, d_y, st);
 }
 
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
@@ -414,41 +500,12 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
         return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
-    const int act_type = lbq::vec_dot_type(w->type);
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (lbq::is_dense(w->type)) {
-        // candle's dense variant: an f32 matmul, no activation quantisation
-        hipError_t e = lbq::launch_dense(w->type, w->d_blocks, w->n, w->k, d_x, m, d_y, st);
-        return e == hipSuccess ? LBQ_OK : hip_fail(e, "dense matmul launch");
-    }
-    const ActLayout L = act_layout(act_type, m, w->k);
-    if (m <= 8 && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
-        // decode: the GEMV quantises x in its own prologue -- one launch, no scratch
-        const lbq::ActView av{nullptr, nullptr, nullptr, w->k, L.nb};
-        hipError_t e = lbq::launch_gemv_x(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, d_x, (int)m, d_y, st);
-        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
-        return LBQ_OK;
-    }
-    std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::gemm_prepass_fuses_quant(w->type, w->k, d_x)) {
-        // batched: the operand pre-pass quantises x itself
-        int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), "GEMM workspace");
-        if (s) return s;
-        const lbq::ActView none{nullptr, nullptr, nullptr, w->k, L.nb};
-        hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, none, d_x, m, d_y,
-                                        ctx->ws, st);
-        if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
-        return LBQ_OK;
-    }
-    int s = ensure_scratch(ctx, L.total);
-    if (s) return s;
-    const lbq::ActView av = view_of(ctx->scratch, L, w->k);
-    hipError_t e = quant_into(act_type, d_x, m, w->k, av, st);
-    if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
-    return run_dot(ctx, w, av, m, d_y, st);
+    Scratch sc;
+    sc.ctx = ctx;
+    return forward(ctx, w, d_x, m, d_y, static_cast<hipStream_t>(stream), sc, &ctx->mu);
 }
 
 int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
@@ -532,7 +589,9 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     for (int i = 0; i < count; i++) {
-        s = run_dot(ctx, ws[i], av, m, d_ys[i], st);
+        Scratch sc;
+        sc.ctx = ctx;
+        s = run_dot(sc, ws[i], av, m, d_ys[i], st);
         if (s) return s;
     }
     return LBQ_OK;
@@ -739,7 +798,9 @@ int lbq_qmatmul_act_f32(lbq_ctx *ctx, const lbq_weight *w, const lbq_act *a, flo
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
     std::lock_guard<std::mutex> lock(ctx->mu);
-    return run_dot(ctx, w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
+    Scratch sc;
+    sc.ctx = ctx;
+    return run_dot(sc, w, a->view, a->m, d_y, static_cast<hipStream_t>(stream));
 }
 
 int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stream) {
