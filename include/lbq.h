@@ -124,6 +124,23 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * variant: no quantisation, an f32 matmul.  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
+/* QMatMul::forward as lbq_qmatmul_f32 computes it (the same kernels, the same
+ * bits), allocating nothing: no hipMalloc, hipFree or allocating library call.
+ * No counterpart in the reference; for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid it.  The quantised activations and the batched GEMM's workspace live
+ * in a fixed array of LBQ_NOALLOC_SCRATCH_BYTES per device, resolved by
+ * lbq_init and held until the process ends.  A call that needs more (roughly
+ * m * k * 2 bytes of fp16 operands plus split-k partials above m = 8; every
+ * Llama-3-8B projection fits up to m = 512, down_proj up to m = 2048) returns
+ * LBQ_ERR_LIMIT before launching anything.  All contexts on a device share the
+ * one array, which keeps the last call's contents: calls that overlap on one
+ * device (on different streams or threads) race and must be ordered by the
+ * caller. */
+#define LBQ_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int lbq_qmatmul_f32_noalloc(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y,
+                            void *stream);
+
 /* Several weights applied to one x: ys[i][m][n_i] = x . W_i^T, exactly as
  * `count` separate lbq_qmatmul_f32 calls compute them (bit-identical), with x
  * quantised once and, at m = 1, every weight's rows streamed by one launch.

@@ -21,8 +21,15 @@
 
 static_assert(LBQ_GROUP_MAX == lbq::GROUP_MAX, "one group limit for the ABI and the kernels");
 
+// Scratch of lbq_qmatmul_f32_noalloc: one array per device (each GPU holds its
+// own copy while the process lives).  Host code never uses the array's name as
+// an address: lbq_init resolves it once per device with hipGetSymbolAddress.
+// Calls that overlap on one device share it and race.
+static __device__ __align__(256) uint8_t scratch[LBQ_NOALLOC_SCRATCH_BYTES];
+
 struct lbq_ctx {
     int device;
+    uint8_t *noalloc_scratch;  // this device's `scratch`, from hipGetSymbolAddress
     lbq::Tuning tune;     // launch-plan overrides, read from the environment at lbq_init
     std::mutex mu;        // guards scratch growth
     uint8_t *scratch;     // quantised activations (split layout)
@@ -367,6 +374,25 @@ int lbq_make_owned_weight(lbq_ctx *ctx, uint32_t type, int64_t n, int64_t k, voi
     return make_weight(ctx, type, n, k, static_cast<const uint8_t *>(d_blocks), nbytes, true, out);
 }
 
+namespace {
+// Per device: the address of `scratch` there, resolved once with the device current.
+std::mutex g_noalloc_mu;
+uint8_t *g_noalloc_ptr[64];
+
+int noalloc_scratch_of(int device, uint8_t **out) {
+    if (device >= 64) return fail(LBQ_ERR_LIMIT, "device %d: the allocation-free scratch covers devices 0..63", device);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[device] = static_cast<uint8_t *>(p);
+    }
+    *out = g_noalloc_ptr[device];
+    return LBQ_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char *lbq_last_error(void) { return g_err.c_str(); }
@@ -404,6 +430,7 @@ int lbq_type_size(uint32_t t) {
 
 int lbq_type_block_bytes(uint32_t t) { return t == LBQ_TYPE_Q2_K ? 84 : lbq_type_size(t); }
 
+
 int lbq_init(int device, lbq_ctx **out_ctx) {
     if (!out_ctx) return fail(LBQ_ERR_INVALID_ARG, "out_ctx is null");
     *out_ctx = nullptr;
@@ -413,9 +440,13 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
     if (device < 0 || device >= count) return fail(LBQ_ERR_INVALID_ARG, "device %d out of range (%d devices)", device, count);
     DeviceGuard g(device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    uint8_t *noalloc = nullptr;
+    const int s = noalloc_scratch_of(device, &noalloc);
+    if (s) return s;
     lbq_ctx *c = new (std::nothrow) lbq_ctx;
     if (!c) return fail(LBQ_ERR_OOM, "host allocation failed");
     c->device = device;
+    c->noalloc_scratch = noalloc;
     c->tune = lbq::tuning_from_env();
     c->scratch = nullptr;
     c->scratch_bytes = 0;
@@ -506,6 +537,29 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     Scratch sc;
     sc.ctx = ctx;
     return forward(ctx, w, d_x, m, d_y, static_cast<hipStream_t>(stream), sc, &ctx->mu);
+}
+
+int lbq_qmatmul_f32_noalloc(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y,
+                            void *stream) {
+    if (!ctx || !w) return fail(LBQ_ERR_INVALID_ARG, "null context or weight");
+    if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
+    if (m == 0) return LBQ_OK;
+    if (!d_x || !d_y) return fail(LBQ_ERR_INVALID_ARG, "null activation or output pointer");
+    if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
+        return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
+    if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    if (!ctx->noalloc_scratch) return fail(LBQ_ERR_INVALID_ARG, "context has no allocation-free scratch");
+    DeviceGuard g(ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    lbq::TuningScope tsc(&ctx->tune);
+    // every buffer the kernels need comes from this device's `scratch` (through
+    // the address lbq_init resolved); nothing is allocated, nothing needs clearing
+    // (each kernel writes every scratch byte it later reads)
+    Scratch sc;
+    sc.ctx = ctx;
+    sc.fixed = ctx->noalloc_scratch;
+    sc.fixed_bytes = LBQ_NOALLOC_SCRATCH_BYTES;
+    return forward(ctx, w, d_x, m, d_y, static_cast<hipStream_t>(stream), sc, nullptr);
 }
 
 int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
