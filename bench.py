@@ -58,6 +58,9 @@ def parse():
     p.add_argument("--no-gemm", action="store_true", help="skip the M = 512 MFMA measurement")
     p.add_argument("--no-configs", action="store_true",
                    help="skip configs 1, 3 and 4 (Q8_0 GEMV, Q6_K head / Q5_K batch 1-8, M crossover)")
+    p.add_argument("--prefill-profile", action="store_true",
+                   help="only run QMatMul::forward for Q4_K gate_proj 14336x4096 at M = 16, 32 and 512 "
+                        "(a short, fixed workload for rocprofv3 counter runs of the batched kernels)")
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a 256 MiB device copy 4 times (reference kernel of known size for "
                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -102,6 +105,58 @@ def timed_graph(torch, graph, reps, stream):
     return s.elapsed_time(e) / reps  # ms per replay
 
 
+def timed_graph_median(torch, graph, reps, stream):
+    """Median over `reps` replays, each bracketed by its own events (ms per replay)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for s, e in evs:
+        s.record(stream)
+        graph.replay()
+        e.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) for s, e in evs)
+    return t[len(t) // 2]
+
+
+class StepGraphs:
+    """Exactly n steps of a per-copy step function: a graph over all C copies
+    (C steps per replay) replayed n // C times, then a graph over the first n % C
+    copies once."""
+
+    def __init__(self, torch, step_fn, copies):
+        self.torch, self.copies = torch, copies
+        self.step_fn = step_fn
+        self.full = capture(torch, lambda: [step_fn(c) for c in copies])
+        self.part = {}
+
+    def _part(self, r):
+        if r not in self.part:
+            self.part[r] = capture(self.torch, lambda: [self.step_fn(c) for c in self.copies[:r]])
+        return self.part[r]
+
+    def run(self, n):
+        q, r = divmod(n, len(self.copies))
+        g = self._part(r) if r else None
+        for _ in range(q):
+            self.full.replay()
+        if g is not None:
+            g.replay()
+
+    def time(self, n, stream):
+        """ms per step over exactly n steps."""
+        q, r = divmod(n, len(self.copies))
+        if r:
+            self._part(r)  # captured outside the timed region
+        s = self.torch.cuda.Event(enable_timing=True)
+        e = self.torch.cuda.Event(enable_timing=True)
+        self.torch.cuda.synchronize()
+        s.record(stream)
+        self.run(n)
+        e.record(stream)
+        self.torch.cuda.synchronize()
+        return s.elapsed_time(e) / n
+
+
 def capture(torch, fn):
     g = torch.cuda.CUDAGraph()
     fn()  # eager pass: sizes scratch and warms the allocator outside capture
@@ -112,29 +167,43 @@ def capture(torch, fn):
     return g
 
 
-def cpu_baseline(layer_blocks, xs, budget_s):
-    """Oracle (C restatement of the reference CPU QMatMul) on one layer, all host cores."""
-    import numpy as np
-
-    import oracle
-    nthreads = oracle.nproc()
+def _cpu_layer_rate(oracle, layer_blocks, xs, budget_s, nthreads, native):
     total_bytes = sum(b.size for b in layer_blocks)
     reps = 0
     t0 = time.perf_counter()
     while True:
         for (name, n, k), blk, x in zip(LAYER, layer_blocks, xs):
-            oracle.qmatmul(oracle.Q4_K, blk, n, k, x, nthreads=nthreads)
+            oracle.qmatmul(oracle.Q4_K, blk, n, k, x, nthreads=nthreads, native=native)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 200:
             break
+    return total_bytes, reps, el
+
+
+def cpu_baseline(layer_blocks, xs, budget_s):
+    """Oracle (C restatement of the reference CPU QMatMul) on one layer, all host cores: the
+    scalar-faithful build (candle's default x86-64 target runs the generic vec_dot), and the same
+    source built with -march=native on this host (an upper bound for the CPU path)."""
+    import oracle
+    nthreads = oracle.nproc()
+    total_bytes, reps, el = _cpu_layer_rate(oracle, layer_blocks, xs, budget_s, nthreads, False)
     per = el / reps
-    return {"value": round(total_bytes / per / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-            "sample": f"oracle qmatmul (Q8_K activation quant + integer vec_dot, rows split over {nthreads} "
-                      f"threads) on the 7 Q4_K projections of one layer at batch 1 ({total_bytes / 1e6:.1f} MB "
-                      f"of blocks), {reps} passes in {el:.1f} s; {per * 1e3:.2f} ms per layer",
-            "ms_per_step": round(per * 1e3, 3),
-            "cpu_model": _cpu_model()}
+    out = {"value": round(total_bytes / per / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+           "sample": f"oracle qmatmul (Q8_K activation quant + integer vec_dot, rows split over {nthreads} "
+                     f"threads) on the 7 Q4_K projections of one layer at batch 1 ({total_bytes / 1e6:.1f} MB "
+                     f"of blocks), {reps} passes in {el:.1f} s; {per * 1e3:.2f} ms per layer; scalar-faithful "
+                     f"build (-O3, generic x86-64)",
+           "ms_per_step": round(per * 1e3, 3),
+           "cpu_model": _cpu_model()}
+    try:
+        tb, r2, el2 = _cpu_layer_rate(oracle, layer_blocks, xs, budget_s / 2, nthreads, "host")
+        out["native"] = {"value": round(tb / (el2 / r2) / 1e9, 3), "unit": "GB/s", "cores": nthreads,
+                         "ms_per_step": round(el2 / r2 * 1e3, 3),
+                         "sample": f"same oracle built with -O3 -march=native on this host, {r2} passes in {el2:.1f} s"}
+    except Exception as e:  # no compiler on the host
+        out["native"] = {"value": None, "sample": f"unavailable: {e}"}
+    return out
 
 
 def _cpu_model():
@@ -165,6 +234,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.copy_probe:
         copy_probe(torch, dev)
+    if args.prefill_profile:
+        prefill_profile(torch, qz, dev)
+        return
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B1)
     Q4K, Q6K = qz.GgmlDType.Q4K, qz.GgmlDType.Q6K
@@ -178,58 +250,59 @@ def main():
     io_bytes = sum(4 * (n + k) for (_, n, k) in LAYER)
     log(f"weights ready: {args.copies} x {layer_bytes / 1e6:.1f} MB in {time.perf_counter() - t0:.1f} s")
 
-    def full_step_all_copies():
-        for layer in copies:
-            for qm, x in zip(layer, xs):
-                qm.forward(x)
+    def full_step(layer):
+        for qm, x in zip(layer, xs):
+            qm.forward(x)
 
     # the same step through the grouped entry point (q|k|v and gate|up as the
     # reference's call sites feed them one x): 4 launches instead of 7
-    def grouped_step_all_copies():
-        for layer in copies:
-            qz.qmatmul_group(layer[0:3], xs[0])
-            layer[3].forward(xs[3])
-            qz.qmatmul_group(layer[4:6], xs[4])
-            layer[6].forward(xs[6])
+    def grouped_step(layer):
+        qz.qmatmul_group(layer[0:3], xs[0])
+        layer[3].forward(xs[3])
+        qz.qmatmul_group(layer[4:6], xs[4])
+        layer[6].forward(xs[6])
 
     # the layer as its call sites would run it: input RMS norm + q|k|v in one
     # launch, o, then post-attention RMS norm + gate/up + SiLU product in one
     # launch feeding down_proj
     norm_w = [1.0 + 0.1 * torch.randn(4096, generator=gen, device=dev) for _ in range(2)]
 
-    def fused_step_all_copies():
-        for layer in copies:
-            qz.rmsnorm_qmatmul_group(layer[0:3], xs[0], norm_w[0], 1e-5)
-            layer[3].forward(xs[3])
-            h = qz.rmsnorm_gate_up_silu(layer[4], layer[5], xs[4], norm_w[1], 1e-5)
-            layer[6].forward(h)
+    def fused_step(layer):
+        qz.rmsnorm_qmatmul_group(layer[0:3], xs[0], norm_w[0], 1e-5)
+        layer[3].forward(xs[3])
+        h = qz.rmsnorm_gate_up_silu(layer[4], layer[5], xs[4], norm_w[1], 1e-5)
+        layer[6].forward(h)
 
-    # activation handles for the dot-only (roofline) graph
+    # activation handles for the dot-only graph
     acts = {k: qz.QActivation(qz.GgmlDType.Q8K, 1, k, dev) for k in (4096, 14336)}
     for (_, n, k), x in zip(LAYER, xs):
         acts[k].quantize(x)
 
-    def dot_all_copies():
-        for layer in copies:
-            for qm, (_, n, k), y in zip(layer, LAYER, ys):
-                qm.forward_quantized(acts[k], y)
+    def dot_step(layer):
+        for qm, (_, n, k), y in zip(layer, LAYER, ys):
+            qm.forward_quantized(acts[k], y)
 
     stream = torch.cuda.current_stream(dev)
-    g_full = capture(torch, full_step_all_copies)
-    g_dot = capture(torch, dot_all_copies)
-    g_grp = capture(torch, grouped_step_all_copies)
-    g_fus = capture(torch, fused_step_all_copies)
-    reps = max(1, (args.steps + args.copies - 1) // args.copies)
-    wreps = max(1, (args.warmup + args.copies - 1) // args.copies)
-    steps = reps * args.copies
-    timed_graph(torch, g_full, wreps, stream)
-    ms_full = timed_graph(torch, g_full, reps, stream) / args.copies
-    timed_graph(torch, g_dot, wreps, stream)
-    ms_dot = timed_graph(torch, g_dot, reps, stream) / args.copies
-    timed_graph(torch, g_grp, wreps, stream)
-    ms_grp = timed_graph(torch, g_grp, reps, stream) / args.copies
-    timed_graph(torch, g_fus, wreps, stream)
-    ms_fus = timed_graph(torch, g_fus, reps, stream) / args.copies
+    for fn in (full_step, dot_step, grouped_step, fused_step):
+        fn(copies[0])  # eager pass: sizes scratch outside capture
+    torch.cuda.synchronize()
+    g_full = StepGraphs(torch, full_step, copies)
+    g_dot = StepGraphs(torch, dot_step, copies)
+    g_grp = StepGraphs(torch, grouped_step, copies)
+    g_fus = StepGraphs(torch, fused_step, copies)
+    steps, warmup = args.steps, args.warmup
+    # the headline: exactly `warmup` untimed steps, then exactly `steps` timed ones
+    if warmup:
+        g_full.run(warmup)
+    ms_full = g_full.time(steps, stream)
+    reps = max(1, (steps + args.copies - 1) // args.copies)
+    wreps = max(1, (warmup + args.copies - 1) // args.copies)
+    side = max(args.copies, min(steps, 8 * args.copies))  # steps timed for the side measurements
+    ms = {}
+    for name, g in (("dot", g_dot), ("grp", g_grp), ("fus", g_fus)):
+        g.run(args.copies)
+        ms[name] = g.time(side, stream)
+    ms_dot, ms_grp, ms_fus = ms["dot"], ms["grp"], ms["fus"]
     value = layer_bytes / (ms_full * 1e-3) / 1e9
     full_gbs = (layer_bytes + io_bytes) / (ms_full * 1e-3) / 1e9
     dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
@@ -260,7 +333,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": wreps * args.copies,
+        "warmup": warmup,
         "ms_per_step": round(ms_full, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -327,11 +400,11 @@ def main():
 
     # ---------------------------------------------------------------- config 4: M = 512 MFMA path
     if not args.no_gemm:
-        result["prefill_gemm"] = gemm_bench(torch, qz, gen, dev, stream, reps)
+        result["prefill_gemm"] = gemm_bench(torch, qz, gen, dev, stream)
 
     # ---------------------------------------------------------------- configs 1, 3, 4: other shapes
     if not args.no_configs:
-        result["configs"] = configs_bench(torch, qz, gen, dev, stream)
+        result["configs"] = configs_bench(torch, qz, gen, dev, stream, result.get("prefill_gemm"))
 
     # ---------------------------------------------------------------- config 5: 32-layer stack
     if not args.no_stack:
@@ -340,36 +413,69 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def gemm_bench(torch, qz, gen, dev, stream, reps):
-    """Q4_K gate_proj / down_proj at M = 512: QMatMul::forward (quantise, operand pre-pass, MFMA
-    GEMM) and the dot half alone, 2*M*N*K flops over the time, against dense bf16 peak."""
+def prefill_profile(torch, qz, dev):
+    """Q4_K gate_proj 14336x4096 forward at M = 16 (k-sliced tiles), 32 (k-sliced) and 512 (wide
+    tiles), 8 weight copies rotated, 5 graph replays each, for counter collection."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x1B4)
+    stream = torch.cuda.current_stream(dev)
+    qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, 14336, 4096, gen, dev) for _ in range(8)]
+    out = {}
+    for M in (16, 32, 512):
+        x = torch.randn(M, 4096, generator=gen, device=dev)
+        out[f"q4_k_gate_proj_14336x4096_m{M}"] = round(time_forwards(torch, qms, x, stream, reps=5, warm=1), 2)
+    print(json.dumps({"prefill_profile_us": out}), flush=True)
+
+
+def time_forwards(torch, qms, x, stream, reps=25, warm=3):
+    """us per QMatMul::forward: one graph replay runs forward over every weight copy in qms
+    (rotating copies keeps the working set out of the MALL); median over `reps` replays."""
+    g = capture(torch, lambda: [qm.forward(x) for qm in qms])
+    timed_graph(torch, g, warm, stream)
+    us = timed_graph_median(torch, g, reps, stream) / len(qms) * 1e3
+    del g
+    return us
+
+
+def gemm_bench(torch, qz, gen, dev, stream):
+    """Q4_K gate_proj / down_proj at M = 512 (configs[3]): QMatMul::forward (quantise + operand
+    pre-pass + MFMA GEMM) and the dot half alone (forward_quantized: pre-pass from Q8_K codes +
+    GEMM), 2*M*N*K flops over the median of 25 graph replays, against dense bf16/fp16 peak."""
     out = {}
     M = 512
     for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
-        qm = make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev)
+        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(2)]
         x = torch.randn(M, k, generator=gen, device=dev)
         y = torch.empty(M, n, device=dev)
-        act = qz.QActivation.for_weight(qm, M).quantize(x)
-        g_f = capture(torch, lambda: qm.forward(x))
-        g_d = capture(torch, lambda: qm.forward_quantized(act, y))
-        r = max(5, reps // 4)
-        timed_graph(torch, g_f, 3, stream)
-        ms_f = timed_graph(torch, g_f, r, stream)
+        act = qz.QActivation.for_weight(qms[0], M).quantize(x)
+        us_f = time_forwards(torch, qms, x, stream)
+        g_d = capture(torch, lambda: [qm.forward_quantized(act, y) for qm in qms])
         timed_graph(torch, g_d, 3, stream)
-        ms_d = timed_graph(torch, g_d, r, stream)
+        us_d = timed_graph_median(torch, g_d, 25, stream) / len(qms) * 1e3
         fl = 2.0 * M * n * k
+        nbytes = qms[0].qtensor().storage_size_in_bytes()
         out[f"{name}_{n}x{k}_m{M}"] = {
-            "us_forward": round(ms_f * 1e3, 2), "us_dot": round(ms_d * 1e3, 2),
-            "TFLOP/s_forward": round(fl / (ms_f * 1e-3) / 1e12, 1),
-            "TFLOP/s_dot": round(fl / (ms_d * 1e-3) / 1e12, 1),
-            "frac_bf16_peak_dot": round(fl / (ms_d * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
-        log(f"gemm {name} M={M}: forward {ms_f * 1e3:.1f} us, dot {ms_d * 1e3:.1f} us "
-            f"({fl / (ms_d * 1e-3) / 1e12:.0f} TFLOP/s)")
-        del g_f, g_d, qm, x, y, act
+            "us_forward": round(us_f, 2), "us_dot": round(us_d, 2),
+            "TFLOP/s_forward": round(fl / us_f / 1e6, 1), "TFLOP/s_dot": round(fl / us_d / 1e6, 1),
+            "frac_bf16_peak_forward": round(fl / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "frac_bf16_peak_dot": round(fl / us_d / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "weight_GB/s_forward": round(nbytes / us_f / 1e3, 1)}
+        log(f"gemm {name} M={M}: forward {us_f:.1f} us, dot {us_d:.1f} us ({fl / us_d / 1e6:.0f} TFLOP/s)")
+        del g_d, qms, x, y, act
+    torch.cuda.empty_cache()
+    g, d = out["gate_proj_14336x4096_m512"], out["down_proj_4096x14336_m512"]
+    fl = 2.0 * 512 * 14336 * 4096
+    us = (g["us_forward"] + d["us_forward"]) / 2
+    out["roofline"] = {
+        "bound": "mfma", "achieved": round(fl / us / 1e6, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4), "traffic": None,
+        "kernel": "QMatMul::forward at M = 512 (Q8_K quantise + fp16 operand pre-pass, then k_gemm_w: eight-wave "
+                  "128 x 256 tiles, v_mfma_f32_32x32x16_f16), mean of gate 14336x4096 and down 4096x14336",
+        "us_per_forward": round(us, 2), "flops_per_forward": fl}
     return out
 
 
-def configs_bench(torch, qz, gen, dev, stream):
+def configs_bench(torch, qz, gen, dev, stream, prefill=None):
     """BASELINE configs[0] (Q8_0 4096x4096 GEMV, m = 1), configs[2] (Q6_K LM head 128256x4096 and
     Q5_K gate/up 14336x4096 at batch 1, 4, 8; x ~ N(0, 1) with 1 % of entries x20) and configs[3]
     (Q4_K gate 14336x4096 / down 4096x14336 at M = 16, 64, 512, 2048): QMatMul::forward per launch,
@@ -377,12 +483,7 @@ def configs_bench(torch, qz, gen, dev, stream):
     out = {}
 
     def timed_rot(qms, x, reps):
-        y = torch.empty(x.shape[0], qms[0].qtensor().shape()[0], device=dev)
-        g = capture(torch, lambda: [qm.forward(x) for qm in qms])
-        timed_graph(torch, g, 2, stream)
-        us = timed_graph(torch, g, reps, stream) / len(qms) * 1e3
-        del g, y
-        return us
+        return time_forwards(torch, qms, x, stream, reps=max(20, reps))
 
     def x_outliers(b, k):
         x = torch.randn(b, k, generator=gen, device=dev)
@@ -395,6 +496,33 @@ def configs_bench(torch, qz, gen, dev, stream):
     us = timed_rot(q8, torch.randn(1, 4096, generator=gen, device=dev), 20)
     out["q8_0_4096x4096_m1"] = {"us": round(us, 2), "weight_GB/s": round(wb / us / 1e3, 1),
                                 "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    # dense F16 weights (candle's dense QMatMul variant: an f32 matmul), 4096 x 4096
+    f16 = []
+    for _ in range(8):
+        w = (torch.randn(4096, 4096, generator=gen, device=dev) * 0.02).to(torch.float16)
+        f16.append(qz.QMatMul.from_qtensor(qz.QTensor(w.view(torch.uint8).reshape(-1), qz.GgmlDType.F16, (4096, 4096))))
+    fb = 4096 * 4096 * 2
+    for M in (1, 512):
+        x = torch.randn(M, 4096, generator=gen, device=dev)
+        us = timed_rot(f16 if M == 1 else f16[:2], x, 20)
+        fl = 2.0 * M * 4096 * 4096
+        out[f"f16_dense_4096x4096_m{M}"] = {"us": round(us, 2), "weight_GB/s": round(fb / us / 1e3, 1),
+                                           "frac_hbm": round(fb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                           "TFLOP/s": round(fl / us / 1e6, 1),
+                                           "path": "f32 GEMV (m <= 8) / v_mfma_f32_32x32x2_f32 GEMM (fp32 peak 157.3 TFLOP/s)"}
+        log(f"dense F16 M={M}: {us:.1f} us")
+    del f16
+    # Q8_0 batched on the MFMA path (prefill of the same weight)
+    for M in (16, 64, 512):
+        x = torch.randn(M, 4096, generator=gen, device=dev)
+        us = timed_rot(q8 if M <= 64 else q8[:2], x, 20)
+        fl = 2.0 * M * 4096 * 4096
+        out[f"q8_0_4096x4096_m{M}"] = {"us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                                       "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                       "weight_GB/s": round(wb / us / 1e3, 1),
+                                       "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                       "path": "MFMA (fp16 operands of the Q8_0 activation and d*q weight values)"}
+        log(f"configs[0] Q8_0 M={M}: {us:.1f} us")
     del q8
     torch.cuda.empty_cache()
 
@@ -418,8 +546,12 @@ def configs_bench(torch, qz, gen, dev, stream):
         qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(8)]
         nbytes = qms[0].qtensor().storage_size_in_bytes()
         for M in (16, 64, 512, 2048):
-            x = torch.randn(M, k, generator=gen, device=dev)
-            us = timed_rot(qms if M <= 64 else qms[:2], x, 10 if M <= 64 else 4)
+            key = f"{name}_{n}x{k}_m{M}"
+            if M == 512 and prefill and key in prefill:  # the same measurement as prefill_gemm
+                us = prefill[key]["us_forward"]
+            else:
+                x = torch.randn(M, k, generator=gen, device=dev)
+                us = timed_rot(qms if M <= 64 else qms[:2], x, 20)
             fl = 2.0 * M * n * k
             out[f"q4_k_{name}_{n}x{k}_m{M}"] = {
                 "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),

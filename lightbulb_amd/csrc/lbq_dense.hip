@@ -57,7 +57,7 @@ template <bool F16, int MR>
 __global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ W, int64_t N, int64_t K,
                                                     const float *__restrict__ x, int m, float *__restrict__ y) {
     const bool xv = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;  // K % 8 == 0: every row likewise
-    constexpr int UN = 4;
+    constexpr int UN = 8;  // 4096 f16 / 2048 f32 weights of the row in flight per wave
     constexpr int64_t WB = F16 ? 2 : 4;
     const int lane = threadIdx.x & 63;
     const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), nw = (int64_t)gridDim.x * 4;

@@ -375,7 +375,20 @@ struct Fast<TYPE_Q8_0, 1> {
 // NORM (k-quants, nbx <= 32): x is first RMS-normalised as candle's RmsNorm does
 // in f32 -- x / sqrt(sum(x^2) / k + eps) * alpha -- with the sum of squares taken
 // over the whole workgroup (every workgroup holds all of x).
-template <int TYPE, bool NORM, int XJ, int WPG, class Between>
+// Workgroup barrier.  FENCE: __syncthreads (its release fence also waits for
+// every load to LDS still in flight); otherwise this wave's LDS writes complete,
+// then a plain s_barrier, so loads to LDS issued by `between` stay in flight.
+template <bool FENCE>
+__device__ __forceinline__ void wg_barrier() {
+    if constexpr (FENCE) {
+        __syncthreads();
+    } else {
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched
+        __builtin_amdgcn_s_barrier();
+    }
+}
+
+template <int TYPE, bool NORM, int XJ, int WPG, class Between, bool FENCE = true>
 __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between,
                                                const float *__restrict__ alpha, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -424,7 +437,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             ss = __int_as_float(rl(__float_as_uint(ss), 0)) + __int_as_float(rl(__float_as_uint(ss), 16)) +
                  __int_as_float(rl(__float_as_uint(ss), 32)) + __int_as_float(rl(__float_as_uint(ss), 48));
             if (lane == 0) red[wave] = ss;
-            __syncthreads();
+            wg_barrier<FENCE>();
             float tot = red[0];
 #pragma unroll
             for (int w = 1; w < WPG; w++) tot += red[w];
@@ -492,7 +505,7 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
             }
         }
     }
-    __syncthreads();
+    wg_barrier<FENCE>();
 }
 
 // Pre-quantised activations (split global layout) -> the LDS layout.  Straight-line
@@ -611,7 +624,7 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
-template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4>
+template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4, int RING = 0>
 __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                     ActView act, const float *__restrict__ alpha, float eps) {
     static_assert(WPG == 4 || (FUSED && WPG == 8), "waves per workgroup: 4, or 8 for the fused prologue");
@@ -699,7 +712,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     // wave's whole stream up front, leave every wave waiting for its first rows
     // while the whole matrix is in flight, and bunch the compute at the end.
     // Deep rows (IT > 4) keep two buffers (registers).
-    constexpr int NBUF = (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
+    constexpr int NBUF = RING > 0 ? RING : (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
     Raw ring[NBUF][IT];
     auto issue_ring = [&] {
 #pragma unroll

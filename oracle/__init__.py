@@ -68,12 +68,17 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
 
 
-def _load(native: bool = False) -> ctypes.CDLL:
-    name = "liblbq_oracle_native.so" if native else "liblbq_oracle.so"
+def _load(native: bool | str = False) -> ctypes.CDLL:
+    """The scalar build, the -march=native build made here (native=True), or the
+    build for the host running this process (native="host", made by `make host`)."""
+    name = ("liblbq_oracle_host.so" if native == "host" else "liblbq_oracle_native.so" if native
+            else "liblbq_oracle.so")
     if name in _libs:
         return _libs[name]
     path = _BUILD / name
-    if not path.exists():
+    if native == "host":
+        subprocess.run(["make", "-s", "-C", str(HERE), "host"], check=True)
+    elif not path.exists():
         build()
     lib = ctypes.CDLL(str(path))
     c = ctypes
@@ -146,7 +151,7 @@ def vec_dot(t: int, k: int, wrow: np.ndarray, xrow: np.ndarray) -> float:
 
 
 def qmatmul(t: int, w_blocks: np.ndarray, n: int, k: int, x: np.ndarray, nthreads: int = 1,
-            native: bool = False) -> np.ndarray:
+            native: bool | str = False) -> np.ndarray:
     """candle's CPU QMatMul::forward restated: y[m, n] = x[m, k] . W^T."""
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
     w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
