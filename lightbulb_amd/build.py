@@ -32,7 +32,9 @@ HIP_FLAGS = [
 NO_CONTRACT = {"lbq_wquant.hip"}
 
 SOURCES = ["lbq_act.hip", "lbq_gemv.hip", "lbq_gemv_q4k.hip", "lbq_gemv_q5k.hip", "lbq_gemv_q6k.hip",
-           "lbq_gemv_q8_0.hip", "lbq_gemv_legacy.hip", "lbq_gemv_k23.hip", "lbq_gemm.hip", "lbq_dense.hip", "lbq_wquant.hip",
+           "lbq_gemv_q8_0.hip", "lbq_gemv_legacy.hip", "lbq_gemv_k23.hip", "lbq_gemm.hip", "lbq_gemm_q4k.hip", "lbq_gemm_q5k.hip",
+           "lbq_gemm_q6k.hip", "lbq_gemm_q8_0.hip", "lbq_gemm_q4_0.hip", "lbq_gemm_q5_0.hip",
+           "lbq_gemm_k23.hip", "lbq_dense.hip", "lbq_wquant.hip",
            "lbq_api.cpp", "lbq_gguf.cpp"]
 
 

@@ -1,0 +1,9 @@
+// lbq_gemm_q4k.hip -- the batched-path MFMA kernels for Q4_K weights (one unit per
+// type, so the library builds them in parallel).
+#include "lbq_gemm_kernels.hpp"
+
+namespace lbq {
+template hipError_t launch_typed<TYPE_Q4_K>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,
+                                          const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,
+                                          float *, int64_t, hipStream_t);
+}  // namespace lbq

@@ -1,0 +1,12 @@
+// lbq_gemm_q5_0.hip -- the batched-path MFMA kernels for Q5_0 and Q5_1 weights
+// (one unit per type family, so the library builds them in parallel).
+#include "lbq_gemm_kernels.hpp"
+
+namespace lbq {
+template hipError_t launch_typed<TYPE_Q5_0>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,
+                                          const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,
+                                          float *, int64_t, hipStream_t);
+template hipError_t launch_typed<TYPE_Q5_1>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,
+                                          const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,
+                                          float *, int64_t, hipStream_t);
+}  // namespace lbq

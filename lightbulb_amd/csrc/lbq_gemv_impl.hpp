@@ -861,7 +861,7 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
     g.row_bytes = row_bytes;
     g.nb = (int)(k / D::VALS);
     g.pieces = g.nb * D::PPB;
-    if constexpr (has_mfma_gemm(TYPE)) {  // the types with a Fast<> decoder
+    if constexpr (has_fast_gemv(TYPE)) {  // the types with a Fast<> decoder
         if (m == 1) {
             const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
             if (e != hipErrorNotSupported) return e;

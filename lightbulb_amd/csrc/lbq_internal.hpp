@@ -18,10 +18,22 @@ constexpr bool is_legacy(int t) { return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t =
 constexpr bool is_kquant(int t) {
     return t == TYPE_Q2_K || t == TYPE_Q3_K || t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K;
 }
-// weight types the MFMA GEMM serves at m > 8 (the others run the GEMV over row chunks)
-constexpr bool has_mfma_gemm(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
-// ... at this k: the GEMM steps through k in 256-value super-blocks (Q8_0: 8 blocks)
+// weight types with the register-resident decode GEMV decoders (the m = 1 fast path)
+constexpr bool has_fast_gemv(int t) { return t == TYPE_Q4_K || t == TYPE_Q5_K || t == TYPE_Q6_K || t == TYPE_Q8_0; }
+// weight types the MFMA GEMM serves at m > 8: every quantised weight type
+constexpr bool has_mfma_gemm(int t) { return is_kquant(t) || is_legacy(t) || t == TYPE_Q8_0; }
+// ... at this k: the GEMM steps through k in 256-value super-blocks (32-value
+// types: 8 blocks); other k run the decode GEMV over row chunks of 8
 constexpr bool gemm_serves(int t, int64_t k) { return has_mfma_gemm(t) && k % 256 == 0; }
+// types whose per-lane weight state (raw bytes + expanded operands) is large: one
+// workgroup per CU for the 32-row-tile kernels, no 128-row k_gemm tiles, one
+// k-step of A read-ahead in the tall kernel; the k-sliced kernel up to 64 rows
+// types whose GEMM adds an extra k-step per super-block for the reference's
+// m * s term (Q8_1 activations' stored block sums)
+constexpr bool gemm_offset_step(int t) { return t == TYPE_Q4_1 || t == TYPE_Q5_1; }
+constexpr bool gemm_heavy(int t) {
+    return t == TYPE_Q6_K || t == TYPE_Q8_0 || t == TYPE_Q3_K || t == TYPE_Q5_0 || t == TYPE_Q5_1;
+}
 // activation type of QMatMul's vec_dot for a weight type (candle GgmlType::VecDotType)
 constexpr int vec_dot_type(int t) {
     return is_kquant(t) ? TYPE_Q8_K : (t == TYPE_Q4_1 || t == TYPE_Q5_1) ? TYPE_Q8_1 : TYPE_Q8_0;

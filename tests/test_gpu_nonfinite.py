@@ -20,10 +20,15 @@ import torch
 import blockpack as bp
 from test_gpu_parity import Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, assert_rows_close, gpu_qmatmul, tight_bound, to_dev
 
+Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K = 2, 3, 6, 7, 10, 11
+ALL = [Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K]
+
 pytestmark = pytest.mark.gpu
 
-HDR = {Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,), Q8_0: (0,)}  # byte offsets of the f16 scales
-BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34}
+# byte offsets of the f16 scales (and mins / offsets) in a block
+HDR = {Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,), Q8_0: (0,), Q4_0: (0,), Q4_1: (0, 2), Q5_0: (0,), Q5_1: (0, 2),
+       Q2_K: (80, 82), Q3_K: (108,)}
+BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q2_K: 84, Q3_K: 110}
 
 
 def _nan_rows(rng, m, k):
@@ -44,7 +49,7 @@ def test_quantize_act_nan_bitwise(oracle, lbq, dev, act):
     assert np.array_equal(got, oracle.quantize_act(act, x))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("t", ALL)
 def test_forward_nan_activations(oracle, lbq, dev, t):
     rng = np.random.default_rng(310 + t)
     n, k = 300, 4096
@@ -76,7 +81,7 @@ def _poison(raw, t, n, nbpr, rng):
     return sorted(int(r) for r in rows), sorted(nan_rows)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("t", ALL)
 def test_dequant_nonfinite_scales(oracle, lbq, dev, t):
     from lightbulb_amd.quantized import dequantize_tensor
     rng = np.random.default_rng(320 + t)
@@ -92,7 +97,7 @@ def test_dequant_nonfinite_scales(oracle, lbq, dev, t):
     assert np.isnan(ref).any() and np.isinf(ref).any()
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("t", ALL)
 def test_forward_nonfinite_scales(oracle, lbq, dev, t):
     rng = np.random.default_rng(330 + t)
     n, k = 200, 1024
@@ -115,7 +120,7 @@ def test_forward_nonfinite_scales(oracle, lbq, dev, t):
         assert_rows_close(y[rows][:, good], ref[:, good], tight_bound(t, m))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("t", ALL)
 @pytest.mark.parametrize("d_scale", [1e-6, 1e-7])
 def test_tiny_scales_mfma(oracle, lbq, dev, t, d_scale):
     # |d| ~ 1e-6 .. 1e-7: dequantised values far below the fp16 normal range

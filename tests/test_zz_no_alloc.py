@@ -19,11 +19,11 @@ import blockpack as bp
 from test_gpu_parity import Q4_K, Q5_K, Q6_K, Q8_0, assert_rows_close, tight_bound, to_dev
 
 pytestmark = pytest.mark.gpu
-F16, Q4_0 = 1, 2
+F16, Q4_0, Q4_1 = 1, 2, 3
 
 
 def _weight(L, ctx, t, n, k, rng, dev):
-    bs = 1 if t == F16 else (32 if t in (Q8_0, Q4_0) else 256)
+    bs = 1 if t == F16 else (32 if t in (Q8_0, Q4_0, Q4_1) else 256)
     if t == F16:
         raw = (rng.standard_normal(n * k) * 0.05).astype(np.float16).view(np.uint8)
     else:
@@ -52,7 +52,8 @@ def _both(L, ctx, h, x, n, dev):
     (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then k-sliced
     (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then k-sliced
     (Q8_0, 512, 4096, (64, 12)),       # Q8_0 on MFMA
-    (Q4_0, 300, 1024, (20, 9)),        # activation scratch + GEMV row chunks
+    (Q4_0, 300, 1184, (20, 9)),        # activation scratch + GEMV row chunks (k % 256 != 0)
+    (Q4_1, 300, 1024, (20, 9)),        # MFMA with the offset k-step operands in the workspace
     (F16, 300, 1024, (20, 3)),         # dense
 ])
 def test_noalloc_matches_qmatmul(oracle, lbq, dev, t, n, k, ms):
@@ -72,7 +73,7 @@ def test_noalloc_matches_qmatmul(oracle, lbq, dev, t, n, k, ms):
                 assert_rows_close(y2[rows], ref, 1e-5)
             else:
                 ref = oracle.qmatmul(t, raw, n, k, x[rows], nthreads=8).astype(np.float64)
-                assert_rows_close(y2[rows], ref, tight_bound(t, m) if t != Q4_0 else 1e-4)
+                assert_rows_close(y2[rows], ref, tight_bound(t, m) if k % 256 == 0 else 1e-4)
     finally:
         L.lbq_weight_destroy(h)
 
