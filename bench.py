@@ -525,6 +525,23 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
         log(f"configs[0] Q8_0 M={M}: {us:.1f} us")
     del q8
     torch.cuda.empty_cache()
+    # the 32-value legacy types on the same MFMA path (not BASELINE configs: the GGUF
+    # files the reference's own tests serve, e.g. a Q4_0 TinyLlama, prefill this way)
+    for t, tname in ((qz.GgmlDType.Q4_0, "q4_0"), (qz.GgmlDType.Q4_1, "q4_1"), (qz.GgmlDType.Q5_0, "q5_0"),
+                     (qz.GgmlDType.Q5_1, "q5_1")):
+        qms = [make_weights(torch, qz, t, 4096, 4096, gen, dev) for _ in range(8)]
+        lb = qms[0].qtensor().storage_size_in_bytes()
+        for M in (16, 512):
+            x = torch.randn(M, 4096, generator=gen, device=dev)
+            us = timed_rot(qms if M <= 64 else qms[:2], x, 20)
+            fl = 2.0 * M * 4096 * 4096
+            out[f"{tname}_4096x4096_m{M}"] = {"us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                                              "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                              "weight_GB/s": round(lb / us / 1e3, 1),
+                                              "frac_hbm": round(lb / us / 1e3 / HBM_PEAK_GBS, 4)}
+        log(f"{tname}: M=16 {out[f'{tname}_4096x4096_m16']['us']} us, M=512 {out[f'{tname}_4096x4096_m512']['us']} us")
+        del qms
+    torch.cuda.empty_cache()
 
     # Q6_K LM head (431 MB, one copy exceeds the MALL) and Q5_K gate/up (8 copies)
     head = [make_weights(torch, qz, qz.GgmlDType.Q6K, VOCAB, 4096, gen, dev)]
