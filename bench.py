@@ -282,14 +282,27 @@ def main():
         for qm, (_, n, k), y in zip(layer, LAYER, ys):
             qm.forward_quantized(acts[k], y)
 
+    # the step as a caller holding x and y in host memory runs it (a shim over host
+    # tensors): per projection x host -> device, forward, y device -> host, through
+    # pinned buffers on the same stream -- the PCIe-inclusive rate, never `value`
+    hxs = [torch.randn(1, k, generator=gen, device=dev).cpu().pin_memory() for (_, n, k) in LAYER]
+    hys = [torch.empty(1, n, pin_memory=True) for (_, n, k) in LAYER]
+    dxs = [torch.empty(1, k, device=dev) for (_, n, k) in LAYER]
+
+    def host_step(layer):
+        for qm, hx, hy, dx in zip(layer, hxs, hys, dxs):
+            dx.copy_(hx, non_blocking=True)
+            hy.copy_(qm.forward(dx), non_blocking=True)
+
     stream = torch.cuda.current_stream(dev)
-    for fn in (full_step, dot_step, grouped_step, fused_step):
+    for fn in (full_step, dot_step, grouped_step, fused_step, host_step):
         fn(copies[0])  # eager pass: sizes scratch outside capture
     torch.cuda.synchronize()
     g_full = StepGraphs(torch, full_step, copies)
     g_dot = StepGraphs(torch, dot_step, copies)
     g_grp = StepGraphs(torch, grouped_step, copies)
     g_fus = StepGraphs(torch, fused_step, copies)
+    g_host = StepGraphs(torch, host_step, copies)
     steps, warmup = args.steps, args.warmup
     # the headline: exactly `warmup` untimed steps, then exactly `steps` timed ones
     if warmup:
@@ -299,17 +312,18 @@ def main():
     wreps = max(1, (warmup + args.copies - 1) // args.copies)
     side = max(args.copies, min(steps, 8 * args.copies))  # steps timed for the side measurements
     ms = {}
-    for name, g in (("dot", g_dot), ("grp", g_grp), ("fus", g_fus)):
+    for name, g in (("dot", g_dot), ("grp", g_grp), ("fus", g_fus), ("host", g_host)):
         g.run(args.copies)
         ms[name] = g.time(side, stream)
-    ms_dot, ms_grp, ms_fus = ms["dot"], ms["grp"], ms["fus"]
+    ms_dot, ms_grp, ms_fus, ms_host = ms["dot"], ms["grp"], ms["fus"], ms["host"]
     value = layer_bytes / (ms_full * 1e-3) / 1e9
     full_gbs = (layer_bytes + io_bytes) / (ms_full * 1e-3) / 1e9
     dot_gbs = (layer_bytes + io_bytes) / (ms_dot * 1e-3) / 1e9
     log(f"step (7 x QMatMul::forward): {ms_full * 1e3:.2f} us -> {value:.0f} GB/s; "
         f"dot kernels alone {ms_dot * 1e3:.2f} us -> {dot_gbs:.0f} GB/s; "
         f"grouped (4 launches) {ms_grp * 1e3:.2f} us -> {layer_bytes / (ms_grp * 1e-3) / 1e9:.0f} GB/s; "
-        f"call-site fused (norm+q|k|v, o, norm+gate|up+SiLU, down) {ms_fus * 1e3:.2f} us")
+        f"call-site fused (norm+q|k|v, o, norm+gate|up+SiLU, down) {ms_fus * 1e3:.2f} us; "
+        f"host-staged x/y {ms_host * 1e3:.2f} us")
 
     # per-shape dot kernel times (same graphs, one shape at a time)
     kernels = {}
@@ -377,9 +391,15 @@ def main():
                                     "prologue), lbq_qmatmul_f32 (o), lbq_rmsnorm_gate_up_silu_f32 (post-attention "
                                     "norm + gate|up, silu(gate)*up in the epilogue), lbq_qmatmul_f32 (down on that "
                                     "product): the reference's layer data flow, its two RMS norms included"},
+        "host_staged": {"us_per_step": round(ms_host * 1e3, 3),
+                        "GB/s": round(layer_bytes / (ms_host * 1e-3) / 1e9, 1),
+                        "pcie_bytes_per_step": io_bytes,
+                        "path": "per projection: x copied from pinned host memory, lbq_qmatmul_f32, y copied "
+                                "back to pinned host memory, on one stream (a caller whose tensors live on "
+                                "the host); PCIe-inclusive, not the headline"},
         "kernels": kernels,
     }
-    del g_full, g_dot, g_grp, g_fus
+    del g_full, g_dot, g_grp, g_fus, g_host
     tr = load_traffic()
     if tr and "bytes_per_launch" in tr:
         result["roofline"]["traffic"] = tr["bytes_per_launch"]
