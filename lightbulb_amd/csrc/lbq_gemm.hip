@@ -263,6 +263,57 @@ __global__ __launch_bounds__(256) void k_split_sum(const float *__restrict__ par
     }
 }
 
+// The k-sliced layout's operand rows with Q8_K activations: one wave per (row m,
+// exponent group g of KS_BLOCKS blocks), 16 lanes per block.  Each block is
+// quantised as k_quant_f16 does (q8k_lane16) or read from Q8_K codes; the group's
+// largest |d| gives e (as k_act_f16's row exponent, over the group's blocks only),
+// stored at erow[g * M + m]; the codes are converted with k_act_f16's arithmetic.
+// So every row costs one memory round trip instead of a 1024-thread pass per row.
+// SRC_X: quantise f32 x (k <= 16384, 16-byte aligned); otherwise codes from act.
+template <bool SRC_X>
+__global__ __launch_bounds__(64) void k_ops_ks(const float *__restrict__ x, ActView act, int64_t K, int64_t M,
+                                               _Float16 *__restrict__ A, int *__restrict__ erow, int opmajor) {
+    const int nb = (int)(K / KB), ng = (nb + KS_BLOCKS - 1) / KS_BLOCKS;
+    const int64_t m = blockIdx.x / ng;
+    const int g = (int)(blockIdx.x % ng);
+    const int lane = threadIdx.x, sub = lane & 15;
+    const int b = KS_BLOCKS * g + (lane >> 4);
+    const bool live = b < nb;  // a short last group: lanes of missing blocks only help reduce
+    const int bc = live ? b : nb - 1;
+    uint32_t packed[4];
+    float d;
+    if constexpr (SRC_X) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + m * K + (int64_t)bc * KB + 16 * sub);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = src[i];
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+        int sum;
+        q8k_lane16(v, sub, packed, &sum, &d);
+    } else {
+        const uint4 w = *reinterpret_cast<const uint4 *>(act.xq + m * act.k + (int64_t)bc * KB + 16 * sub);
+        packed[0] = w.x; packed[1] = w.y; packed[2] = w.z; packed[3] = w.w;
+        d = act.xd[m * act.nb + bc];
+    }
+    float mx = live ? fabsf(d) : 0.f;
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;  // as k_act_f16, over the group
+    if (lane == 0) erow[(int64_t)g * M + m] = e;
+    if (!live) return;
+    const float sx = __builtin_amdgcn_ldexpf(d, -e);
+    const float cc = -1152.f * sx;
+    uint32_t w8[8];
+    codes_to_f16(packed[0], sx, cc, &w8[0], &w8[1]);
+    codes_to_f16(packed[1], sx, cc, &w8[2], &w8[3]);
+    codes_to_f16(packed[2], sx, cc, &w8[4], &w8[5]);
+    codes_to_f16(packed[3], sx, cc, &w8[6], &w8[7]);
+    *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, 2 * sub, K)) = make_uint4(w8[0], w8[1], w8[2], w8[3]);
+    *reinterpret_cast<uint4 *>(A + op_pos(opmajor, m, b, 2 * sub + 1, K)) = make_uint4(w8[4], w8[5], w8[6], w8[7]);
+}
+
 // ---------------------------------------------------------------------------
 // Per-row operand exponents, once per weight: e_n such that the largest value
 // any block of row n can produce, B_n, satisfies B_n * 2^-e_n < 2^15.  The
@@ -359,9 +410,10 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
         // row tiles: 2 (the activation slice is 32 KB per block)
         const int nb = (int)(k / KB);
         const int smax = p.rt == 1 ? KS_BLOCKS : 2;
+        // (1, 2 or 4 blocks: a slice stays inside one exponent group of KS_BLOCKS)
         int bps = smax;
-        while (bps > 2 && (int64_t)p.tiles_n * ((nb + bps - 1) / bps) < (int64_t)num_cus()) bps--;
-        if (tu.gemm_ks) bps = std::max(1, std::min(tu.gemm_ks, smax));  // tuning
+        if (bps == 4 && (int64_t)p.tiles_n * ((nb + 3) / 4) < (int64_t)num_cus()) bps = 2;
+        if (tu.gemm_ks) bps = std::max(1, std::min(tu.gemm_ks == 3 ? 2 : tu.gemm_ks, smax));  // tuning
         p.bps = bps;
         p.splits = (nb + bps - 1) / bps;
         return p;
@@ -408,7 +460,10 @@ WsLayout ws_layout(int type, const Plan &p, int64_t n, int64_t k, int64_t m) {
     WsLayout L;
     L.a_off = 0;
     L.e_off = L.a_off + up(rows * (size_t)k * sizeof(_Float16));  // whole row tiles
-    L.o_off = L.e_off + up((size_t)m * sizeof(int));
+    // exponents: per row, or per (exponent group, row) for the k-sliced layout with Q8_K rows
+    const bool grouped_e = operand_major(p) && vec_dot_type(type) == TYPE_Q8_K;
+    const size_t ne = grouped_e ? (size_t)m * (size_t)((k / KB + KS_BLOCKS - 1) / KS_BLOCKS) : (size_t)m;
+    L.o_off = L.e_off + up(ne * sizeof(int));
     L.part_off = L.o_off + (gemm_offset_step(type) ? up(rows * (size_t)(k / KB) * 16 * sizeof(_Float16)) : 0);
     L.total = L.part_off + (p.splits > 1 ? up((size_t)p.splits * (size_t)(m * n) * sizeof(float)) : 0);
     return L;
@@ -437,6 +492,16 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     // row; otherwise 256-thread workgroups (measured at m = 512 and 2048)
     const bool wide_wg = m <= 64 || (k > 8192 && m <= 1024);
     const int om = operand_major(p);
+    if (om && vec_dot_type(type) == TYPE_Q8_K) {  // k-sliced layout: exponents per (group, row)
+        const unsigned grid = (unsigned)(m * ((k / KB + KS_BLOCKS - 1) / KS_BLOCKS));
+        if (x) {
+            if (!gemm_prepass_fuses_quant(type, k, x)) return hipErrorInvalidValue;
+            k_ops_ks<true><<<grid, 64, 0, st>>>(x, act, k, m, a, erow, om);
+        } else {
+            k_ops_ks<false><<<grid, 64, 0, st>>>(nullptr, act, k, m, a, erow, om);
+        }
+        return hipGetLastError();
+    }
     if (x) {
         if (!gemm_prepass_fuses_quant(type, k, x)) return hipErrorInvalidValue;
         if (vec_dot_type(type) != TYPE_Q8_K) {  // Q8_0 codes (the Q8_1 codes are the same)

@@ -1129,6 +1129,13 @@ constexpr int KSN = 128;  // columns per k-sliced workgroup
 
 constexpr int KS_BLOCKS = 4;  // longest slice: 4 x 16 KB of LDS, two workgroups per CU
 
+// With Q8_K activations the k-sliced layout's operand rows carry one exponent per
+// group of KS_BLOCKS blocks (erow[group][m]) rather than per row, so its pre-pass
+// runs one wave per (row, group); a slice (1, 2 or 4 blocks, aligned) never spans
+// two groups.
+template <int TYPE>
+constexpr bool ks_group_exponents() { return vec_dot_type(TYPE) == TYPE_Q8_K; }
+
 template <int TYPE, int S, int T>
 __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N, int64_t row_bytes,
                                                     const _Float16 *__restrict__ A, const int *__restrict__ erow,
@@ -1228,7 +1235,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
-            if (r < M && n < N) y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], erow[r] + en);
+            if (r < M && n < N) {
+                const int e = ks_group_exponents<TYPE>() ? erow[(int64_t)(b0 / KS_BLOCKS) * M + r] : erow[r];
+                y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], e + en);
+            }
         }
 }
 
