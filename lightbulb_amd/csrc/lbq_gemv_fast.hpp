@@ -624,6 +624,21 @@ enum : int { MAP_ONE = 0, MAP_SEGMENTS = 1, MAP_SILU_PAIRS = 2 };
 // candle's silu for f32: v / (1 + exp(-v))
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
+// Pairwise lane-half sums for reducing several accumulators at once.
+// swap32_sum(a, b): lanes 0..31 get a[l] + a[l + 32], lanes 32..63 get b[l - 32] + b[l]
+// (v_permlane32_swap exchanges a's upper half with b's lower half).
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// swap16_sum(a, b): 16-lane rows 0, 1, 2, 3 get a.row0 + a.row1, b.row0 + b.row1,
+// a.row2 + a.row3, b.row2 + b.row3 (v_permlane16_swap exchanges a's odd rows with
+// b's even rows)
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4, int RING = 0>
 __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                     ActView act, const float *__restrict__ alpha, float eps) {
@@ -761,7 +776,37 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
             // several rows: one piece's unpacked codes live at a time
             if constexpr (MR > 1) __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (MR > 1) {
+        if constexpr (MR > 1 && LPR == 64 && (MR == 2 || MR == 4 || MR == 8)) {
+            // one weight row per wave, 2 / 4 / 8 activation rows: the MR 64-lane sums
+            // by halving exchanges (lane halves, then 16-lane rows), so each 16-lane
+            // row ends with two (MR = 8) or one of the sums to finish with the row
+            // butterfly -- 20 VALU for eight rows instead of 88
+            const int rowi = lane >> 4;
+            float s0, s1 = 0.f;
+            int m0, m1 = -1;
+            if constexpr (MR == 8) {
+                const float a0 = swap32_sum(accm[0], accm[4]), a1 = swap32_sum(accm[1], accm[5]);
+                const float a2 = swap32_sum(accm[2], accm[6]), a3 = swap32_sum(accm[3], accm[7]);
+                s0 = row_sum_f32(swap16_sum(a0, a2));  // rows: activation rows 0, 2, 4, 6
+                s1 = row_sum_f32(swap16_sum(a1, a3));  // 1, 3, 5, 7
+                m0 = 2 * rowi;
+                m1 = 2 * rowi + 1;
+            } else if constexpr (MR == 4) {
+                const float a0 = swap32_sum(accm[0], accm[2]), a1 = swap32_sum(accm[1], accm[3]);
+                s0 = row_sum_f32(swap16_sum(a0, a1));  // rows: activation rows 0, 1, 2, 3
+                m0 = rowi;
+            } else {
+                const float a0 = swap32_sum(accm[0], accm[1]);
+                s0 = row_sum_f32(swap16_sum(a0, a0));  // rows: 0, 0, 1, 1
+                m0 = (rowi & 1) ? -1 : rowi >> 1;
+            }
+            const int64_t rq = g;  // RPW = 1
+            if (store && (lane & 15) == 0 && rq < n) {
+                if (m0 >= 0) y[(int64_t)m0 * n + rq] = s0;
+                if (m1 >= 0) y[(int64_t)m1 * n + rq] = s1;
+            }
+            return;
+        } else if constexpr (MR > 1) {
             // several activation rows (one weight, MAP_ONE): row q of the group,
             // activation row m goes to y[m][row]
 #pragma unroll
