@@ -129,6 +129,7 @@ struct ActView {
     int64_t k;  // row length in values
     int nb;     // scale blocks per row (k/256 or k/32)
     const float *xs = nullptr;  // Q8_1: per-block s = d * sum(codes), widened from f16
+    int rows = 0;               // multi-row GEMV: real rows of the MR it runs (0: all MR)
 };
 
 struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };

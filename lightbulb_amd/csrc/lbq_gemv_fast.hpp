@@ -544,17 +544,20 @@ __device__ __forceinline__ void copy_x_row_lds(const ActView &a, int nbx, uint8_
 }
 
 // MR pre-quantised activation rows -> MR consecutive LDS row images of nbx
-// blocks each; `between` runs once, inside the first row's copy.
+// blocks each; `between` runs once, inside the first row's copy.  With
+// a.rows < MR the rows past a.rows repeat the last real one (they are computed
+// and never stored).
 template <int TYPE, int MR, class Between>
 __device__ __forceinline__ void copy_x_lds(const ActView &a, int nbx, uint8_t *sx, Between between) {
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
     copy_x_row_lds<TYPE>(a, nbx, sx, between);
 #pragma unroll 1
     for (int m = 1; m < MR; m++) {
+        const int src = a.rows > 0 ? min(m, a.rows - 1) : m;
         ActView r = a;
-        r.xq = a.xq + (int64_t)m * a.k;
-        r.xd = a.xd + (int64_t)m * a.nb;
-        if constexpr (TYPE != TYPE_Q8_0) r.xbs = a.xbs + (int64_t)m * (a.k / 16);
+        r.xq = a.xq + (int64_t)src * a.k;
+        r.xd = a.xd + (int64_t)src * a.nb;
+        if constexpr (TYPE != TYPE_Q8_0) r.xbs = a.xbs + (int64_t)src * (a.k / 16);
         copy_x_row_lds<TYPE>(r, nbx, sx + (int64_t)m * nbx * XS, [] {});
     }
     __syncthreads();
@@ -727,7 +730,12 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     // wave's whole stream up front, leave every wave waiting for its first rows
     // while the whole matrix is in flight, and bunch the compute at the end.
     // Deep rows (IT > 4) keep two buffers (registers).
-    constexpr int NBUF = RING > 0 ? RING : (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
+    constexpr int NBUF3 = RING > 0 ? RING : (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
+    // several activation rows: a two-deep ring where that keeps their activation
+    // images in registers (below) and the three-deep one would not
+    constexpr bool XFIT3 = MR * IT * F::XW <= 160 && NBUF3 * IT * F::RAW + MR * IT * F::XW <= 190;
+    constexpr bool XFIT2 = MR * IT * F::XW <= 160 && 2 * IT * F::RAW + MR * IT * F::XW <= 190;
+    constexpr int NBUF = (RING == 0 && MR > 1 && !XFIT3 && XFIT2) ? 2 : NBUF3;
     Raw ring[NBUF][IT];
     auto issue_ring = [&] {
 #pragma unroll
@@ -753,6 +761,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     }
 
     float pend = 0.f;  // silu pairs: the gate sum waiting for its up sum (wave-uniform)
+    const int nrows = act.rows > 0 ? act.rows : MR;  // several rows: the ones stored
     auto compute_group = [&](int64_t g, const Raw *buf, bool store) {
         float accm[MR];
 #pragma unroll
@@ -802,8 +811,8 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
             }
             const int64_t rq = g;  // RPW = 1
             if (store && (lane & 15) == 0 && rq < n) {
-                if (m0 >= 0) y[(int64_t)m0 * n + rq] = s0;
-                if (m1 >= 0) y[(int64_t)m1 * n + rq] = s1;
+                if (m0 >= 0 && m0 < nrows) y[(int64_t)m0 * n + rq] = s0;
+                if (m1 >= 0 && m1 < nrows) y[(int64_t)m1 * n + rq] = s1;
             }
             return;
         } else if constexpr (MR > 1) {
@@ -825,7 +834,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
                         s = __int_as_float(rl(__float_as_uint(a), 16 * q));
                     }
                     const int64_t rq = g * RPW + q;
-                    if (store && lane == LPR * q && rq < n) y[(int64_t)m * n + rq] = s;
+                    if (store && lane == LPR * q && rq < n && m < nrows) y[(int64_t)m * n + rq] = s;
                 }
             }
             return;

@@ -806,14 +806,19 @@ static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const
     const size_t row_lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
     const int mr_max = fast_rows_max<TYPE>(nb);
     for (int m0 = 0; m0 < m;) {
+        // the smallest allowed chunk that takes every remaining row (padded with
+        // rows that repeat the last one and are not stored), else the largest
         int mr = 8;
-        while (mr > 1 && (mr > m - m0 || mr > mr_max || (size_t)mr * row_lds > 80 * 1024)) mr >>= 1;
+        while (mr > 1 && (mr > mr_max || (size_t)mr * row_lds > 80 * 1024)) mr >>= 1;
+        while (mr > 1 && mr / 2 >= m - m0) mr >>= 1;
+        const int real = std::min(mr, m - m0);
         RowMap rm = rm0;
         rm.y[0] = rm0.y[0] + (int64_t)m0 * rm0.n;
         ActView a = act;
         a.xq = act.xq + (int64_t)m0 * act.k;
         a.xd = act.xd + (int64_t)m0 * act.nb;
         if (act.xbs) a.xbs = act.xbs + (int64_t)m0 * (act.k / 16);
+        a.rows = real < mr ? real : 0;
         hipError_t e;
         switch (mr) {
         case 8: e = run_fast_rows<TYPE, 8>(rm, row_bytes, nb, a, st); break;
@@ -822,7 +827,7 @@ static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const
         default: e = run_fast_rows<TYPE, 1>(rm, row_bytes, nb, a, st); break;
         }
         if (e != hipSuccess) return e;
-        m0 += mr;
+        m0 += real;
     }
     return hipSuccess;
 }

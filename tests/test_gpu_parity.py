@@ -180,8 +180,9 @@ SMALL = [(48, 256), (100, 512), (257, 768), (1024, 1024)]
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 17])
 def test_qmatmul_small(oracle, lbq, dev, t, m):
+    # m = 3, 5, 6, 7 run the 4- and 8-row decode kernels with unstored padding rows
     rng = np.random.default_rng(1000 * t + m)
     for n, k in SMALL:
         bs = oracle.block_size(t)
