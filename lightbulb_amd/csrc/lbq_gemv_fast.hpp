@@ -79,6 +79,8 @@ constexpr int XS_0 = 48;
 template <int TYPE, int PPB>
 struct Fast;
 
+typedef short short2v __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_halves(uint32_t lo_word, uint32_t hi_word, int h) {
     const uint32_t a = (lo_word >> (16 * h)) & 0xffffu, b = (hi_word >> (16 * h)) & 0xffffu;
     return a | (b << 16);
@@ -110,7 +112,8 @@ struct FastK45 {  // Q4_K and Q5_K
         return r;
     }
     // activation registers for piece p: codes 64p .. 64p + 63 (xr[0..15]), the
-    // bsums of its four 16-value runs (xr[16], xr[17]) and the block's d (xr[18])
+    // code sums of its two 32-value sub-blocks as an int16 pair (xr[16], from the
+    // bsums of its four 16-value runs; |sum| <= 4096) and the block's d (xr[18])
     __device__ static void xload_lds(const uint8_t *xb, int p, uint32_t *xr) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -118,8 +121,10 @@ struct FastK45 {  // Q4_K and Q5_K
             xr[4 * j] = a.x; xr[4 * j + 1] = a.y; xr[4 * j + 2] = a.z; xr[4 * j + 3] = a.w;
         }
         const uint2 s = *reinterpret_cast<const uint2 *>(xb + 256 + 8 * p);
-        xr[16] = s.x;
-        xr[17] = s.y;
+        // (run 0, run 2) + (run 1, run 3), lane-wise 16-bit adds
+        const uint32_t r02 = __builtin_amdgcn_perm(s.y, s.x, 0x05040100u), r13 = __builtin_amdgcn_perm(s.y, s.x, 0x07060302u);
+        xr[16] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2v, r02) + __builtin_bit_cast(short2v, r13));
+        xr[17] = 0u;
         xr[18] = *reinterpret_cast<const uint32_t *>(xb + 288);
     }
     // Piece p of one weight block against MR activation rows: the weight codes are
@@ -154,8 +159,10 @@ struct FastK45 {  // Q4_K and Q5_K
                 hi[i] |= ((qh >> (2 * p + 1)) & 0x01010101u) << 4;
             }
         }
-        const float dw = h2f(h0 & 0xffffu), dmw = h2f(h0 >> 16);
-        const int scl = (int)(sc2 & 0xffu), sch = (int)(sc2 >> 8), ml = (int)(m2 & 0xffu), mh = (int)(m2 >> 8);
+        // a clamped (duplicate) block contributes through zero scales
+        const float dw = valid ? h2f(h0 & 0xffffu) : 0.f, dmw = valid ? h2f(h0 >> 16) : 0.f;
+        const int scl = (int)(sc2 & 0xffu), sch = (int)(sc2 >> 8);
+        const short2v mins = __builtin_bit_cast(short2v, (m2 & 0xffu) | ((m2 >> 8) << 16));  // (m_lo, m_hi)
 #pragma unroll
         for (int m = 0; m < MR; m++) {
             uint32_t xr[XW];
@@ -166,14 +173,11 @@ struct FastK45 {  // Q4_K and Q5_K
                 sl = dot4(lo[i], xr[i], sl);
                 sh = dot4(hi[i], xr[8 + i], sh);
             }
-            // bsums of the two sub-blocks: runs (4p, 4p + 1) and (4p + 2, 4p + 3)
-            const int bl = (int)(int16_t)(xr[16] & 0xffffu) + ((int)xr[16] >> 16);
-            const int bh = (int)(int16_t)(xr[17] & 0xffffu) + ((int)xr[17] >> 16);
             const int isum = __mul24(scl, sl) + __mul24(sch, sh);
-            const int msum = __mul24(ml, bl) + __mul24(mh, bh);
+            const int msum = __builtin_amdgcn_sdot2(mins, __builtin_bit_cast(short2v, xr[16]), 0, false);
             const float dx = __uint_as_float(xr[18]);
-            const float v = (dw * dx) * (float)isum - (dmw * dx) * (float)msum;
-            acc[m] += valid ? v : 0.f;
+            acc[m] = fmaf(dw * dx, (float)isum, acc[m]);
+            acc[m] = fmaf(-(dmw * dx), (float)msum, acc[m]);
         }
     }
 };
