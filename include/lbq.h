@@ -21,7 +21,7 @@
  *     [n][k / block_size] blocks, rows contiguous along k
  *     (GGUF ne0 = k; /root/reference/src/gguf/parser.rs:180-199).
  *   - A context owns per-device scratch (quantised activations, the batched
- *     GEMM's workspace), grown on demand.  Calls that share a context must be
+ *     GEMM's workspace, grown on demand, and 64 KiB of its tile counters).  Calls that share a context must be
  *     ordered on one stream (the reference runs every forward on one model
  *     thread, src/engine/model_runner.rs:236,383).  Weight handles are
  *     immutable and may be read concurrently.
@@ -129,8 +129,9 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
  * No counterpart in the reference; for callers that cannot allocate device
  * memory -- code under HIP graph capture, tight serving loops, harnesses that
  * forbid it.  The quantised activations and the batched GEMM's workspace live
- * in a fixed array of LBQ_NOALLOC_SCRATCH_BYTES per device, resolved by
- * lbq_init and held until the process ends.  A call that needs more (roughly
+ * in a fixed array of LBQ_NOALLOC_SCRATCH_BYTES per device (its last 64 KiB
+ * are the GEMM's tile counters, zeroed by lbq_init and left zero by every
+ * call), resolved by lbq_init and held until the process ends.  A call that needs more (roughly
  * m * k * 2 bytes of fp16 operands plus split-k partials above m = 8; every
  * Llama-3-8B projection fits up to m = 512, down_proj up to m = 2048) returns
  * LBQ_ERR_LIMIT before launching anything.  All contexts on a device share the

@@ -26,6 +26,9 @@ static_assert(LBQ_GROUP_MAX == lbq::GROUP_MAX, "one group limit for the ABI and 
 // an address: lbq_init resolves it once per device with hipGetSymbolAddress.
 // Calls that overlap on one device share it and race.
 static __device__ __align__(256) uint8_t scratch[LBQ_NOALLOC_SCRATCH_BYTES];
+// its last bytes hold the k-sliced GEMM's tile counters, the rest the buffers
+constexpr size_t NOALLOC_COUNTER_BYTES = sizeof(uint32_t) * lbq::KS_COUNTERS;
+constexpr size_t NOALLOC_FIXED_BYTES = LBQ_NOALLOC_SCRATCH_BYTES - NOALLOC_COUNTER_BYTES;
 
 struct lbq_ctx {
     int device;
@@ -38,6 +41,7 @@ struct lbq_ctx {
     size_t ws_bytes;
     uint8_t *tmp;         // gate and up outputs when their product is not fused
     size_t tmp_bytes;
+    uint32_t *tile_counters;  // KS_COUNTERS zeroed words of the k-sliced GEMM (each launch leaves them zero)
 };
 
 struct lbq_weight {
@@ -77,6 +81,7 @@ Tuning tuning_from_env() {
     t.gemm_ks = std::max(0, env_int("LBQ_GEMM_KS"));
     if (const char *e = getenv("LBQ_GEMM_BIG")) t.gemm_big = e[0] == 't' ? 2 : 1;
     t.gemm_splits = std::max(0, env_int("LBQ_GEMM_SPLITS"));
+    t.gemm_split_launch = getenv("LBQ_GEMM_SPLIT_LAUNCH") != nullptr;
     t.gemv1_nofuse = getenv("LBQ_GEMV1_NOFUSE") != nullptr;
     t.gemv_rows_off = getenv("LBQ_GEMV_ROWS_OFF") != nullptr;
     if (const char *e = getenv("LBQ_GEMV1_CFG")) {
@@ -218,7 +223,10 @@ struct Scratch {
     lbq_ctx *ctx = nullptr;
     uint8_t *fixed = nullptr;
     size_t fixed_bytes = 0;
+    uint32_t *fixed_counters = nullptr;  // fixed region: its tile counters
     size_t act_used = 0;  // fixed region: bytes taken by the activations
+
+    uint32_t *counters() const { return fixed ? fixed_counters : ctx->tile_counters; }
 
     int limit(size_t need) const {
         return fail(LBQ_ERR_LIMIT,
@@ -260,7 +268,8 @@ int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m,
             int s = sc.ws(wsb, &ws);
             if (s) return s;
         }
-        e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ws, st);
+        e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, av, nullptr, m, d_y, ws,
+                             sc.counters(), st);
     }
     if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
     return LBQ_OK;
@@ -295,7 +304,7 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
         if (s) return s;
         const lbq::ActView none{nullptr, nullptr, nullptr, w->k, L.nb};
         hipError_t e = lbq::launch_gemm(w->type, w->d_blocks, w->d_rexp, w->n, w->k, w->row_bytes, none, d_x, m, d_y, ws,
-                                        st);
+                                        sc.counters(), st);
         if (e != hipSuccess) return hip_fail(e, "quantized matmul launch");
         return LBQ_OK;
     }
@@ -384,8 +393,13 @@ int noalloc_scratch_of(int device, uint8_t **out) {
     std::lock_guard<std::mutex> lock(g_noalloc_mu);
     if (!g_noalloc_ptr[device]) {
         void *p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        // the tile counters at the array's end start at zero; each launch that
+        // uses them leaves them zero again
+        e = hipMemset(static_cast<uint8_t *>(p) + NOALLOC_FIXED_BYTES, 0, NOALLOC_COUNTER_BYTES);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "clearing the allocation-free tile counters");
         g_noalloc_ptr[device] = static_cast<uint8_t *>(p);
     }
     *out = g_noalloc_ptr[device];
@@ -454,6 +468,15 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
     c->ws_bytes = 0;
     c->tmp = nullptr;
     c->tmp_bytes = 0;
+    c->tile_counters = nullptr;
+    e = hipMalloc(&c->tile_counters, NOALLOC_COUNTER_BYTES);
+    if (e == hipSuccess) e = hipMemset(c->tile_counters, 0, NOALLOC_COUNTER_BYTES);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (c->tile_counters) (void)hipFree(c->tile_counters);
+        delete c;
+        return hip_fail(e, "tile counter allocation");
+    }
     *out_ctx = c;
     return LBQ_OK;
 }
@@ -461,12 +484,11 @@ int lbq_init(int device, lbq_ctx **out_ctx) {
 int lbq_ctx_destroy(lbq_ctx *ctx) {
     if (!ctx) return LBQ_OK;
     DeviceGuard g(ctx->device);
-    if (ctx->scratch || ctx->ws || ctx->tmp) {
-        (void)hipDeviceSynchronize();
-        if (ctx->scratch) (void)hipFree(ctx->scratch);
-        if (ctx->ws) (void)hipFree(ctx->ws);
-        if (ctx->tmp) (void)hipFree(ctx->tmp);
-    }
+    (void)hipDeviceSynchronize();
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->tmp) (void)hipFree(ctx->tmp);
+    if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
     delete ctx;
     return LBQ_OK;
 }
@@ -553,12 +575,15 @@ int lbq_qmatmul_f32_noalloc(lbq_ctx *ctx, const lbq_weight *w, const float *d_x,
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
     // every buffer the kernels need comes from this device's `scratch` (through
-    // the address lbq_init resolved); nothing is allocated, nothing needs clearing
-    // (each kernel writes every scratch byte it later reads)
+    // the address lbq_init resolved); nothing is allocated and nothing needs
+    // clearing: each kernel writes every scratch byte it later reads, and the
+    // tile counters at the array's end were zeroed at lbq_init and are left zero
+    // by every launch
     Scratch sc;
     sc.ctx = ctx;
     sc.fixed = ctx->noalloc_scratch;
-    sc.fixed_bytes = LBQ_NOALLOC_SCRATCH_BYTES;
+    sc.fixed_bytes = NOALLOC_FIXED_BYTES;
+    sc.fixed_counters = reinterpret_cast<uint32_t *>(ctx->noalloc_scratch + NOALLOC_FIXED_BYTES);
     return forward(ctx, w, d_x, m, d_y, static_cast<hipStream_t>(stream), sc, nullptr);
 }
 
@@ -630,7 +655,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
         for (int i = 0; i < count; i++) {
             e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->d_rexp, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i],
-                               ctx->ws, st);
+                               ctx->ws, ctx->tile_counters, st);
             if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
         }
         return LBQ_OK;

@@ -11,7 +11,7 @@ namespace lbq {
 #define LBQ_GEMM_EXTERN(T)                                                                                          \
     extern template hipError_t launch_typed<T>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,      \
                                                const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,    \
-                                               float *, int64_t, hipStream_t);
+                                               float *, int64_t, uint32_t *, float *, hipStream_t);
 LBQ_GEMM_EXTERN(TYPE_Q4_K)
 LBQ_GEMM_EXTERN(TYPE_Q5_K)
 LBQ_GEMM_EXTERN(TYPE_Q6_K)
@@ -523,7 +523,7 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
 }
 
 hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
-                     float *y, void *ws, hipStream_t st) {
+                     float *y, void *ws, uint32_t *counters, hipStream_t st) {
     if (!ws || !rexp || !gemm_serves(type, k)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, n, k, m);
     const WsLayout L = ws_layout(type, p, n, k, m);
@@ -534,32 +534,42 @@ hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, 
     float *part = reinterpret_cast<float *>(base + L.part_off);
     float *out = p.splits > 1 ? part : y;
     const int64_t stride = p.splits > 1 ? m * n : 0;
+    // the k-sliced kernel adds its own slices when given zeroed tile counters
+    // (with few column tiles the one workgroup per tile that adds the slices is
+    // slower than the separate launch, which spreads the sum over the chip)
+    uint32_t *cnt = (p.mt == MT_KS && p.splits > 1 && p.splits <= KS_FUSED_SLICES && n % 4 == 0 && counters &&
+                     !tuning().gemm_split_launch &&
+                     p.tiles_n >= KS_FUSED_MIN_TILES && p.tiles_n <= KS_COUNTERS &&
+                     (int64_t)p.splits * m * n * 4 < ((int64_t)1 << 31))
+                        ? counters
+                        : nullptr;
     hipError_t e;
     switch (type) {
-    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q6_K: e = launch_typed<TYPE_Q6_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q8_0: e = launch_typed<TYPE_Q8_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q4_0: e = launch_typed<TYPE_Q4_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q4_1: e = launch_typed<TYPE_Q4_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q5_0: e = launch_typed<TYPE_Q5_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q5_1: e = launch_typed<TYPE_Q5_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q2_K: e = launch_typed<TYPE_Q2_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
-    case TYPE_Q3_K: e = launch_typed<TYPE_Q3_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, st); break;
+    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q6_K: e = launch_typed<TYPE_Q6_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q8_0: e = launch_typed<TYPE_Q8_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q4_0: e = launch_typed<TYPE_Q4_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q4_1: e = launch_typed<TYPE_Q4_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q5_0: e = launch_typed<TYPE_Q5_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q5_1: e = launch_typed<TYPE_Q5_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q2_K: e = launch_typed<TYPE_Q2_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q3_K: e = launch_typed<TYPE_Q3_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
     default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess || p.splits == 1) return e;
+    if (e != hipSuccess || p.splits == 1 || cnt) return e;
     const int64_t count = m * n;
     k_split_sum<<<(unsigned)((count + 1023) / 1024), 256, 0, st>>>(part, p.splits, count, y);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes,
-                       const ActView &act, const float *x, int64_t m, float *y, void *ws, hipStream_t st) {
+                       const ActView &act, const float *x, int64_t m, float *y, void *ws, uint32_t *counters,
+                       hipStream_t st) {
     if (gemm_serves(type, k)) {
         hipError_t e = gemm_prepass(type, k, act, x, m, ws, st);
         if (e != hipSuccess) return e;
-        return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, st);
+        return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, counters, st);
     }
     if (x) return hipErrorInvalidValue;  // the GEMV over row chunks takes quantised activations
     // k % 256 != 0: the decode GEMV over row chunks of 8

@@ -504,6 +504,8 @@ struct GemmGrid {
     int splits;
     const int8_t *rexp;         // per weight row: e_n (w operands carry 2^-e_n)
     const _Float16 *ofs;        // OFS types: per operand row and super-block, 16 f16 A values of the extra k-step
+    uint32_t *cnt;              // k-sliced split: per column tile, slices done (null: k_split_sum adds them)
+    float *y;                   // ... and the output the last slice of a tile writes
 };
 
 // whether a weight type adds an extra k-step per super-block (odw)
@@ -1128,6 +1130,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
 constexpr int KSN = 128;  // columns per k-sliced workgroup
 
 constexpr int KS_BLOCKS = 4;  // longest slice: 4 x 16 KB of LDS, two workgroups per CU
+constexpr int KS_FUSED_SLICES = 8;  // most slices the k-sliced kernel adds itself
+constexpr int KS_FUSED_MIN_TILES = 64;  // ... and fewest column tiles
+constexpr int KS_SC1 = 16;          // buffer-load cache policy: sc1 (agent-scope coherent)
+constexpr int KS_SUM_Q = 4;         // slices each thread loads per round of the in-kernel sum
 
 // With Q8_K activations the k-sliced layout's operand rows carry one exponent per
 // group of KS_BLOCKS blocks (erow[group][m]) rather than per row, so its pre-pass
@@ -1229,17 +1235,91 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
 
     float *y = out + (int64_t)z * split_stride;
     const int64_t n = n0 + lr;
-    // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
+    // D layout of a 32x32 MFMA tile: lane holds column l%32, rows 8(v/4) + 4h + v%4.
+    // Every row's exponent is loaded before the first store (rows past m read row
+    // m - 1 and are never stored), so the loads overlap instead of each waiting
+    // behind the stores before it.
+    const int *ex_row = erow + (ks_group_exponents<TYPE>() ? (int64_t)(b0 / KS_BLOCKS) * M : 0);
+    int ex[T][16];
 #pragma unroll
     for (int u = 0; u < T; u++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
+            ex[u][v] = ex_row[r < M ? r : M - 1];
+        }
+#pragma unroll
+    for (int u = 0; u < T; u++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
+            acc[u][v] = __builtin_amdgcn_ldexpf(acc[u][v], ex[u][v] + en);
             if (r < M && n < N) {
-                const int e = ks_group_exponents<TYPE>() ? erow[(int64_t)(b0 / KS_BLOCKS) * M + r] : erow[r];
-                y[(int64_t)r * N + n] = __builtin_amdgcn_ldexpf(acc[u][v], e + en);
+                if (g.cnt) __hip_atomic_store(y + (int64_t)r * N + n, acc[u][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else y[(int64_t)r * N + n] = acc[u][v];
             }
         }
+    if (!g.cnt) return;
+    // Split sum in the kernel: the partial stores above are agent-scope (written
+    // through to memory, not held in this XCD's L2), so once they have completed
+    // (vmcnt(0)) a counter increment publishes them without an L2 write-back.  The
+    // workgroup that completes a column tile's count adds the tile's slices in
+    // slice order -- the order k_split_sum uses, so the bits are the same -- reading
+    // them with the same agent-scope (sc1) policy, writes y and resets the counter
+    // for the next call.  The host uses this only for N % 4 == 0 (16-byte partial
+    // rows) and at most KS_FUSED_SLICES slices.
+    __shared__ uint32_t last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0) last = __hip_atomic_fetch_add(g.cnt + tn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (last != (uint32_t)(slices - 1)) return;
+    // thread t: columns 4(t % 32) .. +3 of the tile, rows t / 32, t / 32 + 8, ...
+    const int64_t col = (int64_t)tn * KSN + 4 * (t & 31);
+    const int rows = (int)min<int64_t>(M, 32 * T);
+    if (col < N) {
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            out, (short)0, (int)(split_stride * slices * (int64_t)sizeof(float)), 0x00020000);
+        constexpr int RQ = 32 * T / 8;  // rows per thread, two at a time, KS_SUM_Q slices per round
+#pragma unroll
+        for (int r0 = 0; r0 < RQ; r0 += 2) {
+            float4 sum[2];
+            for (int q0 = 0; q0 < slices; q0 += KS_SUM_Q) {
+                float4 v[2][KS_SUM_Q];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int r = (t >> 5) + 8 * (r0 + j);
+#pragma unroll
+                    for (int q = 0; q < KS_SUM_Q; q++)
+                        if (r < rows && q0 + q < slices)
+                            v[j][q] = __builtin_bit_cast(
+                                float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, (int)(((int64_t)(q0 + q) * split_stride + (int64_t)r * N + col) * 4),
+                                            0, KS_SC1));
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int q = 0; q < KS_SUM_Q; q++) {
+                        if (q0 + q >= slices) continue;
+                        if (q0 + q == 0) {
+                            sum[j] = v[j][q];
+                        } else {
+                            sum[j].x += v[j][q].x; sum[j].y += v[j][q].y;
+                            sum[j].z += v[j][q].z; sum[j].w += v[j][q].w;
+                        }
+                    }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = (t >> 5) + 8 * (r0 + j);
+                if (r >= rows) continue;
+                float *yo = g.y + (int64_t)r * N + col;
+                yo[0] = sum[j].x; yo[1] = sum[j].y; yo[2] = sum[j].z; yo[3] = sum[j].w;
+            }
+        }
+    }
+    if (t == 0) __hip_atomic_store(g.cnt + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct Plan {
@@ -1255,8 +1335,8 @@ inline int operand_major(const Plan &p) { return p.mt == MT_KS ? p.rt : 0; }
 template <int TYPE>
 hipError_t launch_typed(const Plan &p, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t row_bytes,
                         const _Float16 *a, const int *erow, const _Float16 *ofs, int64_t k, int64_t m, float *out,
-                        int64_t split_stride, hipStream_t st) {
-    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits, rexp, ofs};
+                        int64_t split_stride, uint32_t *cnt, float *y, hipStream_t st) {
+    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits, rexp, ofs, cnt, y};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
     if (p.mt == MT_KS) {
         if (p.rt == 2) {  // two row tiles: slices of 1 or 2 blocks

@@ -55,6 +55,7 @@ struct Tuning {
     int gemm_ks = 0;      // k-sliced tiles: blocks per slice (0: planned)
     int gemm_big = 0;     // 1: wide tiles, 2: tall tiles (0: planned)
     int gemm_splits = 0;  // split-k count (0: planned)
+    bool gemm_split_launch = false;  // k-sliced slices added by the separate launch, never in the kernel
     bool gemv1_nofuse = false, gemv_rows_off = false;
     int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
     int gemv1_wpc = 0, gemv1_wpg = 0;
@@ -76,6 +77,8 @@ struct TuningScope {
 // entries past the last segment have end = INT32_MAX.  A plain single weight is
 // the one-segment map.  A row space has fewer than 2^31 - 1 rows.
 constexpr int GROUP_MAX = 4;
+// tile counters of the k-sliced GEMM's in-kernel slice sum (column tiles per launch)
+constexpr int KS_COUNTERS = 16384;
 constexpr int64_t MAX_ROWS = 0x7ffffffe;
 struct RowMap {
     const uint8_t *w[GROUP_MAX];
@@ -144,10 +147,14 @@ size_t gemm_workspace_bytes(int type, int64_t n, int64_t k, int64_t m);
 bool gemm_prepass_fuses_quant(int type, int64_t k, const float *x);
 hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x, int64_t m, void *ws, hipStream_t st);
 // rexp: the weight's per-row operand exponents (launch_row_exponents).
+// counters: KS_COUNTERS zeroed words the k-sliced kernel uses to add its own
+// slices (the last workgroup of a column tile sums them and puts the word back
+// to zero); nullptr keeps the separate slice-sum launch.
 hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
-                     float *y, void *ws, hipStream_t st);
+                     float *y, void *ws, uint32_t *counters, hipStream_t st);
 hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes,
-                       const ActView &act, const float *x, int64_t m, float *y, void *ws, hipStream_t st);
+                       const ActView &act, const float *x, int64_t m, float *y, void *ws, uint32_t *counters,
+                       hipStream_t st);
 // Per-row operand exponents of a weight the MFMA GEMM serves (gemm_serves):
 // rexp[i] = e such that every value row i's blocks can produce is below
 // 2^(15 + e), so the GEMM's fp16 weight operands, scaled by 2^-e, stay clear

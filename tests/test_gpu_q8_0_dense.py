@@ -256,6 +256,31 @@ def test_ksliced_long_slices_large_n(oracle, lbq, dev, t):
         assert_rows_close(y[rows], ref, tight_bound(t, 32))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q8_0])
+def test_ksliced_slice_sum_in_kernel(oracle, lbq, dev, t, monkeypatch):
+    # k-sliced shapes with at least 64 column tiles add their slices in the kernel
+    # (the last workgroup of a tile, found through a per-tile counter); the bits
+    # equal those of the separate slice-sum launch, call after call (the counters
+    # are left zero), with a ragged last tile, and through the grouped entry point
+    from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
+    rng = np.random.default_rng(620 + t)
+    for (m, n, k) in ((16, 8192, 4096), (32, 8196, 2048), (13, 8192, 256 * 6)):
+        w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y_sep = forward_with_env(monkeypatch, {"LBQ_GEMM_SPLIT_LAUNCH": "1"}, t, w_raw, n, k, x, dev)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+        xd = to_dev(x, dev)
+        for _ in range(3):
+            y = qm.forward(xd).cpu().numpy()
+            assert np.array_equal(y.view(np.uint32), y_sep.view(np.uint32)), (m, n, k)
+        ys = qmatmul_group([qm, qm], xd)
+        for yg in ys:
+            assert np.array_equal(yg.cpu().numpy().view(np.uint32), y_sep.view(np.uint32)), (m, n, k)
+        rows = [0, m // 2, m - 1]
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y[rows], ref, tight_bound(t, m))
+
+
 def test_tuning_read_once_per_context(oracle, lbq, dev, monkeypatch):
     # an override set after a context exists does not change that context's plan
     from lightbulb_amd.quantized import QMatMul, QTensor

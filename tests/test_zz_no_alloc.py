@@ -50,7 +50,8 @@ def _both(L, ctx, h, x, n, dev):
     (Q4_K, 1000, 4096, (8, 4)),        # pre-quantised multi-row GEMV
     (Q6_K, 700, 4096, (300, 40)),      # tall / k-sliced MFMA tiles
     (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then k-sliced
-    (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then k-sliced
+    (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then k-sliced (slices added in the kernel)
+    (Q4_K, 8192, 4096, (16, 13)),      # slices added in the kernel twice (tile counters left zero)
     (Q8_0, 512, 4096, (64, 12)),       # Q8_0 on MFMA
     (Q4_0, 300, 1184, (20, 9)),        # activation scratch + GEMV row chunks (k % 256 != 0)
     (Q4_1, 300, 1024, (20, 9)),        # MFMA with the offset k-step operands in the workspace
