@@ -82,6 +82,7 @@ Tuning tuning_from_env() {
     if (const char *e = getenv("LBQ_GEMM_BIG")) t.gemm_big = e[0] == 't' ? 2 : 1;
     t.gemm_splits = std::max(0, env_int("LBQ_GEMM_SPLITS"));
     t.gemm_split_launch = getenv("LBQ_GEMM_SPLIT_LAUNCH") != nullptr;
+    t.gemm_prepass = getenv("LBQ_GEMM_PREPASS") != nullptr;
     t.gemv1_nofuse = getenv("LBQ_GEMV1_NOFUSE") != nullptr;
     t.gemv_rows_off = getenv("LBQ_GEMV_ROWS_OFF") != nullptr;
     if (const char *e = getenv("LBQ_GEMV1_CFG")) {
@@ -641,8 +642,15 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         for (int i = 0; i < count; i++) wsb = std::max(wsb, lbq::gemm_workspace_bytes(w0->type, ws[i]->n, w0->k, m));
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
         if (s) return s;
-        hipError_t e;
-        if (lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x)) {
+        hipError_t e = hipSuccess;
+        bool in_kernel[LBQ_GROUP_MAX], all_in_kernel = true;
+        for (int i = 0; i < count; i++) {
+            in_kernel[i] = lbq::gemm_quantises_in_kernel(w0->type, ws[i]->n, w0->k, m, d_x);
+            all_in_kernel = all_in_kernel && in_kernel[i];
+        }
+        if (all_in_kernel) {
+            // every weight's k-sliced GEMM quantises x itself
+        } else if (lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x)) {
             const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, L.nb};
             e = lbq::gemm_prepass(w0->type, w0->k, none, d_x, m, ctx->ws, st);
         } else {
@@ -655,7 +663,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
         for (int i = 0; i < count; i++) {
             e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->d_rexp, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i],
-                               ctx->ws, ctx->tile_counters, st);
+                               ctx->ws, ctx->tile_counters, in_kernel[i] ? d_x : nullptr, st);
             if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
         }
         return LBQ_OK;

@@ -11,7 +11,7 @@ namespace lbq {
 #define LBQ_GEMM_EXTERN(T)                                                                                          \
     extern template hipError_t launch_typed<T>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,      \
                                                const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,    \
-                                               float *, int64_t, uint32_t *, float *, hipStream_t);
+                                               float *, int64_t, uint32_t *, float *, const float *, hipStream_t);
 LBQ_GEMM_EXTERN(TYPE_Q4_K)
 LBQ_GEMM_EXTERN(TYPE_Q5_K)
 LBQ_GEMM_EXTERN(TYPE_Q6_K)
@@ -522,9 +522,19 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
     return hipGetLastError();
 }
 
+bool gemm_quantises_in_kernel(int type, int64_t n, int64_t k, int64_t m, const float *x) {
+    if (!gemm_prepass_fuses_quant(type, k, x) || vec_dot_type(type) != TYPE_Q8_K || tuning().gemm_prepass) return false;
+    // every column tile's workgroups quantise their slice again: with many tiles
+    // that repeated VALU work costs more than the pre-pass launch (measured at
+    // m = 16: 1.8 us faster at 1024 and 4096 columns, 2.5 us slower at 14336)
+    const Plan p = plan_for(type, n, k, m);
+    return p.mt == MT_KS && p.tiles_n <= KS_FX_MAX_TILES && ks_fx_shape(p.bps, ks_fx_rows(m, p.rt));
+}
+
 hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
-                     float *y, void *ws, uint32_t *counters, hipStream_t st) {
+                     float *y, void *ws, uint32_t *counters, const float *x, hipStream_t st) {
     if (!ws || !rexp || !gemm_serves(type, k)) return hipErrorInvalidValue;
+    if (x && !gemm_quantises_in_kernel(type, n, k, m, x)) return hipErrorInvalidValue;
     const Plan p = plan_for(type, n, k, m);
     const WsLayout L = ws_layout(type, p, n, k, m);
     uint8_t *base = static_cast<uint8_t *>(ws);
@@ -545,16 +555,16 @@ hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, 
                         : nullptr;
     hipError_t e;
     switch (type) {
-    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q6_K: e = launch_typed<TYPE_Q6_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q8_0: e = launch_typed<TYPE_Q8_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q4_0: e = launch_typed<TYPE_Q4_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q4_1: e = launch_typed<TYPE_Q4_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q5_0: e = launch_typed<TYPE_Q5_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q5_1: e = launch_typed<TYPE_Q5_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q2_K: e = launch_typed<TYPE_Q2_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
-    case TYPE_Q3_K: e = launch_typed<TYPE_Q3_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, st); break;
+    case TYPE_Q4_K: e = launch_typed<TYPE_Q4_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q5_K: e = launch_typed<TYPE_Q5_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q6_K: e = launch_typed<TYPE_Q6_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q8_0: e = launch_typed<TYPE_Q8_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q4_0: e = launch_typed<TYPE_Q4_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q4_1: e = launch_typed<TYPE_Q4_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q5_0: e = launch_typed<TYPE_Q5_0>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q5_1: e = launch_typed<TYPE_Q5_1>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q2_K: e = launch_typed<TYPE_Q2_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
+    case TYPE_Q3_K: e = launch_typed<TYPE_Q3_K>(p, w, rexp, n, row_bytes, a, erow, ofs, k, m, out, stride, cnt, y, x, st); break;
     default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess || p.splits == 1 || cnt) return e;
@@ -567,9 +577,11 @@ hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n
                        const ActView &act, const float *x, int64_t m, float *y, void *ws, uint32_t *counters,
                        hipStream_t st) {
     if (gemm_serves(type, k)) {
+        if (gemm_quantises_in_kernel(type, n, k, m, x))  // no operand pre-pass
+            return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, counters, x, st);
         hipError_t e = gemm_prepass(type, k, act, x, m, ws, st);
         if (e != hipSuccess) return e;
-        return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, counters, st);
+        return gemm_main(type, w, rexp, n, k, row_bytes, m, y, ws, counters, nullptr, st);
     }
     if (x) return hipErrorInvalidValue;  // the GEMV over row chunks takes quantised activations
     // k % 256 != 0: the decode GEMV over row chunks of 8

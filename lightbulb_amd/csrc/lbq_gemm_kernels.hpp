@@ -506,6 +506,7 @@ struct GemmGrid {
     const _Float16 *ofs;        // OFS types: per operand row and super-block, 16 f16 A values of the extra k-step
     uint32_t *cnt;              // k-sliced split: per column tile, slices done (null: k_split_sum adds them)
     float *y;                   // ... and the output the last slice of a tile writes
+    const float *x;             // k-sliced, Q8_K rows: f32 x [m][k] each workgroup quantises itself
 };
 
 // whether a weight type adds an extra k-step per super-block (odw)
@@ -1126,8 +1127,18 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
 // wave has its whole slice of weight bytes in flight (the stream's latency is
 // paid once per workgroup, not once per block).  Slices write partial sums that
 // k_split_sum adds in a fixed order.
+//
+// With f32 x and Q8_K activations (FX) there is no pre-pass: each workgroup
+// quantises the rows of its own slice (Q8_K codes and scales as the reference,
+// one operand exponent per row and slice) straight into LDS while its weight
+// bytes are in flight.  The operand slots are then XOR-swizzled within each 1 KB
+// (block, row tile, k-step) chunk (ks_swz) so that a wave's stores of one row
+// spread over the banks; the MFMA reads apply the same swizzle.
 // ---------------------------------------------------------------------------
 constexpr int KSN = 128;  // columns per k-sliced workgroup
+
+// FX operand slot swizzle of block b, k-step s: slot (32 h + row) ^ ks_swz
+__device__ __forceinline__ constexpr int ks_swz(int b, int s) { return ((s >> 1) | ((b & 3) << 3)) & 31; }
 
 constexpr int KS_BLOCKS = 4;  // longest slice: 4 x 16 KB of LDS, two workgroups per CU
 constexpr int KS_FUSED_SLICES = 8;  // most slices the k-sliced kernel adds itself
@@ -1142,7 +1153,85 @@ constexpr int KS_SUM_Q = 4;         // slices each thread loads per round of the
 template <int TYPE>
 constexpr bool ks_group_exponents() { return vec_dot_type(TYPE) == TYPE_Q8_K; }
 
-template <int TYPE, int S, int T>
+// FX: the rows 0 .. min(M, 32 T) - 1 of blocks b0 .. b0 + cnt - 1 of x, quantised
+// to Q8_K (q8k_lane16: 16 lanes per (row, block), 16 values each), become the
+// operands f16(q d 2^-e) in the slice's LDS layout (operand-major, swizzled), e
+// = the row's exponent over the slice's blocks (as k_ops_ks over a group), in
+// Es.  A wave takes 4 / S rows per pass.  ks_load_slice issues every pass's
+// loads (before the weight loads, so no wait for x is held up behind them);
+// ks_quantise_slice stores.  Rows past M and blocks past the slice are neither
+// loaded nor stored (their MFMA rows are never written out, their blocks never
+// multiplied).
+template <int S, int MR>  // MR: rows quantised (16, 32 or 64; at least M)
+struct KsSlice {
+    static constexpr int RPW = KS_BLOCKS / S;  // rows per wave and pass
+    static constexpr int NP = MR / (4 * RPW);  // passes
+    float v[NP][16];
+};
+
+template <int S, int MR>
+__device__ __forceinline__ void ks_load_slice(KsSlice<S, MR> &xs, const float *__restrict__ x, int64_t K, int64_t M,
+                                              int b0, int cnt, int wave, int lane) {
+    using X = KsSlice<S, MR>;
+    const int sub = lane & 15, bi = (lane >> 4) % S, ri = (lane >> 4) / S;
+#pragma unroll
+    for (int p = 0; p < X::NP; p++) {
+        const int row = (p * 4 + wave) * X::RPW + ri;
+        const bool live = row < M && bi < cnt;
+        const float4 *src = reinterpret_cast<const float4 *>(
+            x + (live ? (int64_t)row * K + (int64_t)(b0 + bi) * KB + 16 * sub : 0));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = live ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xs.v[p][4 * i] = f.x; xs.v[p][4 * i + 1] = f.y; xs.v[p][4 * i + 2] = f.z; xs.v[p][4 * i + 3] = f.w;
+        }
+    }
+}
+
+template <int S, int T, int MR>
+__device__ __forceinline__ void ks_quantise_slice(KsSlice<S, MR> &xs, int64_t M, int cnt, int wave, int lane,
+                                                  uint8_t *As, int *Es) {
+    using X = KsSlice<S, MR>;
+    const int sub = lane & 15, bi = (lane >> 4) % S, ri = (lane >> 4) / S;
+#pragma unroll
+    for (int p = 0; p < X::NP; p++) {
+        const int row = (p * 4 + wave) * X::RPW + ri;
+        const bool live = row < M && bi < cnt;
+        uint32_t packed[4];
+        int sum;
+        float d;
+        q8k_lane16(xs.v[p], sub, packed, &sum, &d);
+        float mx = live ? fabsf(d) : 0.f;
+        if constexpr (S >= 2) mx = fmaxf(mx, __shfl_xor(mx, 16));
+        if constexpr (S >= 4) mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;
+        if (bi == 0 && sub == 0 && row < M) Es[row] = e;
+        if (!live) continue;
+        const float sx = __builtin_amdgcn_ldexpf(d, -e);
+        const float cc = -1152.f * sx;
+        uint32_t w8[8];
+        codes_to_f16(packed[0], sx, cc, &w8[0], &w8[1]);
+        codes_to_f16(packed[1], sx, cc, &w8[2], &w8[3]);
+        codes_to_f16(packed[2], sx, cc, &w8[4], &w8[5]);
+        codes_to_f16(packed[3], sx, cc, &w8[6], &w8[7]);
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int p8 = 2 * sub + q, st = p8 & 15, hh = p8 >> 4;
+            const int chunk = (T * bi + (row >> 5)) * 16 + st;
+            const int slot = (32 * hh + (row & 31)) ^ ks_swz(bi, st);
+            *reinterpret_cast<uint4 *>(As + chunk * 1024 + slot * 16) =
+                make_uint4(w8[4 * q], w8[4 * q + 1], w8[4 * q + 2], w8[4 * q + 3]);
+        }
+    }
+}
+
+// slice shapes whose x fits the registers beside the weight bytes (64 floats a
+// lane): MR quantised rows (16 for m <= 16, else 32 per row tile) times S blocks
+constexpr int ks_fx_rows(int64_t m, int T) { return m <= 16 ? 16 : 32 * T; }
+constexpr bool ks_fx_shape(int S, int MR) { return (S == 1 || S == 2 || S == 4) && MR * S <= 64; }
+constexpr int KS_FX_MAX_TILES = 32;  // most column tiles (4096 columns) that quantise x in the kernel
+
+template <int TYPE, int S, int T, int FXR = 0>
 __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N, int64_t row_bytes,
                                                     const _Float16 *__restrict__ A, const int *__restrict__ erow,
                                                     int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
@@ -1150,7 +1239,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     const int64_t split_stride = g.split_stride;
     using B = GB<TYPE>;
     static_assert(S >= 1 && S <= KS_BLOCKS && (T == 1 || T == 2), "slice length, row tiles");
+    constexpr bool FX = FXR > 0;  // FXR: rows this kernel quantises from x
+    static_assert(!FX || (ks_group_exponents<TYPE>() && ks_fx_shape(S, FXR) && FXR <= 32 * T), "FX: Q8_K, x in registers");
     __shared__ __align__(1024) uint8_t As[S * T * 16384];
+    __shared__ int Es[FX ? 32 * T : 1];  // FX: the slice's operand exponent per row
     const int tn = (int)blockIdx.x / slices, z = (int)blockIdx.x % slices;
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
               lr = lane & 31;
@@ -1166,18 +1258,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     // (((T b + u) 16 + s) 64 + l) 16; 1 KB per wave instruction, chunk 4i + wave;
     // chunks past the slice's last block read as zero (outside the buffer
     // resource) and are never used
-    const uint64_t abase = reinterpret_cast<uint64_t>(A + (int64_t)b0 * T * 16 * 512);
-    const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
-                             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
-    const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane(cnt * T * 16384), 0x00020000);
+    if constexpr (!FX) {
+        const uint64_t abase = reinterpret_cast<uint64_t>(A + (int64_t)b0 * T * 16 * 512);
+        const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
+                                 ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
+        const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void *>(abase_s), (short)0, __builtin_amdgcn_readfirstlane(cnt * T * 16384), 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 4 * S * T; i++) {
-        const int chunk = 4 * i + wave;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)(As + chunk * 1024),
-                                                 16, (uint32_t)lane * 16, chunk * 1024, 0, 0);
+        for (int i = 0; i < 4 * S * T; i++) {
+            const int chunk = 4 * i + wave;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)(As + chunk * 1024),
+                                                     16, (uint32_t)lane * 16, chunk * 1024, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
+    // FX: the slice's x, before the weights
+    KsSlice<FX ? S : 1, FX ? FXR : 16> xs;
+    if constexpr (FX) {
+        ks_load_slice<S, FXR>(xs, g.x, K, M, b0, cnt, wave, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // OFS types: the extra k-step's A operands of the slice, before the weights
     constexpr bool OFS = gemm_ofs<TYPE>();
     half8 oa[OFS ? S : 1][T];
@@ -1200,6 +1300,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     // to LDS and, before the barrier, waits for exactly those (vmcnt = the number
     // of weight load instructions issued after them, as it emitted them -- it may
     // merge neighbouring loads, so a count written here could be too high).
+    if constexpr (FX) ks_quantise_slice<S, T, FXR>(xs, M, cnt, wave, lane, As, Es);
     __syncthreads();
 
     floatx16 acc[T];
@@ -1221,7 +1322,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
                 const half8 bo = __builtin_bit_cast(half8, make_uint4(bw[0], bw[1], bw[2], bw[3]));
 #pragma unroll
                 for (int u = 0; u < T; u++) {
-                    const half8 a = *reinterpret_cast<const half8 *>(arow + ((b * T + u) * 16 + s) * 1024);
+                    const half8 a = FX ? *reinterpret_cast<const half8 *>(As + ((b * T + u) * 16 + s) * 1024 +
+                                                                          ((lane ^ ks_swz(b, s)) << 4))
+                                       : *reinterpret_cast<const half8 *>(arow + ((b * T + u) * 16 + s) * 1024);
                     acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc[u], 0, 0, 0);
                 }
             }
@@ -1246,7 +1349,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const int r = 32 * u + 8 * (v >> 2) + 4 * h + (v & 3);
-            ex[u][v] = ex_row[r < M ? r : M - 1];
+            ex[u][v] = FX ? Es[r < M ? r : M - 1] : ex_row[r < M ? r : M - 1];
         }
 #pragma unroll
     for (int u = 0; u < T; u++)
@@ -1335,9 +1438,26 @@ inline int operand_major(const Plan &p) { return p.mt == MT_KS ? p.rt : 0; }
 template <int TYPE>
 hipError_t launch_typed(const Plan &p, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t row_bytes,
                         const _Float16 *a, const int *erow, const _Float16 *ofs, int64_t k, int64_t m, float *out,
-                        int64_t split_stride, uint32_t *cnt, float *y, hipStream_t st) {
-    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits, rexp, ofs, cnt, y};
+                        int64_t split_stride, uint32_t *cnt, float *y, const float *x, hipStream_t st) {
+    const GemmGrid g{p.tiles_m, p.tiles_n, p.bps, split_stride, p.splits, rexp, ofs, cnt, y, x};
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * p.splits));
+    if constexpr (ks_group_exponents<TYPE>()) {
+        if (x) {  // k-sliced, quantising x in the kernel (ks_fx_shape slices)
+            const int mr = ks_fx_rows(m, p.rt);
+            if (p.mt != MT_KS || !ks_fx_shape(p.bps, mr)) return hipErrorInvalidValue;
+#define LBQ_KS_FX(S_, T_, MR_) k_gemm_ks<TYPE, S_, T_, MR_><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g)
+            if (p.rt == 2) LBQ_KS_FX(1, 2, 64);
+            else if (mr == 16 && p.bps == 4) LBQ_KS_FX(4, 1, 16);
+            else if (mr == 16 && p.bps == 2) LBQ_KS_FX(2, 1, 16);
+            else if (mr == 16) LBQ_KS_FX(1, 1, 16);
+            else if (p.bps == 2) LBQ_KS_FX(2, 1, 32);
+            else LBQ_KS_FX(1, 1, 32);
+#undef LBQ_KS_FX
+            return hipGetLastError();
+        }
+    } else if (x) {
+        return hipErrorInvalidValue;
+    }
     if (p.mt == MT_KS) {
         if (p.rt == 2) {  // two row tiles: slices of 1 or 2 blocks
             if (p.bps == 1) k_gemm_ks<TYPE, 1, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g);

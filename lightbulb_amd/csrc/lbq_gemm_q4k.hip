@@ -5,5 +5,5 @@
 namespace lbq {
 template hipError_t launch_typed<TYPE_Q4_K>(const Plan &, const uint8_t *, const int8_t *, int64_t, int64_t,
                                           const _Float16 *, const int *, const _Float16 *, int64_t, int64_t,
-                                          float *, int64_t, uint32_t *, float *, hipStream_t);
+                                          float *, int64_t, uint32_t *, float *, const float *, hipStream_t);
 }  // namespace lbq

@@ -56,6 +56,7 @@ struct Tuning {
     int gemm_big = 0;     // 1: wide tiles, 2: tall tiles (0: planned)
     int gemm_splits = 0;  // split-k count (0: planned)
     bool gemm_split_launch = false;  // k-sliced slices added by the separate launch, never in the kernel
+    bool gemm_prepass = false;       // k-sliced operands always from the separate pre-pass
     bool gemv1_nofuse = false, gemv_rows_off = false;
     int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
     int gemv1_wpc = 0, gemv1_wpg = 0;
@@ -150,8 +151,13 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
 // counters: KS_COUNTERS zeroed words the k-sliced kernel uses to add its own
 // slices (the last workgroup of a column tile sums them and puts the word back
 // to zero); nullptr keeps the separate slice-sum launch.
+// x: f32 activations the k-sliced kernel quantises itself (gemm_quantises_in_kernel;
+// no pre-pass then), or nullptr for the operands gemm_prepass left in ws.
 hipError_t gemm_main(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes, int64_t m,
-                     float *y, void *ws, uint32_t *counters, hipStream_t st);
+                     float *y, void *ws, uint32_t *counters, const float *x, hipStream_t st);
+// whether the GEMM for (type, n, k, m) quantises f32 x itself (the k-sliced
+// kernel with Q8_K activations, on slices whose x fits its registers)
+bool gemm_quantises_in_kernel(int type, int64_t n, int64_t k, int64_t m, const float *x);
 hipError_t launch_gemm(int type, const uint8_t *w, const int8_t *rexp, int64_t n, int64_t k, int64_t row_bytes,
                        const ActView &act, const float *x, int64_t m, float *y, void *ws, uint32_t *counters,
                        hipStream_t st);

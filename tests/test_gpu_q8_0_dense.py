@@ -281,6 +281,41 @@ def test_ksliced_slice_sum_in_kernel(oracle, lbq, dev, t, monkeypatch):
         assert_rows_close(y[rows], ref, tight_bound(t, m))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+def test_ksliced_quantise_in_kernel(oracle, lbq, dev, t, monkeypatch):
+    # k-sliced launches of at most 32 column tiles quantise f32 x themselves (no
+    # pre-pass launch): every slice shape (1, 2, 4 blocks; 16 and 32 quantised
+    # rows; two row tiles), ragged m and n, a short last slice; checked against
+    # the oracle and against the pre-pass operands (the same Q8_K values; the
+    # operand exponent is per slice instead of per group of four blocks, which
+    # moves no bit unless an operand is an f16 subnormal)
+    from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
+    rng = np.random.default_rng(640 + t)
+    cases = [(16, 4096, 4096, {}), (13, 1000, 256 * 6, {}), (32, 1024, 4096, {}), (9, 300, 256 * 5, {}),
+             (12, 4096, 256 * 34, {}),  # 4-block slices, a short last one
+             (16, 4096, 4096, {"LBQ_GEMM_KS": "1"}), (20, 700, 256 * 7, {"LBQ_GEMM_KS": "2"})]
+    if t != Q4_K:
+        cases.append((48, 500, 4096, {"LBQ_GEMM_KS": "1"}))  # two row tiles, 64 quantised rows
+    for (m, n, k, env) in cases:
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = forward_with_env(monkeypatch, env, t, w_raw, n, k, x, dev)
+        y_pre = forward_with_env(monkeypatch, {**env, "LBQ_GEMM_PREPASS": "1"}, t, w_raw, n, k, x, dev)
+        np.testing.assert_allclose(y, y_pre, rtol=1e-6, atol=1e-6 * float(np.abs(y_pre).max()))
+        rows = sorted({0, m // 2, m - 1})
+        ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+        assert_rows_close(y[rows], ref, tight_bound(t, m))
+    # a group whose weights take both paths (4096 rows in the kernel, 14336 after
+    # the pre-pass) equals separate calls bit for bit
+    k, m = 4096, 16
+    raws = [bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3) for n in (4096, 14336)]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, (4096, 14336))]
+    xd = to_dev(rng.standard_normal((m, k)).astype(np.float32), dev)
+    ys = qmatmul_group(qms, xd)
+    for q, yg in zip(qms, ys):
+        assert np.array_equal(yg.cpu().numpy().view(np.uint32), q.forward(xd).cpu().numpy().view(np.uint32))
+
+
 def test_tuning_read_once_per_context(oracle, lbq, dev, monkeypatch):
     # an override set after a context exists does not change that context's plan
     from lightbulb_amd.quantized import QMatMul, QTensor
