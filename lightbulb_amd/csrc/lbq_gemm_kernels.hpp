@@ -1145,6 +1145,7 @@ constexpr int KS_FUSED_SLICES = 8;  // most slices the k-sliced kernel adds itse
 constexpr int KS_FUSED_MIN_TILES = 64;  // ... and fewest column tiles
 constexpr int KS_SC1 = 16;          // buffer-load cache policy: sc1 (agent-scope coherent)
 constexpr int KS_SUM_Q = 4;         // slices each thread loads per round of the in-kernel sum
+constexpr int KS_RING = 2;          // weight blocks in flight per wave
 
 // With Q8_K activations the k-sliced layout's operand rows carry one exponent per
 // group of KS_BLOCKS blocks (erow[group][m]) rather than per row, so its pre-pass
@@ -1288,12 +1289,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
             for (int u = 0; u < T; u++) oa[b][u] = ofs_operand(g.ofs, 32 * u + lr, nb, b0 + min(b, cnt - 1), h);
     }
     // weight loads block by block, in order (each block's wait then covers only
-    // the blocks before it)
-    typename B::Raw raw[S];
+    // the blocks before it).  Q4_K / Q5_K keep KS_RING blocks ahead: block b + D
+    // goes out as soon as block b's bytes are in its Prep, so the stream feeds the
+    // compute instead of every workgroup's whole slice arriving at once (1.5-2 us
+    // faster at 4096 x 14336, m = 16); the other types issue the whole slice at
+    // once (Q6_K: 1.4 us slower with the ring)
+    constexpr int D = (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) && KS_RING < S ? KS_RING : S;
+    typename B::Raw raw[D];
+    auto w_issue = [&](int b) {
 #pragma unroll
-    for (int b = 0; b < S; b++) {
+        for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b % D], q);
+    };
 #pragma unroll
-        for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b], q);
+    for (int b = 0; b < D; b++) {
+        w_issue(b);
         __builtin_amdgcn_sched_barrier(0);
     }
     // The activation loads are the oldest in flight.  The compiler tracks loads
@@ -1313,7 +1322,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     for (int b = 0; b < S; b++) {
         if (b < cnt) {
             typename B::Prep p;
-            gb_prep<TYPE>(raw[b], h, wrow + (int64_t)b * B::BYTES, wsc, p);
+            gb_prep<TYPE>(raw[b % D], h, wrow + (int64_t)b * B::BYTES, wsc, p);
+            if (b + D < S) w_issue(b + D);
 #pragma unroll
             for (int s = 0; s < 16; s++) {
                 uint32_t bw[4];
