@@ -70,18 +70,27 @@ __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return (uint32_t)
 // an all-zero block gives d = 0 and zero codes.  Out: the lane's 16 codes packed
 // little-endian, their sum (one bsums entry) and the block's d.
 __device__ __forceinline__ void q8k_lane16(const float *v, int sub, uint32_t packed[4], int *sum_out, float *d_out) {
-    // the lane's largest |x| and the first value holding it (ascending
-    // scan, strict >: ties keep the lower index; a NaN compares false
-    // and is never chosen)
-    float am = 0.f, av = 0.f;
+    // the lane's largest |x| and the sign of the first value holding it (the
+    // reference scans in ascending order with a strict >, so ties keep the lower
+    // index and a NaN, comparing false, is never chosen): the signed maximum and
+    // minimum (maximumNumber / minimumNumber: any NaN, signalling included, is
+    // passed over), then, only where both +am and -am occur, the first of them
+    float mxp = v[0], mnn = v[0];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const bool gt = fabsf(v[i]) > am;
-        av = gt ? v[i] : av;
-        am = gt ? fabsf(v[i]) : am;
+    for (int i = 1; i < 16; i++) {
+        mxp = __builtin_fmaximum_numf(mxp, v[i]);
+        mnn = __builtin_fminimum_numf(mnn, v[i]);
     }
-    const uint32_t bmax = row_max_u32(__float_as_uint(am));  // non-negative: bits order as values
-    uint32_t key = __float_as_uint(am) == bmax ? ((uint32_t)sub << 1) | (__float_as_uint(av) >> 31) : 0xffffffffu;
+    const float am = __builtin_fmaximum_numf(__builtin_fmaximum_numf(mxp, -mnn), 0.f);  // 0 if every value is NaN
+    uint32_t neg = -mnn == am ? 1u : 0u;
+    if (mxp == am && neg && am > 0.f) {  // +am and -am both present: the first one decides
+#pragma unroll
+        for (int i = 15; i >= 0; i--)
+            if (fabsf(v[i]) == am) neg = __float_as_uint(v[i]) >> 31;
+    }
+    const uint32_t amb = __float_as_uint(am) & 0x7fffffffu;  // +0 for a zero lane
+    const uint32_t bmax = row_max_u32(amb);  // non-negative: bits order as values
+    uint32_t key = amb == bmax ? ((uint32_t)sub << 1) | neg : 0xffffffffu;
     key = row_min_u32(key);  // the first lane holding the block max, and that value's sign
     packed[0] = packed[1] = packed[2] = packed[3] = 0u;
     int sum = 0;

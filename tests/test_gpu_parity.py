@@ -140,13 +140,44 @@ def _special_rows(k: int) -> np.ndarray:
     return rows
 
 
+def _tie_rows(k: int) -> np.ndarray:
+    """Rows whose block maximum is decided by order, sign, NaN kind or size:
+    |max| held by both signs (first occurrence wins, within one 16-value lane and
+    across lanes), signalling NaNs (passed over like quiet ones), subnormal and
+    largest finite maxima, signed zeros.  k >= 768."""
+    f = np.float32
+    snan, nsnan, snan2 = (np.array([v], np.uint32).view(np.float32)[0] for v in (0x7F800001, 0xFF800001, 0x7FA00000))
+    rows = np.zeros((6, k), dtype=np.float32)
+    rows[0, 17], rows[0, 40] = -5.0, 5.0            # across lanes: -5 first
+    rows[0, 256 + 3], rows[0, 256 + 200] = 6.0, -6.0
+    rows[0, 512 + 1], rows[0, 512 + 2] = 0.25, -0.25
+    rows[1, 0], rows[1, 9] = 7.0, -7.0              # within one lane: +7 first
+    rows[1, 256 + 20], rows[1, 256 + 30] = -7.0, 7.0
+    rows[1, 256 + 33], rows[1, 256 + 34] = 3.0, -3.0  # a lane tie below the block maximum
+    rows[1, 512 + 100:512 + 116] = np.where(np.arange(16) % 2 == 0, f(-2.5), f(2.5))
+    rows[2, 5], rows[2, 100] = f(1e-40), f(-3e-41)  # subnormal maxima: iscale overflows
+    rows[2, 256 + 44], rows[2, 256 + 45] = f(-2e-39), f(1e-45)
+    rows[2, 512 + 7] = f(1.4e-45)
+    rows[3, :] = np.random.default_rng(5).standard_normal(k).astype(np.float32)
+    rows[3, 0], rows[3, 7] = snan, snan             # signalling NaNs among normal values
+    rows[3, 256 + 5], rows[3, 256 + 6] = nsnan, np.nan
+    rows[3, 512:768] = snan2                        # a block of signalling NaNs only
+    rows[4, 0:256] = -0.0                           # signed zeros (and a NaN) only
+    rows[4, 256:512:2] = -0.0
+    rows[4, 300] = np.nan
+    rows[4, 512 + 9] = -0.0
+    rows[5, 3], rows[5, 600] = f(-3.4028235e38), f(3.4028235e38)
+    rows[5, 4] = f(1e30)
+    return rows
+
+
 @pytest.mark.parametrize("act", [Q8_K, Q8_0])
 def test_quantize_act_bit_exact(oracle, lbq, dev, act):
     rng = np.random.default_rng(30 + act)
     k = 4096
     x = rng.standard_normal((9, k)).astype(np.float32)
     x[rng.random(x.shape) < 0.01] *= 20      # outliers, as in the LM-head config
-    x = np.concatenate([x, _special_rows(k)])
+    x = np.concatenate([x, _special_rows(k), _tie_rows(k)])
     from lightbulb_amd.quantized import quantize_activations
     got = quantize_activations(to_dev(x, dev), act).cpu().numpy()
     ref = oracle.quantize_act(act, x)
@@ -257,7 +288,7 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
     n = 300
     w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
     qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
-    xs = np.concatenate([_special_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
+    xs = np.concatenate([_special_rows(k), _tie_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
     xs[-1, rng.random(k) < 0.01] *= 20
     for row in xs:
         xd = to_dev(row[None, :], dev)
@@ -279,6 +310,7 @@ def test_batched_prepass_quantisation_is_bit_exact(oracle, lbq, dev, t):
         qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
         x = rng.standard_normal((m, k)).astype(np.float32)
         x[:7] = _special_rows(k)
+        x[7:13] = _tie_rows(k)
         x[-1, rng.random(k) < 0.01] *= 20
         xd = to_dev(x, dev)
         y_fused = qm.forward(xd)
