@@ -14,7 +14,27 @@ hipError_t gemv_k23(int, const RowMap &, int64_t, int64_t, const ActView &, cons
 
 bool gemv_fuses_quant(int type, int64_t n, int64_t k, int m, const float *x) {
     (void)n;
-    if (m != 1 || (reinterpret_cast<uintptr_t>(x) & 15u)) return false;
+    if (m < 1 || m > 8 || (reinterpret_cast<uintptr_t>(x) & 15u)) return false;
+    if (m > 1) {
+        // m = 2..4: the multi-row kernel quantises the x rows in its prologue (Q8_K
+        // rows, at most four (row, 16-block pass) items) instead of a separate
+        // quantisation launch before it.  Every workgroup quantises all its rows, so
+        // with more items that repeated work outweighs the launch: measured on
+        // Q5_K 14336 x 4096 at m = 2 / 4 / 8: 14.3 -> 12.0, 17.3 -> 15.6, 22.8 -> 24.0 us;
+        // Q4_K 4096 x 8192 at m = 5 (a four-row chunk of two passes): 17.1 -> 21.3 us
+        if (tuning().gemv1_nofuse || tuning().gemv_rows_off) return false;
+        const int nbk = (int)(k / QK_K);
+        int ppb, rpw, it;
+        switch (type) {
+        case TYPE_Q4_K:
+            return fast_rows_max<TYPE_Q4_K>(nbk) >= 4 && fast_shape<TYPE_Q4_K>(nbk, &ppb, &rpw, &it, 2) && m * it <= 4;
+        case TYPE_Q5_K:
+            return fast_rows_max<TYPE_Q5_K>(nbk) >= 4 && fast_shape<TYPE_Q5_K>(nbk, &ppb, &rpw, &it, 2) && m * it <= 4;
+        case TYPE_Q6_K:
+            return fast_rows_max<TYPE_Q6_K>(nbk) >= 4 && fast_shape<TYPE_Q6_K>(nbk, &ppb, &rpw, &it, 2) && m * it <= 4;
+        default: return false;
+        }
+    }
     // Every workgroup quantises all of x before its first dot, so the prologue
     // grows with k, but even at k = 14336 it costs less than a separate
     // quantisation launch (4096 x 14336 Q4_K: fused 10.3 us, quantise + GEMV 11.7).

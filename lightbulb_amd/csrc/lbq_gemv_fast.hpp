@@ -512,6 +512,56 @@ __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int 
     wg_barrier<FENCE>();
 }
 
+// MR rows of f32 x (row stride nbx * 256) quantised to Q8_K into MR consecutive
+// LDS row images, as quantise_x_lds does for one row (same code, same bytes).
+// IT passes of 16 blocks per row (nbx <= 16 * IT); every (row, pass) load is
+// issued before `between` (the weight ring), so none of them waits behind the
+// weight stream (memory loads complete in order).  With rows < MR the rows past
+// `rows` repeat the last real one (computed, never stored); rows == 0 means MR.
+template <int TYPE, int MR, int IT, class Between>
+__device__ __forceinline__ void quantise_rows_lds(const float *__restrict__ x, int rows, int nbx, uint8_t *sx,
+                                                  Between between) {
+    static_assert(TYPE != TYPE_Q8_0 && MR * IT <= 8, "Q8_K rows, at most 8 (row, pass) items");
+    // (the host fuses at most four items; eight are compiled for the 8-row shape)
+    constexpr int NI = MR * IT;
+    const int t = threadIdx.x, sub = t & 15;
+    const int64_t k = (int64_t)nbx * QK_K;
+    float v[NI][16];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int m = i / IT, j = i % IT;
+        const int src = rows > 0 ? min(m, rows - 1) : m;
+        const int b = min(16 * j + (t >> 4), nbx - 1);
+        const float4 *p = reinterpret_cast<const float4 *>(x + (int64_t)src * k + (int64_t)b * QK_K + 16 * sub);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = p[q];
+            v[i][4 * q] = f.x; v[i][4 * q + 1] = f.y; v[i][4 * q + 2] = f.z; v[i][4 * q + 3] = f.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    between();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int m = i / IT, j = i % IT;
+        if (j == 0 || 16 * j < nbx) {  // workgroup-uniform: the DPP reductions stay convergent
+            uint32_t packed[4];
+            int sum;
+            float d;
+            q8k_lane16(v[i], sub, packed, &sum, &d);
+            const int b = 16 * j + (t >> 4);
+            if (b < nbx) {
+                uint8_t *xb = sx + ((int64_t)m * nbx + b) * XS_K;
+                *reinterpret_cast<uint4 *>(xb + 16 * sub) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                *reinterpret_cast<int16_t *>(xb + 256 + 2 * sub) = (int16_t)sum;
+                if (sub == 0) *reinterpret_cast<float *>(xb + 288) = d;
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Pre-quantised activations (split global layout) -> the LDS layout.  Straight-line
 // code for nbx <= 64 (k <= 16384, the fast path's limit): every load is issued
 // before any store, with indices clamped into range instead of branches;
@@ -651,7 +701,8 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
                                                     ActView act, const float *__restrict__ alpha, float eps) {
     static_assert(WPG == 4 || (FUSED && WPG == 8), "waves per workgroup: 4, or 8 for the fused prologue");
     static_assert(!NORM || (FUSED && TYPE != TYPE_Q8_0), "the RMS norm runs in the quantising prologue");
-    static_assert(MR == 1 || (!FUSED && MAP == MAP_ONE), "several activation rows: pre-quantised, one weight");
+    static_assert(MR == 1 || (MAP == MAP_ONE && !NORM && WPG == 4 && (!FUSED || TYPE != TYPE_Q8_0)),
+                  "several activation rows: one weight; quantised in the prologue for Q8_K rows only");
     constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
     static_assert(!PAIRED || RPW <= 2, "a silu pair spans two row groups or one");
     const int64_t n = rm.n;
@@ -750,7 +801,8 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     constexpr int XS = TYPE == TYPE_Q8_0 ? XS_0 : XS_K;
     // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 32 WPG per pass
     constexpr int XJ = (64 * IT + 32 * WPG - 1) / (32 * WPG);
-    if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (XJ < 4 ? XJ : 4), WPG>(x, nb, sx, issue_ring, alpha, eps);
+    if constexpr (FUSED && MR > 1) quantise_rows_lds<TYPE, MR, IT>(x, act.rows, nb, sx, issue_ring);
+    else if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (XJ < 4 ? XJ : 4), WPG>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its

@@ -747,13 +747,17 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
 // MR pre-quantised activation rows (m = MR) against one weight: the weight is
 // streamed once for all MR rows, the activation rows sit in LDS (or registers).
 template <int TYPE, int PPB, int RPW, int IT, int MR>
-static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, hipStream_t st) {
+static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, const float *x,
+                                   hipStream_t st) {
     const int64_t n = rm.n;
     const int64_t ng = (n + RPW - 1) / RPW;
     constexpr int BPI = 64 / RPW / PPB;
     if (!(BPI * (IT - 1) < nb && nb <= BPI * IT)) return hipErrorNotSupported;
     const size_t lds = (size_t)MR * nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
-    auto kern = k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE>;
+    // x: f32 rows quantised in the prologue (Q8_K types), else pre-quantised rows
+    constexpr bool FX = TYPE != TYPE_Q8_0 && MR > 1 && MR * IT <= 8;
+    if (x && !FX) return hipErrorNotSupported;
+    auto kern = x ? k_gemv1<TYPE, PPB, RPW, IT, MR, FX, MAP_ONE> : k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE>;
     if (lds > 65536) {
         static const hipError_t attr =
             hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
@@ -765,19 +769,20 @@ static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, 
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
-    kern<<<grid, 256, lds, st>>>(rm, row_bytes, nb, nullptr, act, nullptr, 0.f);
+    kern<<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     return hipGetLastError();
 }
 
 template <int TYPE, int MR>
-static hipError_t run_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, hipStream_t st) {
+static hipError_t run_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, const ActView &act, const float *x,
+                                hipStream_t st) {
     int ppb, rpw, it;
     // every chunk of a multi-row call (its single-row remainder too) uses the multi-row shape
     if (!fast_shape<TYPE>(nb, &ppb, &rpw, &it, 2)) return hipErrorNotSupported;
     // only the (shape, rows) pairs fast_rows_max admits are compiled
 #define LBQ_FAST(Q, R, I)                                                                                   \
     if constexpr (MR <= (I <= 1 ? 8 : I == 2 ? 4 : 1))                                                     \
-        if (ppb == Q && rpw == R && it == I) return launch_fast_rows<TYPE, Q, R, I, MR>(rm, row_bytes, nb, act, st);
+        if (ppb == Q && rpw == R && it == I) return launch_fast_rows<TYPE, Q, R, I, MR>(rm, row_bytes, nb, act, x, st);
     if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
         LBQ_FAST(4, 4, 1) LBQ_FAST(4, 2, 1) LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
     } else if constexpr (TYPE == TYPE_Q6_K) {
@@ -799,10 +804,16 @@ static int fast_rows_max(int nb) {
     return it <= 1 ? 8 : it == 2 ? 4 : 1;
 }
 
-// m = 2..8 pre-quantised rows: chunks of 8, 4, 2 and 1 rows, each chunk one launch
-// (the largest chunk within fast_rows_max whose activation image fits 80 KB of LDS).
 template <int TYPE>
-static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const ActView &act, int m, hipStream_t st) {
+static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const float *x, const ActView &act, int map,
+                           const float *alpha, float eps, hipStream_t st);
+
+// m = 2..8 rows: chunks of 8, 4, 2 and 1 rows, each chunk one launch (the largest
+// chunk within fast_rows_max whose activation image fits 80 KB of LDS); rows
+// pre-quantised (act), or f32 x that each launch quantises in its prologue.
+template <int TYPE>
+static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const ActView &act, const float *x, int m,
+                             hipStream_t st) {
     const size_t row_lds = (size_t)nb * (TYPE == TYPE_Q8_0 ? XS_0 : XS_K);
     const int mr_max = fast_rows_max<TYPE>(nb);
     for (int m0 = 0; m0 < m;) {
@@ -819,12 +830,16 @@ static hipError_t run_fast_m(const RowMap &rm0, int64_t row_bytes, int nb, const
         a.xd = act.xd + (int64_t)m0 * act.nb;
         if (act.xbs) a.xbs = act.xbs + (int64_t)m0 * (act.k / 16);
         a.rows = real < mr ? real : 0;
+        const float *xc = x ? x + (int64_t)m0 * nb * (TYPE == TYPE_Q8_0 ? QK8_0 : QK_K) : nullptr;
         hipError_t e;
         switch (mr) {
-        case 8: e = run_fast_rows<TYPE, 8>(rm, row_bytes, nb, a, st); break;
-        case 4: e = run_fast_rows<TYPE, 4>(rm, row_bytes, nb, a, st); break;
-        case 2: e = run_fast_rows<TYPE, 2>(rm, row_bytes, nb, a, st); break;
-        default: e = run_fast_rows<TYPE, 1>(rm, row_bytes, nb, a, st); break;
+        case 8: e = run_fast_rows<TYPE, 8>(rm, row_bytes, nb, a, xc, st); break;
+        case 4: e = run_fast_rows<TYPE, 4>(rm, row_bytes, nb, a, xc, st); break;
+        case 2: e = run_fast_rows<TYPE, 2>(rm, row_bytes, nb, a, xc, st); break;
+        default:  // a single remaining row: the m = 1 kernel (its own fused prologue with x)
+            e = x ? run_fast<TYPE>(rm, row_bytes, nb, xc, a, MAP_ONE, nullptr, 0.f, st)
+                  : run_fast_rows<TYPE, 1>(rm, row_bytes, nb, a, nullptr, st);
+            break;
         }
         if (e != hipSuccess) return e;
         m0 += real;
@@ -870,10 +885,12 @@ static hipError_t run_type(const RowMap &rm, int64_t k, int64_t row_bytes, const
         if (m == 1) {
             const hipError_t e = run_fast<TYPE>(rm, row_bytes, g.nb, x, act, map, alpha, eps, st);
             if (e != hipErrorNotSupported) return e;
-        } else if (m <= 8 && !x && !alpha && map == MAP_ONE && rm.end[0] == n && !tuning().gemv_rows_off) {
+        } else if (m <= 8 && !alpha && map == MAP_ONE && rm.end[0] == n && !tuning().gemv_rows_off) {
             // one launch per chunk of rows, each streaming the weight once: worth it
-            // while a chunk holds at least half the rows (one or two sweeps per row)
-            if (fast_rows_max<TYPE>(g.nb) >= 4) return run_fast_m<TYPE>(rm, row_bytes, g.nb, act, m, st);
+            // while a chunk holds at least half the rows (one or two sweeps per row);
+            // f32 x (gemv_fuses_quant) is quantised in each launch's prologue
+            if (fast_rows_max<TYPE>(g.nb) >= 4 && (!x || TYPE != TYPE_Q8_0))
+                return run_fast_m<TYPE>(rm, row_bytes, g.nb, act, x, m, st);
         }
     }
     if (alpha || map != MAP_ONE || rm.end[0] != n) return hipErrorNotSupported;  // m = 1 fast path only

@@ -299,6 +299,34 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
+@pytest.mark.parametrize("k", [4096, 8192])
+def test_multi_row_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
+    # At m = 2..4 (k = 4096; m = 2 at k = 8192) forward() quantises the rows in the
+    # multi-row GEMV's prologue; fed the standalone kernel's codes the same kernel
+    # must give the same bits (2- and 4-row launches, a padded one, special and tie
+    # rows); m = 5 and 8 take the standalone quantiser and must agree as well
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    rng = np.random.default_rng(150 + t + k)
+    n = 300
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+    pool = np.concatenate([_special_rows(k), _tie_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
+    pool[-1, rng.random(k) < 0.01] *= 20
+    for m in (2, 3, 5, 8):
+        x = pool[rng.choice(len(pool), m, replace=False)]
+        xd = to_dev(x, dev)
+        y_fused = qm.forward(xd)
+        y_act = qm.forward_quantized(QActivation.for_weight(qm, m).quantize(xd))
+        torch.cuda.synchronize()
+        assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32)), m
+    rows = [0, m - 1]
+    ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+    ok = np.isfinite(ref).all(axis=1)
+    if ok.any():
+        assert_rows_close(y_fused.cpu().numpy()[rows][ok], ref[ok])
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 def test_batched_prepass_quantisation_is_bit_exact(oracle, lbq, dev, t):
     # At m > 8 forward() quantises x inside the GEMM's operand pre-pass; fed the
     # standalone kernel's codes instead, the same GEMM must give the same bits
