@@ -1232,6 +1232,73 @@ constexpr int ks_fx_rows(int64_t m, int T) { return m <= 16 ? 16 : 32 * T; }
 constexpr bool ks_fx_shape(int S, int MR) { return (S == 1 || S == 2 || S == 4) && MR * S <= 64; }
 constexpr int KS_FX_MAX_TILES = 32;  // most column tiles (4096 columns) that quantise x in the kernel
 
+// Slices added in the kernel (k_gemm_ks): the partial stores before
+// this call are agent-scope (written through to memory, not held in this XCD's
+// L2), so once they have completed (vmcnt(0)) a counter increment publishes them
+// without an L2 write-back.  The workgroup that completes a column tile's count
+// adds the tile's slices in slice order -- the order k_split_sum uses, so the bits
+// are the same -- reading them with the same agent-scope (sc1) policy, writes y
+// and puts the counter back to zero for the next call.  The host uses this only
+// for N % 4 == 0 (16-byte partial rows) and at most KS_FUSED_SLICES slices.
+// Every thread of the workgroup (NT) calls it.
+template <int T, int NT>
+__device__ __forceinline__ void ks_slice_sum(const float *out, int64_t split_stride, int slices, int tn, int t,
+                                             int64_t M, int64_t N, const GemmGrid &g) {
+    __shared__ uint32_t last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0) last = __hip_atomic_fetch_add(g.cnt + tn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (last != (uint32_t)(slices - 1)) return;
+    // thread t: columns 4(t % 32) .. +3 of the tile, rows t / 32 + (NT / 32) j
+    constexpr int RS = NT / 32;                      // rows apart
+    constexpr int RQ = (32 * T + RS - 1) / RS;       // rows per thread, two at a time
+    const int64_t col = (int64_t)tn * KSN + 4 * (t & 31);
+    const int rows = (int)min<int64_t>(M, 32 * T);
+    if (col < N) {
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(out), (short)0, (int)(split_stride * slices * (int64_t)sizeof(float)), 0x00020000);
+#pragma unroll
+        for (int r0 = 0; r0 < RQ; r0 += 2) {
+            float4 sum[2];
+            for (int q0 = 0; q0 < slices; q0 += KS_SUM_Q) {
+                float4 v[2][KS_SUM_Q];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int r = (t >> 5) + RS * (r0 + j);
+#pragma unroll
+                    for (int q = 0; q < KS_SUM_Q; q++)
+                        if (r < rows && q0 + q < slices)
+                            v[j][q] = __builtin_bit_cast(
+                                float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            prs, (int)(((int64_t)(q0 + q) * split_stride + (int64_t)r * N + col) * 4),
+                                            0, KS_SC1));
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int q = 0; q < KS_SUM_Q; q++) {
+                        if (q0 + q >= slices) continue;
+                        if (q0 + q == 0) {
+                            sum[j] = v[j][q];
+                        } else {
+                            sum[j].x += v[j][q].x; sum[j].y += v[j][q].y;
+                            sum[j].z += v[j][q].z; sum[j].w += v[j][q].w;
+                        }
+                    }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int r = (t >> 5) + RS * (r0 + j);
+                if (r >= rows) continue;
+                float *yo = g.y + (int64_t)r * N + col;
+                yo[0] = sum[j].x; yo[1] = sum[j].y; yo[2] = sum[j].z; yo[3] = sum[j].w;
+            }
+        }
+    }
+    if (t == 0) __hip_atomic_store(g.cnt + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int TYPE, int S, int T, int FXR = 0>
 __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N, int64_t row_bytes,
                                                     const _Float16 *__restrict__ A, const int *__restrict__ erow,
@@ -1373,66 +1440,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
             }
         }
     if (!g.cnt) return;
-    // Split sum in the kernel: the partial stores above are agent-scope (written
-    // through to memory, not held in this XCD's L2), so once they have completed
-    // (vmcnt(0)) a counter increment publishes them without an L2 write-back.  The
-    // workgroup that completes a column tile's count adds the tile's slices in
-    // slice order -- the order k_split_sum uses, so the bits are the same -- reading
-    // them with the same agent-scope (sc1) policy, writes y and resets the counter
-    // for the next call.  The host uses this only for N % 4 == 0 (16-byte partial
-    // rows) and at most KS_FUSED_SLICES slices.
-    __shared__ uint32_t last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t == 0) last = __hip_atomic_fetch_add(g.cnt + tn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (last != (uint32_t)(slices - 1)) return;
-    // thread t: columns 4(t % 32) .. +3 of the tile, rows t / 32, t / 32 + 8, ...
-    const int64_t col = (int64_t)tn * KSN + 4 * (t & 31);
-    const int rows = (int)min<int64_t>(M, 32 * T);
-    if (col < N) {
-        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-            out, (short)0, (int)(split_stride * slices * (int64_t)sizeof(float)), 0x00020000);
-        constexpr int RQ = 32 * T / 8;  // rows per thread, two at a time, KS_SUM_Q slices per round
-#pragma unroll
-        for (int r0 = 0; r0 < RQ; r0 += 2) {
-            float4 sum[2];
-            for (int q0 = 0; q0 < slices; q0 += KS_SUM_Q) {
-                float4 v[2][KS_SUM_Q];
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const int r = (t >> 5) + 8 * (r0 + j);
-#pragma unroll
-                    for (int q = 0; q < KS_SUM_Q; q++)
-                        if (r < rows && q0 + q < slices)
-                            v[j][q] = __builtin_bit_cast(
-                                float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            prs, (int)(((int64_t)(q0 + q) * split_stride + (int64_t)r * N + col) * 4),
-                                            0, KS_SC1));
-                }
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int q = 0; q < KS_SUM_Q; q++) {
-                        if (q0 + q >= slices) continue;
-                        if (q0 + q == 0) {
-                            sum[j] = v[j][q];
-                        } else {
-                            sum[j].x += v[j][q].x; sum[j].y += v[j][q].y;
-                            sum[j].z += v[j][q].z; sum[j].w += v[j][q].w;
-                        }
-                    }
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int r = (t >> 5) + 8 * (r0 + j);
-                if (r >= rows) continue;
-                float *yo = g.y + (int64_t)r * N + col;
-                yo[0] = sum[j].x; yo[1] = sum[j].y; yo[2] = sum[j].z; yo[3] = sum[j].w;
-            }
-        }
-    }
-    if (t == 0) __hip_atomic_store(g.cnt + tn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ks_slice_sum<T, 256>(out, split_stride, slices, tn, t, M, N, g);
 }
 
 struct Plan {
