@@ -14,6 +14,8 @@
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 namespace lbq {
@@ -98,26 +100,34 @@ __device__ __forceinline__ void q8k_lane16(const float *v, int sub, uint32_t pac
     if (bmax != 0u) {  // uniform within the 16-lane block
         const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
         const float iscale = -128.f / mx;
-        int q[16];
+        // min(roundf(iscale * x), 127) as i8: for |t| <= 2^23, adding 0.5 - 2^-25
+        // with t's sign and truncating rounds exactly the halves (and everything
+        // above them) away from zero -- checked for every such float; fminf sends
+        // NaN to 127 as the reference's min does.  Separate roundings: no fma
+        // contraction.  With a finite iscale |iscale * x| <= 128 (1 + 2^-23), so no
+        // code falls below -128; only a subnormal block maximum (iscale infinite)
+        // needs the saturation of Rust's `as i8` (uniform within the block).
+        auto codes = [&](auto lower) {
+            int q[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
+            for (int i = 0; i < 16; i++) {
 #pragma clang fp contract(off)
-            // min(roundf(iscale * x), 127): for |t| <= 2^23, adding 0.5 - 2^-25
-            // with t's sign and truncating rounds exactly the halves (and
-            // everything above them) away from zero -- checked for every
-            // such float; fminf sends NaN to 127 as the reference's min
-            // does.  Separate roundings: no fma contraction.
-            const float tt = iscale * v[i];
-            const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
-            q[i] = max(-128, (int)r);
-            sum += q[i];
-        }
+                const float tt = iscale * v[i];
+                const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
+                q[i] = decltype(lower)::value ? max(-128, (int)r) : (int)r;
+            }
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
-            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
-            packed[w] = lo | (hi << 16);
-        }
+            for (int w = 0; w < 4; w++) {
+                const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
+                const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
+                packed[w] = lo | (hi << 16);
+            }
+        };
+        if (fabsf(iscale) <= 3.4028235e38f) codes(std::false_type{});
+        else codes(std::true_type{});
+        // the bsums entry: the 16 codes summed four at a time (sdot4 with ones)
+#pragma unroll
+        for (int w = 0; w < 4; w++) sum = __builtin_amdgcn_sdot4((int)packed[w], 0x01010101, sum, false);
         d = 1.f / iscale;
     }
     *sum_out = sum;
