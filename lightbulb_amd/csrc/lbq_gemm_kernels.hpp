@@ -1363,13 +1363,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
     // once (Q6_K: 1.4 us slower with the ring)
     constexpr int D = (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) && KS_RING < S ? KS_RING : S;
     typename B::Raw raw[D];
-    auto w_issue = [&](int b) {
-#pragma unroll
-        for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b % D], q);
-    };
 #pragma unroll
     for (int b = 0; b < D; b++) {
-        w_issue(b);
+#pragma unroll
+        for (int q = 0; q < B::NL; q++) B::load_part(wrow + (int64_t)min(b, cnt - 1) * B::BYTES, h, raw[b], q);
         __builtin_amdgcn_sched_barrier(0);
     }
     // The activation loads are the oldest in flight.  The compiler tracks loads
@@ -1390,7 +1387,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
         if (b < cnt) {
             typename B::Prep p;
             gb_prep<TYPE>(raw[b % D], h, wrow + (int64_t)b * B::BYTES, wsc, p);
-            if (b + D < S) w_issue(b + D);
+            if constexpr (D < S) {
+                if (b + D < S) {
+#pragma unroll
+                    for (int q = 0; q < B::NL; q++)
+                        B::load_part(wrow + (int64_t)min(b + D, cnt - 1) * B::BYTES, h, raw[b % D], q);
+                }
+            }
 #pragma unroll
             for (int s = 0; s < 16; s++) {
                 uint32_t bw[4];
