@@ -316,6 +316,37 @@ def test_ksliced_quantise_in_kernel(oracle, lbq, dev, t, monkeypatch):
         assert np.array_equal(yg.cpu().numpy().view(np.uint32), q.forward(xd).cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+def test_unaligned_output_on_every_small_m_path(oracle, lbq, dev, t):
+    # y only 4-byte aligned (the ABI's requirement) on the k-sliced paths that write
+    # y from the kernel: slices added in the kernel (14336 columns), quantisation in
+    # the kernel (4096), the separate slice sum, and the multi-row decode (m = 3)
+    rng = np.random.default_rng(680 + t)
+    from lightbulb_amd import _lib
+    L = _lib.lib()
+    for (m, n, k) in ((16, 14336, 4096), (16, 4096, 4096), (32, 1024, 4096), (3, 4096, 4096)):
+        w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y_ref = gpu_qmatmul(t, w_raw, n, k, x, dev)
+        ctx = ctypes.c_void_p()
+        _lib.check(L.lbq_init(dev.index or 0, ctypes.byref(ctx)))
+        try:
+            wd = to_dev(w_raw, dev)
+            h = ctypes.c_void_p()
+            _lib.check(L.lbq_weight_wrap_device(ctx, t, n, k, wd.data_ptr(), wd.numel(), ctypes.byref(h)))
+            xd = to_dev(x, dev)
+            base = torch.full((m * n + 1,), float("nan"), device=dev)
+            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            _lib.check(L.lbq_qmatmul_f32(ctx, h, xd.data_ptr(), m, base.data_ptr() + 4, st))
+            torch.cuda.synchronize()
+            L.lbq_weight_destroy(h)
+            y = base[1:].reshape(m, n).cpu().numpy()
+            assert np.isnan(base[0].item())
+            assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), (m, n, k)
+        finally:
+            L.lbq_ctx_destroy(ctx)
+
+
 def test_tuning_read_once_per_context(oracle, lbq, dev, monkeypatch):
     # an override set after a context exists does not change that context's plan
     from lightbulb_amd.quantized import QMatMul, QTensor
