@@ -179,6 +179,20 @@ __device__ __forceinline__ uint32_t gld4(gbytes_c p) {
     return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t *>(p);
 }
 
+// 16 / 4 bytes at a 2-byte aligned address as single unaligned global loads
+// (dwordx4 / dword at the field's own address: the hardware's unaligned access
+// mode, which the compiler itself relies on for under-aligned types on this
+// target); they read exactly the field's bytes.
+typedef uint32_t u32x4v2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32a2 __attribute__((aligned(2)));
+__device__ __forceinline__ void ld16_u2(const uint8_t *p, uint32_t out[4]) {
+    const u32x4v2 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4v2 *>(reinterpret_cast<uintptr_t>(p));
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+__device__ __forceinline__ uint32_t ld4_u2(const uint8_t *p) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) u32a2 *>(reinterpret_cast<uintptr_t>(p));
+}
+
 // 16 bytes starting at a 2-byte aligned address p.  Reads only aligned dwords that
 // hold at least one byte of [p, p+16), so it never touches a dword outside the
 // caller's buffer.

@@ -269,11 +269,11 @@ struct Fast<TYPE_Q6_K, 4> {
     __device__ static Raw load(const uint8_t *blk, int p) {
         const int n = p >> 1, h = p & 1;
         Raw r;
-        ld16_a2(blk + 64 * n + 16 * h, r.qa);
-        ld16_a2(blk + 64 * n + 32 + 16 * h, r.qb);
-        ld16_a2(blk + 128 + 32 * n + 16 * h, r.qh);
-        r.s0 = ld4_a2(blk + 192 + 8 * n);
-        r.s1 = ld4_a2(blk + 196 + 8 * n);
+        ld16_u2(blk + 64 * n + 16 * h, r.qa);
+        ld16_u2(blk + 64 * n + 32 + 16 * h, r.qb);
+        ld16_u2(blk + 128 + 32 * n + 16 * h, r.qh);
+        r.s0 = ld4_u2(blk + 192 + 8 * n);
+        r.s1 = ld4_u2(blk + 196 + 8 * n);
         r.dbits = ld2_a2(blk + 208);
         return r;
     }
