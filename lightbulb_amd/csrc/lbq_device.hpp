@@ -193,31 +193,6 @@ __device__ __forceinline__ uint32_t ld4_u2(const uint8_t *p) {
     return *reinterpret_cast<const __attribute__((address_space(1))) u32a2 *>(reinterpret_cast<uintptr_t>(p));
 }
 
-// 16 bytes starting at a 2-byte aligned address p.  Reads only aligned dwords that
-// hold at least one byte of [p, p+16), so it never touches a dword outside the
-// caller's buffer.
-__device__ __forceinline__ void ld16_a2(const uint8_t *p, uint32_t out[4]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t mis = (uint32_t)(a & 3u);
-    const gbytes_c base = align4_global(a);
-    const u32x4a4 v = gld16(base);
-    const uint32_t t = gld4(base + (mis ? 16 : 12));
-    out[0] = __builtin_amdgcn_alignbyte(v.y, v.x, mis);
-    out[1] = __builtin_amdgcn_alignbyte(v.z, v.y, mis);
-    out[2] = __builtin_amdgcn_alignbyte(v.w, v.z, mis);
-    out[3] = __builtin_amdgcn_alignbyte(t, v.w, mis);
-}
-
-// 4 bytes at a 2-byte aligned address.
-__device__ __forceinline__ uint32_t ld4_a2(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t mis = (uint32_t)(a & 3u);
-    const gbytes_c base = align4_global(a);
-    const uint32_t lo = gld4(base);
-    const uint32_t hi = gld4(base + (mis ? 4 : 0));
-    return __builtin_amdgcn_alignbyte(hi, lo, mis);
-}
-
 // 2 bytes (f16 bits) at a 2-byte aligned address.
 __device__ __forceinline__ uint32_t ld2_a2(const uint8_t *p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);

@@ -149,11 +149,11 @@ struct Dec<TYPE_Q6_K> {
     __device__ static Raw load(const uint8_t *blk, int p) {
         const int n = p >> 1, h = p & 1;
         Raw r;
-        ld16_a2(blk + 64 * n + 16 * h, r.qa);
-        ld16_a2(blk + 64 * n + 32 + 16 * h, r.qb);
-        ld16_a2(blk + 128 + 32 * n + 16 * h, r.qh);
-        r.s0 = ld4_a2(blk + 192 + 8 * n);
-        r.s1 = ld4_a2(blk + 196 + 8 * n);
+        ld16_u2(blk + 64 * n + 16 * h, r.qa);
+        ld16_u2(blk + 64 * n + 32 + 16 * h, r.qb);
+        ld16_u2(blk + 128 + 32 * n + 16 * h, r.qh);
+        r.s0 = ld4_u2(blk + 192 + 8 * n);
+        r.s1 = ld4_u2(blk + 196 + 8 * n);
         r.dbits = ld2_a2(blk + 208);
         return r;
     }
@@ -307,9 +307,9 @@ struct Dec<TYPE_Q3_K> {
     struct Raw { uint32_t hm[4], qs[4], tl[4]; };
     __device__ static Raw load(const uint8_t *blk, int p) {
         Raw r;
-        ld16_a2(blk + 16 * (p & 1), r.hm);  // hmask[16t .. 16t+16)
-        ld16_a2(blk + 32 + 16 * p, r.qs);
-        ld16_a2(blk + 94, r.tl);
+        ld16_u2(blk + 16 * (p & 1), r.hm);  // hmask[16t .. 16t+16)
+        ld16_u2(blk + 32 + 16 * p, r.qs);
+        ld16_u2(blk + 94, r.tl);
         return r;
     }
     template <int M>
