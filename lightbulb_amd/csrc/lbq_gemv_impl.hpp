@@ -19,6 +19,9 @@
 #pragma once
 #include <stdio.h>
 #include <stdlib.h>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "lbq_device.hpp"
 #include "lbq_gemv_fast.hpp"
@@ -736,12 +739,37 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
         fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS>,
               k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_SEGMENTS, false, W8>, nullptr, 0.f);
     } else if (x) {
+        // Q6_K keeps one row group in flight (two-buffer ring: its pieces take 15
+        // registers each); a long per-wave stream (the 128256-row head: 62 groups per
+        // wave) takes three in flight instead (head 97.6 -> 92.0 us).  Short streams
+        // lose with the deeper ring (14336 rows: 13.7 -> 14.8 us; 1024: 6.7 -> 8.8).
+        if constexpr (TYPE == TYPE_Q6_K && IT <= 2)
+            if (ng >= 32 * waves) {
+                fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, 4, 4>,
+                      k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, W8, 4>, nullptr, 0.f);
+                return hipGetLastError();
+            }
         fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE>, k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, W8>,
               nullptr, 0.f);
     } else {
         k_gemv1<TYPE, PPB, RPW, IT, 1, false, MAP_ONE><<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     }
     return hipGetLastError();
+}
+
+// Lifts a kernel's dynamic LDS limit to the CU's 160 KB, once per (device, kernel).
+static hipError_t allow_big_lds(const void *kern) {
+    static std::mutex mu;
+    static std::vector<std::pair<int, const void *>> done;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto &d : done)
+        if (d.first == dev && d.second == kern) return hipSuccess;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+    if (e == hipSuccess) done.emplace_back(dev, kern);
+    return e;
 }
 
 // MR pre-quantised activation rows (m = MR) against one weight: the weight is
@@ -757,18 +785,26 @@ static hipError_t launch_fast_rows(const RowMap &rm, int64_t row_bytes, int nb, 
     // x: f32 rows quantised in the prologue (Q8_K types), else pre-quantised rows
     constexpr bool FX = TYPE != TYPE_Q8_0 && MR > 1 && MR * IT <= 8;
     if (x && !FX) return hipErrorNotSupported;
-    auto kern = x ? k_gemv1<TYPE, PPB, RPW, IT, MR, FX, MAP_ONE> : k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE>;
-    if (lds > 65536) {
-        static const hipError_t attr =
-            hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
-        if (attr != hipSuccess) return attr;
-    }
     // two workgroups per CU while both fit the CU's 160 KB of LDS
     int wpc = lds <= 80 * 1024 ? 8 : 4;
     if (tuning().gemv1_wpc > 0) wpc = tuning().gemv1_wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
     const unsigned grid = (unsigned)((waves + 3) / 4);
+    // Q6_K keeps one row group in flight; a long per-wave stream with up to four
+    // rows takes two (three-buffer ring): head 128256 x 4096 m = 2 / 4 98 -> 94 /
+    // 105 -> 99.5 us.  At eight rows (registers) and on short streams (14336 rows:
+    // 16.2 -> 16.7 us) the two-buffer ring stays ahead.
+    constexpr bool R3 = TYPE == TYPE_Q6_K && MR <= 4;
+    const bool ring3 = R3 && ng >= 32 * waves;
+    auto kern = x ? (ring3 ? k_gemv1<TYPE, PPB, RPW, IT, MR, FX, MAP_ONE, false, 4, R3 ? 3 : 0>
+                           : k_gemv1<TYPE, PPB, RPW, IT, MR, FX, MAP_ONE>)
+                  : (ring3 ? k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE, false, 4, R3 ? 3 : 0>
+                           : k_gemv1<TYPE, PPB, RPW, IT, MR, false, MAP_ONE>);
+    if (lds > 65536) {
+        const hipError_t attr = allow_big_lds(reinterpret_cast<const void *>(kern));
+        if (attr != hipSuccess) return attr;
+    }
     kern<<<grid, 256, lds, st>>>(rm, row_bytes, nb, x, act, nullptr, 0.f);
     return hipGetLastError();
 }

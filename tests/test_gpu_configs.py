@@ -59,6 +59,16 @@ def test_config3_q6k_head_and_q5k(oracle, lbq, dev, b):
     check(oracle, qm, raw, Q5_K, 14336, 4096, x)
 
 
+@pytest.mark.parametrize("b", [2, 3])
+def test_config3_q6k_head_few_rows(oracle, lbq, dev, b):
+    # the head's long per-wave stream takes the deeper weight ring at m = 1..4
+    rng = np.random.default_rng(30 + b)
+    x = rng.standard_normal((b, 4096)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    qm, raw = quantised(Q6_K, 128256, 4096, dev, 0x1B2)
+    check(oracle, qm, raw, Q6_K, 128256, 4096, x)
+
+
 @pytest.mark.parametrize("m", [16, 64, 512, 2048])
 def test_config4_q4k_prefill(oracle, lbq, dev, m):
     rng = np.random.default_rng(4 + m)
