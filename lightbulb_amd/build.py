@@ -30,9 +30,12 @@ HIP_FLAGS = [
 ]
 # Sources whose float arithmetic must be rounded op by op (bit-exact restatements).
 NO_CONTRACT = {"lbq_wquant.hip"}
+# Matrix-core results consumed by VALU right away: keep them in VGPRs (no AGPR
+# copies, fewer registers, so two waves per SIMD).
+EXTRA_FLAGS = {"lbq_gemv_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 SOURCES = ["lbq_act.hip", "lbq_gemv.hip", "lbq_gemv_q4k.hip", "lbq_gemv_q5k.hip", "lbq_gemv_q6k.hip",
-           "lbq_gemv_q8_0.hip", "lbq_gemv_legacy.hip", "lbq_gemv_k23.hip", "lbq_gemm.hip", "lbq_gemm_q4k.hip", "lbq_gemm_q5k.hip",
+           "lbq_gemv_q8_0.hip", "lbq_gemv_legacy.hip", "lbq_gemv_k23.hip", "lbq_gemv_mx.hip", "lbq_gemm.hip", "lbq_gemm_q4k.hip", "lbq_gemm_q5k.hip",
            "lbq_gemm_q6k.hip", "lbq_gemm_q8_0.hip", "lbq_gemm_q4_0.hip", "lbq_gemm_q5_0.hip",
            "lbq_gemm_k23.hip", "lbq_dense.hip", "lbq_wquant.hip",
            "lbq_api.cpp", "lbq_gguf.cpp"]
@@ -51,6 +54,7 @@ def _compile(src: str) -> Path:
     cmd = [hipcc, *HIP_FLAGS]
     if src in NO_CONTRACT:
         cmd.append("-ffp-contract=off")
+    cmd += EXTRA_FLAGS.get(src, [])
     if src.endswith(".cpp"):
         cmd += ["-x", "hip"]
     cmd += ["-c", str(CSRC / src), "-o", str(out)]

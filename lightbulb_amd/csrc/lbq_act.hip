@@ -17,32 +17,40 @@
 namespace lbq {
 
 // ---------------------------------------------------------------------------
-// Q8_K: one 64-lane wave per 256-value block, 4 values per lane.
-// candle: the signed value `max` of largest |x| (first on ties; NaN is never
-// selected because `amax < NaN` is false) gives iscale = -128/max;
-// q = min(127, round(iscale*x)) as i8; d = 1/iscale; bsums over 16 codes.
+// Q8_K: sixteen lanes per 256-value block (a DPP row), 16 values per lane, four
+// blocks per wave (q8k_lane16: the selection and arithmetic every Q8_K quantiser
+// here shares).  candle: the signed value `max` of largest |x| (first on ties;
+// NaN is never selected because `amax < NaN` is false) gives iscale = -128/max;
+// q = min(127, round(iscale*x)) as i8; d = 1/iscale; bsums over 16 codes -- a
+// lane's own 16 codes.
 // ---------------------------------------------------------------------------
 template <bool GGUF_OUT, bool VEC_IN>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int64_t nblocks, int8_t *__restrict__ xq,
                                                    float *__restrict__ xd, int16_t *__restrict__ xbs,
                                                    uint8_t *__restrict__ gguf) {
-    const int lane = threadIdx.x & 63;
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= nblocks) return;  // whole wave exits together
-    float v[4];
-    load4f(x + blk * QK_K + lane * 4, VEC_IN, v);
+    const int sub = threadIdx.x & 15;
+    // the 16 lanes of a row share the block (wave-uniform exits only at the end)
+    const int64_t blk0 = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool ok = blk0 < nblocks;
+    const int64_t blk = ok ? blk0 : nblocks - 1;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) load4f(x + blk * QK_K + sub * 16 + 4 * i, VEC_IN, &v[4 * i]);
+    uint32_t packed[4];
     int s;
     float d;
-    const uint32_t packed = q8k_block_wave(v, lane, &s, &d);
+    q8k_lane16(v, sub, packed, &s, &d);
+    if (!ok) return;
     if (GGUF_OUT) {
-        uint8_t *b = gguf + blk * 292;
-        *reinterpret_cast<uint32_t *>(b + 4 + lane * 4) = packed;
-        if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(b + 260 + 2 * (lane >> 2)) = (int16_t)s;
-        if (lane == 0) *reinterpret_cast<float *>(b) = d;
+        uint8_t *b = gguf + blk * 292;  // 4-byte aligned: dword stores
+#pragma unroll
+        for (int w = 0; w < 4; w++) *reinterpret_cast<uint32_t *>(b + 4 + 16 * sub + 4 * w) = packed[w];
+        *reinterpret_cast<int16_t *>(b + 260 + 2 * sub) = (int16_t)s;
+        if (sub == 0) *reinterpret_cast<float *>(b) = d;
     } else {
-        *reinterpret_cast<uint32_t *>(xq + blk * QK_K + lane * 4) = packed;
-        if ((lane & 3) == 0) xbs[blk * 16 + (lane >> 2)] = (int16_t)s;
-        if (lane == 0) xd[blk] = d;
+        *reinterpret_cast<uint4 *>(xq + blk * QK_K + 16 * sub) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        xbs[blk * 16 + sub] = (int16_t)s;
+        if (sub == 0) xd[blk] = d;
     }
 }
 
@@ -272,7 +280,7 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);
-        const dim3 grid((unsigned)((nb + 3) / 4));
+        const dim3 grid((unsigned)((nb + 15) / 16));
         if (gguf) {
             if (vec) k_quant_q8k<true, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
             else k_quant_q8k<true, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);

@@ -91,6 +91,7 @@ Tuning tuning_from_env() {
     }
     t.gemv1_wpc = std::max(0, env_int("LBQ_GEMV1_WPC"));
     t.gemv1_wpg = std::max(0, env_int("LBQ_GEMV1_WPG"));
+    t.gemv_mx_off = getenv("LBQ_GEMV_MX_OFF") != nullptr;
     if (const char *e = getenv("LBQ_GEMV")) {
         int v[4] = {0, 0, 0, 0};
         if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)
@@ -257,10 +258,16 @@ struct Scratch {
     }
 };
 
-// The dot half of QMatMul::forward: decode GEMV for m <= 8, MFMA GEMM above.
+// Batch decode on the matrix cores for this weight and row count
+static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 8 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
+
+// The dot half of QMatMul::forward: decode GEMV for m <= 8 (the i8 matrix-core
+// kernel at m = 5..8 where it serves), MFMA GEMM above.
 int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
     hipError_t e;
-    if (m <= 8) {
+    if (uses_mx(w, m)) {
+        e = lbq::launch_gemv_mx(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
+    } else if (m <= 8) {
         e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
     } else {
         const size_t wsb = lbq::gemm_workspace_bytes(w->type, w->n, w->k, m);
@@ -288,7 +295,7 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
         return e == hipSuccess ? LBQ_OK : hip_fail(e, "dense matmul launch");
     }
     const ActLayout L = act_layout(act_type, m, w->k);
-    if (m <= 8 && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
+    if (m <= 8 && !uses_mx(w, m) && lbq::gemv_fuses_quant(w->type, w->n, w->k, (int)m, d_x)) {
         // decode: the GEMV quantises x in its own prologue -- one launch, no scratch
         const lbq::ActView av{nullptr, nullptr, nullptr, w->k, L.nb};
         hipError_t e = lbq::launch_gemv_x(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, d_x, (int)m, d_y, st);

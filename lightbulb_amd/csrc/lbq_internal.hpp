@@ -60,6 +60,7 @@ struct Tuning {
     bool gemv1_nofuse = false, gemv_rows_off = false;
     int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
     int gemv1_wpc = 0, gemv1_wpg = 0;
+    bool gemv_mx_off = false;  // batch decode never on the matrix cores
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
 };
 Tuning tuning_from_env();
@@ -108,6 +109,13 @@ hipError_t launch_embedding(int type, const uint8_t *w, int64_t n, int64_t k, in
 // Requires m <= 8 (decode GEMV) -- the kernels keep one accumulator per row of x.
 hipError_t launch_gemv(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act,
                        int m, float *y, hipStream_t st);
+
+// Batch decode on the matrix cores (i8 MFMA, exact integer sums) for pre-quantised
+// Q8_K rows: Q4_K / Q5_K, k % 256 == 0, k <= 16384, 5 <= m <= 8, where it is the
+// faster kernel (n >= 4096, or k > 8192).
+bool gemv_mx_serves(int type, int64_t n, int64_t k, int m);
+hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
+                          float *y, hipStream_t st);
 
 // True when the decode GEMV quantises x itself (m = 1, k within the fast path,
 // x 16-byte aligned).

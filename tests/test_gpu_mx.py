@@ -1,0 +1,82 @@
+"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K, m = 5..8, n >= 4096
+or k > 8192) against the oracle.
+
+The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
+the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
+decode bound (f32 summation order only).  Shapes cover uneven splits of a row's
+blocks over the four waves (5 blocks), waves with no block (2 blocks), the
+largest k (64 blocks), a row count that is not a multiple of 32, NaN activations
+and NaN / Inf weight scales.  The same calls with the kernel switched off
+(LBQ_GEMV_MX_OFF, the multi-row or general decode kernel) must differ in some
+bits, which shows the matrix-core kernel is the one that ran.
+"""
+import numpy as np
+import pytest
+
+import blockpack as bp
+from test_gpu_nonfinite import _nan_rows, _poison
+from test_gpu_parity import Q4_K, Q5_K, assert_rows_close, gpu_qmatmul
+from test_gpu_q8_0_dense import forward_with_env
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (64, 14336), (96, 16384)]
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [5, 8])
+def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
+    rng = np.random.default_rng(n * 7 + k + 31 * m + t)
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx t={t} n={n} k={k} m={m}", flush=True)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
+    off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_OFF": "1"}, t, w_raw, n, k, x, dev)
+    assert_rows_close(off, ref, 1e-4)
+    assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m", [6, 7])
+def test_mx_row_counts(oracle, lbq, dev, t, m):
+    rng = np.random.default_rng(900 + 10 * m + t)
+    n, k = 4096, 4096
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+def test_mx_nan_activations(oracle, lbq, dev, t):
+    rng = np.random.default_rng(910 + t)
+    n, k, m = 96, 14336, 8
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = _nan_rows(rng, m, k)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert np.all(np.isfinite(ref))
+    assert_rows_close(y, ref, 1e-4)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+def test_mx_nonfinite_scales(oracle, lbq, dev, t):
+    rng = np.random.default_rng(920 + t)
+    n, k, m = 200, 14336, 8
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    bad, nan_rows = _poison(w_raw, t, n, k // 256, rng)
+    good = np.setdiff1d(np.arange(n), bad)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert not np.isfinite(ref[:, bad]).any() and np.isfinite(ref[:, good]).all()
+    assert np.array_equal(np.isfinite(y), np.isfinite(ref))
+    assert np.isnan(y[:, nan_rows]).all() and np.isnan(ref[:, nan_rows]).all()
+    assert_rows_close(y[:, good], ref[:, good], 1e-4)
