@@ -1,4 +1,5 @@
-// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 5 <= m <= 8
+// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 2 <= m <= 8
+// (the shapes gemv_mx_serves admits),
 // Q8_K activation rows against Q4_K / Q5_K weights, in the reference's integer
 // arithmetic (candle-core 0.10.2 k_quants.rs, BlockQ4K / BlockQ5K vec_dot with
 // BlockQ8K: integer sub-block sums scaled by the 6-bit scales, mins against the
@@ -51,7 +52,6 @@ template <int TYPE>
 struct MxW {
     uint4 hd, qh, qs[4];  // block header (d, dmin, scales), the lane half's qh, its four 16-byte qs quarters
 };
-
 template <int TYPE>
 __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &r) {
     constexpr int QS = TYPE == TYPE_Q4_K ? 16 : 48;
@@ -220,17 +220,22 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
 }
 
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
-    // Measured against the multi-row decode kernel (one launch of eight rows, x
-    // quantised by the same separate pass): Q5_K 14336 x 4096 m = 8 22.8 -> 18.2
-    // us, Q4_K 14336 x 4096 21.4 -> 16.8, 4096 x 4096 13.4 -> 12.5, 4096 x 14336
-    // (which the multi-row kernel cannot hold: general GEMV) 52.7 -> 21.9; with
-    // 1024 rows (32 workgroups) 10.8 -> 12.0, so fewer than 4096 rows keep the
-    // decode kernel where it serves.  At m <= 4 the decode kernel quantises x in
-    // its own prologue and stays ahead (m = 2: 12.8 vs 17.9 us).
+    // Measured against the decode kernels (x quantised by the same separate pass
+    // unless noted): Q5_K 14336 x 4096 m = 8 22.8 -> 18.2 us, Q4_K 14336 x 4096
+    // 21.4 -> 16.8, 4096 x 4096 13.4 -> 12.5; with 1024 rows (32 workgroups)
+    // 10.8 -> 12.0, so fewer than 4096 rows keep the multi-row kernel.  At m <= 4
+    // that kernel quantises x in its own prologue and stays ahead (m = 2: 12.8 vs
+    // 17.9 us) -- except at k > 8192, where it cannot hold the activation rows and
+    // the general GEMV runs: Q4_K 4096 x 14336 m = 2 / 3 / 4 / 8 22.2 / 26.3 /
+    // 30.2 / 52.8 -> 21.0 / 20.9 / 20.8 / 21.0 us.  A Q6_K version (sixteen
+    // 16-value groups per block, one v_mfma_i32_32x32x16_i8 each, the -32 offset
+    // through the bsums) was correct but slower (14336 x 4096 m = 8 24.4 -> 30.1
+    // us: fourteen 8-byte weight loads per block and lane) and was not kept.
     if (tuning().gemv_mx_off) return false;
     if (type != TYPE_Q4_K && type != TYPE_Q5_K) return false;
-    if (k % 256 || k / 256 > 64 || m < 5 || m > 8 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
-    return n >= 4096 || k / 256 > 32;
+    if (k % 256 || k / 256 > 64 || m < 2 || m > 8 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    if (k / 256 > 32) return true;  // the multi-row decode kernel cannot hold these rows
+    return m >= 5 && n >= 4096;
 }
 
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,

@@ -1,5 +1,5 @@
-"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K, m = 5..8, n >= 4096
-or k > 8192) against the oracle.
+"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..8 with
+n >= 4096, and m = 2..8 at k > 8192) against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -43,10 +43,10 @@ def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
-@pytest.mark.parametrize("m", [6, 7])
-def test_mx_row_counts(oracle, lbq, dev, t, m):
-    rng = np.random.default_rng(900 + 10 * m + t)
-    n, k = 4096, 4096
+@pytest.mark.parametrize("m,k", [(6, 4096), (7, 4096), (2, 14336), (3, 14336), (4, 9216)])
+def test_mx_row_counts(oracle, lbq, dev, t, m, k):
+    rng = np.random.default_rng(900 + 10 * m + t + k)
+    n = 4096 if k == 4096 else 160
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = rng.standard_normal((m, k)).astype(np.float32)
     y = gpu_qmatmul(t, w_raw, n, k, x, dev)
