@@ -43,10 +43,12 @@ def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
-@pytest.mark.parametrize("m,k", [(6, 4096), (7, 4096), (2, 14336), (3, 14336), (4, 9216)])
-def test_mx_row_counts(oracle, lbq, dev, t, m, k):
-    rng = np.random.default_rng(900 + 10 * m + t + k)
-    n = 4096 if k == 4096 else 160
+@pytest.mark.parametrize("m,k,n", [(6, 4096, 4096), (7, 4096, 4096), (2, 14336, 160), (3, 14336, 33), (4, 9216, 160),
+                                   (2, 8448, 1), (5, 8448, 70)])
+def test_mx_row_counts(oracle, lbq, dev, t, m, k, n):
+    # k = 8448: 33 blocks, the smallest k the kernel takes at m <= 4; n = 1 and 33:
+    # a workgroup of one row, a last workgroup of one row
+    rng = np.random.default_rng(900 + 10 * m + t + k + n)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = rng.standard_normal((m, k)).astype(np.float32)
     y = gpu_qmatmul(t, w_raw, n, k, x, dev)
