@@ -6,9 +6,10 @@
 // whatever type output.weight or a projection has, custom_transformer.rs:360-363,
 // custom_attention.rs:195-206, mlp_wrapper.rs:127-135).  Here the weight stays
 // in its file layout ([n][k], f16 or f32) and is widened on the fly:
-//   m <= 8  k_dense_gemv: one wave per weight row at a time, 16-byte weight
-//           loads, f32 FMA against up to 8 activation rows, DPP row sums --
-//           HBM-bound like the quantised decode GEMV;
+//   m <= 8  k_dense_gemv: waves stream weight rows in 4096-column units with
+//           the next unit's 16-byte loads in flight, x staged in LDS, f32 FMA
+//           against up to 8 activation rows, DPP row sums -- HBM-bound like the
+//           quantised decode GEMV;
 //   m > 8   k_dense_gemm: 64 x 128 output tiles on v_mfma_f32_32x32x2_f32
 //           (f32 operands, f32 accumulation), operands staged through LDS.
 // Both compute in f32 throughout; only the summation order differs from
@@ -42,10 +43,12 @@ __device__ __forceinline__ void load_w8(const uint8_t *row, int64_t c, float w[8
 }
 
 // ---------------------------------------------------------------------------
-// m <= 8.  Waves take rows gw, gw + nw, ...; a lane covers 8 consecutive
-// columns per 512-column step (k % 8 == 0; a partial last step is masked), UN
-// steps in flight.  x rows are read through the caches (every wave reads all
-// of them).
+// m <= 8.  Waves take rows gw, gw + nw, ...; a row is cut into units of 512 UN
+// columns (a lane covers 8 consecutive columns per 512-column step; k % 8 == 0,
+// a partial last step is masked), and each wave keeps the next unit's weight
+// loads in flight while it computes the current one.  With XL the x rows are
+// staged in LDS once per workgroup (m k f32 <= 64 KB), else every wave reads
+// them through the caches.
 // ---------------------------------------------------------------------------
 // 8 consecutive values of x at c (vec: 16-byte aligned, else four-byte loads)
 __device__ __forceinline__ void load_x8(const float *p, bool vec, float v[8]) {
@@ -53,55 +56,110 @@ __device__ __forceinline__ void load_x8(const float *p, bool vec, float v[8]) {
     load4f(p + 4, vec, v + 4);
 }
 
-template <bool F16, int MR>
+constexpr int DENSE_XL_BYTES = 65536;  // x staged in LDS up to this size
+
+template <bool F16>
+struct DenseUnit {
+    static constexpr int UN = 8;  // 4096 f16 / 4096 f32 weights of a row per unit and wave
+    uint4 w[F16 ? UN : 2 * UN];
+};
+
+template <bool F16, int MR, bool XL>
 __global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ W, int64_t N, int64_t K,
                                                     const float *__restrict__ x, int m, float *__restrict__ y) {
+    extern __shared__ __align__(16) float xs[];  // XL: x [m][K]
     const bool xv = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;  // K % 8 == 0: every row likewise
-    constexpr int UN = 8;  // 4096 f16 / 2048 f32 weights of the row in flight per wave
-    constexpr int64_t WB = F16 ? 2 : 4;
-    const int lane = threadIdx.x & 63;
-    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), nw = (int64_t)gridDim.x * 4;
-    for (int64_t r = gw; r < N; r += nw) {
-        const uint8_t *row = W + r * K * WB;
-        float acc[MR];
+    constexpr int UN = DenseUnit<F16>::UN;
+    constexpr int64_t WB = F16 ? 2 : 4, CH = 512 * UN;
+    const int t = threadIdx.x, lane = t & 63;
+    if constexpr (XL) {
+        const int64_t total = (int64_t)m * K;
+        if (xv) {
+            for (int64_t i = 4 * t; i < total; i += 1024)
+                *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(x + i);
+        } else {
+            for (int64_t i = t; i < total; i += 256) xs[i] = x[i];
+        }
+        __syncthreads();
+    }
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (t >> 6), nw = (int64_t)gridDim.x * 4;
+    const int64_t nch = (K + CH - 1) / CH;
+    const int64_t rows = gw < N ? (N - gw + nw - 1) / nw : 0, units = rows * nch;
+    auto load = [&](int64_t u, DenseUnit<F16> &d) {
+        const uint8_t *row = W + (gw + (u / nch) * nw) * K * WB;
+        const int64_t c0 = (u % nch) * CH;
 #pragma unroll
-        for (int i = 0; i < MR; i++) acc[i] = 0.f;
-        for (int64_t c0 = 0; c0 < K; c0 += 512 * UN) {
-            float w[UN][8];
+        for (int v = 0; v < UN; v++) {
+            const int64_t c = c0 + 512 * v + 8 * lane;
+            if constexpr (F16) {
+                d.w[v] = c < K ? *reinterpret_cast<const uint4 *>(row + 2 * c) : make_uint4(0, 0, 0, 0);
+            } else {
+                d.w[2 * v] = c < K ? *reinterpret_cast<const uint4 *>(row + 4 * c) : make_uint4(0, 0, 0, 0);
+                d.w[2 * v + 1] = c < K ? *reinterpret_cast<const uint4 *>(row + 4 * c + 16) : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    float acc[MR];
 #pragma unroll
-            for (int u = 0; u < UN; u++) {
-                const int64_t c = c0 + 512 * u + 8 * lane;
-                if (c < K) load_w8<F16>(row, c, w[u]);
-                else {
+    for (int i = 0; i < MR; i++) acc[i] = 0.f;
+    auto compute = [&](int64_t u, const DenseUnit<F16> &d) {
+        const int64_t c0 = (u % nch) * CH;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) w[u][e] = 0.f;
+        for (int v = 0; v < UN; v++) {
+            const int64_t c = c0 + 512 * v + 8 * lane;
+            if (c >= K) continue;
+            float w[8];
+            if constexpr (F16) {
+                const uint32_t dw[4] = {d.w[v].x, d.w[v].y, d.w[v].z, d.w[v].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    w[2 * e] = h2f(dw[e] & 0xffffu);
+                    w[2 * e + 1] = h2f(dw[e] >> 16);
                 }
+            } else {
+                const uint4 a = d.w[2 * v], b = d.w[2 * v + 1];
+                w[0] = __uint_as_float(a.x); w[1] = __uint_as_float(a.y); w[2] = __uint_as_float(a.z); w[3] = __uint_as_float(a.w);
+                w[4] = __uint_as_float(b.x); w[5] = __uint_as_float(b.y); w[6] = __uint_as_float(b.z); w[7] = __uint_as_float(b.w);
             }
 #pragma unroll
-            for (int u = 0; u < UN; u++) {
-                const int64_t c = c0 + 512 * u + 8 * lane;
-                if (c < K) {
-#pragma unroll
-                    for (int i = 0; i < MR; i++) {
-                        if (i < m) {
-                            float xv8[8];
-                            load_x8(x + (int64_t)i * K + c, xv, xv8);
-#pragma unroll
-                            for (int e = 0; e < 8; e++) acc[i] = fmaf(w[u][e], xv8[e], acc[i]);
-                        }
+            for (int i = 0; i < MR; i++) {
+                if (i < m) {
+                    float xv8[8];
+                    if constexpr (XL) {
+                        const float4 p = *reinterpret_cast<const float4 *>(xs + (int64_t)i * K + c);
+                        const float4 q = *reinterpret_cast<const float4 *>(xs + (int64_t)i * K + c + 4);
+                        xv8[0] = p.x; xv8[1] = p.y; xv8[2] = p.z; xv8[3] = p.w;
+                        xv8[4] = q.x; xv8[5] = q.y; xv8[6] = q.z; xv8[7] = q.w;
+                    } else {
+                        load_x8(x + (int64_t)i * K + c, xv, xv8);
                     }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[i] = fmaf(w[e], xv8[e], acc[i]);
                 }
             }
         }
+        if (u % nch == nch - 1) {  // the row's last unit: its sums
+            const int64_t r = gw + (u / nch) * nw;
 #pragma unroll
-        for (int i = 0; i < MR; i++) {
-            if (i < m) {
-                const float s = row_sum_f32(acc[i]);
-                const float t = __int_as_float(rl(__float_as_uint(s), 0)) + __int_as_float(rl(__float_as_uint(s), 16)) +
-                                __int_as_float(rl(__float_as_uint(s), 32)) + __int_as_float(rl(__float_as_uint(s), 48));
-                if (lane == 0) y[(int64_t)i * N + r] = t;
+            for (int i = 0; i < MR; i++) {
+                if (i < m) {
+                    const float s = row_sum_f32(acc[i]);
+                    const float tt = __int_as_float(rl(__float_as_uint(s), 0)) + __int_as_float(rl(__float_as_uint(s), 16)) +
+                                     __int_as_float(rl(__float_as_uint(s), 32)) + __int_as_float(rl(__float_as_uint(s), 48));
+                    if (lane == 0) y[(int64_t)i * N + r] = tt;
+                }
+                acc[i] = 0.f;
             }
         }
+    };
+    DenseUnit<F16> ring[2];
+    if (units > 0) load(0, ring[0]);
+    for (int64_t u = 0; u < units; u += 2) {
+        if (u + 1 < units) load(u + 1, ring[1]);
+        compute(u, ring[0]);
+        if (u + 1 >= units) break;
+        if (u + 2 < units) load(u + 2, ring[0]);
+        compute(u + 1, ring[1]);
     }
 }
 
@@ -177,10 +235,16 @@ static hipError_t dense_typed(const uint8_t *w, int64_t n, int64_t k, const floa
         const int64_t waves = std::min<int64_t>(n, (int64_t)num_cus() * 8);
         const unsigned grid = (unsigned)((waves + 3) / 4);
         const int mi = (int)m;
-        if (m == 1) k_dense_gemv<F16, 1><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
-        else if (m <= 2) k_dense_gemv<F16, 2><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
-        else if (m <= 4) k_dense_gemv<F16, 4><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
-        else k_dense_gemv<F16, 8><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);
+        const size_t xb = (size_t)m * (size_t)k * 4;
+        const bool xl = xb <= DENSE_XL_BYTES;
+        const size_t lds = xl ? xb : 0;
+#define LBQ_DG(MR)                                                                    \
+    {                                                                                 \
+        if (xl) k_dense_gemv<F16, MR, true><<<grid, 256, lds, st>>>(w, n, k, x, mi, y); \
+        else k_dense_gemv<F16, MR, false><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);     \
+    }
+        if (m == 1) LBQ_DG(1) else if (m <= 2) LBQ_DG(2) else if (m <= 4) LBQ_DG(4) else LBQ_DG(8)
+#undef LBQ_DG
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((n + DBN - 1) / DBN), (unsigned)((m + DBM - 1) / DBM));

@@ -109,7 +109,9 @@ def _assert_dense(y, ref):
 @pytest.mark.parametrize("m", [1, 3, 8, 9, 40, 130])
 def test_dense_forward(lbq, dev, t, m):
     rng = np.random.default_rng(450 + m + t)
-    for n, k in ((1, 8), (77, 520), (300, 4096), (129, 1000)):
+    # k = 14336 / 16392: x staged in LDS at m = 1 (57 KB) and not (64 KB + 32 B), the
+    # latter also a row of five 4096-column units with a partial last one
+    for n, k in ((1, 8), (77, 520), (300, 4096), (129, 1000), (64, 14336), (40, 16392)):
         qm, w = _dense(t, n, k, rng, dev)
         x = rng.standard_normal((m, k)).astype(np.float32)
         y = qm.forward(to_dev(x, dev)).cpu().numpy()
