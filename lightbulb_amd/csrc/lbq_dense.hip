@@ -166,12 +166,22 @@ __global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ 
 // ---------------------------------------------------------------------------
 // m > 8.  Workgroup tile 64 (m) x 128 (n), four waves; wave w owns columns
 // 32w..32w+31 for all 64 rows (two 32 x 32 MFMA tiles that share the B operand).
-// k advances in stages of 32: x [64][32] and W [128][32] are loaded (f16 widened)
-// and stored k-major into LDS (row stride padded), then 16 k-steps of
+// k advances in stages of 64: x [64][64] and W [128][64] (f16 widened) are stored
+// k-major into LDS (row stride padded), then 32 k-steps of
 // v_mfma_f32_32x32x2_f32: lane l supplies A[row l%32][k 2s + l/32] and
-// B[k 2s + l/32][column l%32].  Out-of-range rows, columns and k read as zero.
+// B[k 2s + l/32][column l%32].  The next stage's global loads are issued into
+// registers before the current stage's MFMAs, so their latency hides behind 64
+// MFMAs (F16 4096^2 at M = 512: 276 -> 254 us against 32-deep stages loaded
+// after the previous stage's MFMAs).  Out-of-range rows, columns and k read as
+// zero.
 // ---------------------------------------------------------------------------
-constexpr int DBM = 64, DBN = 128, DBK = 32;
+constexpr int DBM = 64, DBN = 128, DBK = 64;
+
+template <bool F16>
+struct DenseStage {
+    float4 x[4];                    // x rows (t / 16) + 16 j, k 4 (t % 16)
+    uint4 w[F16 ? 4 : 8];           // W rows (t / 8) + 32 j, k 8 (t % 8): f16 x 8, or f32 x 8 as two
+};
 
 template <bool F16>
 __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ W, int64_t N, int64_t K,
@@ -187,25 +197,60 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ 
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
-    // staging: x tile 64 x 32 as 512 float4 (2 per thread: row t/8 + 32j, k 4(t%8));
-    // W tile 128 x 32 as 512 runs of 8 (2 per thread: row t/4 + 64j, k 8(t%4))
-    for (int64_t k0 = 0; k0 < K; k0 += DBK) {
+    auto load = [&](int64_t k0, DenseStage<F16> &g) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int r = (t >> 3) + 32 * j, kk = 4 * (t & 7);
+        for (int j = 0; j < 4; j++) {
+            const int r = (t >> 4) + 16 * j, kk = 4 * (t & 15);
             float v[4] = {0.f, 0.f, 0.f, 0.f};
             if (m0 + r < M && k0 + kk < K) load4f(x + (m0 + r) * K + k0 + kk, xv, v);
-            As[kk][r] = v[0]; As[kk + 1][r] = v[1]; As[kk + 2][r] = v[2]; As[kk + 3][r] = v[3];
+            g.x[j] = make_float4(v[0], v[1], v[2], v[3]);
         }
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int r = (t >> 2) + 64 * j, kk = 8 * (t & 3);
-            float w[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (n0 + r < N && k0 + kk < K) load_w8<F16>(W + (n0 + r) * K * WB, k0 + kk, w);
+        for (int j = 0; j < 4; j++) {
+            const int r = (t >> 3) + 32 * j, kk = 8 * (t & 7);
+            const bool ok = n0 + r < N && k0 + kk < K;
+            const uint8_t *src = W + (n0 + r) * K * WB + (k0 + kk) * WB;
+            if constexpr (F16) {
+                g.w[j] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
+            } else {
+                g.w[2 * j] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
+                g.w[2 * j + 1] = ok ? *reinterpret_cast<const uint4 *>(src + 16) : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto store = [&](const DenseStage<F16> &g) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = (t >> 4) + 16 * j, kk = 4 * (t & 15);
+            As[kk][r] = g.x[j].x; As[kk + 1][r] = g.x[j].y; As[kk + 2][r] = g.x[j].z; As[kk + 3][r] = g.x[j].w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = (t >> 3) + 32 * j, kk = 8 * (t & 7);
+            float w[8];
+            if constexpr (F16) {
+                const uint32_t d[4] = {g.w[j].x, g.w[j].y, g.w[j].z, g.w[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    w[2 * e] = h2f(d[e] & 0xffffu);
+                    w[2 * e + 1] = h2f(d[e] >> 16);
+                }
+            } else {
+                const uint4 a = g.w[2 * j], b = g.w[2 * j + 1];
+                w[0] = __uint_as_float(a.x); w[1] = __uint_as_float(a.y); w[2] = __uint_as_float(a.z); w[3] = __uint_as_float(a.w);
+                w[4] = __uint_as_float(b.x); w[5] = __uint_as_float(b.y); w[6] = __uint_as_float(b.z); w[7] = __uint_as_float(b.w);
+            }
 #pragma unroll
             for (int e = 0; e < 8; e++) Bs[kk + e][r] = w[e];
         }
-        __syncthreads();
+    };
+    DenseStage<F16> g;
+    load(0, g);
+    store(g);
+    __syncthreads();
+    for (int64_t k0 = 0; k0 < K; k0 += DBK) {
+        const bool more = k0 + DBK < K;
+        if (more) load(k0 + DBK, g);  // in flight during this stage's MFMAs
 #pragma unroll
         for (int s = 0; s < DBK / 2; s++) {
             const float b = Bs[2 * s + h][32 * wave + lr];
@@ -216,6 +261,10 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ 
             }
         }
         __syncthreads();
+        if (more) {
+            store(g);
+            __syncthreads();
+        }
     }
     // D layout of a 32 x 32 tile: lane holds column l%32, rows 8(v/4) + 4h + v%4
     const int64_t n = n0 + 32 * wave + lr;
