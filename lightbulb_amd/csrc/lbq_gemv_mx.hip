@@ -20,8 +20,9 @@
 // activation row, the matrix core does all rows at once: its VALU work per weight
 // does not grow with m.
 //
-// Workgroup: 32 weight rows, four waves splitting the row's blocks into four
-// contiguous ranges; the four partial tiles are added in wave order in LDS.
+// Workgroup: 32 weight rows, four (or, with at most one workgroup per CU, eight)
+// waves splitting the row's blocks into contiguous ranges; the partial tiles are
+// added in wave order in LDS.
 //
 // Activations go through a wave-private LDS stage.  Per block, the wave's eight
 // activation rows (2 KB of codes, 256 B of 16-value sums; rows past m repeat row
@@ -45,7 +46,6 @@ typedef int i32x16v __attribute__((ext_vector_type(16)));
 typedef float f32x16v __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
 
-constexpr int MX_WAVES = 4;
 constexpr int MX_STAGE = 8 * 256 + 256;  // codes of 8 activation rows, then their 16-value sums
 
 template <int TYPE>
@@ -63,9 +63,16 @@ __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &
 
 // One block: xa = the 8 sub-blocks' A operands, xbv = the lane half's four pairs
 // of 16-value sums; accumulators e = 0..3 are C rows 4h + e.
-template <int TYPE>
-__device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const i32x4v *xa, i32x4v xbv, int h, const float *sdx,
+template <int TYPE, bool JIT>
+__device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, const int *ro, int h, const float *sdx,
                                          float *acc) {
+    // A operands: all nine stage reads up front, or (JIT, fewer registers) each
+    // right before its MFMA
+    i32x4v xa[8];
+    if constexpr (!JIT) {
+#pragma unroll
+        for (int s = 0; s < 8; s++) xa[s] = *reinterpret_cast<const i32x4v *>(st + ro[s]);
+    }
     constexpr int E = 4;
     const uint32_t hw0 = r.hd.x, hw1 = r.hd.y, hw2 = r.hd.z, hw3 = r.hd.w;
     // get_scale_min_k4 for the 8 sub-blocks, as packed bytes: j < 4 from bytes j,
@@ -90,6 +97,7 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const i32x4v *xa, i
             bw[w] = (int)v;
         }
         const i32x16v zero = {};
+        if constexpr (JIT) xa[s] = *reinterpret_cast<const i32x4v *>(st + ro[s]);
         const i32x16v o = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[s], bw, zero, 0, 0, 0);
         const int sc = (int)(((s < 4 ? sc03 : sc47) >> (8 * (s & 3))) & 0xffu);
 #pragma unroll
@@ -97,6 +105,7 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const i32x4v *xa, i
     }
     // mins: sub-blocks 4h + t of the lane half (k slots 8h + 2t, 8h + 2t + 1)
     const uint32_t mm = h ? m47 : m03;
+    const i32x4v xbv = *reinterpret_cast<const i32x4v *>(st + ro[8]);
     const uint32_t xbw[4] = {(uint32_t)xbv.x, (uint32_t)xbv.y, (uint32_t)xbv.z, (uint32_t)xbv.w};
     f16x8v a, b;
 #pragma unroll
@@ -123,7 +132,7 @@ struct MxX {
     i32x4v c[2], s;  // codes (rows 4q + lane/16, chunk lane%16), sums (row (lane%16)/2, half lane%2)
 };
 
-template <int TYPE>
+template <int TYPE, int MX_WAVES>
 __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
                                                          int nb, ActView act, int m, float *__restrict__ y) {
     constexpr int E = 4;
@@ -194,11 +203,7 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
                 // xr[1 - q] holds block b + q + 1 (loaded a block ago); xr[q] takes b + q + 2
                 load_x(min(b + q + 2, bl), xr[q]);
                 load_w(min(b + q + 1, bl), rw[1 - q]);
-                i32x4v xa[8], xbv;
-#pragma unroll
-                for (int s = 0; s < 8; s++) xa[s] = *reinterpret_cast<const i32x4v *>(st + ro[s]);
-                xbv = *reinterpret_cast<const i32x4v *>(st + ro[8]);
-                mx_block<TYPE>(rw[q], xa, xbv, h, sdx + 8 * (b + q), acc);
+                mx_block<TYPE, (MX_WAVES > 4)>(rw[q], st, ro, h, sdx + 8 * (b + q), acc);
                 if (b + q == bl) break;
                 write_x(xr[1 - q]);  // after this block's stage reads (the MFMAs consumed them)
             }
@@ -208,8 +213,8 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
 #pragma unroll
     for (int e = 0; e < E; e++) red[wave][e][lane] = acc[e];
     __syncthreads();
-    // wave w stores accumulator w (C row 4h + w), the four partials added in wave order
-    {
+    // wave w < 4 stores accumulator w (C row 4h + w), the partials added in wave order
+    if (wave < E) {
         const int e = wave;
         float s = red[0][e][lane];
 #pragma unroll
@@ -245,10 +250,18 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
     if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)((n + 31) / 32);
     const size_t lds = (size_t)nb * 8 * sizeof(float);
-    if (type == TYPE_Q4_K)
-        k_gemv_mx<TYPE_Q4_K><<<grid, 64 * MX_WAVES, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
-    else
-        k_gemv_mx<TYPE_Q5_K><<<grid, 64 * MX_WAVES, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+    // Up to one workgroup per CU: eight waves split a row's blocks (2 per wave at
+    // k = 4096), A operands read just in time to stay within four waves per SIMD
+    // (4096 x 14336 m = 4: 21.8 -> 19.5 us; 4096 x 4096 m = 8: 12.9 -> 12.4).  With
+    // more workgroups, four waves (14336 x 4096 m = 8: 16.9 at four, 18.7 at eight).
+    const bool w8 = (int64_t)grid <= (int64_t)num_cus();
+    if (type == TYPE_Q4_K) {
+        if (w8) k_gemv_mx<TYPE_Q4_K, 8><<<grid, 64 * 8, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+        else k_gemv_mx<TYPE_Q4_K, 4><<<grid, 64 * 4, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+    } else {
+        if (w8) k_gemv_mx<TYPE_Q5_K, 8><<<grid, 64 * 8, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+        else k_gemv_mx<TYPE_Q5_K, 4><<<grid, 64 * 4, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+    }
     return hipGetLastError();
 }
 

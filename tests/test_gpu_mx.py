@@ -20,7 +20,9 @@ from test_gpu_q8_0_dense import forward_with_env
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (64, 14336), (96, 16384)]
+# (8224 rows: 257 workgroups, the four-wave kernel; fewer rows: one workgroup per CU at
+# most, the eight-wave kernel)
+SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (64, 14336), (96, 16384), (8224, 1024)]
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
