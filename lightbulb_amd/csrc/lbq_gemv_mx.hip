@@ -227,8 +227,9 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // Measured against the decode kernels (x quantised by the same separate pass
     // unless noted): Q5_K 14336 x 4096 m = 8 22.8 -> 18.2 us, Q4_K 14336 x 4096
-    // 21.4 -> 16.8, 4096 x 4096 13.4 -> 12.5; with 1024 rows (32 workgroups)
-    // 10.8 -> 12.0, so fewer than 4096 rows keep the multi-row kernel.  At m <= 4
+    // 21.4 -> 16.8, 4096 x 4096 13.4 -> 12.5, 2048 x 4096 12.5 -> 11.9, 3072 x
+    // 4096 m = 6 12.9 -> 11.9; with 1024 rows (32 eight-wave workgroups) 11.5 ->
+    // 11.8, so fewer than 2048 rows keep the multi-row kernel.  At m <= 4
     // that kernel quantises x in its own prologue and stays ahead (m = 2: 12.8 vs
     // 17.9 us) -- except at k > 8192, where it cannot hold the activation rows and
     // the general GEMV runs: Q4_K 4096 x 14336 m = 2 / 3 / 4 / 8 22.2 / 26.3 /
@@ -240,7 +241,7 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     if (type != TYPE_Q4_K && type != TYPE_Q5_K) return false;
     if (k % 256 || k / 256 > 64 || m < 2 || m > 8 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
     if (k / 256 > 32) return true;  // the multi-row decode kernel cannot hold these rows
-    return m >= 5 && n >= 4096;
+    return m >= 5 && n >= 2048;
 }
 
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,

@@ -1,5 +1,5 @@
 """Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..8 with
-n >= 4096, and m = 2..8 at k > 8192) against the oracle.
+n >= 2048, and m = 2..8 at k > 8192) against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 # (8224 rows: 257 workgroups, the four-wave kernel; fewer rows: one workgroup per CU at
 # most, the eight-wave kernel)
-SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (64, 14336), (96, 16384), (8224, 1024)]
+SHAPES = [(4096, 4096), (2050, 2048), (4100, 1280), (4096, 512), (64, 14336), (96, 16384), (8224, 1024)]
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
