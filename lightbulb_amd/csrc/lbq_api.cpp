@@ -92,6 +92,9 @@ Tuning tuning_from_env() {
     t.gemv1_wpc = std::max(0, env_int("LBQ_GEMV1_WPC"));
     t.gemv1_wpg = std::max(0, env_int("LBQ_GEMV1_WPG"));
     t.gemv_mx_off = getenv("LBQ_GEMV_MX_OFF") != nullptr;
+    t.gemv_mx_wide_off = getenv("LBQ_GEMV_MX_WIDE_OFF") != nullptr;
+    t.gemv_mx_splits = env_int("LBQ_GEMV_MX_SPLITS");
+    t.gemv_mx_waves = env_int("LBQ_GEMV_MX_WAVES");
     if (const char *e = getenv("LBQ_GEMV")) {
         int v[4] = {0, 0, 0, 0};
         if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)
@@ -259,14 +262,21 @@ struct Scratch {
 };
 
 // Batch decode on the matrix cores for this weight and row count
-static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 8 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
+static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 32 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
 
 // The dot half of QMatMul::forward: decode GEMV for m <= 8 (the i8 matrix-core
 // kernel at m = 5..8 where it serves), MFMA GEMM above.
 int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
     hipError_t e;
     if (uses_mx(w, m)) {
-        e = lbq::launch_gemv_mx(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
+        const size_t wsb = lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m);
+        uint8_t *ws = nullptr;
+        if (wsb) {
+            int s = sc.ws(wsb, &ws);
+            if (s) return s;
+        }
+        e = lbq::launch_gemv_mx(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y,
+                                reinterpret_cast<float *>(ws), sc.counters(), st);
     } else if (m <= 8) {
         e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
     } else {
@@ -305,7 +315,7 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
     std::unique_lock<std::mutex> lock;
     if (mu) lock = std::unique_lock<std::mutex>(*mu);
     (void)ctx;
-    if (m > 8 && lbq::gemm_prepass_fuses_quant(w->type, w->k, d_x)) {
+    if (m > 8 && !uses_mx(w, m) && lbq::gemm_prepass_fuses_quant(w->type, w->k, d_x)) {
         // batched: the operand pre-pass quantises x itself
         uint8_t *ws = nullptr;
         int s = sc.ws(lbq::gemm_workspace_bytes(w->type, w->n, w->k, m), &ws);
@@ -319,9 +329,11 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
     uint8_t *abuf = nullptr;
     int s = sc.act(L.total, &abuf);
     if (s) return s;
-    if (m > 8) {  // reserve the GEMM workspace too before anything is launched
+    {  // reserve the GEMM's (or the matrix-core decode's) workspace too before anything is launched
         uint8_t *ws = nullptr;
-        const size_t wsb = lbq::gemm_workspace_bytes(w->type, w->n, w->k, m);
+        const size_t wsb = uses_mx(w, m) ? lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m)
+                           : m > 8       ? lbq::gemm_workspace_bytes(w->type, w->n, w->k, m)
+                                         : 0;
         if (wsb && (s = sc.ws(wsb, &ws))) return s;
     }
     const lbq::ActView av = view_of(abuf, L, w->k);
@@ -642,36 +654,58 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
     std::lock_guard<std::mutex> lock(ctx->mu);
-    if (m > 8 && lbq::gemm_serves(w0->type, w0->k)) {
+    bool all_mx = true;  // every weight on the integer matrix-core kernel: x quantised once below
+    for (int i = 0; i < count; i++) all_mx = all_mx && uses_mx(ws[i], m);
+    if (m > 8 && !all_mx && lbq::gemm_serves(w0->type, w0->k)) {
         // batched: one operand pre-pass (quantising x itself when it can) shared
-        // by every weight's GEMM
+        // by every weight's GEMM; weights on the integer matrix-core kernel share
+        // one Q8_K quantisation of x and run after the GEMMs (their split partials
+        // reuse the workspace the pre-pass operands occupy)
         size_t wsb = 0;
-        for (int i = 0; i < count; i++) wsb = std::max(wsb, lbq::gemm_workspace_bytes(w0->type, ws[i]->n, w0->k, m));
+        bool mx[LBQ_GROUP_MAX], any_mx = false;
+        for (int i = 0; i < count; i++) {
+            mx[i] = uses_mx(ws[i], m);
+            any_mx = any_mx || mx[i];
+            wsb = std::max(wsb, mx[i] ? lbq::gemv_mx_workspace_bytes(w0->type, ws[i]->n, w0->k, (int)m)
+                                      : lbq::gemm_workspace_bytes(w0->type, ws[i]->n, w0->k, m));
+        }
         int s = ensure_buffer(&ctx->ws, &ctx->ws_bytes, wsb, "GEMM workspace");
         if (s) return s;
-        hipError_t e = hipSuccess;
         bool in_kernel[LBQ_GROUP_MAX], all_in_kernel = true;
         for (int i = 0; i < count; i++) {
-            in_kernel[i] = lbq::gemm_quantises_in_kernel(w0->type, ws[i]->n, w0->k, m, d_x);
-            all_in_kernel = all_in_kernel && in_kernel[i];
+            in_kernel[i] = !mx[i] && lbq::gemm_quantises_in_kernel(w0->type, ws[i]->n, w0->k, m, d_x);
+            all_in_kernel = all_in_kernel && (mx[i] || in_kernel[i]);
         }
+        const bool fused_prepass = !all_in_kernel && lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x);
+        if ((any_mx || (!all_in_kernel && !fused_prepass)) && (s = ensure_scratch(ctx, L.total))) return s;
+        const lbq::ActView av = ctx->scratch ? view_of(ctx->scratch, L, w0->k) : lbq::ActView{nullptr, nullptr, nullptr, w0->k, L.nb};
+        bool quantised = false;
+        hipError_t e = hipSuccess;
         if (all_in_kernel) {
-            // every weight's k-sliced GEMM quantises x itself
-        } else if (lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x)) {
+            // every GEMM weight's k-sliced kernel quantises x itself
+        } else if (fused_prepass) {
             const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, L.nb};
             e = lbq::gemm_prepass(w0->type, w0->k, none, d_x, m, ctx->ws, st);
         } else {
-            s = ensure_scratch(ctx, L.total);
-            if (s) return s;
-            const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
             e = quant_into(act_type, d_x, m, w0->k, av, st);
+            quantised = true;
             if (e == hipSuccess) e = lbq::gemm_prepass(w0->type, w0->k, av, nullptr, m, ctx->ws, st);
         }
         if (e != hipSuccess) return hip_fail(e, "operand pre-pass launch");
         for (int i = 0; i < count; i++) {
+            if (mx[i]) continue;
             e = lbq::gemm_main(w0->type, ws[i]->d_blocks, ws[i]->d_rexp, ws[i]->n, w0->k, w0->row_bytes, m, d_ys[i],
                                ctx->ws, ctx->tile_counters, in_kernel[i] ? d_x : nullptr, st);
             if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
+        }
+        if (!any_mx) return LBQ_OK;
+        if (!quantised && (e = quant_into(act_type, d_x, m, w0->k, av, st)) != hipSuccess)
+            return hip_fail(e, "activation quantisation launch");
+        for (int i = 0; i < count; i++) {
+            if (!mx[i]) continue;
+            Scratch sc;
+            sc.ctx = ctx;
+            if ((s = run_dot(sc, ws[i], av, m, d_ys[i], st))) return s;
         }
         return LBQ_OK;
     }

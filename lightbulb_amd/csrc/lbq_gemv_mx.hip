@@ -36,6 +36,8 @@
 // waves per SIMD).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "lbq_device.hpp"
 #include "lbq_internal.hpp"
 
@@ -45,8 +47,6 @@ typedef int i32x4v __attribute__((ext_vector_type(4)));
 typedef int i32x16v __attribute__((ext_vector_type(16)));
 typedef float f32x16v __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-
-constexpr int MX_STAGE = 8 * 256 + 256;  // codes of 8 activation rows, then their 16-value sums
 
 template <int TYPE>
 struct MxW {
@@ -61,9 +61,12 @@ __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &
     for (int c = 0; c < 4; c++) r.qs[c] = ld_u4(blk + QS + 32 * c + 16 * h);
 }
 
+// C row (activation row) of accumulator e in lane half h
+__device__ __forceinline__ constexpr int mx_row(int e, int h) { return 8 * (e >> 2) + 4 * h + (e & 3); }
+
 // One block: xa = the 8 sub-blocks' A operands, xbv = the lane half's four pairs
-// of 16-value sums; accumulators e = 0..3 are C rows 4h + e.
-template <int TYPE, bool JIT>
+// of 16-value sums; accumulator e (of E = MR / 2) is C row mx_row(e, h).
+template <int TYPE, bool JIT, int E>
 __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, const int *ro, int h, const float *sdx,
                                          float *acc) {
     // A operands: all nine stage reads up front, or (JIT, fewer registers) each
@@ -73,7 +76,6 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, 
 #pragma unroll
         for (int s = 0; s < 8; s++) xa[s] = *reinterpret_cast<const i32x4v *>(st + ro[s]);
     }
-    constexpr int E = 4;
     const uint32_t hw0 = r.hd.x, hw1 = r.hd.y, hw2 = r.hd.z, hw3 = r.hd.w;
     // get_scale_min_k4 for the 8 sub-blocks, as packed bytes: j < 4 from bytes j,
     // j + 4; j >= 4 from the nibbles of bytes j + 4 and the top bits of j - 4, j
@@ -122,68 +124,93 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, 
     const float d = h2f(hw0 & 0xffffu), dmin = h2f(hw0 >> 16);
 #pragma unroll
     for (int e = 0; e < E; e++) {
-        const float dx = sdx[4 * h + e];
+        const float dx = sdx[mx_row(e, h)];
         acc[e] = fmaf(d * dx, (float)isum[e], acc[e]);
         acc[e] = fmaf(-(dmin * dx), ms[e], acc[e]);
     }
 }
 
+template <int MR>
 struct MxX {
-    i32x4v c[2], s;  // codes (rows 4q + lane/16, chunk lane%16), sums (row (lane%16)/2, half lane%2)
+    i32x4v c[MR / 4], s;  // codes (rows 4q + lane/16, chunk lane%16), sums (row lane/2, half lane%2)
 };
 
-template <int TYPE, int MX_WAVES>
+// Split k: `splits` workgroups share a 32-row tile, each taking a contiguous
+// range of its blocks, and store their partial tiles (part[split][m][n]) with
+// agent-scope stores, which write through to memory instead of staying in this
+// XCD's L2.  Once they have completed (vmcnt(0)), a counter increment publishes
+// them; the workgroup that completes the tile's count adds the partials in split
+// order (the bits do not depend on which workgroup came last), reading them with
+// the same agent-scope policy, writes y and puts the counter back to zero for the
+// next call.
+constexpr int MX_MAX_SPLITS = 16;
+
+struct MxSplit {
+    int splits;     // workgroups per 32-row tile (1: no partials)
+    float *part;    // [splits][m][n]
+    uint32_t *cnt;  // one zeroed word per tile
+};
+
+// MR = the activation rows a launch can hold (8, 16 or 32; m <= MR)
+template <int TYPE, int MX_WAVES, int MR>
 __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
-                                                         int nb, ActView act, int m, float *__restrict__ y) {
-    constexpr int E = 4;
-    extern __shared__ __align__(16) float sdx[];  // [nb][8]: dx of block b, activation row i (0 past m)
-    __shared__ float red[MX_WAVES][E][64];
-    __shared__ __align__(16) uint8_t xs[MX_WAVES][MX_STAGE];
+                                                         int nb, ActView act, int m, float *__restrict__ y, MxSplit sp) {
+    constexpr int E = MR / 2, STAGE = MR * 256 + MR * 32;  // codes of MR rows, then their 16-value sums
+    static_assert(E * 64 * 4 <= STAGE, "the partial tile overlays the wave's stage");
+    extern __shared__ __align__(16) float sdx[];  // [nb][MR]: dx of block b, activation row i (0 past m)
+    __shared__ __align__(16) uint8_t xs[MX_WAVES][STAGE];
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int row0 = blockIdx.x * 32;
+    const int tile = blockIdx.x / sp.splits, part = blockIdx.x % sp.splits;
+    const int row0 = tile * 32;
     const int64_t k = act.k;
     const uint8_t *wr = W + (int64_t)min(row0 + j, n - 1) * row_bytes;
-    const int b0 = wave * nb / MX_WAVES, b1 = (wave + 1) * nb / MX_WAVES;
+    const int p0 = part * nb / sp.splits, np = (part + 1) * nb / sp.splits - p0;  // this workgroup's blocks
+    const int b0 = p0 + wave * np / MX_WAVES, b1 = p0 + (wave + 1) * np / MX_WAVES;
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
     uint8_t *st = xs[wave];
-    // this lane's share of a block's activations: two code chunks and a sums chunk
-    const int8_t *xc[2];
-    int wo[2];
+    // this lane's share of a block's activations: MR / 4 code chunks (row 4q +
+    // lane / 16, chunk lane % 16) and a sums chunk (row lane / 2, half lane % 2);
+    // rows past m are not loaded (their stage rows are never read)
+    const int8_t *xc = act.xq + (int64_t)min(lane >> 4, m - 1) * k + 16 * (lane & 15);
+    int wo[MR / 4];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
+    for (int q = 0; q < MR / 4; q++) {
         const int r = 4 * q + (lane >> 4), c = lane & 15;
-        xc[q] = act.xq + (int64_t)min(r, m - 1) * k + 16 * c;
         wo[q] = r * 256 + 16 * (c ^ (r & 15));
     }
-    const int16_t *xsum = act.xbs + (int64_t)min((lane & 15) >> 1, m - 1) * (k / 16) + 8 * (lane & 1);
-    const int so = 2048 + 16 * (lane & 15);  // lanes 16..63 load copies and write nothing
-    auto load_x = [&](int b, MxX &x) {
+    const int srow = (lane >> 1) & (MR - 1);
+    const int16_t *xsum = act.xbs + (int64_t)min(srow, m - 1) * (k / 16) + 8 * (lane & 1);
+    const bool sl = lane < 2 * MR;  // lanes past 2 MR load copies and write nothing
+    const int so = MR * 256 + 16 * (lane & (2 * MR - 1));
+    auto load_x = [&](int b, MxX<MR> &x) {
 #pragma unroll
-        for (int q = 0; q < 2; q++) x.c[q] = *reinterpret_cast<const i32x4v *>(xc[q] + 256 * b);
+        for (int q = 0; q < MR / 4; q++)
+            if (q == 0 || 4 * q + (lane >> 4) < m)
+                x.c[q] = *reinterpret_cast<const i32x4v *>(xc + (int64_t)(4 * q) * k + 256 * b);
         x.s = *reinterpret_cast<const i32x4v *>(xsum + 16 * b);
     };
-    auto write_x = [&](const MxX &x) {
+    auto write_x = [&](const MxX<MR> &x) {
 #pragma unroll
-        for (int q = 0; q < 2; q++) *reinterpret_cast<i32x4v *>(st + wo[q]) = x.c[q];
-        if (lane < 16) *reinterpret_cast<i32x4v *>(st + so) = x.s;
+        for (int q = 0; q < MR / 4; q++) *reinterpret_cast<i32x4v *>(st + wo[q]) = x.c[q];
+        if (sl) *reinterpret_cast<i32x4v *>(st + so) = x.s;
     };
     // A-operand reads: row ra (A rows past m read row m - 1), chunk 2s + h
     const int ra = min(j, m - 1);
     int ro[9];
 #pragma unroll
     for (int s = 0; s < 8; s++) ro[s] = ra * 256 + 16 * ((2 * s + h) ^ (ra & 15));
-    ro[8] = 2048 + ra * 32 + 16 * h;
+    ro[8] = MR * 256 + ra * 32 + 16 * h;
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; e++) acc[e] = 0.f;
     // Loads are unconditional, their block clamped to the wave's last one (the
-    // tail re-reads it and never uses the copy).  A wave with no blocks (nb < 4)
-    // loads nothing.
+    // tail re-reads it and never uses the copy).  A wave with no blocks (nb < the
+    // wave count) loads nothing.
     const bool any = b0 < b1;
     const int bl = b1 - 1;
     MxW<TYPE> rw[2];
-    MxX xr[2];
+    MxX<MR> xr[2];
     auto load_w = [&](int b, MxW<TYPE> &dst) { mx_load_w<TYPE>(wr + (int64_t)b * BYTES, h, dst); };
     if (any) {
         load_x(b0, xr[0]);
@@ -191,8 +218,8 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
         load_w(b0, rw[0]);
         write_x(xr[0]);
     }
-    for (int q = t; q < nb * 8; q += 64 * MX_WAVES) {
-        const int b = q >> 3, i = q & 7;
+    for (int q = p0 * MR + t; q < (p0 + np) * MR; q += 64 * MX_WAVES) {
+        const int b = q / MR, i = q % MR;
         sdx[q] = i < m ? act.xd[(int64_t)i * nb + b] : 0.f;
     }
     __syncthreads();  // sdx (each wave's first stage is its own)
@@ -203,25 +230,49 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
                 // xr[1 - q] holds block b + q + 1 (loaded a block ago); xr[q] takes b + q + 2
                 load_x(min(b + q + 2, bl), xr[q]);
                 load_w(min(b + q + 1, bl), rw[1 - q]);
-                mx_block<TYPE, (MX_WAVES > 4)>(rw[q], st, ro, h, sdx + 8 * (b + q), acc);
+                mx_block<TYPE, (MX_WAVES > 4), E>(rw[q], st, ro, h, sdx + MR * (b + q), acc);
                 if (b + q == bl) break;
                 write_x(xr[1 - q]);  // after this block's stage reads (the MFMAs consumed them)
             }
             if (b + 2 > bl) break;
         }
     }
+    // the wave's partial tile replaces its own stage (its stage reads are done:
+    // LDS operations of one wave complete in order)
+    float *red = reinterpret_cast<float *>(st);
 #pragma unroll
-    for (int e = 0; e < E; e++) red[wave][e][lane] = acc[e];
+    for (int e = 0; e < E; e++) red[e * 64 + lane] = acc[e];
     __syncthreads();
-    // wave w < 4 stores accumulator w (C row 4h + w), the partials added in wave order
-    if (wave < E) {
-        const int e = wave;
-        float s = red[0][e][lane];
+    // accumulator e (C row mx_row(e, h)) is stored by wave e % MX_WAVES, the
+    // partials added in wave order
+    const int col = row0 + j;
+    for (int e = wave; e < E; e += MX_WAVES) {
+        float s = reinterpret_cast<const float *>(xs[0])[e * 64 + lane];
 #pragma unroll
-        for (int w = 1; w < MX_WAVES; w++) s += red[w][e][lane];
-        const int i = 4 * h + e;
-        if (i < m && row0 + j < n) y[(int64_t)i * n + row0 + j] = s;
+        for (int w = 1; w < MX_WAVES; w++) s += reinterpret_cast<const float *>(xs[w])[e * 64 + lane];
+        const int i = mx_row(e, h);
+        if (i < m && col < n) {
+            if (sp.splits == 1) y[(int64_t)i * n + col] = s;
+            else __hip_atomic_store(sp.part + ((int64_t)part * m + i) * n + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
+    if (sp.splits == 1) return;
+    __shared__ uint32_t last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0) last = __hip_atomic_fetch_add(sp.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (last != (uint32_t)(sp.splits - 1)) return;
+    for (int e = wave; e < E; e += MX_WAVES) {
+        const int i = mx_row(e, h);
+        if (i >= m || col >= n) continue;
+        const float *pp = sp.part + (int64_t)i * n + col;
+        const int64_t stride = (int64_t)m * n;
+        float s = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = 1; q < sp.splits; q++) s += __hip_atomic_load(pp + q * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        y[(int64_t)i * n + col] = s;
+    }
+    if (t == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
@@ -239,29 +290,63 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // us: fourteen 8-byte weight loads per block and lane) and was not kept.
     if (tuning().gemv_mx_off) return false;
     if (type != TYPE_Q4_K && type != TYPE_Q5_K) return false;
-    if (k % 256 || k / 256 > 64 || m < 2 || m > 8 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    if (k % 256 || k / 256 > 64 || m < 2 || m > 32 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    // m = 9..32 (the fp16 GEMM otherwise): Q4_K 14336 x 4096 m = 16 / 32 22.1 / 23.4
+    // -> 18.3 / 21.8 us, Q5_K m = 12 / 24 23.9 / 24.3 -> 18.4 / 21.8, 4096 x 14336
+    // m = 16 23.6 -> 20.3, 4096 x 4096 m = 32 16.1 -> 14.9 (two workgroups per
+    // tile); with 1024 / 2048 rows the GEMM stays ahead (m = 32 12.9 against 13.5,
+    // m = 16 11.3 against 11.8)
+    if (m > 8) return !tuning().gemv_mx_wide_off && n >= 4096;
     if (k / 256 > 32) return true;  // the multi-row decode kernel cannot hold these rows
     return m >= 5 && n >= 2048;
 }
 
+// Workgroups per 32-row tile: two up to 128 tiles (4096 rows), which fills the
+// chip's 256 CUs with eight-wave workgroups.  Measured (Q4_K, x quantised by the
+// separate pass): 4096 x 14336 m = 8 / 16 / 32 20.6 / 24.1 / 30.5 -> 17.5 / 20.3
+// / 25.4 us, 4096 x 4096 m = 8 / 16 / 32 12.0 / 13.0 / 15.6 -> 11.2 / 12.1 /
+// 14.9; four workgroups per tile (or four waves each) measured slower.
+static int mx_splits(int64_t n, int64_t k, int m) {
+    (void)m;
+    const int64_t tiles = (n + 31) / 32;
+    const int nb = (int)(k / 256);
+    int s = tuning().gemv_mx_splits;
+    if (s <= 0) s = tiles <= 128 ? 2 : 1;
+    s = (int)std::min<int64_t>({(int64_t)s, (int64_t)nb, (int64_t)MX_MAX_SPLITS});
+    if (tiles > KS_COUNTERS) s = 1;
+    return std::max(s, 1);
+}
+
+size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m) {
+    if (!gemv_mx_serves(type, n, k, m)) return 0;
+    const int s = mx_splits(n, k, m);
+    return s > 1 ? (size_t)s * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
+
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
-                          float *y, hipStream_t st) {
+                          float *y, float *ws, uint32_t *counters, hipStream_t st) {
     if (!gemv_mx_serves(type, n, k, m)) return hipErrorNotSupported;
     const int nb = (int)(k / 256);
     if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)((n + 31) / 32);
-    const size_t lds = (size_t)nb * 8 * sizeof(float);
+    MxSplit sp{mx_splits(n, k, m), ws, counters};
+    if (sp.splits > 1 && (!ws || !counters)) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)((n + 31) / 32 * sp.splits);
     // Up to one workgroup per CU: eight waves split a row's blocks (2 per wave at
     // k = 4096), A operands read just in time to stay within four waves per SIMD
     // (4096 x 14336 m = 4: 21.8 -> 19.5 us; 4096 x 4096 m = 8: 12.9 -> 12.4).  With
     // more workgroups, four waves (14336 x 4096 m = 8: 16.9 at four, 18.7 at eight).
-    const bool w8 = (int64_t)grid <= (int64_t)num_cus();
+    const bool w8 = tuning().gemv_mx_waves ? tuning().gemv_mx_waves == 8 : (int64_t)grid <= (int64_t)num_cus();
+    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
+    const size_t lds = (size_t)nb * mr * sizeof(float);
+    auto go = [&](auto kern, int waves) { kern<<<grid, 64 * waves, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y, sp); };
     if (type == TYPE_Q4_K) {
-        if (w8) k_gemv_mx<TYPE_Q4_K, 8><<<grid, 64 * 8, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
-        else k_gemv_mx<TYPE_Q4_K, 4><<<grid, 64 * 4, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+        if (mr == 8) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 8>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 8>, 4);
+        else if (mr == 16) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 16>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 16>, 4);
+        else w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 32>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 32>, 4);
     } else {
-        if (w8) k_gemv_mx<TYPE_Q5_K, 8><<<grid, 64 * 8, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
-        else k_gemv_mx<TYPE_Q5_K, 4><<<grid, 64 * 4, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y);
+        if (mr == 8) w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 8>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 8>, 4);
+        else if (mr == 16) w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 16>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 16>, 4);
+        else w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 32>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 32>, 4);
     }
     return hipGetLastError();
 }

@@ -50,6 +50,9 @@ struct ActView;
 //   LBQ_GEMV1_NOFUSE, LBQ_GEMV1_CFG=<ppb>,<rpw>, LBQ_GEMV1_WPC=<waves per CU>,
 //   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
 //   LBQ_GEMV_ROWS_OFF                               decode GEMV plan
+//   LBQ_GEMV_MX_OFF, LBQ_GEMV_MX_WIDE_OFF (m = 9..32 only),
+//   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8
+//                                                   matrix-core batch decode plan
 struct Tuning {
     bool gemm_ks64 = false, gemm_no_ks = false, gemm_no_tall = false;
     int gemm_ks = 0;      // k-sliced tiles: blocks per slice (0: planned)
@@ -61,6 +64,8 @@ struct Tuning {
     int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
     int gemv1_wpc = 0, gemv1_wpg = 0;
     bool gemv_mx_off = false;  // batch decode never on the matrix cores
+    bool gemv_mx_wide_off = false;  // m = 9..32 never on the integer matrix-core kernel
+    int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
 };
 Tuning tuning_from_env();
@@ -114,8 +119,11 @@ hipError_t launch_gemv(int type, const uint8_t *w, int64_t n, int64_t k, int64_t
 // Q8_K rows: Q4_K / Q5_K, k % 256 == 0, k <= 16384, 5 <= m <= 8, where it is the
 // faster kernel (n >= 4096, or k > 8192).
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m);
+// device memory launch_gemv_mx needs at ws (0: none); counters: KS_COUNTERS
+// zeroed words (each launch leaves them zero)
+size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m);
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
-                          float *y, hipStream_t st);
+                          float *y, float *ws, uint32_t *counters, hipStream_t st);
 
 // True when the decode GEMV quantises x itself (m = 1, k within the fast path,
 // x 16-byte aligned).

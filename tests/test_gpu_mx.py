@@ -1,5 +1,5 @@
 """Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..8 with
-n >= 2048, and m = 2..8 at k > 8192) against the oracle.
+n >= 2048, m = 2..8 at k > 8192, and m = 9..32 with n >= 4096) against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -44,9 +44,36 @@ def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
 
 
+# m = 9..32 runs on the kernel from 4096 rows: 128 tiles (two workgroups each), 129-130
+# tiles (one, eight waves), 257 (one, four waves); k from 2 to 64 blocks
+WIDE_SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (8224, 1024), (4096, 14336), (4160, 16384)]
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("n,k", WIDE_SHAPES)
+@pytest.mark.parametrize("m", [9, 16, 17, 32])
+def test_mx_wide_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
+    # m = 9..16 and 17..32: the kernel's 16- and 32-row forms (every C row of the
+    # 32 x 32 tile in use at m = 32)
+    rng = np.random.default_rng(n * 5 + k + 37 * m + t)
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx wide t={t} n={n} k={k} m={m}", flush=True)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
+    # switched off: the fp16 GEMM (its own bound), which must differ in some bits
+    off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_WIDE_OFF": "1"}, t, w_raw, n, k, x, dev)
+    assert_rows_close(off, ref, 2e-3)
+    assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
 @pytest.mark.parametrize("m,k,n", [(6, 4096, 4096), (7, 4096, 4096), (2, 14336, 160), (3, 14336, 33), (4, 9216, 160),
-                                   (2, 8448, 1), (5, 8448, 70)])
+                                   (2, 8448, 1), (5, 8448, 70), (12, 512, 4097), (31, 768, 4127), (25, 8448, 4100)])
 def test_mx_row_counts(oracle, lbq, dev, t, m, k, n):
     # k = 8448: 33 blocks, the smallest k the kernel takes at m <= 4; n = 1 and 33:
     # a workgroup of one row, a last workgroup of one row
@@ -59,9 +86,9 @@ def test_mx_row_counts(oracle, lbq, dev, t, m, k, n):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
-def test_mx_nan_activations(oracle, lbq, dev, t):
-    rng = np.random.default_rng(910 + t)
-    n, k, m = 96, 14336, 8
+@pytest.mark.parametrize("m,n,k", [(8, 96, 14336), (32, 4096, 4096)])
+def test_mx_nan_activations(oracle, lbq, dev, t, m, n, k):
+    rng = np.random.default_rng(910 + t + m)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = _nan_rows(rng, m, k)
     y = gpu_qmatmul(t, w_raw, n, k, x, dev)
@@ -71,9 +98,9 @@ def test_mx_nan_activations(oracle, lbq, dev, t):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
-def test_mx_nonfinite_scales(oracle, lbq, dev, t):
-    rng = np.random.default_rng(920 + t)
-    n, k, m = 200, 14336, 8
+@pytest.mark.parametrize("m,n,k", [(8, 200, 14336), (32, 4128, 4096)])
+def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k):
+    rng = np.random.default_rng(920 + t + m)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     bad, nan_rows = _poison(w_raw, t, n, k // 256, rng)
     good = np.setdiff1d(np.arange(n), bad)
