@@ -49,9 +49,11 @@ def _both(L, ctx, h, x, n, dev):
     (Q4_K, 1000, 4096, (1, 1)),        # fused decode GEMV (no scratch)
     (Q4_K, 1000, 4096, (8, 4)),        # pre-quantised multi-row GEMV
     (Q6_K, 700, 4096, (300, 40)),      # tall / k-sliced MFMA tiles
-    (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then k-sliced
-    (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then k-sliced (slices added in the kernel)
-    (Q4_K, 8192, 4096, (16, 13)),      # slices added in the kernel twice (tile counters left zero)
+    (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then the integer matrix-core decode (split)
+    (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then the integer matrix-core decode
+    (Q6_K, 8192, 4096, (16, 13)),      # slices added in the kernel twice (tile counters left zero)
+    (Q4_K, 4096, 4096, (8, 6)),        # integer matrix-core decode, two workgroups per tile (partials, counters)
+    (Q5_K, 4096, 4096, (32, 12)),      # the same at 32 and 16 rows
     (Q8_0, 512, 4096, (64, 12)),       # Q8_0 on MFMA
     (Q4_0, 300, 1184, (20, 9)),        # activation scratch + GEMV row chunks (k % 256 != 0)
     (Q4_1, 300, 1024, (20, 9)),        # MFMA with the offset k-step operands in the workspace
