@@ -571,8 +571,14 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
         x = x_outliers(B, 4096)
         for name, qms, nbytes in (("q6_k_head_128256x4096", head, hb), ("q5_k_gate_up_14336x4096", q5, q5b)):
             us = timed_rot(qms, x, 10 if qms is head else 20)
+            if B <= 4:
+                path = "decode GEMV quantising the rows of x in its prologue (one launch)"
+            elif qms is head:
+                path = "Q8_K quantisation, then the multi-row decode GEMV (Q6_K)"
+            else:
+                path = "Q8_K quantisation, then the integer matrix-core kernel (v_mfma_i32_32x32x32_i8)"
             out[f"{name}_b{B}"] = {"us": round(us, 2), "weight_GB/s": round(nbytes / us / 1e3, 1),
-                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "path": path}
         log(f"configs[2] batch {B}: head {out[f'q6_k_head_128256x4096_b{B}']['us']} us, "
             f"q5_k {out[f'q5_k_gate_up_14336x4096_b{B}']['us']} us")
     del head, q5
@@ -594,7 +600,10 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
                 "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
                 "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                 "weight_GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-                "bound": "hbm" if M <= 64 else "mfma"}
+                "bound": "hbm" if M <= 64 else "mfma",
+                "path": ("Q8_K quantisation, then the integer matrix-core kernel (v_mfma_i32_32x32x32_i8, "
+                         "the reference's integer sums)" if M <= 32 else
+                         "fp16 operand pre-pass, then the fp16 MFMA GEMM (v_mfma_f32_32x32x16_f16)")}
             log(f"configs[3] {name} M={M}: {us:.1f} us")
         del qms
         torch.cuda.empty_cache()
