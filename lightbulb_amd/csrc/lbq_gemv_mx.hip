@@ -1,4 +1,4 @@
-// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 2 <= m <= 8
+// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 2 <= m <= 32
 // (the shapes gemv_mx_serves admits),
 // Q8_K activation rows against Q4_K / Q5_K weights, in the reference's integer
 // arithmetic (candle-core 0.10.2 k_quants.rs, BlockQ4K / BlockQ5K vec_dot with
@@ -17,23 +17,25 @@
 // every operand and partial sum is an integer below 2^24, so it is exact too.
 // The block then adds d*dx*isum - dmin*dx*msum in f32, as the decode GEMV does.
 // Where the multi-row decode kernel re-does its 16 sdot4 per 64 weights for every
-// activation row, the matrix core does all rows at once: its VALU work per weight
-// does not grow with m.
+// activation row, the matrix core does all rows at once: its MFMA work per weight
+// does not grow with m (up to the tile's 32 rows), only the per-row scaling does.
 //
 // Workgroup: 32 weight rows, four (or, with at most one workgroup per CU, eight)
 // waves splitting the row's blocks into contiguous ranges; the partial tiles are
-// added in wave order in LDS.
+// added in wave order in LDS.  With few tiles, two workgroups share a tile's
+// blocks (split k, MxSplit below).
 //
-// Activations go through a wave-private LDS stage.  Per block, the wave's eight
-// activation rows (2 KB of codes, 256 B of 16-value sums; rows past m repeat row
-// m - 1) arrive by three loads in which every lane fetches its own 16-byte chunk
-// -- two blocks ahead, into registers -- and are written to the stage one block
-// ahead; the A operands are LDS reads.  A block then costs three activation loads
-// (not nine) and 24 activation registers (not 72), for three waves per SIMD.
-// Rows are 256 bytes apart in the stage, so chunk c of row r sits in slot
-// c ^ (r & 15): the 16 distinct chunks an A read touches fall in different banks.
-// Weights: one block ahead in registers (a deeper ring measured slower: it costs
-// waves per SIMD).
+// Activations go through a wave-private LDS stage holding MR rows (8, 16 or 32:
+// the launch's m rounded up).  Per block (MR * 256 B of codes, MR * 32 B of
+// 16-value sums) every lane fetches its own 16-byte chunks -- MR / 4 code chunks
+// and one sums chunk, two blocks ahead, into registers -- which are written to the
+// stage one block ahead; the A operands are LDS reads.  At MR = 8 a block then
+// costs three activation loads (not nine per-lane A-operand loads) and 24
+// activation registers (not 72), for three waves per SIMD.  Stage rows past m hold
+// a copy of row m - 1 or stale bytes and are never read.  Rows are 256 bytes apart in the stage, so chunk c of
+// row r sits in slot c ^ (r & 15): the 16 distinct chunks an A read touches fall
+// in different banks.  Weights: one block ahead in registers (a deeper ring
+// measured slower: it costs waves per SIMD).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
