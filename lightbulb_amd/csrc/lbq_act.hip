@@ -27,7 +27,11 @@ namespace lbq {
 template <bool GGUF_OUT, bool VEC_IN>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int64_t nblocks, int8_t *__restrict__ xq,
                                                    float *__restrict__ xd, int16_t *__restrict__ xbs,
-                                                   uint8_t *__restrict__ gguf) {
+                                                   uint8_t *__restrict__ gguf, ZeroList zero) {
+    for (int z = 0; z < zero.count; z++) {
+        float *p = zero.p[z];
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < zero.n[z]; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
+    }
     const int sub = threadIdx.x & 15;
     // the 16 lanes of a row share the block (wave-uniform exits only at the end)
     const int64_t blk0 = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -276,17 +280,19 @@ __global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__
 // launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd, int16_t *xbs,
-                            float *xs, uint8_t *gguf, hipStream_t st) {
+                            float *xs, uint8_t *gguf, hipStream_t st, const ZeroList *zero) {
+    const ZeroList zl = zero ? *zero : ZeroList{};
+    if (zl.count && act_type != TYPE_Q8_K) return hipErrorInvalidValue;
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);
         const dim3 grid((unsigned)((nb + 15) / 16));
         if (gguf) {
-            if (vec) k_quant_q8k<true, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
-            else k_quant_q8k<true, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
+            if (vec) k_quant_q8k<true, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);
+            else k_quant_q8k<true, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);
         } else {
-            if (vec) k_quant_q8k<false, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
-            else k_quant_q8k<false, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf);
+            if (vec) k_quant_q8k<false, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);
+            else k_quant_q8k<false, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);
         }
     } else if (act_type == TYPE_Q8_0 || act_type == TYPE_Q8_1) {
         const int64_t nb = m * (k / QK8_0);

@@ -213,10 +213,12 @@ lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
                         q81 ? reinterpret_cast<const float *>(base + L.bs_off) : nullptr};
 }
 
-// the activation quantisation into the split layout of av
-hipError_t quant_into(int act_type, const float *d_x, int64_t m, int64_t k, const lbq::ActView &av, hipStream_t st) {
+// the activation quantisation into the split layout of av (zeroing the ranges of
+// `zero` in the same launch)
+hipError_t quant_into(int act_type, const float *d_x, int64_t m, int64_t k, const lbq::ActView &av, hipStream_t st,
+                      const lbq::ZeroList *zero = nullptr) {
     return lbq::launch_quant_act(act_type, d_x, m, k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
-                                 const_cast<int16_t *>(av.xbs), const_cast<float *>(av.xs), nullptr, st);
+                                 const_cast<int16_t *>(av.xbs), const_cast<float *>(av.xs), nullptr, st, zero);
 }
 
 // Device memory of one forward call: the quantised activations, then the batched
@@ -263,20 +265,34 @@ struct Scratch {
 
 // Batch decode on the matrix cores for this weight and row count
 static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 32 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
+// ... with its two split halves added into y, which the quantisation launch zeroes
+static bool mx_adds(const lbq_weight *w, int64_t m) { return uses_mx(w, m) && lbq::gemv_mx_adds(w->type, w->n, w->k, (int)m); }
+
+// adds y (m rows of w) to the quantisation launch's zero list where the
+// matrix-core kernel adds into it; returns whether it did
+static bool zero_for_mx(lbq::ZeroList &zl, const lbq_weight *w, int64_t m, float *y) {
+    if (!mx_adds(w, m) || zl.count >= 4) return false;
+    zl.p[zl.count] = y;
+    zl.n[zl.count] = m * w->n;
+    zl.count++;
+    return true;
+}
 
 // The dot half of QMatMul::forward: decode GEMV for m <= 8 (the i8 matrix-core
 // kernel at m = 5..8 where it serves), MFMA GEMM above.
-int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st) {
+int run_dot(Scratch &sc, const lbq_weight *w, const lbq::ActView &av, int64_t m, float *d_y, hipStream_t st,
+            bool y_zeroed = false) {
     hipError_t e;
     if (uses_mx(w, m)) {
-        const size_t wsb = lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m);
+        const bool add = y_zeroed && mx_adds(w, m);
+        const size_t wsb = add ? 0 : lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m);
         uint8_t *ws = nullptr;
         if (wsb) {
             int s = sc.ws(wsb, &ws);
             if (s) return s;
         }
         e = lbq::launch_gemv_mx(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y,
-                                reinterpret_cast<float *>(ws), sc.counters(), st);
+                                reinterpret_cast<float *>(ws), sc.counters(), st, add);
     } else if (m <= 8) {
         e = lbq::launch_gemv(w->type, w->d_blocks, w->n, w->k, w->row_bytes, av, (int)m, d_y, st);
     } else {
@@ -329,17 +345,20 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
     uint8_t *abuf = nullptr;
     int s = sc.act(L.total, &abuf);
     if (s) return s;
+    lbq::ZeroList zl;
+    const bool zeroed = zero_for_mx(zl, w, m, d_y);
     {  // reserve the GEMM's (or the matrix-core decode's) workspace too before anything is launched
         uint8_t *ws = nullptr;
-        const size_t wsb = uses_mx(w, m) ? lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m)
+        const size_t wsb = zeroed        ? 0
+                           : uses_mx(w, m) ? lbq::gemv_mx_workspace_bytes(w->type, w->n, w->k, (int)m)
                            : m > 8       ? lbq::gemm_workspace_bytes(w->type, w->n, w->k, m)
                                          : 0;
         if (wsb && (s = sc.ws(wsb, &ws))) return s;
     }
     const lbq::ActView av = view_of(abuf, L, w->k);
-    hipError_t e = quant_into(act_type, d_x, m, w->k, av, st);
+    hipError_t e = quant_into(act_type, d_x, m, w->k, av, st, &zl);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
-    return run_dot(sc, w, av, m, d_y, st);
+    return run_dot(sc, w, av, m, d_y, st, zeroed);
 }
 
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
@@ -677,6 +696,9 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
             all_in_kernel = all_in_kernel && (mx[i] || in_kernel[i]);
         }
         const bool fused_prepass = !all_in_kernel && lbq::gemm_prepass_fuses_quant(w0->type, w0->k, d_x);
+        lbq::ZeroList zl;
+        bool zeroed[LBQ_GROUP_MAX];
+        for (int i = 0; i < count; i++) zeroed[i] = mx[i] && zero_for_mx(zl, ws[i], m, d_ys[i]);
         if ((any_mx || (!all_in_kernel && !fused_prepass)) && (s = ensure_scratch(ctx, L.total))) return s;
         const lbq::ActView av = ctx->scratch ? view_of(ctx->scratch, L, w0->k) : lbq::ActView{nullptr, nullptr, nullptr, w0->k, L.nb};
         bool quantised = false;
@@ -687,7 +709,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
             const lbq::ActView none{nullptr, nullptr, nullptr, w0->k, L.nb};
             e = lbq::gemm_prepass(w0->type, w0->k, none, d_x, m, ctx->ws, st);
         } else {
-            e = quant_into(act_type, d_x, m, w0->k, av, st);
+            e = quant_into(act_type, d_x, m, w0->k, av, st, &zl);
             quantised = true;
             if (e == hipSuccess) e = lbq::gemm_prepass(w0->type, w0->k, av, nullptr, m, ctx->ws, st);
         }
@@ -699,13 +721,13 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
             if (e != hipSuccess) return hip_fail(e, "grouped matmul launch");
         }
         if (!any_mx) return LBQ_OK;
-        if (!quantised && (e = quant_into(act_type, d_x, m, w0->k, av, st)) != hipSuccess)
+        if (!quantised && (e = quant_into(act_type, d_x, m, w0->k, av, st, &zl)) != hipSuccess)
             return hip_fail(e, "activation quantisation launch");
         for (int i = 0; i < count; i++) {
             if (!mx[i]) continue;
             Scratch sc;
             sc.ctx = ctx;
-            if ((s = run_dot(sc, ws[i], av, m, d_ys[i], st))) return s;
+            if ((s = run_dot(sc, ws[i], av, m, d_ys[i], st, zeroed[i]))) return s;
         }
         return LBQ_OK;
     }
@@ -714,12 +736,15 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     int s = ensure_scratch(ctx, L.total);
     if (s) return s;
     const lbq::ActView av = view_of(ctx->scratch, L, w0->k);
-    hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st);
+    lbq::ZeroList zl;
+    bool zeroed[LBQ_GROUP_MAX];
+    for (int i = 0; i < count; i++) zeroed[i] = zero_for_mx(zl, ws[i], m, d_ys[i]);
+    hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st, &zl);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     for (int i = 0; i < count; i++) {
         Scratch sc;
         sc.ctx = ctx;
-        s = run_dot(sc, ws[i], av, m, d_ys[i], st);
+        s = run_dot(sc, ws[i], av, m, d_ys[i], st, zeroed[i]);
         if (s) return s;
     }
     return LBQ_OK;

@@ -147,10 +147,15 @@ struct MxX {
 // next call.
 constexpr int MX_MAX_SPLITS = 16;
 
+// With two workgroups per tile and a y set to zero beforehand (`add`), each
+// workgroup instead adds its half into y atomically: two addends give the same
+// bits in either order, and no partials, counter or read-back are needed (1-2 us
+// less per call on the 4096-row shapes).
 struct MxSplit {
     int splits;     // workgroups per 32-row tile (1: no partials)
     float *part;    // [splits][m][n]
     uint32_t *cnt;  // one zeroed word per tile
+    int add;        // splits == 2 and y zeroed: atomic adds into y
 };
 
 // MR = the activation rows a launch can hold (8, 16 or 32; m <= MR)
@@ -255,10 +260,11 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
         const int i = mx_row(e, h);
         if (i < m && col < n) {
             if (sp.splits == 1) y[(int64_t)i * n + col] = s;
+            else if (sp.add) atomicAdd(y + (int64_t)i * n + col, s);
             else __hip_atomic_store(sp.part + ((int64_t)part * m + i) * n + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (sp.splits == 1) return;
+    if (sp.splits == 1 || sp.add) return;
     __shared__ uint32_t last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -325,13 +331,18 @@ size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m) {
     return s > 1 ? (size_t)s * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
+bool gemv_mx_adds(int type, int64_t n, int64_t k, int m) {
+    return gemv_mx_serves(type, n, k, m) && mx_splits(n, k, m) == 2;
+}
+
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
-                          float *y, float *ws, uint32_t *counters, hipStream_t st) {
+                          float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed) {
     if (!gemv_mx_serves(type, n, k, m)) return hipErrorNotSupported;
     const int nb = (int)(k / 256);
     if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
-    MxSplit sp{mx_splits(n, k, m), ws, counters};
-    if (sp.splits > 1 && (!ws || !counters)) return hipErrorInvalidValue;
+    MxSplit sp{mx_splits(n, k, m), ws, counters, 0};
+    sp.add = sp.splits == 2 && y_zeroed;
+    if (sp.splits > 1 && !sp.add && (!ws || !counters)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)((n + 31) / 32 * sp.splits);
     // Up to one workgroup per CU: eight waves split a row's blocks (2 per wave at
     // k = 4096), A operands read just in time to stay within four waves per SIMD

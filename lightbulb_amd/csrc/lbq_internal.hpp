@@ -95,11 +95,20 @@ struct RowMap {
 };
 RowMap single_row_map(const uint8_t *w, int64_t n, float *y);
 
+// f32 ranges a Q8_K quantisation launch also sets to zero (the outputs that the
+// matrix-core decode kernel then adds its two split halves into)
+struct ZeroList {
+    float *p[4] = {nullptr, nullptr, nullptr, nullptr};
+    int64_t n[4] = {0, 0, 0, 0};
+    int count = 0;
+};
+
 // Quantise x[m][k] to Q8_K (act_type 15), Q8_0 (8) or Q8_1 (9).  Writes the split
 // internal layout (codes xq, scales xd, Q8_K sub-block sums xbs, Q8_1 block sums
-// xs) when gguf == nullptr, else GGUF blocks to gguf.
+// xs) when gguf == nullptr, else GGUF blocks to gguf.  Q8_K: the same launch
+// zeroes the ranges of `zero` (if any).
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
-                            int16_t *xbs, float *xs, uint8_t *gguf, hipStream_t st);
+                            int16_t *xbs, float *xs, uint8_t *gguf, hipStream_t st, const ZeroList *zero = nullptr);
 
 // Dequantise nelem values (multiple of the block size) of `type` blocks to f32
 // (F32 / F16: any nelem, a copy / an exact widening).
@@ -122,8 +131,12 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m);
 // device memory launch_gemv_mx needs at ws (0: none); counters: KS_COUNTERS
 // zeroed words (each launch leaves them zero)
 size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m);
+// true where the launch splits each tile over two workgroups: given a y that is
+// already zero (y_zeroed), their halves are then added into it atomically (two
+// addends: the same bits in either order) instead of through the workspace
+bool gemv_mx_adds(int type, int64_t n, int64_t k, int m);
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
-                          float *y, float *ws, uint32_t *counters, hipStream_t st);
+                          float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed = false);
 
 // True when the decode GEMV quantises x itself (m = 1, k within the fast path,
 // x 16-byte aligned).

@@ -111,3 +111,34 @@ def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k):
     assert np.array_equal(np.isfinite(y), np.isfinite(ref))
     assert np.isnan(y[:, nan_rows]).all() and np.isnan(ref[:, nan_rows]).all()
     assert_rows_close(y[:, good], ref[:, good], 1e-4)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (16, 4096, 14336), (32, 4096, 2048), (6, 2080, 8192)])
+def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
+    # Up to 4096 rows a tile is split over two workgroups.  forward() zeroes y in the
+    # quantisation launch and the halves are added into it atomically; the
+    # pre-quantised handle (no quantisation launch) adds them through the workspace
+    # and a tile counter.  Two addends: both give the same bits, as does a grouped
+    # call (one quantisation zeroing both outputs) for each of its weights.
+    import torch
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor, qmatmul_group
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(930 + t + m + n + k)
+    raws = [bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3) for _ in range(2)]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r in raws]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    xd = to_dev(x, dev)
+    print(f"mx split t={t} m={m} n={n} k={k}", flush=True)
+    y = qms[0].forward(xd)
+    y2 = qms[0].forward_quantized(QActivation.for_weight(qms[0], m).quantize(xd))
+    yg = qmatmul_group(qms, xd)
+    y1b = qms[1].forward(xd)
+    torch.cuda.synchronize()
+    ref = oracle.qmatmul(t, raws[0], n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y.cpu().numpy(), ref, 1e-4)
+    bits = lambda a: a.cpu().numpy().view(np.uint32)
+    assert np.array_equal(bits(y), bits(y2))
+    assert np.array_equal(bits(y), bits(yg[0]))
+    assert np.array_equal(bits(y1b), bits(yg[1]))
