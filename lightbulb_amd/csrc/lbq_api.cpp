@@ -95,6 +95,7 @@ Tuning tuning_from_env() {
     t.gemv_mx_wide_off = getenv("LBQ_GEMV_MX_WIDE_OFF") != nullptr;
     t.gemv_mx_splits = env_int("LBQ_GEMV_MX_SPLITS");
     t.gemv_mx_waves = env_int("LBQ_GEMV_MX_WAVES");
+    t.gemv_mx_all = getenv("LBQ_GEMV_MX_ALL") != nullptr;
     if (const char *e = getenv("LBQ_GEMV")) {
         int v[4] = {0, 0, 0, 0};
         if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)

@@ -301,12 +301,15 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     if (k % 256 || k / 256 > 64 || m < 2 || m > 32 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
     // m = 9..32 (the fp16 GEMM otherwise): Q4_K 14336 x 4096 m = 16 / 32 22.1 / 23.4
     // -> 18.3 / 21.8 us, Q5_K m = 12 / 24 23.9 / 24.3 -> 18.4 / 21.8, 4096 x 14336
-    // m = 16 23.6 -> 20.3, 4096 x 4096 m = 32 16.1 -> 14.9 (two workgroups per
-    // tile); with 1024 / 2048 rows the GEMM stays ahead (m = 32 12.9 against 13.5,
-    // m = 16 11.3 against 11.8)
-    if (m > 8) return !tuning().gemv_mx_wide_off && n >= 4096;
+    // m = 16 23.6 -> 20.3, 4096 x 4096 m = 32 16.1 -> 14.9; with two workgroups per
+    // tile adding into y atomically, 1024 / 2048 rows too (1024 x 4096 m = 16 / 32
+    // 10.7 / 13.0 -> 10.2 / 11.9, 2048 x 4096 11.3 / 13.9 -> 10.4 / 12.1), and at
+    // m = 5..8 from 1024 rows (1024 x 4096 m = 8 11.2 -> 9.5).  Below 1024 rows:
+    // not measured, the other kernels keep those.
+    if (tuning().gemv_mx_all) return m <= 8 || !tuning().gemv_mx_wide_off;
+    if (m > 8) return !tuning().gemv_mx_wide_off && n >= 1024;
     if (k / 256 > 32) return true;  // the multi-row decode kernel cannot hold these rows
-    return m >= 5 && n >= 2048;
+    return m >= 5 && n >= 1024;
 }
 
 // Workgroups per 32-row tile: two up to 128 tiles (4096 rows), which fills the

@@ -51,7 +51,7 @@ struct ActView;
 //   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
 //   LBQ_GEMV_ROWS_OFF                               decode GEMV plan
 //   LBQ_GEMV_MX_OFF, LBQ_GEMV_MX_WIDE_OFF (m = 9..32 only),
-//   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8
+//   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8, LBQ_GEMV_MX_ALL
 //                                                   matrix-core batch decode plan
 struct Tuning {
     bool gemm_ks64 = false, gemm_no_ks = false, gemm_no_tall = false;
@@ -66,6 +66,7 @@ struct Tuning {
     bool gemv_mx_off = false;  // batch decode never on the matrix cores
     bool gemv_mx_wide_off = false;  // m = 9..32 never on the integer matrix-core kernel
     int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)
+    bool gemv_mx_all = false;  // matrix-core batch decode wherever it can run (m = 2..32, Q4_K / Q5_K)
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
 };
 Tuning tuning_from_env();

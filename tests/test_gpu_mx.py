@@ -1,5 +1,5 @@
-"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..8 with
-n >= 2048, m = 2..8 at k > 8192, and m = 9..32 with n >= 4096) against the oracle.
+"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..32 with
+n >= 1024, and m = 2..8 at k > 8192) against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -44,9 +44,9 @@ def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
 
 
-# m = 9..32 runs on the kernel from 4096 rows: 128 tiles (two workgroups each), 129-130
-# tiles (one, eight waves), 257 (one, four waves); k from 2 to 64 blocks
-WIDE_SHAPES = [(4096, 4096), (4100, 1280), (4096, 512), (8224, 1024), (4096, 14336), (4160, 16384)]
+# m = 9..32 runs on the kernel from 1024 rows: 32-128 tiles (two workgroups each),
+# 129-130 tiles (one, eight waves), 257 (one, four waves); k from 2 to 64 blocks
+WIDE_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (4096, 512), (8224, 1024), (4096, 14336), (4160, 16384)]
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
