@@ -96,6 +96,7 @@ Tuning tuning_from_env() {
     t.gemv_mx_splits = env_int("LBQ_GEMV_MX_SPLITS");
     t.gemv_mx_waves = env_int("LBQ_GEMV_MX_WAVES");
     t.gemv_mx_all = getenv("LBQ_GEMV_MX_ALL") != nullptr;
+    t.gemv_mx_pair_off = getenv("LBQ_GEMV_MX_PAIR_OFF") != nullptr;
     if (const char *e = getenv("LBQ_GEMV")) {
         int v[4] = {0, 0, 0, 0};
         if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)
@@ -773,6 +774,19 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
         hipError_t e = lbq::launch_gemv_silu_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n, w_gate->k,
                                                   w_gate->row_bytes, d_x, d_out, st);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "gate/up launch");
+    }
+    if (m >= 2 && lbq::gemv_mx_pair_serves(w_gate->type, w_gate->n, w_gate->k, (int)m)) {
+        // one Q8_K quantisation, then both weights and the product in one launch
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        const ActLayout L = act_layout(lbq::vec_dot_type(w_gate->type), m, w_gate->k);
+        int s = ensure_scratch(ctx, L.total);
+        if (s) return s;
+        const lbq::ActView av = view_of(ctx->scratch, L, w_gate->k);
+        hipError_t e = quant_into(L.act_type, d_x, m, w_gate->k, av, st);
+        if (e == hipSuccess)
+            e = lbq::launch_gemv_mx_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n, w_gate->k,
+                                         w_gate->row_bytes, av, (int)m, d_out, st);
+        return e == hipSuccess ? LBQ_OK : hip_fail(e, "gate/up launch");
     }
     // otherwise gate and up through the grouped path into context memory, then
     // one elementwise launch

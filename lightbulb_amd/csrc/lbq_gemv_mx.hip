@@ -158,10 +158,17 @@ struct MxSplit {
     int add;        // splits == 2 and y zeroed: atomic adds into y
 };
 
-// MR = the activation rows a launch can hold (8, 16 or 32; m <= MR)
-template <int TYPE, int MX_WAVES, int MR>
+// MR = the activation rows a launch can hold (8, 16 or 32; m <= MR).
+// PAIR: a gate/up pair (W gate, W2 up, n rows each; one workgroup per tile, no
+// split): a tile holds gate rows 16t..16t+15 in columns 0..15 and the same up rows
+// in columns 16..31, and the epilogue writes silu(gate) * up (candle's f32 silu,
+// v / (1 + exp(-v)), as the separate product launch computes it) for its 16 rows.
+// Every column's sums are those of the single-weight launch with the same wave
+// count, so the product has the bits of the separate gate and up calls.
+template <int TYPE, int MX_WAVES, int MR, bool PAIR = false>
 __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
-                                                         int nb, ActView act, int m, float *__restrict__ y, MxSplit sp) {
+                                                         int nb, ActView act, int m, float *__restrict__ y, MxSplit sp,
+                                                         const uint8_t *__restrict__ W2 = nullptr) {
     constexpr int E = MR / 2, STAGE = MR * 256 + MR * 32;  // codes of MR rows, then their 16-value sums
     static_assert(E * 64 * 4 <= STAGE, "the partial tile overlays the wave's stage");
     extern __shared__ __align__(16) float sdx[];  // [nb][MR]: dx of block b, activation row i (0 past m)
@@ -169,9 +176,10 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int j = lane & 31, h = lane >> 5;
     const int tile = blockIdx.x / sp.splits, part = blockIdx.x % sp.splits;
-    const int row0 = tile * 32;
+    const int row0 = tile * (PAIR ? 16 : 32);
     const int64_t k = act.k;
-    const uint8_t *wr = W + (int64_t)min(row0 + j, n - 1) * row_bytes;
+    const uint8_t *wr = PAIR ? (j < 16 ? W : W2) + (int64_t)min(row0 + (j & 15), n - 1) * row_bytes
+                             : W + (int64_t)min(row0 + j, n - 1) * row_bytes;
     const int p0 = part * nb / sp.splits, np = (part + 1) * nb / sp.splits - p0;  // this workgroup's blocks
     const int b0 = p0 + wave * np / MX_WAVES, b1 = p0 + (wave + 1) * np / MX_WAVES;
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
@@ -252,6 +260,22 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
     __syncthreads();
     // accumulator e (C row mx_row(e, h)) is stored by wave e % MX_WAVES, the
     // partials added in wave order
+    if constexpr (PAIR) {
+        const int col = row0 + (lane & 15);
+        if (j >= 16) return;
+        for (int e = wave; e < E; e += MX_WAVES) {
+            float g = reinterpret_cast<const float *>(xs[0])[e * 64 + lane];
+            float u = reinterpret_cast<const float *>(xs[0])[e * 64 + lane + 16];
+#pragma unroll
+            for (int w = 1; w < MX_WAVES; w++) {
+                g += reinterpret_cast<const float *>(xs[w])[e * 64 + lane];
+                u += reinterpret_cast<const float *>(xs[w])[e * 64 + lane + 16];
+            }
+            const int i = mx_row(e, h);
+            if (i < m && col < n) y[(int64_t)i * n + col] = g / (1.f + expf(-g)) * u;
+        }
+        return;
+    }
     const int col = row0 + j;
     for (int e = wave; e < E; e += MX_WAVES) {
         float s = reinterpret_cast<const float *>(xs[0])[e * 64 + lane];
@@ -338,6 +362,35 @@ bool gemv_mx_adds(int type, int64_t n, int64_t k, int m) {
     return gemv_mx_serves(type, n, k, m) && mx_splits(n, k, m) == 2;
 }
 
+bool gemv_mx_pair_serves(int type, int64_t n, int64_t k, int m) {
+    // above 8192 rows the single-weight launches take one four-wave workgroup per
+    // 32-row tile, as the pair launch does per 16-row pair tile (the same sums)
+    return !tuning().gemv_mx_pair_off && n > 8192 && gemv_mx_serves(type, n, k, m) && mx_splits(n, k, m) == 1 &&
+           (n + 31) / 32 > (int64_t)num_cus() && !tuning().gemv_mx_waves;
+}
+
+hipError_t launch_gemv_mx_pair(int type, const uint8_t *w_gate, const uint8_t *w_up, int64_t n, int64_t k,
+                               int64_t row_bytes, const ActView &act, int m, float *out, hipStream_t st) {
+    if (!gemv_mx_pair_serves(type, n, k, m)) return hipErrorNotSupported;
+    const int nb = (int)(k / 256);
+    if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
+    const MxSplit sp{1, nullptr, nullptr, 0};
+    const unsigned grid = (unsigned)((n + 15) / 16);
+    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
+    const size_t lds = (size_t)nb * mr * sizeof(float);
+    auto go = [&](auto kern) { kern<<<grid, 64 * 4, lds, st>>>(w_gate, row_bytes, (int)n, nb, act, m, out, sp, w_up); };
+    if (type == TYPE_Q4_K) {
+        if (mr == 8) go(k_gemv_mx<TYPE_Q4_K, 4, 8, true>);
+        else if (mr == 16) go(k_gemv_mx<TYPE_Q4_K, 4, 16, true>);
+        else go(k_gemv_mx<TYPE_Q4_K, 4, 32, true>);
+    } else {
+        if (mr == 8) go(k_gemv_mx<TYPE_Q5_K, 4, 8, true>);
+        else if (mr == 16) go(k_gemv_mx<TYPE_Q5_K, 4, 16, true>);
+        else go(k_gemv_mx<TYPE_Q5_K, 4, 32, true>);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
                           float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed) {
     if (!gemv_mx_serves(type, n, k, m)) return hipErrorNotSupported;
@@ -354,7 +407,7 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
     const bool w8 = tuning().gemv_mx_waves ? tuning().gemv_mx_waves == 8 : (int64_t)grid <= (int64_t)num_cus();
     const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
     const size_t lds = (size_t)nb * mr * sizeof(float);
-    auto go = [&](auto kern, int waves) { kern<<<grid, 64 * waves, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y, sp); };
+    auto go = [&](auto kern, int waves) { kern<<<grid, 64 * waves, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y, sp, nullptr); };
     if (type == TYPE_Q4_K) {
         if (mr == 8) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 8>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 8>, 4);
         else if (mr == 16) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 16>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 16>, 4);

@@ -51,7 +51,8 @@ struct ActView;
 //   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
 //   LBQ_GEMV_ROWS_OFF                               decode GEMV plan
 //   LBQ_GEMV_MX_OFF, LBQ_GEMV_MX_WIDE_OFF (m = 9..32 only),
-//   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8, LBQ_GEMV_MX_ALL
+//   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8, LBQ_GEMV_MX_ALL,
+//   LBQ_GEMV_MX_PAIR_OFF
 //                                                   matrix-core batch decode plan
 struct Tuning {
     bool gemm_ks64 = false, gemm_no_ks = false, gemm_no_tall = false;
@@ -67,6 +68,7 @@ struct Tuning {
     bool gemv_mx_wide_off = false;  // m = 9..32 never on the integer matrix-core kernel
     int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)
     bool gemv_mx_all = false;  // matrix-core batch decode wherever it can run (m = 2..32, Q4_K / Q5_K)
+    bool gemv_mx_pair_off = false;  // gate/up pairs at m = 2..32 as two launches and a product launch
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
 };
 Tuning tuning_from_env();
@@ -138,6 +140,11 @@ size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m);
 bool gemv_mx_adds(int type, int64_t n, int64_t k, int m);
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
                           float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed = false);
+// gate/up pair at m = 2..32: out[i][r] = silu(x_i . gate_r) * (x_i . up_r) in one
+// launch, with the bits of the two single-weight launches and the product launch
+bool gemv_mx_pair_serves(int type, int64_t n, int64_t k, int m);
+hipError_t launch_gemv_mx_pair(int type, const uint8_t *w_gate, const uint8_t *w_up, int64_t n, int64_t k,
+                               int64_t row_bytes, const ActView &act, int m, float *out, hipStream_t st);
 
 // True when the decode GEMV quantises x itself (m = 1, k within the fast path,
 // x 16-byte aligned).

@@ -142,3 +142,58 @@ def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
     assert np.array_equal(bits(y), bits(y2))
     assert np.array_equal(bits(y), bits(yg[0]))
     assert np.array_equal(bits(y1b), bits(yg[1]))
+
+
+def _gate_up_env(monkeypatch, env, t, g_raw, u_raw, n, k, x, dev):
+    """lbq_gate_up_silu_f32 through a context created with the given plan overrides."""
+    import ctypes
+    import torch
+    from lightbulb_amd import _lib
+    from test_gpu_parity import to_dev
+    L = _lib.lib()
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    ctx = ctypes.c_void_p()
+    try:
+        _lib.check(L.lbq_init(dev.index or 0, ctypes.byref(ctx)))
+    finally:
+        for key in env:
+            monkeypatch.delenv(key)
+    hs, keep = [], []
+    try:
+        for raw in (g_raw, u_raw):
+            wd = to_dev(raw, dev)
+            keep.append(wd)
+            h = ctypes.c_void_p()
+            _lib.check(L.lbq_weight_wrap_device(ctx, t, n, k, wd.data_ptr(), wd.numel(), ctypes.byref(h)))
+            hs.append(h)
+        xd = to_dev(x, dev)
+        out = torch.empty(x.shape[0], n, device=dev)
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(L.lbq_gate_up_silu_f32(ctx, hs[0], hs[1], xd.data_ptr(), x.shape[0], out.data_ptr(), st))
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+    finally:
+        for h in hs:
+            L.lbq_weight_destroy(h)
+        L.lbq_ctx_destroy(ctx)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m,n,k", [(2, 8224, 9216), (5, 8224, 2048), (16, 8240, 1024), (32, 8256, 4096)])
+def test_mx_gate_up_pair(oracle, lbq, dev, t, m, n, k, monkeypatch):
+    # above 8192 rows a gate/up pair at m = 2..32 is one launch (16 gate and 16 up
+    # rows per tile, silu(gate) * up in the epilogue): the bits of the two separate
+    # launches and the product launch (LBQ_GEMV_MX_PAIR_OFF), and the oracle's value
+    rng = np.random.default_rng(940 + t + m + n + k)
+    g_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    u_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx pair t={t} m={m} n={n} k={k}", flush=True)
+    y = _gate_up_env(monkeypatch, {}, t, g_raw, u_raw, n, k, x, dev)
+    off = _gate_up_env(monkeypatch, {"LBQ_GEMV_MX_PAIR_OFF": "1"}, t, g_raw, u_raw, n, k, x, dev)
+    assert np.array_equal(y.view(np.uint32), off.view(np.uint32))
+    gr = oracle.qmatmul(t, g_raw, n, k, x, nthreads=8).astype(np.float64)
+    ur = oracle.qmatmul(t, u_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, gr / (1.0 + np.exp(-gr)) * ur, 1e-4)
