@@ -160,9 +160,9 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
  * m = 1, and for Q4_K / Q5_K weights of more than 8192 rows at m = 2..32 (after
  * one activation quantisation), both weights stream through one launch and the
  * product is formed in its epilogue, so neither product is written out; otherwise
- * the grouped path fills context memory and one elementwise launch combines it.
- * Either way the result has the bits of the separate products combined by that
- * elementwise launch.  gate and up share the ggml type, n and k. */
+ * the grouped path fills context memory and one elementwise launch combines it
+ * (the m = 2..32 pair launch gives the same bits as that).  gate and up share the
+ * ggml type, n and k. */
 int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
                          float *d_out, void *stream);
 
