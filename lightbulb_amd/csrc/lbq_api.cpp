@@ -743,6 +743,19 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     for (int i = 0; i < count; i++) zeroed[i] = zero_for_mx(zl, ws[i], m, d_ys[i]);
     hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st, &zl);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
+    bool one = count >= 2;  // every weight on the matrix-core kernel: one launch for all
+    for (int i = 0; i < count; i++) one = one && uses_mx(ws[i], m) && (!mx_adds(ws[i], m) || zeroed[i]);
+    if (one) {
+        const uint8_t *wp[LBQ_GROUP_MAX];
+        int64_t ns[LBQ_GROUP_MAX];
+        for (int i = 0; i < count; i++) {
+            wp[i] = ws[i]->d_blocks;
+            ns[i] = ws[i]->n;
+        }
+        e = lbq::launch_gemv_mx_group(w0->type, count, wp, ns, w0->k, w0->row_bytes, av, (int)m, d_ys, st);
+        if (e == hipSuccess) return LBQ_OK;
+        if (e != hipErrorNotSupported) return hip_fail(e, "grouped matmul launch");
+    }
     for (int i = 0; i < count; i++) {
         Scratch sc;
         sc.ctx = ctx;

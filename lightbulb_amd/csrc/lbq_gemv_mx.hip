@@ -165,17 +165,18 @@ struct MxSplit {
 // v / (1 + exp(-v)), as the separate product launch computes it) for its 16 rows.
 // Every column's sums are those of the single-weight launch with the same wave
 // count, so the product has the bits of the separate gate and up calls.
-template <int TYPE, int MX_WAVES, int MR, bool PAIR = false>
-__global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
-                                                         int nb, ActView act, int m, float *__restrict__ y, MxSplit sp,
-                                                         const uint8_t *__restrict__ W2 = nullptr) {
+// The body of one workgroup (bid: its index within its weight's launch).
+template <int TYPE, int MX_WAVES, int MR, bool PAIR>
+__device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int64_t row_bytes, int n, int nb,
+                                             const ActView &act, int m, float *__restrict__ y, const MxSplit &sp,
+                                             const uint8_t *__restrict__ W2, int bid) {
     constexpr int E = MR / 2, STAGE = MR * 256 + MR * 32;  // codes of MR rows, then their 16-value sums
     static_assert(E * 64 * 4 <= STAGE, "the partial tile overlays the wave's stage");
     extern __shared__ __align__(16) float sdx[];  // [nb][MR]: dx of block b, activation row i (0 past m)
     __shared__ __align__(16) uint8_t xs[MX_WAVES][STAGE];
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int tile = blockIdx.x / sp.splits, part = blockIdx.x % sp.splits;
+    const int tile = bid / sp.splits, part = bid % sp.splits;
     const int row0 = tile * (PAIR ? 16 : 32);
     const int64_t k = act.k;
     const uint8_t *wr = PAIR ? (j < 16 ? W : W2) + (int64_t)min(row0 + (j & 15), n - 1) * row_bytes
@@ -307,6 +308,34 @@ __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__rest
     if (t == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int TYPE, int MX_WAVES, int MR, bool PAIR = false>
+__global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
+                                                         int nb, ActView act, int m, float *__restrict__ y, MxSplit sp,
+                                                         const uint8_t *__restrict__ W2) {
+    mx_workgroup<TYPE, MX_WAVES, MR, PAIR>(W, row_bytes, n, nb, act, m, y, sp, W2, (int)blockIdx.x);
+}
+
+// A grouped call's weights (same type and k) in one launch: segment s owns the
+// workgroups [wg_end[s - 1], wg_end[s]) and runs them exactly as its own launch
+// would (same tiles, splits and wave count), so every output keeps its bits.
+// Two-way split segments add into their y, which the quantisation launch zeroed.
+struct MxSegs {
+    const uint8_t *w[4];
+    float *y[4];
+    int n[4], splits[4], wg_end[4];
+    int count;
+};
+
+template <int TYPE, int MX_WAVES, int MR>
+__global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx_seg(int64_t row_bytes, int nb, ActView act, int m, MxSegs g) {
+    const int bid = (int)blockIdx.x;
+    int s = 0;
+    while (s + 1 < g.count && bid >= g.wg_end[s]) s++;
+    const MxSplit sp{g.splits[s], nullptr, nullptr, g.splits[s] == 2};
+    mx_workgroup<TYPE, MX_WAVES, MR, false>(g.w[s], row_bytes, g.n[s], nb, act, m, g.y[s], sp, nullptr,
+                                            bid - (s ? g.wg_end[s - 1] : 0));
+}
+
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // Measured against the decode kernels (x quantised by the same separate pass
     // unless noted): Q5_K 14336 x 4096 m = 8 22.8 -> 18.2 us, Q4_K 14336 x 4096
@@ -360,6 +389,56 @@ size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m) {
 
 bool gemv_mx_adds(int type, int64_t n, int64_t k, int m) {
     return gemv_mx_serves(type, n, k, m) && mx_splits(n, k, m) == 2;
+}
+
+hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, const int64_t *n, int64_t k,
+                                int64_t row_bytes, const ActView &act, int m, float *const *y, hipStream_t st) {
+    if (count < 2 || count > 4) return hipErrorNotSupported;
+    const int nb = (int)(k / 256);
+    if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
+    MxSegs g{};
+    int waves = 0, wg = 0;
+    for (int i = 0; i < count; i++) {
+        if (!gemv_mx_serves(type, n[i], k, m)) return hipErrorNotSupported;
+        const int s = mx_splits(n[i], k, m);
+        if (s > 2) return hipErrorNotSupported;  // only the atomic form of a split
+        const int64_t tiles = (n[i] + 31) / 32;
+        const int wv = tuning().gemv_mx_waves ? tuning().gemv_mx_waves : tiles * s <= (int64_t)num_cus() ? 8 : 4;
+        if (i && wv != waves) return hipErrorNotSupported;  // each weight as its own launch would run it
+        waves = wv;
+        wg += (int)(tiles * s);
+        g.w[i] = w[i];
+        g.y[i] = y[i];
+        g.n[i] = (int)n[i];
+        g.splits[i] = s;
+        g.wg_end[i] = wg;
+    }
+    g.count = count;
+    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
+    const size_t lds = (size_t)nb * mr * sizeof(float);
+    auto go = [&](auto kern) { kern<<<(unsigned)wg, 64 * waves, lds, st>>>(row_bytes, nb, act, m, g); };
+    if (type == TYPE_Q4_K) {
+        if (waves == 8) {
+            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q4_K, 8, 8>);
+            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q4_K, 8, 16>);
+            else go(k_gemv_mx_seg<TYPE_Q4_K, 8, 32>);
+        } else {
+            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q4_K, 4, 8>);
+            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q4_K, 4, 16>);
+            else go(k_gemv_mx_seg<TYPE_Q4_K, 4, 32>);
+        }
+    } else {
+        if (waves == 8) {
+            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q5_K, 8, 8>);
+            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q5_K, 8, 16>);
+            else go(k_gemv_mx_seg<TYPE_Q5_K, 8, 32>);
+        } else {
+            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q5_K, 4, 8>);
+            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q5_K, 4, 16>);
+            else go(k_gemv_mx_seg<TYPE_Q5_K, 4, 32>);
+        }
+    }
+    return hipGetLastError();
 }
 
 bool gemv_mx_pair_serves(int type, int64_t n, int64_t k, int m) {

@@ -140,6 +140,12 @@ size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m);
 bool gemv_mx_adds(int type, int64_t n, int64_t k, int m);
 hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int64_t row_bytes, const ActView &act, int m,
                           float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed = false);
+// a grouped call's weights (2..4, same type and k, each served by the kernel with
+// at most two workgroups per tile, and the same wave count) in one launch, with the
+// bits of their own launches; every two-way split y must already be zero
+// (hipErrorNotSupported: launch them one by one)
+hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, const int64_t *n, int64_t k,
+                                int64_t row_bytes, const ActView &act, int m, float *const *y, hipStream_t st);
 // gate/up pair at m = 2..32: out[i][r] = silu(x_i . gate_r) * (x_i . up_r) in one
 // launch, with the bits of the two single-weight launches and the product launch
 bool gemv_mx_pair_serves(int type, int64_t n, int64_t k, int m);

@@ -197,3 +197,28 @@ def test_mx_gate_up_pair(oracle, lbq, dev, t, m, n, k, monkeypatch):
     gr = oracle.qmatmul(t, g_raw, n, k, x, nthreads=8).astype(np.float64)
     ur = oracle.qmatmul(t, u_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, gr / (1.0 + np.exp(-gr)) * ur, 1e-4)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m,ns,k", [(6, (4096, 1024, 2080), 4096), (16, (4096, 1024, 2080), 2048),
+                                    (32, (1024, 4096), 4096), (8, (14336, 14336), 4096)])
+def test_mx_group_one_launch(oracle, lbq, dev, t, m, ns, k):
+    # a grouped call whose weights all run on the kernel is one launch (each weight's
+    # workgroups as its own launch would run them): the bits of the separate calls
+    import torch
+    from lightbulb_amd.quantized import QMatMul, QTensor, qmatmul_group
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(950 + t + m + k + len(ns))
+    raws = [bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3) for n in ns]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xd = to_dev(x, dev)
+    print(f"mx group t={t} m={m} ns={ns} k={k}", flush=True)
+    ys = qmatmul_group(qms, xd)
+    sep = [q.forward(xd) for q in qms]
+    torch.cuda.synchronize()
+    for a, b in zip(ys, sep):
+        assert np.array_equal(a.cpu().numpy().view(np.uint32), b.cpu().numpy().view(np.uint32))
+    i = int(np.argmin(ns))
+    ref = oracle.qmatmul(t, raws[i], ns[i], k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(ys[i].cpu().numpy(), ref, 1e-4)
