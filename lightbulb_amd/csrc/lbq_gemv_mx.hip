@@ -149,8 +149,9 @@ constexpr int MX_MAX_SPLITS = 16;
 
 // With two workgroups per tile and a y set to zero beforehand (`add`), each
 // workgroup instead adds its half into y atomically: two addends give the same
-// bits in either order, and no partials, counter or read-back are needed (1-2 us
-// less per call on the 4096-row shapes).
+// bits in either order (a NaN output may carry either half's NaN payload), and no
+// partials, counter or read-back are needed (1-2 us less per call on the 4096-row
+// shapes).
 struct MxSplit {
     int splits;     // workgroups per 32-row tile (1: no partials)
     float *part;    // [splits][m][n]
