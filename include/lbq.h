@@ -113,15 +113,17 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
 
 /* y[m][n] = x[m][k] . W^T in f32 -- QMatMul::forward (candle-core 0.10.2,
  * reached through /root/reference/src/model/quantizable_linear.rs:67).
- * x and y are contiguous f32 device buffers; any leading dims of the
+ * x and y are contiguous f32 device buffers (device memory from hipMalloc: at
+ * m = 2..32 y may be written with f32 atomic adds); any leading dims of the
  * reference's [.., k] tensor are flattened into m.  The activation is
  * quantised to Q8_K (k-quant weights), Q8_1 (Q4_1/Q5_1) or Q8_0 (the other
- * 32-value types) exactly as the reference CPU path does.  For m <= 8 each
- * output is formed from integer sub-block dot products as in the reference;
- * for Q4_K/Q5_K/Q6_K/Q8_0 weights at m > 8 (Q8_0: k % 256 == 0) the products
- * run on MFMA from fp16 roundings of the same activation and weight values
- * (about 4e-4 relative on a row).  Dense F32/F16 weights are candle's dense
- * variant: no quantisation, an f32 matmul.  m == 0 is a no-op. */
+ * 32-value types) exactly as the reference CPU path does.  For m <= 8, and for
+ * Q4_K/Q5_K weights of 1024 rows or more up to m = 32, each output is formed
+ * from integer sub-block dot products as in the reference; otherwise for
+ * Q4_K/Q5_K/Q6_K/Q8_0 weights at m > 8 (Q8_0: k % 256 == 0) the products run on
+ * MFMA from fp16 roundings of the same activation and weight values (about 4e-4
+ * relative on a row).  Dense F32/F16 weights are candle's dense variant: no
+ * quantisation, an f32 matmul.  m == 0 is a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
 /* QMatMul::forward as lbq_qmatmul_f32 computes it (the same kernels, the same
