@@ -91,6 +91,7 @@ Tuning tuning_from_env() {
     }
     t.gemv1_wpc = std::max(0, env_int("LBQ_GEMV1_WPC"));
     t.gemv1_wpg = std::max(0, env_int("LBQ_GEMV1_WPG"));
+    t.gemv1_dynamic = getenv("LBQ_GEMV1_DYNAMIC") != nullptr;
     t.gemv_mx_off = getenv("LBQ_GEMV_MX_OFF") != nullptr;
     t.gemv_mx_wide_off = getenv("LBQ_GEMV_MX_WIDE_OFF") != nullptr;
     t.gemv_mx_splits = env_int("LBQ_GEMV_MX_SPLITS");

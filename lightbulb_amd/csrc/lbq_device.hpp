@@ -134,6 +134,75 @@ __device__ __forceinline__ void q8k_lane16(const float *v, int sub, uint32_t pac
     *d_out = d;
 }
 
+// max / min of each 32-lane half's two 16-lane rows (v_permlane16_swap exchanges
+// a's odd rows with the even rows of its second operand: with both a, the two
+// results hold each row and its partner row)
+__device__ __forceinline__ uint32_t row_pair_max_u32(uint32_t a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+    return max((uint32_t)r[0], (uint32_t)r[1]);
+}
+__device__ __forceinline__ uint32_t row_pair_min_u32(uint32_t a) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+    return min((uint32_t)r[0], (uint32_t)r[1]);
+}
+
+// Q8_K quantisation of one 256-value block by 32 aligned lanes, 8 consecutive
+// values per lane (lane sub = lane % 32 holds values 8 sub .. 8 sub + 7): the
+// selection and arithmetic of q8k_lane16, so the same codes and d.  Out: the
+// lane's 8 codes packed little-endian, the bsums entry sub / 2 (the codes of
+// lanes sub and sub ^ 1; both lanes hold it) and the block's d.
+__device__ __forceinline__ void q8k_lane8(const float *v, int sub, uint32_t packed[2], int *sum_out, float *d_out) {
+    float mxp = v[0], mnn = v[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) {
+        mxp = __builtin_fmaximum_numf(mxp, v[i]);
+        mnn = __builtin_fminimum_numf(mnn, v[i]);
+    }
+    const float am = __builtin_fmaximum_numf(__builtin_fmaximum_numf(mxp, -mnn), 0.f);  // 0 if every value is NaN
+    uint32_t neg = -mnn == am ? 1u : 0u;
+    if (mxp == am && neg && am > 0.f) {  // +am and -am both present: the first one decides
+#pragma unroll
+        for (int i = 7; i >= 0; i--)
+            if (fabsf(v[i]) == am) neg = __float_as_uint(v[i]) >> 31;
+    }
+    const uint32_t amb = __float_as_uint(am) & 0x7fffffffu;
+    const uint32_t bmax = row_pair_max_u32(row_max_u32(amb));
+    uint32_t key = amb == bmax ? ((uint32_t)sub << 1) | neg : 0xffffffffu;
+    key = row_pair_min_u32(row_min_u32(key));  // the first lane holding the block max, and its sign
+    packed[0] = packed[1] = 0u;
+    int sum = 0;
+    float d = 0.f;
+    if (bmax != 0u) {  // uniform within the 32-lane block
+        const float mx = (key & 1u) ? -__uint_as_float(bmax) : __uint_as_float(bmax);
+        const float iscale = -128.f / mx;
+        // codes exactly as q8k_lane16 forms them
+        auto codes = [&](auto lower) {
+            int q[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+#pragma clang fp contract(off)
+                const float tt = iscale * v[i];
+                const float r = fminf(tt + copysignf(0x1.fffffep-2f, tt), 127.f);
+                q[i] = decltype(lower)::value ? max(-128, (int)r) : (int)r;
+            }
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q[4 * w + 1], (uint32_t)q[4 * w], 0x0c0c0400u);
+                const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q[4 * w + 3], (uint32_t)q[4 * w + 2], 0x0c0c0400u);
+                packed[w] = lo | (hi << 16);
+            }
+        };
+        if (fabsf(iscale) <= 3.4028235e38f) codes(std::false_type{});
+        else codes(std::true_type{});
+        sum = __builtin_amdgcn_sdot4((int)packed[0], 0x01010101, 0, false);
+        sum = __builtin_amdgcn_sdot4((int)packed[1], 0x01010101, sum, false);
+        d = 1.f / iscale;
+    }
+    sum += (int)dpp_u32<0xB1>((uint32_t)sum);  // + lane sub ^ 1 (quad_perm [1,0,3,2])
+    *sum_out = sum;
+    *d_out = d;
+}
+
 constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 

@@ -392,17 +392,42 @@ __device__ __forceinline__ void wg_barrier() {
     }
 }
 
-template <int TYPE, bool NORM, int XJ, int WPG, class Between, bool FENCE = true>
+template <int TYPE, bool NORM, int XJ, int WPG, int NBMAX = 64, class Between = void, bool FENCE = true>
 __device__ __forceinline__ void quantise_x_lds(const float *__restrict__ x, int nbx, uint8_t *sx, Between between,
                                                const float *__restrict__ alpha, float eps) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr bool vec = true;  // the host only fuses for 16-byte aligned x
-    if constexpr (TYPE != TYPE_Q8_0) {
+    if constexpr (TYPE != TYPE_Q8_0 && !NORM && 2 * WPG >= NBMAX) {
+        // 32 lanes per 256-value block, 8 consecutive values each (q8k_lane8): one
+        // pass covers the row (nbx <= NBMAX <= 2 WPG), every lane quantises values
+        // of its own.  With 16 lanes per block an eight-wave workgroup would leave
+        // half its waves quantising clamped duplicates on the SIMDs the other half
+        // runs on (Q4_K 14336 x 4096: 8.2 -> 7.8 us per launch).  Same bytes as
+        // q8k_lane16.
+        const int t = threadIdx.x, sub = t & 31, b = min(t >> 5, nbx - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(x + (int64_t)b * QK_K + 8 * sub);
+        const float4 f0 = src[0], f1 = src[1];
+        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+        __builtin_amdgcn_sched_barrier(0);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t packed[2];
+        int sum;
+        float d;
+        q8k_lane8(v, sub, packed, &sum, &d);
+        if ((t >> 5) < nbx) {
+            uint8_t *xb = sx + b * XS_K;
+            *reinterpret_cast<uint2 *>(xb + 8 * sub) = make_uint2(packed[0], packed[1]);
+            if (!(sub & 1)) *reinterpret_cast<int16_t *>(xb + 256 + sub) = (int16_t)sum;  // entry sub / 2
+            if (sub == 0) *reinterpret_cast<float *>(xb + 288) = d;
+        }
+    } else if constexpr (TYPE != TYPE_Q8_0) {
         // 16 lanes per 256-value block, 16 consecutive values per lane
         // (q8k_lane16), so a workgroup of WPG waves quantises BPP = 4 WPG blocks
-        // per pass (nbx <= 64, 32 with the norm); a lane's 16 codes are exactly
-        // one bsums entry.
-        constexpr int BPP = 4 * WPG, MAXP = (NORM ? 32 : 64) / BPP;
+        // per pass (nbx <= NBMAX <= 64, 32 with the norm); a lane's 16 codes are
+        // exactly one bsums entry.
+        constexpr int BPP = 4 * WPG, NBM = NBMAX < (NORM ? 32 : 64) ? NBMAX : (NORM ? 32 : 64);
+        constexpr int MAXP = (NBM + BPP - 1) / BPP;
         const int t = threadIdx.x, sub = t & 15;
         const int np = (nbx + BPP - 1) / BPP;  // workgroup-uniform
         float v[MAXP][16], al[NORM ? MAXP : 1][16];
@@ -696,7 +721,8 @@ __device__ __forceinline__ float swap16_sum(float a, float b) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4, int RING = 0>
+template <int TYPE, int PPB, int RPW, int IT, int MR, bool FUSED, int MAP, bool NORM = false, int WPG = 4, int RING = 0,
+          int RMAX = 0>
 __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes, int nb, const float *__restrict__ x,
                                                     ActView act, const float *__restrict__ alpha, float eps) {
     static_assert(WPG == 4 || (FUSED && WPG == 8), "waves per workgroup: 4, or 8 for the fused prologue");
@@ -705,6 +731,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
                   "several activation rows: one weight; quantised in the prologue for Q8_K rows only");
     constexpr bool GROUPED = MAP == MAP_SEGMENTS, PAIRED = MAP == MAP_SILU_PAIRS;
     static_assert(!PAIRED || RPW <= 2, "a silu pair spans two row groups or one");
+    static_assert(RMAX == 0 || (MAP == MAP_ONE && MR == 1 && RING >= 2), "static schedule: one weight, one row, a given ring");
     const int64_t n = rm.n;
     const uint8_t *__restrict__ W = rm.w[0];
     float *__restrict__ y = rm.y[0];
@@ -785,6 +812,14 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     // wave's whole stream up front, leave every wave waiting for its first rows
     // while the whole matrix is in flight, and bunch the compute at the end.
     // Deep rows (IT > 4) keep two buffers (registers).
+    // Static schedule (RMAX > 0: the host guarantees at most RMAX groups per wave):
+    // the group loop is unrolled at compile time, so no load past the wave's last
+    // group is ever issued -- the dynamic loop below issues clamped duplicates of
+    // the last group for every slot past it (up to three per wave), which cost
+    // issue slots and L2 bandwidth -- and the ring depth is the host's: the first
+    // RING - 1 groups ahead of the x prologue, one more after each computed group.
+    // Q4_K Llama-3-8B layer step (per launch): q/o 4.5 -> 4.1, k/v 3.1 -> 2.8,
+    // gate/up 7.8 -> 7.5 us (with the 32-lane quantiser).
     constexpr int NBUF3 = RING > 0 ? RING : (F::NBUF == 3 && IT <= (MR > 1 ? 2 : 4)) ? 3 : 2;
     // several activation rows: a two-deep ring where that keeps their activation
     // images in registers (below) and the three-deep one would not
@@ -792,9 +827,10 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     constexpr bool XFIT2 = MR * IT * F::XW <= 160 && 2 * IT * F::RAW + MR * IT * F::XW <= 190;
     constexpr int NBUF = (RING == 0 && MR > 1 && !XFIT3 && XFIT2) ? 2 : NBUF3;
     Raw ring[NBUF][IT];
+    constexpr int PRE = (RMAX > 0 && RMAX < NBUF - 1) ? RMAX : NBUF - 1;  // groups issued before the prologue
     auto issue_ring = [&] {
 #pragma unroll
-        for (int k = 0; k < NBUF - 1; k++) load_group(gc(g0 + k), ring[k]);
+        for (int k = 0; k < PRE; k++) load_group(gc(g0 + k), ring[k]);
     };
 
     extern __shared__ __align__(16) uint8_t sx[];
@@ -802,7 +838,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     // Q8_0: at most 64 IT activation blocks (the sweeps cover the row), 32 WPG per pass
     constexpr int XJ = (64 * IT + 32 * WPG - 1) / (32 * WPG);
     if constexpr (FUSED && MR > 1) quantise_rows_lds<TYPE, MR, IT>(x, act.rows, nb, sx, issue_ring);
-    else if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (XJ < 4 ? XJ : 4), WPG>(x, nb, sx, issue_ring, alpha, eps);
+    else if constexpr (FUSED) quantise_x_lds<TYPE, NORM, (XJ < 4 ? XJ : 4), WPG, BPI * IT>(x, nb, sx, issue_ring, alpha, eps);
     else copy_x_lds<TYPE, MR>(act, nb, sx, issue_ring);
 
     // A lane decodes the same piece slots in every row, so when they fit its
@@ -927,6 +963,18 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
         }
     };
 
+    if constexpr (RMAX > 0) {
+        // group i of the wave (i < RMAX); the load for group i + NBUF - 1 goes out
+        // before group i is computed, if the wave can have that group at all
+#pragma unroll
+        for (int i = 0; i < RMAX; i++) {
+            if (i + NBUF - 1 < RMAX && i + NBUF - 1 >= PRE) load_group(gc(g0 + i + NBUF - 1), ring[(i + NBUF - 1) % NBUF]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (i == 0 || g0 + i < g1) compute_group(g0 + i, ring[i % NBUF], g0 + i < g1);  // wave-uniform
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
     // The first pass runs even for a wave without groups (it stores nothing):
     // the ring's first loads then have an unconditional use and stay where they
     // are issued, ahead of the prologue, instead of being sunk into the loop.

@@ -656,7 +656,7 @@ static bool fast_shape(int nb, int *ppb, int *rpw, int *it, int mr = 1) {
         // of 32-weight pieces leave no registers for more than one row)
         if (nb <= 4) { q = 4; r = 4; }
         else if (nb <= 8) { q = 4; r = 2; }
-        else if (nb <= 64 && (nb > 56 || nb <= 48 || mr > 1)) { q = 4; r = 1; }
+        else if (nb <= 64 && (nb > 56 || nb <= 48 || mr > 1 || TYPE == TYPE_Q4_K)) { q = 4; r = 1; }
         else if (nb <= 56) { q = 8; r = 1; }
     } else if (TYPE == TYPE_Q6_K) {
         if (nb <= 16 && mr == 1) { q = 4; r = 2; }
@@ -671,6 +671,39 @@ static bool fast_shape(int nb, int *ppb, int *rpw, int *it, int mr = 1) {
     *rpw = r;
     *it = (nb + bpi - 1) / bpi;  // the smallest sweep count covering the row (the kernel relies on it)
     return true;
+}
+
+// The fused m = 1 launch of one weight on the static schedule (k_gemv1 with
+// RMAX = R: at most R row groups per wave, the group loop unrolled, no load past
+// a wave's last group).  Ring depth: one group ahead of the prologue at k > 8192
+// (IT 4: an x of 56 KB per workgroup arrives later behind more weight loads --
+// 4096 x 14336 two groups ahead 10.7 us, one 8.7 us), else up to three
+// (4096 rows: 4.1 us with all four ahead and with three, 4.5 us in the dynamic
+// loop's two).
+template <int TYPE, int PPB, int RPW, int IT, int WPG, int R>
+static void launch_static(const RowMap &rm, int64_t row_bytes, int nb, const float *x, unsigned grid, size_t lds,
+                          hipStream_t st) {
+    constexpr int D = IT >= 4 ? 2 : (R < 3 ? R : 3) + 1;
+    const ActView none{nullptr, nullptr, nullptr, (int64_t)nb * QK_K, 0};
+    k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, WPG, D, R><<<grid, 64 * WPG, lds, st>>>(rm, row_bytes, nb, x,
+                                                                                              none, nullptr, 0.f);
+}
+// The smallest compiled R (1, 2, 4, 7, 8) holding rpw groups per wave; 0: none.
+static inline int static_rmax(int64_t rpw) {
+    return rpw <= 1 ? 1 : rpw <= 2 ? 2 : rpw <= 4 ? 4 : rpw <= 7 ? 7 : rpw <= 8 ? 8 : 0;
+}
+template <int TYPE, int PPB, int RPW, int IT, int WPG>
+static bool try_static(const RowMap &rm, int64_t row_bytes, int nb, const float *x, int64_t ng, unsigned grid,
+                       size_t lds, hipStream_t st) {
+    const int64_t nw = (int64_t)grid * WPG;
+    switch (static_rmax((ng + nw - 1) / nw)) {
+    case 1: launch_static<TYPE, PPB, RPW, IT, WPG, 1>(rm, row_bytes, nb, x, grid, lds, st); return true;
+    case 2: launch_static<TYPE, PPB, RPW, IT, WPG, 2>(rm, row_bytes, nb, x, grid, lds, st); return true;
+    case 4: launch_static<TYPE, PPB, RPW, IT, WPG, 4>(rm, row_bytes, nb, x, grid, lds, st); return true;
+    case 7: launch_static<TYPE, PPB, RPW, IT, WPG, 7>(rm, row_bytes, nb, x, grid, lds, st); return true;
+    case 8: launch_static<TYPE, PPB, RPW, IT, WPG, 8>(rm, row_bytes, nb, x, grid, lds, st); return true;
+    default: return false;
+    }
 }
 
 template <int TYPE, int PPB, int RPW, int IT>
@@ -748,6 +781,19 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
                 fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, 4, 4>,
                       k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, W8, 4>, nullptr, 0.f);
                 return hipGetLastError();
+            }
+        // Q4_K / Q5_K, one row per group, k <= 4096 or k > 12288: the static
+        // schedule where every wave holds at most 8 groups.  At k > 12288 eight-wave
+        // workgroups (8 per CU): the x prologue over 512 threads, two groups per wave
+        // for 4096 rows (4096 x 14336: 10.2 -> 8.7 us with the 64-weight pieces)
+        if constexpr (W8_OK && RPW == 1 && (IT == 1 || IT == 4))
+            if (!tuning().gemv1_dynamic) {
+                const bool s8 = IT == 4 || w8;
+                const int64_t sw = IT == 4 ? std::min<int64_t>((int64_t)num_cus() * 8, ng) : waves;
+                const unsigned sg = (unsigned)((sw + (s8 ? 7 : 3)) / (s8 ? 8 : 4));
+                if (s8 ? try_static<TYPE, PPB, RPW, IT, 8>(rm, row_bytes, nb, x, ng, sg, lds, st)
+                       : try_static<TYPE, PPB, RPW, IT, 4>(rm, row_bytes, nb, x, ng, sg, lds, st))
+                    return hipGetLastError();
             }
         fused(k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE>, k_gemv1<TYPE, PPB, RPW, IT, 1, true, MAP_ONE, false, W8>,
               nullptr, 0.f);

@@ -49,7 +49,7 @@ struct ActView;
 //   LBQ_GEMM_BIG=wide|tall, LBQ_GEMM_SPLITS=<n>     batched GEMM plan
 //   LBQ_GEMV1_NOFUSE, LBQ_GEMV1_CFG=<ppb>,<rpw>, LBQ_GEMV1_WPC=<waves per CU>,
 //   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
-//   LBQ_GEMV_ROWS_OFF                               decode GEMV plan
+//   LBQ_GEMV_ROWS_OFF, LBQ_GEMV1_DYNAMIC            decode GEMV plan
 //   LBQ_GEMV_MX_OFF, LBQ_GEMV_MX_WIDE_OFF (m = 9..32 only),
 //   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8, LBQ_GEMV_MX_ALL,
 //   LBQ_GEMV_MX_PAIR_OFF
@@ -64,6 +64,7 @@ struct Tuning {
     bool gemv1_nofuse = false, gemv_rows_off = false;
     int gemv1_ppb = 0, gemv1_rpw = 0;  // m = 1 shape (0: planned)
     int gemv1_wpc = 0, gemv1_wpg = 0;
+    bool gemv1_dynamic = false;  // m = 1: never the static (compile-time group count) schedule
     bool gemv_mx_off = false;  // batch decode never on the matrix cores
     bool gemv_mx_wide_off = false;  // m = 9..32 never on the integer matrix-core kernel
     int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)

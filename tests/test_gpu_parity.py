@@ -263,7 +263,9 @@ def test_decode_row_partition(oracle, lbq, dev, t, k):
     # (Q8_0 at k = 14336: 448 blocks, more block scales than threads)
     from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
     rng = np.random.default_rng(70 + t + k)
-    for n in (1, 3, 257, 1000, 5000):
+    # 8400 / 16400 rows: eight-wave workgroups, at most 7 / 9 groups per wave (the
+    # static schedule with clamped duplicates / the dynamic loop past 8)
+    for n in (1, 3, 257, 1000, 5000, 8400) + ((16400,) if k == 4096 else ()):
         w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
         x = rng.standard_normal((1, k)).astype(np.float32)
         ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
@@ -284,18 +286,20 @@ def test_fused_quantisation_is_bit_exact(oracle, lbq, dev, t, k):
     # (bit-exact) kernel runs the same integer arithmetic, so the two outputs
     # must agree to the bit.
     from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    # 300 rows: four-wave workgroups (16 lanes per Q8_K block); 8400 rows at
+    # k = 4096: eight-wave workgroups quantising with 32 lanes per block
     rng = np.random.default_rng(90 + t)
-    n = 300
-    w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
-    qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
     xs = np.concatenate([_special_rows(k), _tie_rows(k), rng.standard_normal((4, k)).astype(np.float32)])
     xs[-1, rng.random(k) < 0.01] *= 20
-    for row in xs:
-        xd = to_dev(row[None, :], dev)
-        y_fused = qm.forward(xd)
-        y_act = qm.forward_quantized(QActivation.for_weight(qm, 1).quantize(xd))
-        torch.cuda.synchronize()
-        assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32))
+    for n in (300, 8400):
+        w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(w_raw, dev), t, (n, k)))
+        for row in xs:
+            xd = to_dev(row[None, :], dev)
+            y_fused = qm.forward(xd)
+            y_act = qm.forward_quantized(QActivation.for_weight(qm, 1).quantize(xd))
+            torch.cuda.synchronize()
+            assert np.array_equal(y_fused.cpu().numpy().view(np.uint32), y_act.cpu().numpy().view(np.uint32)), n
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
