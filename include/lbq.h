@@ -52,7 +52,10 @@ enum lbq_status {
     LBQ_ERR_IO = -9                /* a file could not be opened or mapped */
 };
 
-/* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType). */
+/* GGUF/ggml type ids: /root/reference/src/quantization/mod.rs:58-75 (GgmlDType),
+ * plus BF16 (30), which candle-core's GgmlDType carries and the reference's own
+ * table does not: candle's GGUF reader hands a BF16 tensor to QMatMul::from_qtensor
+ * (custom_transformer.rs:358-363), which serves it as its dense variant. */
 enum lbq_ggml_type {
     LBQ_TYPE_F32 = 0,  /* dense: an f32 matmul (candle's dense QMatMul variant), k % 8 == 0 */
     LBQ_TYPE_F16 = 1,  /* dense: widened exactly to f32, then as F32 */
@@ -67,16 +70,19 @@ enum lbq_ggml_type {
     LBQ_TYPE_Q4_K = 12,
     LBQ_TYPE_Q5_K = 13,
     LBQ_TYPE_Q6_K = 14,
-    LBQ_TYPE_Q8_K = 15 /* activation-only type (vec-dot partner of the k-quants) */
+    LBQ_TYPE_Q8_K = 15, /* activation-only type (vec-dot partner of the k-quants) */
+    LBQ_TYPE_BF16 = 30  /* dense: widened exactly to f32 (bits << 16), then as F32 */
 };
 
 /* Thread-local description of the last error on this thread ("" if none). */
 const char *lbq_last_error(void);
 
 /* GgmlDType::block_size / type_size (/root/reference/src/quantization/mod.rs:99-126)
- * for the types above; 0 for any other id.  lbq_type_size returns the table's
- * value, so GGUF extents computed from it agree with the reference's
- * extract_tensor_bytes (src/quantization/gguf_ops.rs:19-59); for Q2_K that is 82. */
+ * for the types above (BF16: candle's 1 and 2); 0 for any other id.  lbq_type_size
+ * returns the table's value, so GGUF extents computed from it agree with the
+ * reference's extract_tensor_bytes (src/quantization/gguf_ops.rs:19-59); for Q2_K
+ * that is 82.  (lbq_gguf_tensor_bytes, the mirror of extract_tensor_bytes, still
+ * refuses BF16 tensors as the reference's GgmlDType::from_u32 does.) */
 int lbq_type_block_size(uint32_t ggml_type);
 int lbq_type_size(uint32_t ggml_type);
 
@@ -102,9 +108,23 @@ int lbq_weight_create(lbq_ctx *ctx, uint32_t ggml_type, int64_t n, int64_t k, co
                       size_t nbytes, lbq_weight **out_w);
 
 /* As lbq_weight_create, but borrows blocks that are already device resident
- * (no copy; the caller keeps the memory alive until lbq_weight_destroy). */
+ * (no copy; the caller keeps the memory alive until lbq_weight_destroy).  Like
+ * lbq_weight_create it derives per-row fp16 operand exponents for the batched
+ * MFMA GEMM (m > 8) from the block scales, so the blocks must already hold their
+ * final contents: the call synchronises the device (whatever writes the blocks,
+ * on any stream, completes first) and allocates n bytes for the exponents.  If
+ * the caller rewrites the blocks while the handle lives, lbq_weight_refresh must
+ * follow before the next forward, or results at m > 8 are wrong (overflowing or
+ * underflowing fp16 operands, no error). */
 int lbq_weight_wrap_device(lbq_ctx *ctx, uint32_t ggml_type, int64_t n, int64_t k, const void *d_blocks,
                            size_t nbytes, lbq_weight **out_w);
+
+/* Recompute a weight's derived state (the per-row operand exponents above) from
+ * its current blocks, stream-ordered on `stream`.  No counterpart in the
+ * reference, whose QTensor is immutable; for callers that fill or change the
+ * device blocks of a wrapped handle after wrapping it.  A no-op for types and
+ * k the MFMA GEMM does not serve (dense weights, k % 256 != 0). */
+int lbq_weight_refresh(lbq_weight *w, void *stream);
 
 int lbq_weight_destroy(lbq_weight *w);
 
@@ -113,21 +133,30 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
 
 /* y[m][n] = x[m][k] . W^T in f32 -- QMatMul::forward (candle-core 0.10.2,
  * reached through /root/reference/src/model/quantizable_linear.rs:67).
- * x and y are contiguous f32 device buffers (device memory from hipMalloc: at
- * m = 2..32 y may be written with f32 atomic adds); any leading dims of the
- * reference's [.., k] tensor are flattened into m.  The activation is
- * quantised to Q8_K (k-quant weights), Q8_1 (Q4_1/Q5_1) or Q8_0 (the other
- * 32-value types) exactly as the reference CPU path does.  For m <= 8, and for
- * Q4_K/Q5_K weights of 1024 rows or more up to m = 32, each output is formed
- * from integer sub-block dot products as in the reference; otherwise for
- * Q4_K/Q5_K/Q6_K/Q8_0 weights at m > 8 (Q8_0: k % 256 == 0) the products run on
- * MFMA from fp16 roundings of the same activation and weight values (about 4e-4
- * relative on a row).  Dense F32/F16 weights are candle's dense variant: no
- * quantisation, an f32 matmul.  m == 0 is a no-op. */
+ * x and y are contiguous f32 device buffers that must not overlap
+ * (LBQ_ERR_INVALID_ARG otherwise; the reference returns a new tensor); any
+ * leading dims of the reference's [.., k] tensor are flattened into m.  The
+ * activation is quantised to Q8_K (k-quant weights), Q8_1 (Q4_1/Q5_1) or Q8_0
+ * (the other 32-value types) exactly as the reference CPU path does.
+ * Arithmetic by (type, m):
+ *   - m <= 8, and Q4_K/Q5_K weights of 1024 rows or more up to m = 32: each
+ *     output from integer sub-block dot products as in the reference (f32
+ *     combine; only the summation order differs, ~1e-7 relative);
+ *   - m > 8 otherwise, for every quantised type when k % 256 == 0 (Q4_0, Q4_1,
+ *     Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K): MFMA on fp16 roundings of
+ *     the same activation and weight values (about 4e-4 relative on a row);
+ *   - m > 8 with k % 256 != 0: the integer GEMV over chunks of 8 rows.
+ * Where the matrix-core decode kernel (Q4_K/Q5_K, m = 2..32) splits a 32-row
+ * tile between two workgroups, their halves are added into y with f32 atomic
+ * adds when y is plain device memory (hipMalloc; checked once per allocation),
+ * else through partial sums in the workspace; either way y = a + b for the two
+ * halves, the same bits for finite normal-range halves.  Dense F32/F16/BF16
+ * weights are candle's dense variant: no quantisation, an f32 matmul.  m == 0 is
+ * a no-op. */
 int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, float *d_y, void *stream);
 
-/* QMatMul::forward as lbq_qmatmul_f32 computes it (the same kernels, the same
- * bits), allocating nothing: no hipMalloc, hipFree or allocating library call.
+/* lbq_qmatmul_f32's result (the same kernels, the same bits), allocating
+ * nothing: no hipMalloc, hipFree or allocating library call.
  * No counterpart in the reference; for callers that cannot allocate device
  * memory -- code under HIP graph capture, tight serving loops, harnesses that
  * forbid it.  The quantised activations and the batched GEMM's workspace live
@@ -159,9 +188,10 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
  * mlp_wrapper.rs:190-194: `silu(gate_proj.forward(x)) * up_proj.forward(x)`):
  * d_out[m][n] = silu(x . Wg^T) * (x . Wu^T), silu(v) = v / (1 + exp(-v)) in f32.
  * The two products are computed exactly as lbq_qmatmul_f32 computes them.  At
- * m = 1, and for Q4_K / Q5_K weights of more than 8192 rows at m = 2..32 (after
- * one activation quantisation), both weights stream through one launch and the
- * product is formed in its epilogue, so neither product is written out; otherwise
+ * m = 1, and for Q4_K / Q5_K weights of more than 8192 rows (and more than 32
+ * rows per CU) at m = 5..32 -- m = 2..32 when k > 8192 -- (after one activation
+ * quantisation), both weights stream through one launch and the product is
+ * formed in its epilogue, so neither product is written out; otherwise
  * the grouped path fills context memory and one elementwise launch combines it
  * (the m = 2..32 pair launch gives the same bits as that).  gate and up share the
  * ggml type, n and k. */
@@ -204,7 +234,7 @@ int lbq_dequantize_f32(lbq_ctx *ctx, const lbq_weight *w, float *d_y, void *stre
 
 /* Dequantise nelem values of raw device blocks -- dequantize_tensor
  * (/root/reference/src/quantization/mod.rs:158-247), extended to every block type
- * above, and F32 / F16 tensors (QTensor::dequantize of the norm weights,
+ * above, and F32 / F16 / BF16 tensors (QTensor::dequantize of the norm weights,
  * custom_transformer_block.rs:229-231, which GGUF files store as F32).
  * nelem must be a multiple of the block size. */
 int lbq_dequantize_blocks_f32(uint32_t ggml_type, const void *d_blocks, int64_t nelem, float *d_y, void *stream);

@@ -38,6 +38,7 @@ SIGNATURES = {
     "lbq_weight_wrap_device": (_c.c_int, [_VP, _U32, _I64, _I64, _VP, _SZ, _c.POINTER(_VP)]),
     "lbq_weight_destroy": (_c.c_int, [_VP]),
     "lbq_weight_info": (_c.c_int, [_VP, _c.POINTER(_U32), _c.POINTER(_I64), _c.POINTER(_I64)]),
+    "lbq_weight_refresh": (_c.c_int, [_VP, _VP]),
     "lbq_qmatmul_f32": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
     "lbq_qmatmul_f32_noalloc": (_c.c_int, [_VP, _VP, _VP, _I64, _VP, _VP]),
     "lbq_qmatmul_group_f32": (_c.c_int, [_VP, _c.POINTER(_VP), _c.c_int, _VP, _I64, _c.POINTER(_VP), _VP]),

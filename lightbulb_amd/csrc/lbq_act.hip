@@ -242,18 +242,18 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint8_t *__restrict__ 
     store16(y + t * 16, out);
 }
 
-// F32 / F16 tensors: y[i] = x[i] (bits) / the exact f16 -> f32 widening
-template <bool F16>
+// F32 / F16 / BF16 tensors: y[i] = x[i] (bits) / the exact f16 or bf16 -> f32 widening
+template <bool F16, bool BF = false>
 __global__ __launch_bounds__(256) void k_dense_f32(const uint8_t *__restrict__ x, int64_t n, float *__restrict__ y) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    if constexpr (F16) y[i] = h2f(reinterpret_cast<const unsigned short *>(x)[i]);
+    if constexpr (F16) y[i] = w16<BF>(reinterpret_cast<const unsigned short *>(x)[i]);
     else y[i] = reinterpret_cast<const float *>(x)[i];
 }
 
-// Embedding rows of an F32 / F16 table (16 values per thread, widened exactly);
-// ids outside [0, n) give NaN rows, as k_embed_rows.
-template <bool F16>
+// Embedding rows of an F32 / F16 / BF16 table (16 values per thread, widened
+// exactly); ids outside [0, n) give NaN rows, as k_embed_rows.
+template <bool F16, bool BF = false>
 __global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__ w, int64_t n, int64_t k,
                                                      const int32_t *__restrict__ ids, int64_t count, int64_t gpr,
                                                      float *__restrict__ y) {
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__
         for (int j = 0; j < 16; j++) out[j] = __int_as_float(0x7fc00000);
     } else if constexpr (F16) {
         const unsigned short *src = reinterpret_cast<const unsigned short *>(w) + id * k + 16 * g;
-        for (int j = 0; j < 16; j++) out[j] = h2f(src[j]);
+        for (int j = 0; j < 16; j++) out[j] = w16<BF>(src[j]);
     } else {
         const float *src = reinterpret_cast<const float *>(w) + id * k + 16 * g;
         for (int j = 0; j < 16; j++) out[j] = src[j];
@@ -317,9 +317,10 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
     X(TYPE_Q4_K) X(TYPE_Q5_K) X(TYPE_Q6_K) X(TYPE_Q8_K)
 
 hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st) {
-    if (type == TYPE_F32 || type == TYPE_F16) {
+    if (is_dense(type)) {
         const dim3 grid((unsigned)((nelem + 255) / 256));
         if (type == TYPE_F16) k_dense_f32<true><<<grid, 256, 0, st>>>(blocks, nelem, y);
+        else if (type == TYPE_BF16) k_dense_f32<true, true><<<grid, 256, 0, st>>>(blocks, nelem, y);
         else k_dense_f32<false><<<grid, 256, 0, st>>>(blocks, nelem, y);
         return hipGetLastError();
     }
@@ -341,6 +342,7 @@ hipError_t launch_embedding(int type, const uint8_t *w, int64_t n, int64_t k, in
     const dim3 grid((unsigned)((count * gpr + 255) / 256));
     switch (type) {
     case TYPE_F16: k_embed_dense<true><<<grid, 256, 0, st>>>(w, n, k, ids, count, gpr, y); break;
+    case TYPE_BF16: k_embed_dense<true, true><<<grid, 256, 0, st>>>(w, n, k, ids, count, gpr, y); break;
     case TYPE_F32: k_embed_dense<false><<<grid, 256, 0, st>>>(w, n, k, ids, count, gpr, y); break;
 #define LBQ_EMB(T) \
     case T: k_embed_rows<T><<<grid, 256, 0, st>>>(w, n, row_bytes, ids, count, gpr, y); break;

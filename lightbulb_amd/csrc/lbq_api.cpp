@@ -271,10 +271,47 @@ static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 32 && lbq::gem
 // ... with its two split halves added into y, which the quantisation launch zeroes
 static bool mx_adds(const lbq_weight *w, int64_t m) { return uses_mx(w, m) && lbq::gemv_mx_adds(w->type, w->n, w->k, (int)m); }
 
+// Whether y[0, count) lies in plain device memory (hipMalloc: device resident, not
+// managed, no allocation flags), where the matrix-core kernel's f32 atomic adds
+// are defined; host-pinned, managed and fine-grained memory are not (the adds are
+// built with -munsafe-fp-atomics).  Queried once per allocation: ranges found to
+// qualify are remembered (at most 64, oldest dropped first).
+static bool y_is_plain_device(const float *y, int64_t count) {
+    static std::mutex mu;
+    static std::vector<std::pair<uintptr_t, size_t>> known;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(y);
+    const size_t bytes = (size_t)count * sizeof(float);
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (const auto &r : known)
+            if (p >= r.first && p - r.first + bytes <= r.second) return true;
+    }
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, y) != hipSuccess) {
+        (void)hipGetLastError();  // an unknown pointer: not plain device memory
+        return false;
+    }
+    if (a.type != hipMemoryTypeDevice || a.isManaged || a.allocationFlags != 0) return false;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<float *>(y)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    if (p < b || p - b + bytes > size) return false;
+    std::lock_guard<std::mutex> lock(mu);
+    if (known.size() >= 64) known.erase(known.begin());
+    known.emplace_back(b, size);
+    return true;
+}
+
 // adds y (m rows of w) to the quantisation launch's zero list where the
-// matrix-core kernel adds into it; returns whether it did
+// matrix-core kernel adds into it; returns whether it did.  Outputs that are not
+// plain device memory take the kernel's other protocol (partials and a tile
+// counter in the workspace, the same bits).
 static bool zero_for_mx(lbq::ZeroList &zl, const lbq_weight *w, int64_t m, float *y) {
-    if (!mx_adds(w, m) || zl.count >= 4) return false;
+    if (!mx_adds(w, m) || zl.count >= 4 || !y_is_plain_device(y, m * w->n)) return false;
     zl.p[zl.count] = y;
     zl.n[zl.count] = m * w->n;
     zl.count++;
@@ -364,8 +401,14 @@ int forward(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t m, floa
     return run_dot(sc, w, av, m, d_y, st, zeroed);
 }
 
+// whether the f32 ranges [a, a + na) and [b, b + nb) share an element
+static bool overlaps(const float *a, int64_t na, const float *b, int64_t nb) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + (uintptr_t)nb * sizeof(float) && pb < pa + (uintptr_t)na * sizeof(float);
+}
+
 int check_weight_args(uint32_t type, int64_t n, int64_t k, size_t nbytes) {
-    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14)", type);
+    if (!weight_type_ok(type)) return fail(LBQ_ERR_UNSUPPORTED_TYPE, "ggml type %u is not served (F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q2_K=10, Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14, BF16=30)", type);
     const int bs = lbq_type_block_size(type);
     if (n <= 0 || k <= 0) return fail(LBQ_ERR_SHAPE, "weight shape (%lld, %lld) must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(LBQ_ERR_SHAPE, "k = %lld is not a multiple of the %d-value block", (long long)k, bs);
@@ -455,7 +498,7 @@ const char *lbq_last_error(void) { return g_err.c_str(); }
 
 int lbq_type_block_size(uint32_t t) {
     switch (t) {
-    case LBQ_TYPE_F32: case LBQ_TYPE_F16: return 1;
+    case LBQ_TYPE_F32: case LBQ_TYPE_F16: case LBQ_TYPE_BF16: return 1;
     case LBQ_TYPE_Q4_0: case LBQ_TYPE_Q4_1: case LBQ_TYPE_Q5_0: case LBQ_TYPE_Q5_1: case LBQ_TYPE_Q8_0: case LBQ_TYPE_Q8_1:
         return 32;
     case LBQ_TYPE_Q2_K: case LBQ_TYPE_Q3_K: case LBQ_TYPE_Q4_K: case LBQ_TYPE_Q5_K: case LBQ_TYPE_Q6_K: case LBQ_TYPE_Q8_K:
@@ -467,7 +510,7 @@ int lbq_type_block_size(uint32_t t) {
 int lbq_type_size(uint32_t t) {
     switch (t) {
     case LBQ_TYPE_F32: return 4;
-    case LBQ_TYPE_F16: return 2;
+    case LBQ_TYPE_F16: case LBQ_TYPE_BF16: return 2;
     case LBQ_TYPE_Q4_0: return 18;
     case LBQ_TYPE_Q4_1: return 20;
     case LBQ_TYPE_Q5_0: return 22;
@@ -579,6 +622,16 @@ int lbq_weight_destroy(lbq_weight *w) {
     return LBQ_OK;
 }
 
+int lbq_weight_refresh(lbq_weight *w, void *stream) {
+    if (!w) return fail(LBQ_ERR_INVALID_ARG, "null weight");
+    if (!w->d_rexp) return LBQ_OK;  // no derived state for this type and k
+    DeviceGuard g(w->ctx->device);
+    if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
+    hipError_t e = lbq::launch_row_exponents(w->type, w->d_blocks, w->n, w->k, w->row_bytes, w->d_rexp,
+                                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? LBQ_OK : hip_fail(e, "per-row exponents of the weight");
+}
+
 int lbq_weight_info(const lbq_weight *w, uint32_t *type, int64_t *n, int64_t *k) {
     if (!w) return fail(LBQ_ERR_INVALID_ARG, "null weight");
     if (type) *type = (uint32_t)w->type;
@@ -595,6 +648,7 @@ int lbq_qmatmul_f32(lbq_ctx *ctx, const lbq_weight *w, const float *d_x, int64_t
     if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
         return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    if (overlaps(d_x, m * w->k, d_y, m * w->n)) return fail(LBQ_ERR_INVALID_ARG, "x and y overlap");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
@@ -612,6 +666,7 @@ int lbq_qmatmul_f32_noalloc(lbq_ctx *ctx, const lbq_weight *w, const float *d_x,
     if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_y)) & 3u)
         return fail(LBQ_ERR_INVALID_ARG, "x and y must be 4-byte aligned f32 buffers");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    if (overlaps(d_x, m * w->k, d_y, m * w->n)) return fail(LBQ_ERR_INVALID_ARG, "x and y overlap");
     if (!ctx->noalloc_scratch) return fail(LBQ_ERR_INVALID_ARG, "context has no allocation-free scratch");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -645,6 +700,8 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     if (!d_x) return fail(LBQ_ERR_INVALID_ARG, "null activation pointer");
     if (reinterpret_cast<uintptr_t>(d_x) & 3u) return fail(LBQ_ERR_INVALID_ARG, "x must be a 4-byte aligned f32 buffer");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
+    for (int i = 0; i < count; i++)
+        if (overlaps(d_x, m * ws[0]->k, d_ys[i], m * ws[i]->n)) return fail(LBQ_ERR_INVALID_ARG, "x and output %d overlap", i);
     const lbq_weight *w0 = ws[0];
     const int act_type = lbq::vec_dot_type(w0->type);
     DeviceGuard g(ctx->device);
@@ -779,6 +836,7 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
         return fail(LBQ_ERR_INVALID_ARG, "x and out must be 4-byte aligned f32 buffers");
     if (m > (int64_t)1 << 24) return fail(LBQ_ERR_LIMIT, "m = %lld exceeds the supported maximum", (long long)m);
     if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
+    if (overlaps(d_x, m * w_gate->k, d_out, m * w_gate->n)) return fail(LBQ_ERR_INVALID_ARG, "x and out overlap");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
@@ -860,6 +918,8 @@ int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int
     if (m == 0) return LBQ_OK;
     if (!d_x || ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_norm_w)) & 3u))
         return fail(LBQ_ERR_INVALID_ARG, "x and the norm weight must be 4-byte aligned f32 buffers");
+    for (int i = 0; i < count; i++)
+        if (overlaps(d_x, m * ws[0]->k, d_ys[i], m * ws[i]->n)) return fail(LBQ_ERR_INVALID_ARG, "x and output %d overlap", i);
     const lbq_weight *w0 = ws[0];
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
@@ -902,6 +962,7 @@ int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const l
                   reinterpret_cast<uintptr_t>(d_out)) & 3u))
         return fail(LBQ_ERR_INVALID_ARG, "x, the norm weight and out must be 4-byte aligned f32 buffers");
     if (w_gate->n > lbq::MAX_ROWS / 2) return fail(LBQ_ERR_LIMIT, "n = %lld exceeds the supported maximum", (long long)w_gate->n);
+    if (overlaps(d_x, m * w_gate->k, d_out, m * w_gate->n)) return fail(LBQ_ERR_INVALID_ARG, "x and out overlap");
     DeviceGuard g(ctx->device);
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);

@@ -1,11 +1,11 @@
-// lbq_dense.hip -- QMatMul over dense F32 / F16 weights.
+// lbq_dense.hip -- QMatMul over dense F32 / F16 / BF16 weights.
 //
 // candle's QMatMul::from_qtensor does not keep F32 / F16 / BF16 tensors
-// quantised: it dequantises them (F16 widened exactly to f32) and forward is a
+// quantised: it dequantises them (F16 and BF16 widened exactly to f32) and forward is a
 // plain f32 matmul, y = x . W^T (the dense variant; the reference reaches it for
 // whatever type output.weight or a projection has, custom_transformer.rs:360-363,
 // custom_attention.rs:195-206, mlp_wrapper.rs:127-135).  Here the weight stays
-// in its file layout ([n][k], f16 or f32) and is widened on the fly:
+// in its file layout ([n][k], f16, bf16 or f32) and is widened on the fly:
 //   m <= 8  k_dense_gemv: waves stream weight rows in 4096-column units with
 //           the next unit's 16-byte loads in flight, x staged in LDS, f32 FMA
 //           against up to 8 activation rows, DPP row sums -- HBM-bound like the
@@ -24,15 +24,15 @@ namespace lbq {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // 8 consecutive weights of row `row` at column c (c % 8 == 0) widened to f32
-template <bool F16>
+template <bool F16, bool BF = false>
 __device__ __forceinline__ void load_w8(const uint8_t *row, int64_t c, float w[8]) {
     if constexpr (F16) {
         const uint4 v = *reinterpret_cast<const uint4 *>(row + 2 * c);
         const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            w[2 * i] = h2f(d[i] & 0xffffu);
-            w[2 * i + 1] = h2f(d[i] >> 16);
+            w[2 * i] = w16<BF>(d[i] & 0xffffu);
+            w[2 * i + 1] = w16<BF>(d[i] >> 16);
         }
     } else {
         const float4 a = *reinterpret_cast<const float4 *>(row + 4 * c);
@@ -64,7 +64,7 @@ struct DenseUnit {
     uint4 w[F16 ? UN : 2 * UN];
 };
 
-template <bool F16, int MR, bool XL>
+template <bool F16, int MR, bool XL, bool BF = false>
 __global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ W, int64_t N, int64_t K,
                                                     const float *__restrict__ x, int m, float *__restrict__ y) {
     extern __shared__ __align__(16) float xs[];  // XL: x [m][K]
@@ -113,8 +113,8 @@ __global__ __launch_bounds__(256) void k_dense_gemv(const uint8_t *__restrict__ 
                 const uint32_t dw[4] = {d.w[v].x, d.w[v].y, d.w[v].z, d.w[v].w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    w[2 * e] = h2f(dw[e] & 0xffffu);
-                    w[2 * e + 1] = h2f(dw[e] >> 16);
+                    w[2 * e] = w16<BF>(dw[e] & 0xffffu);
+                    w[2 * e + 1] = w16<BF>(dw[e] >> 16);
                 }
             } else {
                 const uint4 a = d.w[2 * v], b = d.w[2 * v + 1];
@@ -183,7 +183,7 @@ struct DenseStage {
     uint4 w[F16 ? 4 : 8];           // W rows (t / 8) + 32 j, k 8 (t % 8): f16 x 8, or f32 x 8 as two
 };
 
-template <bool F16>
+template <bool F16, bool BF = false>
 __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ W, int64_t N, int64_t K,
                                                     const float *__restrict__ x, int64_t M, float *__restrict__ y) {
     __shared__ float As[DBK][DBM + 4];
@@ -232,8 +232,8 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ 
                 const uint32_t d[4] = {g.w[j].x, g.w[j].y, g.w[j].z, g.w[j].w};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    w[2 * e] = h2f(d[e] & 0xffffu);
-                    w[2 * e + 1] = h2f(d[e] >> 16);
+                    w[2 * e] = w16<BF>(d[e] & 0xffffu);
+                    w[2 * e + 1] = w16<BF>(d[e] >> 16);
                 }
             } else {
                 const uint4 a = g.w[2 * j], b = g.w[2 * j + 1];
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const uint8_t *__restrict__ 
         }
 }
 
-template <bool F16>
+template <bool F16, bool BF = false>
 static hipError_t dense_typed(const uint8_t *w, int64_t n, int64_t k, const float *x, int64_t m, float *y,
                               hipStream_t st) {
     if (m <= 8) {
@@ -289,15 +289,15 @@ static hipError_t dense_typed(const uint8_t *w, int64_t n, int64_t k, const floa
         const size_t lds = xl ? xb : 0;
 #define LBQ_DG(MR)                                                                    \
     {                                                                                 \
-        if (xl) k_dense_gemv<F16, MR, true><<<grid, 256, lds, st>>>(w, n, k, x, mi, y); \
-        else k_dense_gemv<F16, MR, false><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);     \
+        if (xl) k_dense_gemv<F16, MR, true, BF><<<grid, 256, lds, st>>>(w, n, k, x, mi, y); \
+        else k_dense_gemv<F16, MR, false, BF><<<grid, 256, 0, st>>>(w, n, k, x, mi, y);     \
     }
         if (m == 1) LBQ_DG(1) else if (m <= 2) LBQ_DG(2) else if (m <= 4) LBQ_DG(4) else LBQ_DG(8)
 #undef LBQ_DG
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((n + DBN - 1) / DBN), (unsigned)((m + DBM - 1) / DBM));
-    k_dense_gemm<F16><<<grid, 256, 0, st>>>(w, n, k, x, m, y);
+    k_dense_gemm<F16, BF><<<grid, 256, 0, st>>>(w, n, k, x, m, y);
     return hipGetLastError();
 }
 
@@ -306,6 +306,7 @@ hipError_t launch_dense(int type, const uint8_t *w, int64_t n, int64_t k, const 
     if (k % 8 || m > 65535LL * DBM) return hipErrorInvalidValue;
     if (type == TYPE_F16) return dense_typed<true>(w, n, k, x, m, y, st);
     if (type == TYPE_F32) return dense_typed<false>(w, n, k, x, m, y, st);
+    if (type == TYPE_BF16) return dense_typed<true, true>(w, n, k, x, m, y, st);
     return hipErrorInvalidValue;
 }
 

@@ -223,6 +223,13 @@ struct ActView {
 struct __attribute__((aligned(4))) u32x4a4 { uint32_t x, y, z, w; };
 
 __device__ __forceinline__ float h2f(uint32_t bits16) { return __half2float(__ushort_as_half((unsigned short)bits16)); }
+// a 16-bit dense weight (bits16 < 2^16) widened exactly to f32: IEEE half, or with
+// BF a bfloat16, whose bits are the upper half of the f32 it stands for
+template <bool BF>
+__device__ __forceinline__ float w16(uint32_t bits16) {
+    if constexpr (BF) return __uint_as_float(bits16 << 16);
+    else return h2f(bits16);
+}
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -254,6 +254,9 @@ int tensor_span(const lbq_gguf *g, const char *name, const Tensor **t_out, uint6
     const Tensor &t = g->tensors[it->second];
     uint64_t bs, ts;
     ggml_layout(t.type, &bs, &ts);
+    // candle's reader (the device upload path) also takes BF16 tensors, which the
+    // reference's own table -- and so extract_tensor_bytes -- does not know
+    if (blocks_layout && t.type == LBQ_TYPE_BF16) bs = 1;
     if (!bs) return gfail(LBQ_ERR_UNSUPPORTED_TYPE, "Unknown quantization type: %u", t.type);
     if (blocks_layout && lbq_type_block_bytes(t.type) > 0) ts = (uint64_t)lbq_type_block_bytes(t.type);
     uint64_t numel = 1;

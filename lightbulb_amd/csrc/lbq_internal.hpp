@@ -9,7 +9,8 @@ namespace lbq {
 enum : int {
     TYPE_F32 = 0, TYPE_F16 = 1,
     TYPE_Q4_0 = 2, TYPE_Q4_1 = 3, TYPE_Q5_0 = 6, TYPE_Q5_1 = 7, TYPE_Q8_0 = 8, TYPE_Q8_1 = 9,
-    TYPE_Q2_K = 10, TYPE_Q3_K = 11, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15
+    TYPE_Q2_K = 10, TYPE_Q3_K = 11, TYPE_Q4_K = 12, TYPE_Q5_K = 13, TYPE_Q6_K = 14, TYPE_Q8_K = 15,
+    TYPE_BF16 = 30  // candle's GgmlDType::BF16 (the GGUF id); not in the reference's own table
 };
 
 // 32-value weight blocks that pair with Q8_0 / Q8_1 activations.
@@ -214,7 +215,7 @@ hipError_t launch_row_exponents(int type, const uint8_t *w, int64_t n, int64_t k
 
 // Dense F32 / F16 weights (candle's dense QMatMul variant): y[m][n] = x . W^T in
 // f32, W [n][k] in its file layout widened on the fly; k % 8 == 0.
-constexpr bool is_dense(int t) { return t == TYPE_F32 || t == TYPE_F16; }
+constexpr bool is_dense(int t) { return t == TYPE_F32 || t == TYPE_F16 || t == TYPE_BF16; }
 hipError_t launch_dense(int type, const uint8_t *w, int64_t n, int64_t k, const float *x, int64_t m, float *y,
                         hipStream_t st);
 

@@ -28,7 +28,14 @@ from . import _lib
 
 
 class GgmlDType(IntEnum):
-    """GGML quantisation type ids (GGUF ``ggml_type``)."""
+    """GGML quantisation type ids (GGUF ``ggml_type``).
+
+    The reference's table (src/quantization/mod.rs:60-77) plus ``BF16 = 30``:
+    candle-core's GgmlDType carries it, so a BF16 tensor reaches
+    ``QMatMul::from_qtensor`` through candle's GGUF reader
+    (custom_transformer.rs:358-363) and is served as the dense variant.
+    ``from_u32`` keeps the reference's own table (it returns None for 30).
+    """
 
     F32 = 0
     F16 = 1
@@ -44,16 +51,24 @@ class GgmlDType(IntEnum):
     Q5K = 13
     Q6K = 14
     Q8K = 15
+    BF16 = 30
 
     @classmethod
     def from_u32(cls, value: int) -> "GgmlDType | None":
+        """The reference's ``GgmlDType::from_u32`` (mod.rs:80-97): ids of its table only."""
+        if value == cls.BF16:
+            return None
         try:
             return cls(value)
         except ValueError:
             return None
 
+    def is_dense(self) -> bool:
+        """F32 / F16 / BF16: candle's dense QMatMul variant (an f32 matmul)."""
+        return self in (GgmlDType.F32, GgmlDType.F16, GgmlDType.BF16)
+
     def block_size(self) -> int:
-        if self in (GgmlDType.F32, GgmlDType.F16):
+        if self.is_dense():
             return 1
         if self in (GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0, GgmlDType.Q8_1):
             return 32
@@ -63,7 +78,7 @@ class GgmlDType(IntEnum):
         return {
             GgmlDType.F32: 4, GgmlDType.F16: 2, GgmlDType.Q4_0: 18, GgmlDType.Q4_1: 20, GgmlDType.Q5_0: 22,
             GgmlDType.Q5_1: 24, GgmlDType.Q8_0: 34, GgmlDType.Q8_1: 36, GgmlDType.Q2K: 82, GgmlDType.Q3K: 110,
-            GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292,
+            GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292, GgmlDType.BF16: 2,
         }[self]
 
     def block_bytes(self) -> int:
@@ -81,12 +96,12 @@ class GgmlDType(IntEnum):
 
 
 #: weight types the GPU path serves; the others are rejected with LBQ_ERR_UNSUPPORTED_TYPE.
-#: F32 / F16 are candle's dense QMatMul variant (an f32 matmul, no activation quantisation).
-SERVED = (GgmlDType.F32, GgmlDType.F16, GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1,
+#: F32 / F16 / BF16 are candle's dense QMatMul variant (an f32 matmul, no activation quantisation).
+SERVED = (GgmlDType.F32, GgmlDType.F16, GgmlDType.BF16, GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1,
           GgmlDType.Q8_0, GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.Q4K, GgmlDType.Q5K, GgmlDType.Q6K)
 
 #: weight types quantize_tensor can produce (no Q2_K / Q3_K quantiser; dense types are not quantised)
-QUANTIZABLE = tuple(t for t in SERVED if t not in (GgmlDType.Q2K, GgmlDType.Q3K, GgmlDType.F32, GgmlDType.F16))
+QUANTIZABLE = tuple(t for t in SERVED if t not in (GgmlDType.Q2K, GgmlDType.Q3K) and not t.is_dense())
 
 #: activation-only block types (the vec-dot partners)
 ACT_TYPES = (GgmlDType.Q8_0, GgmlDType.Q8_1, GgmlDType.Q8K)
@@ -499,7 +514,7 @@ def dequantize_tensor(data: torch.Tensor, dtype: GgmlDType, elem_count: int) -> 
     """Raw device blocks -> f32 [elem_count]; blocks beyond elem_count are cut off.
     Errors name the type as the reference's ``{:?}`` does (the variant: ``Q4K``)."""
     dtype = GgmlDType(dtype)
-    if dtype not in SERVED and dtype not in ACT_TYPES and dtype not in (GgmlDType.F32, GgmlDType.F16):
+    if dtype not in SERVED and dtype not in ACT_TYPES:
         raise ValueError(f"Dequantization for {dtype.name} not yet implemented")
     bs, ts = dtype.block_size(), dtype.block_bytes()
     num_blocks = (elem_count + bs - 1) // bs

@@ -29,8 +29,22 @@ def test_type_table_matches_reference(lbq):
                       (10, 256, 82), (11, 256, 110), (12, 256, 144), (13, 256, 176), (14, 256, 210), (15, 256, 292)]:
         assert lbq.lbq_type_block_size(t) == bs and lbq.lbq_type_size(t) == ts
         assert lbq.lbq_type_block_bytes(t) == (84 if t == 10 else ts)
-    for t in (4, 5, 16, 999):
+    for t in (4, 5, 16, 29, 31, 999):
         assert lbq.lbq_type_block_size(t) == 0 and lbq.lbq_type_size(t) == 0 and lbq.lbq_type_block_bytes(t) == 0
+
+
+def test_bf16_is_served(lbq):
+    # candle's GgmlDType::BF16 (GGUF id 30), which QMatMul::from_qtensor serves as
+    # its dense variant: one 2-byte value per block; the weight path accepts it
+    # (lbq_dequantize_blocks_f32 checks the type before the size: an unknown id
+    # gives -2, a served one with a bad size -3)
+    from lightbulb_amd.quantized import SERVED, GgmlDType
+    assert lbq.lbq_type_block_size(30) == 1 and lbq.lbq_type_size(30) == 2 and lbq.lbq_type_block_bytes(30) == 2
+    assert GgmlDType.BF16 == 30 and GgmlDType.BF16 in SERVED and GgmlDType.BF16.is_dense()
+    assert GgmlDType.from_u32(30) is None  # the reference's own from_u32 does not know it
+    dummy = ctypes.c_void_p(256)
+    assert lbq.lbq_dequantize_blocks_f32(29, dummy, -1, dummy, None) == -2
+    assert lbq.lbq_dequantize_blocks_f32(30, dummy, -1, dummy, None) == -3
 
 
 def test_argument_errors_without_device(lbq):

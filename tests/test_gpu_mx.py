@@ -15,7 +15,7 @@ import pytest
 
 import blockpack as bp
 from test_gpu_nonfinite import _nan_rows, _poison
-from test_gpu_parity import Q4_K, Q5_K, assert_rows_close, gpu_qmatmul
+from test_gpu_parity import Q4_K, Q5_K, Q6_K, assert_rows_close, gpu_qmatmul
 from test_gpu_q8_0_dense import forward_with_env
 
 pytestmark = pytest.mark.gpu
@@ -142,6 +142,95 @@ def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
     assert np.array_equal(bits(y), bits(y2))
     assert np.array_equal(bits(y), bits(yg[0]))
     assert np.array_equal(bits(y1b), bits(yg[1]))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+def test_mx_split_halves_subnormal_and_host_output(oracle, lbq, dev, t):
+    # Two-way split tiles at m = 8: with tiny weight scales (f16 d ~1e-7) and a tiny
+    # x (~1e-36, Q8_K scales ~1e-38) the halves are subnormal f32.  forward() adds them with f32 atomics into y (plain device
+    # memory); the pre-quantised handle, and forward() into host-pinned memory
+    # (which takes no atomics), add them through the workspace.  Halves in the
+    # normal range give the same bits either way; subnormal ones may differ only by
+    # the subnormal part (an atomic add may flush it), never by more than 2^-126.
+    import ctypes
+    import torch
+    from lightbulb_amd import _lib
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(960 + t)
+    m, n, k = 8, 2048, 4096
+    L = _lib.lib()
+    bits = lambda a: np.asarray(a).view(np.uint32)
+    for scale, d_scale in ((1.0, 1e-3), (1e-36, 1e-7)):
+        raw = bp.random_blocks(rng, t, n * k // 256, d_scale=d_scale)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(raw, dev), t, (n, k)))
+        x = (rng.standard_normal((m, k)) * scale).astype(np.float32)
+        xd = to_dev(x, dev)
+        print(f"mx split subnormal t={t} scale={scale}", flush=True)
+        y = qm.forward(xd)
+        y2 = qm.forward_quantized(QActivation.for_weight(qm, m).quantize(xd))
+        yh = torch.empty(m, n, dtype=torch.float32, pin_memory=True)
+        _lib.check(L.lbq_qmatmul_f32(qm._ctx, qm._handle, xd.data_ptr(), m, yh.data_ptr(),
+                                     ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        torch.cuda.synchronize()
+        a, b, h = y.cpu().numpy(), y2.cpu().numpy(), yh.numpy()
+        assert np.array_equal(bits(b), bits(h))  # the same protocol, device or host output
+        normal = np.abs(b) >= np.float32(2.0 ** -126)
+        assert np.array_equal(bits(a)[normal], bits(b)[normal])
+        assert np.all(np.abs(a.astype(np.float64) - b) <= 2.0 ** -126)
+        if scale == 1.0:
+            ref = oracle.qmatmul(t, raw, n, k, x, nthreads=8).astype(np.float64)
+            assert_rows_close(a, ref, 1e-4)
+        else:
+            assert (~normal).sum() > 0  # the case exercises subnormal halves
+
+
+def test_overlapping_x_and_y_refused(lbq, dev):
+    # QMatMul::forward returns a new tensor; an output that overlaps the input is refused
+    import torch
+    from lightbulb_amd import _lib
+    from lightbulb_amd.quantized import QMatMul, QTensor
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(970)
+    n = k = 256
+    qm = QMatMul.from_qtensor(QTensor(to_dev(bp.random_blocks(rng, Q4_K, n * k // 256, d_scale=1e-3), dev), Q4_K, (n, k)))
+    buf = torch.zeros(4 * k, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    assert L.lbq_qmatmul_f32(qm._ctx, qm._handle, buf.data_ptr(), 2, buf[k:].data_ptr(), None) == -1
+    assert b"overlap" in L.lbq_last_error()
+    assert L.lbq_qmatmul_f32(qm._ctx, qm._handle, buf.data_ptr(), 1, buf[k:].data_ptr(), None) == 0
+    torch.cuda.synchronize()
+
+
+def test_wrapped_weight_refresh(oracle, lbq, dev):
+    # a handle wrapped over zero-filled device memory, the blocks written afterwards:
+    # lbq_weight_refresh recomputes the MFMA GEMM's per-row exponents, after which
+    # m > 8 forwards are correct (m <= 8 never used them)
+    import ctypes
+    import torch
+    from lightbulb_amd import _lib
+    from lightbulb_amd.quantized import context
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(980)
+    n, k = 512, 4096
+    raw = bp.random_blocks(rng, Q6_K, n * k // 256, d_scale=1e-3)
+    L = _lib.lib()
+    ctx = context(dev)
+    buf = torch.zeros(raw.size, dtype=torch.uint8, device=dev)
+    h = ctypes.c_void_p()
+    _lib.check(L.lbq_weight_wrap_device(ctx, Q6_K, n, k, buf.data_ptr(), raw.size, ctypes.byref(h)))
+    buf.copy_(to_dev(raw, dev))
+    _lib.check(L.lbq_weight_refresh(h, ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+    for m in (1, 64):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = torch.empty(m, n, dtype=torch.float32, device=dev)
+        _lib.check(L.lbq_qmatmul_f32(ctx, h, to_dev(x, dev).data_ptr(), m, y.data_ptr(),
+                                     ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        torch.cuda.synchronize()
+        ref = oracle.qmatmul(Q6_K, raw, n, k, x, nthreads=8).astype(np.float64)
+        assert_rows_close(y.cpu().numpy(), ref, 1e-4 if m == 1 else 1.5e-3)
+    assert L.lbq_weight_refresh(None, None) == -1
+    _lib.check(L.lbq_weight_destroy(h))
 
 
 def _gate_up_env(monkeypatch, env, t, g_raw, u_raw, n, k, x, dev):

@@ -7,10 +7,12 @@
   tiles), at configs[0]'s 4096 x 4096 for M = 16 / 64 / 512, and the operands
   built from f32 x and from pre-quantised codes agree to the bit.
 * Dense weights are candle's dense QMatMul variant (QMatMul::from_qtensor
-  dequantises F32 / F16 and forward is an f32 matmul): checked against a
+  dequantises F32 / F16 / BF16 and forward is an f32 matmul): checked against a
   float64 x . W^T at the 2e-3 bar (and a 1e-5 guard: the device computes in
   f32 too), through forward, the grouped and gate/up entry points, a GGUF
-  file holding F16 and F32 output.weight tensors, and the embedding gather.
+  file holding F16, F32 and BF16 output.weight tensors, and the embedding gather.
+  BF16 values are widened exactly (the 16 bits are the f32's upper half), so
+  dequantisation and the embedding gather are bit-exact against numpy.
 * Launch-plan overrides (read from the environment when a context is created)
   route shapes to every k-slice length and tile kind; results stay within the
   guard.
@@ -25,7 +27,17 @@ import blockpack as bp
 from test_gpu_parity import Q4_K, Q5_K, Q6_K, Q8_0, assert_rows_close, gpu_qmatmul, tight_bound, to_dev
 
 pytestmark = pytest.mark.gpu
-F32, F16 = 0, 1
+F32, F16, BF16 = 0, 1, 30
+
+
+def _bf16_bits(w: np.ndarray) -> np.ndarray:
+    """f32 -> bfloat16 bits (round to nearest even), as uint16."""
+    u = np.ascontiguousarray(w, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
 
 
 # ---------------------------------------------------------------- Q8_0 on MFMA
@@ -97,6 +109,10 @@ def test_q8_0_grouped_batched(oracle, lbq, dev):
 def _dense(t, n, k, rng, dev):
     from lightbulb_amd.quantized import QMatMul, QTensor
     w = (rng.standard_normal((n, k)) * 0.05).astype(np.float16 if t == F16 else np.float32)
+    if t == BF16:
+        b = _bf16_bits(w)
+        qm = QMatMul.from_qtensor(QTensor(to_dev(b.view(np.uint8).reshape(-1), dev), t, (n, k)))
+        return qm, _bf16_to_f32(b).astype(np.float64)
     qm = QMatMul.from_qtensor(QTensor(to_dev(w.view(np.uint8).reshape(-1), dev), t, (n, k)))
     return qm, w.astype(np.float64)
 
@@ -105,7 +121,7 @@ def _assert_dense(y, ref):
     assert_rows_close(y, ref, 1e-5)
 
 
-@pytest.mark.parametrize("t", [F32, F16])
+@pytest.mark.parametrize("t", [F32, F16, BF16])
 @pytest.mark.parametrize("m", [1, 3, 8, 9, 40, 130])
 def test_dense_forward(lbq, dev, t, m):
     rng = np.random.default_rng(450 + m + t)
@@ -143,8 +159,9 @@ def test_dense_unaligned_x_and_entry_points(lbq, dev):
 
 
 def test_dense_gguf_output_weight(lbq, dev, tmp_path):
-    # a GGUF holding F16 and F32 output.weight tensors (and an F16 embedding table):
-    # loaded both ways and forwarded as the reference's dense QMatMul
+    # a GGUF holding F16, F32 and BF16 output.weight tensors (and F16 / BF16
+    # embedding tables): loaded both ways and forwarded as the reference's dense
+    # QMatMul; extract_tensor_bytes' mirror refuses BF16 as the reference does
     import gguf_writer as gw
     from lightbulb_amd import _lib
     from lightbulb_amd.gguf import Content
@@ -153,15 +170,18 @@ def test_dense_gguf_output_weight(lbq, dev, tmp_path):
     n, k = 1000, 256
     w16 = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
     w32 = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    b16 = _bf16_bits(rng.standard_normal((n, k)) * 0.05)
+    wbf = _bf16_to_f32(b16)
     blob, _, _ = gw.build([("general.architecture", gw.STR, "llama")],
                           [("output.weight", [k, n], F16, w16.tobytes()), ("output32.weight", [k, n], F32, w32.tobytes()),
-                           ("token_embd.weight", [k, n], F16, w16.tobytes())])
+                           ("token_embd.weight", [k, n], F16, w16.tobytes()), ("outputbf.weight", [k, n], BF16, b16.tobytes()),
+                           ("token_embd_bf.weight", [k, n], BF16, b16.tobytes())])
     path = tmp_path / "dense.gguf"
     path.write_bytes(blob)
     L = _lib.lib()
     x = rng.standard_normal((4, k)).astype(np.float32)
     with Content.read(path) as c:
-        for name, w in (("output.weight", w16), ("output32.weight", w32)):
+        for name, w in (("output.weight", w16), ("output32.weight", w32), ("outputbf.weight", wbf)):
             qm = QMatMul.from_qtensor(c.tensor(name, dev))
             y = qm.forward(to_dev(x, dev)).cpu().numpy()
             _assert_dense(y, x.astype(np.float64) @ w.astype(np.float64).T)
@@ -177,6 +197,23 @@ def test_dense_gguf_output_weight(lbq, dev, tmp_path):
         ids = np.array([0, 999, 5, 5], dtype=np.int64)
         got = emb.forward(torch.from_numpy(ids).to(dev)).cpu().numpy()
         assert np.array_equal(got, w16.astype(np.float32)[ids])
+        emb = QEmbedding(c.tensor("token_embd_bf.weight", dev))
+        got = emb.forward(torch.from_numpy(ids).to(dev)).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), wbf[ids].view(np.uint32))
+        # extract_tensor_bytes (lbq_gguf_tensor_bytes) keeps the reference's table: no BF16
+        p, nb = ctypes.c_void_p(), ctypes.c_uint64()
+        assert L.lbq_gguf_tensor_bytes(c._h, b"outputbf.weight", ctypes.byref(p), ctypes.byref(nb)) == -2
+        assert b"Unknown quantization type: 30" in L.lbq_last_error()
+
+
+def test_bf16_dequantize_bit_exact(lbq, dev):
+    # QTensor::dequantize of a BF16 tensor: the exact widening, every bit pattern class
+    from lightbulb_amd.quantized import GgmlDType, dequantize_tensor
+    rng = np.random.default_rng(475)
+    b = rng.integers(0, 1 << 16, size=4096, dtype=np.uint32).astype(np.uint16)
+    b[:6] = [0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC1, 0x0001]  # +-0, +-inf, a NaN, a subnormal
+    got = dequantize_tensor(to_dev(b.view(np.uint8), dev), GgmlDType.BF16, 4095).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), _bf16_to_f32(b)[:4095].view(np.uint32))
 
 
 def test_dense_errors(lbq, dev):

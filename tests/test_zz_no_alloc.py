@@ -49,10 +49,10 @@ def _both(L, ctx, h, x, n, dev):
     (Q4_K, 1000, 4096, (1, 1)),        # fused decode GEMV (no scratch)
     (Q4_K, 1000, 4096, (8, 4)),        # pre-quantised multi-row GEMV
     (Q6_K, 700, 4096, (300, 40)),      # tall / k-sliced MFMA tiles
-    (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then the integer matrix-core decode (split)
+    (Q4_K, 4096, 14336, (512, 16)),    # split-k partials, then the integer matrix-core decode (two-way split, atomic adds)
     (Q5_K, 14336, 4096, (200, 32)),    # wide tiles, then the integer matrix-core decode
     (Q6_K, 8192, 4096, (16, 13)),      # slices added in the kernel twice (tile counters left zero)
-    (Q4_K, 4096, 4096, (8, 6)),        # integer matrix-core decode, two workgroups per tile (partials, counters)
+    (Q4_K, 4096, 4096, (8, 6)),        # integer matrix-core decode, two workgroups per tile adding into y
     (Q5_K, 4096, 4096, (32, 12)),      # the same at 32 and 16 rows
     (Q8_0, 512, 4096, (64, 12)),       # Q8_0 on MFMA
     (Q4_0, 300, 1184, (20, 9)),        # activation scratch + GEMV row chunks (k % 256 != 0)
@@ -77,6 +77,34 @@ def test_noalloc_matches_qmatmul(oracle, lbq, dev, t, n, k, ms):
             else:
                 ref = oracle.qmatmul(t, raw, n, k, x[rows], nthreads=8).astype(np.float64)
                 assert_rows_close(y2[rows], ref, tight_bound(t, m) if k % 256 == 0 else 1e-4)
+    finally:
+        L.lbq_weight_destroy(h)
+
+
+def test_noalloc_split_tiles_through_workspace(oracle, lbq, dev):
+    # An output in host-pinned memory takes no atomic adds: the two workgroups of a
+    # split 32-row tile store partials in the fixed array and the one that completes
+    # the tile's counter (at the array's end) adds them.  Same bits as
+    # lbq_qmatmul_f32 into device memory (atomic adds); two calls, the second smaller.
+    from lightbulb_amd.quantized import context
+    L = lbq
+    ctx = context(dev)
+    rng = np.random.default_rng(640)
+    n, k = 4096, 4096
+    h, wd, raw = _weight(L, ctx, Q4_K, n, k, rng, dev)
+    try:
+        for m in (8, 6):
+            x = to_dev(rng.standard_normal((m, k)).astype(np.float32), dev)
+            st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+            y1 = torch.full((m, n), np.nan, device=dev)
+            y2 = torch.full((m, n), np.nan, dtype=torch.float32, pin_memory=True)
+            assert L.lbq_qmatmul_f32(ctx, h, x.data_ptr(), m, y1.data_ptr(), st) == 0
+            assert L.lbq_qmatmul_f32_noalloc(ctx, h, x.data_ptr(), m, y2.data_ptr(), st) == 0, L.lbq_last_error()
+            torch.cuda.synchronize()
+            a, b = y1.cpu().numpy(), y2.numpy()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), m
+            ref = oracle.qmatmul(Q4_K, raw, n, k, x.cpu().numpy()[[0, m - 1]], nthreads=8).astype(np.float64)
+            assert_rows_close(b[[0, m - 1]], ref, 1e-4)
     finally:
         L.lbq_weight_destroy(h)
 
