@@ -64,6 +64,9 @@ def parse():
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a 256 MiB device copy 4 times (reference kernel of known size for "
                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    p.add_argument("--read-probe", action="store_true",
+                   help="only the headline step and the read-only stream over the same bytes (read_floor), "
+                        "a short fixed workload for rocprofv3 counter runs of both")
     return p.parse_args()
 
 
@@ -75,6 +78,43 @@ def copy_probe(torch, dev):
     torch.cuda.synchronize()
     log(f"copy probe: 4 x {src.numel() * 4} B copies")
     del src, dst
+
+
+def read_floor(torch, copies, stream, reps):
+    """The same weight bytes as the headline step, read by a plain read-only stream
+    (liblbq_probe.so: every wave a contiguous range, four 1 KiB steps in flight, eight
+    waves per CU): one launch per projection, the 7 launches of a step and the same
+    copies rotated, HIP-graph replay.  The floor the decode kernels are compared with."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "lightbulb_amd" / "liblbq_probe.so"))
+    lib.lbq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.lbq_probe_read.restype = ctypes.c_int
+    out = torch.zeros(16, dtype=torch.int32, device=stream.device)
+    grid = torch.cuda.get_device_properties(stream.device).multi_processor_count * 2
+
+    def read(qm):
+        d = qm.qtensor().data
+        st = ctypes.c_void_p(torch.cuda.current_stream(d.device).cuda_stream)  # the capturing stream in capture
+        if lib.lbq_probe_read(d.data_ptr(), d.numel(), out.data_ptr(), grid, st) != 0:
+            raise RuntimeError("lbq_probe_read failed")
+
+    def step(layer):
+        for qm in layer:
+            read(qm)
+    g = StepGraphs(torch, step, copies)
+    g.run(len(copies))
+    ms_step = g.time(reps * len(copies), stream)
+    per = {}
+    for i, (name, n, k) in enumerate(LAYER):
+        if name in ("k_proj", "up_proj", "o_proj"):
+            continue  # same shape as v_proj / gate_proj / q_proj
+        gi = capture(torch, lambda i=i: [read(layer[i]) for layer in copies])
+        timed_graph(torch, gi, 2, stream)
+        per[f"{name}_{n}x{k}"] = round(timed_graph(torch, gi, reps, stream) / len(copies) * 1e3, 3)
+        del gi
+    del g
+    return {"us_per_step": round(ms_step * 1e3, 3), "us_per_launch": per, "grid": grid,
+            "kernel": "k_probe_read (liblbq_probe.so): loads only, per-wave contiguous 1 KiB steps, 4 in flight"}
 
 
 def load_traffic():
@@ -308,6 +348,11 @@ def main():
     if warmup:
         g_full.run(warmup)
     ms_full = g_full.time(steps, stream)
+    floor = read_floor(torch, copies, stream, max(2, (steps + args.copies - 1) // args.copies))
+    log(f"read-only stream of the same bytes: {floor['us_per_step']:.2f} us per step; per launch {floor['us_per_launch']}")
+    if args.read_probe:
+        print(json.dumps({"us_per_step": round(ms_full * 1e3, 3), "read_floor": floor}), flush=True)
+        return
     reps = max(1, (steps + args.copies - 1) // args.copies)
     wreps = max(1, (warmup + args.copies - 1) // args.copies)
     side = max(args.copies, min(steps, 8 * args.copies))  # steps timed for the side measurements
@@ -369,9 +414,9 @@ def main():
             "unit": "GB/s",
             "frac": round(full_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "k_gemv1<Q4_K, fused> (quantise x + dequant/int-dot GEMV, one launch per projection: "
-                      "4 lanes per block at k = 4096, 8 at k = 14336; eight-wave workgroups for gate/up); "
-                      "algorithmic bytes per launch = "
+            "kernel": "k_gemv1<Q4_K, fused> (quantise x + dequant/int-dot GEMV, one launch per projection, "
+                      "four lanes per block, static group schedule: q/o 4 and k/v 1 row per wave in four-wave "
+                      "workgroups, gate/up 7 and down 2 in eight-wave workgroups); algorithmic bytes per launch = "
                       "N*K/256*144 + 4K + 4N, averaged over the 7 launches",
             "us_per_launch": round(ms_full * 1e3 / len(LAYER), 3),
             "algorithmic_bytes_per_launch": round((layer_bytes + io_bytes) / len(LAYER)),
@@ -398,6 +443,7 @@ def main():
                                 "back to pinned host memory, on one stream (a caller whose tensors live on "
                                 "the host); PCIe-inclusive, not the headline"},
         "kernels": kernels,
+        "read_floor": floor,
     }
     del g_full, g_dot, g_grp, g_fus, g_host
     tr = load_traffic()
@@ -447,6 +493,19 @@ def prefill_profile(torch, qz, dev):
     print(json.dumps({"prefill_profile_us": out}), flush=True)
 
 
+ROTATE_BYTES = 512e6  # every leg rotates at least this many distinct weight bytes (MALL: 256 MB)
+
+
+def n_copies(nbytes: int) -> int:
+    """Weight copies whose bytes together exceed ROTATE_BYTES (at least 2)."""
+    return max(2, -(-int(ROTATE_BYTES) // int(nbytes)) + (1 if int(ROTATE_BYTES) % int(nbytes) == 0 else 0))
+
+
+def ws_mb(qms) -> float:
+    """Working set of a rotation: the distinct weight bytes one replay streams (MB)."""
+    return round(sum(q.qtensor().storage_size_in_bytes() for q in qms) / 1e6, 1)
+
+
 def time_forwards(torch, qms, x, stream, reps=25, warm=3):
     """us per QMatMul::forward: one graph replay runs forward over every weight copy in qms
     (rotating copies keeps the working set out of the MALL); median over `reps` replays."""
@@ -464,7 +523,8 @@ def gemm_bench(torch, qz, gen, dev, stream):
     out = {}
     M = 512
     for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
-        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(2)]
+        nc = n_copies(n * k // 256 * 144)
+        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(nc)]
         x = torch.randn(M, k, generator=gen, device=dev)
         y = torch.empty(M, n, device=dev)
         act = qz.QActivation.for_weight(qms[0], M).quantize(x)
@@ -479,7 +539,7 @@ def gemm_bench(torch, qz, gen, dev, stream):
             "TFLOP/s_forward": round(fl / us_f / 1e6, 1), "TFLOP/s_dot": round(fl / us_d / 1e6, 1),
             "frac_bf16_peak_forward": round(fl / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
             "frac_bf16_peak_dot": round(fl / us_d / 1e6 / BF16_PEAK_TFLOPS, 4),
-            "weight_GB/s_forward": round(nbytes / us_f / 1e3, 1)}
+            "weight_GB/s_forward": round(nbytes / us_f / 1e3, 1), "working_set_MB": ws_mb(qms)}
         log(f"gemm {name} M={M}: forward {us_f:.1f} us, dot {us_d:.1f} us ({fl / us_d / 1e6:.0f} TFLOP/s)")
         del g_d, qms, x, y, act
     torch.cuda.empty_cache()
@@ -510,23 +570,24 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
         mask = torch.rand(b, k, generator=gen, device=dev) < 0.01
         return torch.where(mask, x * 20.0, x)
 
-    # Q8_0 GEMV (17.8 MB per copy, 16 copies)
-    q8 = [make_weights(torch, qz, qz.GgmlDType.Q8_0, 4096, 4096, gen, dev) for _ in range(16)]
+    # Q8_0 GEMV (17.8 MB per copy, 29 copies)
+    q8 = [make_weights(torch, qz, qz.GgmlDType.Q8_0, 4096, 4096, gen, dev) for _ in range(n_copies(4096 * 128 * 34))]
     wb = q8[0].qtensor().storage_size_in_bytes()
     us = timed_rot(q8, torch.randn(1, 4096, generator=gen, device=dev), 20)
     out["q8_0_4096x4096_m1"] = {"us": round(us, 2), "weight_GB/s": round(wb / us / 1e3, 1),
-                                "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4), "working_set_MB": ws_mb(q8)}
     # dense F16 weights (candle's dense QMatMul variant: an f32 matmul), 4096 x 4096
     f16 = []
-    for _ in range(8):
+    for _ in range(n_copies(4096 * 4096 * 2)):
         w = (torch.randn(4096, 4096, generator=gen, device=dev) * 0.02).to(torch.float16)
         f16.append(qz.QMatMul.from_qtensor(qz.QTensor(w.view(torch.uint8).reshape(-1), qz.GgmlDType.F16, (4096, 4096))))
     fb = 4096 * 4096 * 2
     for M in (1, 512):
         x = torch.randn(M, 4096, generator=gen, device=dev)
-        us = timed_rot(f16 if M == 1 else f16[:2], x, 20)
+        us = timed_rot(f16, x, 20)
         fl = 2.0 * M * 4096 * 4096
         out[f"f16_dense_4096x4096_m{M}"] = {"us": round(us, 2), "weight_GB/s": round(fb / us / 1e3, 1),
+                                           "working_set_MB": ws_mb(f16),
                                            "frac_hbm": round(fb / us / 1e3 / HBM_PEAK_GBS, 4),
                                            "TFLOP/s": round(fl / us / 1e6, 1),
                                            "path": "f32 GEMV (m <= 8) / v_mfma_f32_32x32x2_f32 GEMM (fp32 peak 157.3 TFLOP/s)"}
@@ -535,9 +596,10 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
     # Q8_0 batched on the MFMA path (prefill of the same weight)
     for M in (16, 64, 512):
         x = torch.randn(M, 4096, generator=gen, device=dev)
-        us = timed_rot(q8 if M <= 64 else q8[:2], x, 20)
+        us = timed_rot(q8, x, 20)
         fl = 2.0 * M * 4096 * 4096
         out[f"q8_0_4096x4096_m{M}"] = {"us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                                       "working_set_MB": ws_mb(q8),
                                        "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                                        "weight_GB/s": round(wb / us / 1e3, 1),
                                        "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
@@ -549,13 +611,15 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
     # files the reference's own tests serve, e.g. a Q4_0 TinyLlama, prefill this way)
     for t, tname in ((qz.GgmlDType.Q4_0, "q4_0"), (qz.GgmlDType.Q4_1, "q4_1"), (qz.GgmlDType.Q5_0, "q5_0"),
                      (qz.GgmlDType.Q5_1, "q5_1")):
-        qms = [make_weights(torch, qz, t, 4096, 4096, gen, dev) for _ in range(8)]
+        bpb = {qz.GgmlDType.Q4_0: 18, qz.GgmlDType.Q4_1: 20, qz.GgmlDType.Q5_0: 22, qz.GgmlDType.Q5_1: 24}[t]
+        qms = [make_weights(torch, qz, t, 4096, 4096, gen, dev) for _ in range(n_copies(4096 * 128 * bpb))]
         lb = qms[0].qtensor().storage_size_in_bytes()
         for M in (16, 512):
             x = torch.randn(M, 4096, generator=gen, device=dev)
-            us = timed_rot(qms if M <= 64 else qms[:2], x, 20)
+            us = timed_rot(qms, x, 20)
             fl = 2.0 * M * 4096 * 4096
             out[f"{tname}_4096x4096_m{M}"] = {"us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                                              "working_set_MB": ws_mb(qms),
                                               "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                                               "weight_GB/s": round(lb / us / 1e3, 1),
                                               "frac_hbm": round(lb / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -563,9 +627,9 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
         del qms
     torch.cuda.empty_cache()
 
-    # Q6_K LM head (431 MB, one copy exceeds the MALL) and Q5_K gate/up (8 copies)
-    head = [make_weights(torch, qz, qz.GgmlDType.Q6K, VOCAB, 4096, gen, dev)]
-    q5 = [make_weights(torch, qz, qz.GgmlDType.Q5K, 14336, 4096, gen, dev) for _ in range(8)]
+    # Q6_K LM head (431 MB, two copies) and Q5_K gate/up (13 copies of 40 MB)
+    head = [make_weights(torch, qz, qz.GgmlDType.Q6K, VOCAB, 4096, gen, dev) for _ in range(n_copies(VOCAB * 16 * 210))]
+    q5 = [make_weights(torch, qz, qz.GgmlDType.Q5K, 14336, 4096, gen, dev) for _ in range(n_copies(14336 * 16 * 176))]
     hb, q5b = head[0].qtensor().storage_size_in_bytes(), q5[0].qtensor().storage_size_in_bytes()
     for B in (1, 4, 8):
         x = x_outliers(B, 4096)
@@ -578,15 +642,16 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
             else:
                 path = "Q8_K quantisation, then the integer matrix-core kernel (v_mfma_i32_32x32x32_i8)"
             out[f"{name}_b{B}"] = {"us": round(us, 2), "weight_GB/s": round(nbytes / us / 1e3, 1),
-                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "path": path}
+                                   "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "path": path,
+                                   "working_set_MB": ws_mb(qms)}
         log(f"configs[2] batch {B}: head {out[f'q6_k_head_128256x4096_b{B}']['us']} us, "
             f"q5_k {out[f'q5_k_gate_up_14336x4096_b{B}']['us']} us")
     del head, q5
     torch.cuda.empty_cache()
 
-    # Q4_K gate / down at M = 16, 64, 512, 2048 (8 copies of each: 264 MB)
+    # Q4_K gate / down at M = 16, 64, 512, 2048 (16 copies of each: 528 MB)
     for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
-        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(8)]
+        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(n_copies(n * k // 256 * 144))]
         nbytes = qms[0].qtensor().storage_size_in_bytes()
         for M in (16, 64, 512, 2048):
             key = f"{name}_{n}x{k}_m{M}"
@@ -594,10 +659,10 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
                 us = prefill[key]["us_forward"]
             else:
                 x = torch.randn(M, k, generator=gen, device=dev)
-                us = timed_rot(qms if M <= 64 else qms[:2], x, 20)
+                us = timed_rot(qms, x, 20)
             fl = 2.0 * M * n * k
             out[f"q4_k_{name}_{n}x{k}_m{M}"] = {
-                "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1),
+                "us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1), "working_set_MB": ws_mb(qms),
                 "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                 "weight_GB/s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
                 "bound": "hbm" if M <= 64 else "mfma",

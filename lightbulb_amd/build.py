@@ -64,16 +64,27 @@ def _compile(src: str) -> Path:
     return out
 
 
-def build(verbose: bool = True) -> Path:
-    OBJ.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+# measurement-only kernels for bench.py (a read-only stream), kept out of liblbq.so
+PROBE_SOURCES = ["lbq_probe.hip"]
+PROBE_LIB = PKG / "liblbq_probe.so"
+
+
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES) + len(PROBE_SOURCES), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, SOURCES + PROBE_SOURCES))
+    _link(objs[len(SOURCES):], PROBE_LIB)
+    objs = objs[:len(SOURCES)]
+    _link(objs, LIB)
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
     return LIB

@@ -1,4 +1,4 @@
-"""BASELINE configs[4] at batch 32, on the GPU, against the oracle.
+"""BASELINE configs[4] at batch 32 (and its shapes at batch 1), on the GPU, against the oracle.
 
 The stack's B = 32 step runs every distinct (type, shape) of the Llama-3-8B
 Q4_K_M mix at m = 32, where the k-sliced MFMA kernel's slice length depends on
@@ -40,6 +40,19 @@ def test_stack_shape_b32(oracle, lbq, dev, t, n, k):
     qm, raw = quantised(t, n, k, dev, 0x1B5 + n + k + t)
     x = np.random.default_rng(5 + n + t).standard_normal((B, k)).astype(np.float32)
     _check(oracle, qm, raw, t, n, k, x)
+
+
+@pytest.mark.parametrize("t,n,k", [(Q6_K, 1024, 4096), (Q6_K, 4096, 14336), (Q4_K, 1024, 4096),
+                                   (Q4_K, 4096, 4096), (Q4_K, 14336, 4096), (Q4_K, 4096, 14336)])
+def test_stack_shape_b1(oracle, lbq, dev, t, n, k):
+    # the same stack shapes at batch 1 (the decode launch plan depends on n through
+    # the groups per wave), every row against the oracle at the decode bound
+    qm, raw = quantised(t, n, k, dev, 0x1B9 + n + k + t)
+    x = np.random.default_rng(9 + n + t).standard_normal((1, k)).astype(np.float32)
+    y = qm.forward(torch.from_numpy(x).to(qm.qtensor().data.device))
+    torch.cuda.synchronize()
+    ref = oracle.qmatmul(t, raw, n, k, x, nthreads=oracle.nproc()).astype(np.float64)
+    assert_rows_close(y.cpu().numpy(), ref, tight_bound(t, 1))
 
 
 def test_stack_call_sites_b32(oracle, lbq, dev):
