@@ -348,7 +348,7 @@ def main():
     if warmup:
         g_full.run(warmup)
     ms_full = g_full.time(steps, stream)
-    floor = read_floor(torch, copies, stream, max(2, (steps + args.copies - 1) // args.copies))
+    floor = read_floor(torch, copies, stream, max(20, (steps + args.copies - 1) // args.copies))
     log(f"read-only stream of the same bytes: {floor['us_per_step']:.2f} us per step; per launch {floor['us_per_launch']}")
     if args.read_probe:
         print(json.dumps({"us_per_step": round(ms_full * 1e3, 3), "read_floor": floor}), flush=True)

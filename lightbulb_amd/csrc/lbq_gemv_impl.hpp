@@ -786,10 +786,12 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
         // schedule where every wave holds at most 8 groups.  At k > 12288 eight-wave
         // workgroups (8 per CU): the x prologue over 512 threads, two groups per wave
         // for 4096 rows (4096 x 14336: 10.2 -> 8.7 us with the 64-weight pieces)
-        if constexpr (W8_OK && RPW == 1 && (IT == 1 || IT == 4))
+        if constexpr ((W8_OK || TYPE == TYPE_Q6_K) && RPW == 1 && (IT == 1 || IT == 4))
             if (!tuning().gemv1_dynamic) {
-                const bool s8 = IT == 4 || w8;
-                const int64_t sw = IT == 4 ? std::min<int64_t>((int64_t)num_cus() * 8, ng) : waves;
+                // (Q6_K: eight-wave workgroups at k > 12288 only -- its pieces take 15
+                // registers, and the two groups per wave fit beside them there)
+                const bool s8 = IT == 4 || (W8_OK && w8);
+                const int64_t sw = (IT == 4 && s8) ? std::min<int64_t>((int64_t)num_cus() * 8, ng) : waves;
                 const unsigned sg = (unsigned)((sw + (s8 ? 7 : 3)) / (s8 ? 8 : 4));
                 if (s8 ? try_static<TYPE, PPB, RPW, IT, 8>(rm, row_bytes, nb, x, ng, sg, lds, st)
                        : try_static<TYPE, PPB, RPW, IT, 4>(rm, row_bytes, nb, x, ng, sg, lds, st))
@@ -934,13 +936,38 @@ static hipError_t run_fast(const RowMap &rm, int64_t row_bytes, int nb, const fl
                            const float *alpha, float eps, hipStream_t st) {
     int ppb, rpw, it;
     if (!fast_shape<TYPE>(nb, &ppb, &rpw, &it)) return hipErrorNotSupported;
+    // Q6_K at k <= 4096 pairs rows in a wave (two per group) for long streams
+    // (128256 x 4096: 97 against 107 us with one row per group; 14336 x 4096: 14.7
+    // against 16.2); a weight of at most 8192 rows takes one row per group instead,
+    // so every CU gets a workgroup (1024 x 4096: 512 groups would fill half the
+    // chip; 4.8 -> 3.4 us).  The choice is the weight's, whatever the launch: fused
+    // or not, alone, in a group or a gate/up pair, each row keeps one summation
+    // order; a group whose weights fall on both sides runs weight by weight.
+    if (TYPE == TYPE_Q6_K && rpw == 2 && tuning().gemv1_ppb == 0) {
+        bool small = false, large = false;
+        if (map == MAP_SEGMENTS) {
+            int32_t prev = 0;
+            for (int s = 0; s < GROUP_MAX && prev < rm.n; s++) {
+                const int32_t end = (int32_t)std::min<int64_t>(rm.end[s], rm.n);
+                (end - prev <= 8192 ? small : large) = true;
+                prev = end;
+            }
+        } else {
+            (rm.n / (map == MAP_SILU_PAIRS ? 2 : 1) <= 8192 ? small : large) = true;
+        }
+        if (small && large) return hipErrorNotSupported;
+        if (small) {
+            rpw = 1;
+            it = (nb + 15) / 16;
+        }
+    }
 #define LBQ_FAST(Q, R, I) \
     if (ppb == Q && rpw == R && it == I) return launch_fast<TYPE, Q, R, I>(rm, row_bytes, nb, x, act, map, alpha, eps, st);
     if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
         LBQ_FAST(4, 4, 1) LBQ_FAST(4, 2, 1) LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
         LBQ_FAST(8, 1, 7)
     } else if constexpr (TYPE == TYPE_Q6_K) {
-        LBQ_FAST(4, 2, 1) LBQ_FAST(4, 2, 2) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
+        LBQ_FAST(4, 2, 1) LBQ_FAST(4, 2, 2) LBQ_FAST(4, 1, 1) LBQ_FAST(4, 1, 2) LBQ_FAST(4, 1, 3) LBQ_FAST(4, 1, 4)
     } else {
         LBQ_FAST(1, 1, 1) LBQ_FAST(1, 1, 2) LBQ_FAST(1, 1, 3) LBQ_FAST(1, 1, 4) LBQ_FAST(1, 1, 5) LBQ_FAST(1, 1, 6)
         LBQ_FAST(1, 1, 7) LBQ_FAST(1, 1, 8)
