@@ -91,11 +91,13 @@ __global__ __launch_bounds__(T) void k_act_f16(ActView act, int64_t M, _Float16 
 // quantises its row to Q8_K in registers (q8k_lane16, as the standalone
 // quantiser), shares the block scales through LDS for the row exponent, and
 // converts with the same arithmetic as k_act_f16 -- one launch instead of two,
-// bit-identical operands.
-template <int T>
+// bit-identical operands.  P: passes of T / 16 blocks, the fewest covering the
+// row (every load of a pass is issued, so no more passes than the row needs).
+template <int T, int P>
 __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, int64_t K, _Float16 *__restrict__ A,
                                                  int *__restrict__ erow, int opmajor) {
-    constexpr int BPP = T / 16, MAXP = 64 / BPP;  // passes of BPP blocks, 64 blocks at most
+    constexpr int BPP = T / 16, MAXP = P;  // passes of BPP blocks, 64 blocks at most
+    static_assert(BPP * P <= 64 && P >= 1, "at most 64 blocks per row");
     __shared__ float ds[64];
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x, sub = t & 15;
@@ -508,8 +510,16 @@ hipError_t gemm_prepass(int type, int64_t k, const ActView &act, const float *x,
             if (wide_wg) k_quant_f16_q80<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, om, ofs);
             else k_quant_f16_q80<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, om, ofs);
         } else {
-            if (wide_wg) k_quant_f16<1024><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, om);
-            else k_quant_f16<256><<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, om);
+            const int nbx = (int)(k / KB);
+            if (wide_wg) {
+                k_quant_f16<1024, 1><<<(unsigned)m, 1024, 0, st>>>(x, k, a, erow, om);
+            } else {
+                auto go = [&](auto kern) { kern<<<(unsigned)m, 256, 0, st>>>(x, k, a, erow, om); };
+                if (nbx <= 16) go(k_quant_f16<256, 1>);
+                else if (nbx <= 32) go(k_quant_f16<256, 2>);
+                else if (nbx <= 48) go(k_quant_f16<256, 3>);
+                else go(k_quant_f16<256, 4>);
+            }
         }
     } else if (vec_dot_type(type) != TYPE_Q8_K) {  // Q8_0 / Q8_1 activations
         if (ofs && !act.xs) return hipErrorInvalidValue;  // Q4_1 / Q5_1 need the Q8_1 block sums
