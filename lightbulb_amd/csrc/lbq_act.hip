@@ -11,6 +11,8 @@
 // (lightbulb: /root/reference/src/quantization/mod.rs:158-247): f16 scales are
 // widened exactly, and d1 = d*sc, m1 = dmin*m, y = d1*q - m1 are each rounded
 // to f32 separately -- contraction into FMA is disabled in these functions.
+#include <algorithm>
+
 #include "lbq_device.hpp"
 #include "lbq_internal.hpp"
 
@@ -24,22 +26,41 @@ namespace lbq {
 // q = min(127, round(iscale*x)) as i8; d = 1/iscale; bsums over 16 codes -- a
 // lane's own 16 codes.
 // ---------------------------------------------------------------------------
+// Zero the listed buffers (the matrix-core kernel's y, which its two-way split adds
+// into): 16-byte stores where the buffer is 16-byte aligned, spread over the
+// whole grid.
+__device__ __forceinline__ void zero_fill(const ZeroList &zero) {
+    const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x, nt = (int64_t)gridDim.x * 256;
+    for (int z = 0; z < zero.count; z++) {
+        float *p = zero.p[z];
+        const int64_t n = zero.n[z];
+        int64_t head = 0;
+        if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+            head = n & ~int64_t(3);
+            for (int64_t i = tid; 4 * i < head; i += nt) *reinterpret_cast<float4 *>(p + 4 * i) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (int64_t i = head + tid; i < n; i += nt) p[i] = 0.f;
+    }
+}
+
 template <bool GGUF_OUT, bool VEC_IN>
 __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, int64_t nblocks, int8_t *__restrict__ xq,
                                                    float *__restrict__ xd, int16_t *__restrict__ xbs,
                                                    uint8_t *__restrict__ gguf, ZeroList zero) {
-    for (int z = 0; z < zero.count; z++) {
-        float *p = zero.p[z];
-        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < zero.n[z]; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
-    }
     const int sub = threadIdx.x & 15;
+    // workgroups past the blocks only zero (the grid may be widened for the zeroing)
+    const bool quant = (int64_t)blockIdx.x * 16 < nblocks;
     // the 16 lanes of a row share the block (wave-uniform exits only at the end)
     const int64_t blk0 = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const bool ok = blk0 < nblocks;
     const int64_t blk = ok ? blk0 : nblocks - 1;
     float v[16];
+    if (quant) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) load4f(x + blk * QK_K + sub * 16 + 4 * i, VEC_IN, &v[4 * i]);
+        for (int i = 0; i < 4; i++) load4f(x + blk * QK_K + sub * 16 + 4 * i, VEC_IN, &v[4 * i]);
+    }
+    zero_fill(zero);  // after the x loads are issued: its stores do not delay them
+    if (!quant) return;
     uint32_t packed[4];
     int s;
     float d;
@@ -286,7 +307,10 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);
-        const dim3 grid((unsigned)((nb + 15) / 16));
+        int64_t zn = 0;
+        for (int z = 0; z < zl.count; z++) zn += zl.n[z];
+        // at least one workgroup per 16 K floats to zero (4 stores of 16 bytes per lane), at most 1024
+        const dim3 grid((unsigned)std::max<int64_t>((nb + 15) / 16, std::min<int64_t>((zn + 16383) / 16384, 1024)));
         if (gguf) {
             if (vec) k_quant_q8k<true, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);
             else k_quant_q8k<true, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xbs, gguf, zl);

@@ -98,6 +98,7 @@ Tuning tuning_from_env() {
     t.gemv_mx_waves = env_int("LBQ_GEMV_MX_WAVES");
     t.gemv_mx_all = getenv("LBQ_GEMV_MX_ALL") != nullptr;
     t.gemv_mx_pair_off = getenv("LBQ_GEMV_MX_PAIR_OFF") != nullptr;
+    t.gemv_mx_halves_off = getenv("LBQ_GEMV_MX_HALVES_OFF") != nullptr;
     if (const char *e = getenv("LBQ_GEMV")) {
         int v[4] = {0, 0, 0, 0};
         if (sscanf(e, "%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3]) >= 3 && v[0] > 0 && v[1] > 0 && v[2] > 0)
@@ -267,7 +268,7 @@ struct Scratch {
 };
 
 // Batch decode on the matrix cores for this weight and row count
-static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 32 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
+static bool uses_mx(const lbq_weight *w, int64_t m) { return m <= 64 && lbq::gemv_mx_serves(w->type, w->n, w->k, (int)m); }
 // ... with its two split halves added into y, which the quantisation launch zeroes
 static bool mx_adds(const lbq_weight *w, int64_t m) { return uses_mx(w, m) && lbq::gemv_mx_adds(w->type, w->n, w->k, (int)m); }
 

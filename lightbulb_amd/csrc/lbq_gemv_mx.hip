@@ -154,10 +154,41 @@ constexpr int MX_MAX_SPLITS = 16;
 // shapes).
 struct MxSplit {
     int splits;     // workgroups per 32-row tile (1: no partials)
-    float *part;    // [splits][m][n]
+    float *part;    // [splits][prow][n]
     uint32_t *cnt;  // one zeroed word per tile
     int add;        // splits == 2 and y zeroed: atomic adds into y
+    int prow = 0;   // rows of the partial buffer (the launch's m)
 };
+
+// Row halves (m = 33..64): the activation rows run as two 32-row halves, each
+// workgroup of the m <= 32 launch becoming two -- workgroups b and b + 8 of every
+// 16, which round-robin placement puts on one XCD at about the same time, so the
+// second read of a tile's weight blocks is served by that XCD's L2 and HBM
+// carries the weights once.  Each half is exactly a launch over its 32 rows (same
+// sums, same bits per row).  mx_half_bid: the half of workgroup bid, and bid
+// becomes the workgroup of the m <= 32 launch (-1: a padding workgroup, the grid
+// being rounded up to 16).  mx_half_rows: act, m, y and the split state of the
+// half.
+__device__ __forceinline__ int mx_half_bid(int &bid, int nwg) {
+    const int half = (bid >> 3) & 1;
+    bid = (bid >> 4) * 8 + (bid & 7);
+    return bid < nwg ? half : -1;
+}
+__device__ __forceinline__ void mx_half_rows(int half, int tiles, ActView &act, int &m, float *__restrict__ &y,
+                                             int64_t n, MxSplit &sp) {
+    sp.prow = m;
+    if (half) {
+        act.xq += 32 * act.k;
+        act.xd += 32 * act.nb;
+        act.xbs += 32 * (act.k / 16);
+        y += 32 * n;
+        if (sp.part) sp.part += 32 * n;
+        if (sp.cnt) sp.cnt += tiles;
+        m -= 32;
+    } else {
+        m = 32;
+    }
+}
 
 // MR = the activation rows a launch can hold (8, 16 or 32; m <= MR).
 // PAIR: a gate/up pair (W gate, W2 up, n rows each; one workgroup per tile, no
@@ -287,7 +318,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
         if (i < m && col < n) {
             if (sp.splits == 1) y[(int64_t)i * n + col] = s;
             else if (sp.add) atomicAdd(y + (int64_t)i * n + col, s);
-            else __hip_atomic_store(sp.part + ((int64_t)part * m + i) * n + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else __hip_atomic_store(sp.part + ((int64_t)part * sp.prow + i) * n + col, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     if (sp.splits == 1 || sp.add) return;
@@ -301,7 +332,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
         const int i = mx_row(e, h);
         if (i >= m || col >= n) continue;
         const float *pp = sp.part + (int64_t)i * n + col;
-        const int64_t stride = (int64_t)m * n;
+        const int64_t stride = (int64_t)sp.prow * n;
         float s = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int q = 1; q < sp.splits; q++) s += __hip_atomic_load(pp + q * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         y[(int64_t)i * n + col] = s;
@@ -309,11 +340,19 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     if (t == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int TYPE, int MX_WAVES, int MR, bool PAIR = false>
+template <int TYPE, int MX_WAVES, int MR, bool PAIR = false, bool HALVES = false>
 __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
                                                          int nb, ActView act, int m, float *__restrict__ y, MxSplit sp,
-                                                         const uint8_t *__restrict__ W2) {
-    mx_workgroup<TYPE, MX_WAVES, MR, PAIR>(W, row_bytes, n, nb, act, m, y, sp, W2, (int)blockIdx.x);
+                                                         const uint8_t *__restrict__ W2, int nwg) {
+    int bid = (int)blockIdx.x;
+    if constexpr (HALVES) {
+        const int half = mx_half_bid(bid, nwg);
+        if (half < 0) return;
+        mx_half_rows(half, nwg / sp.splits, act, m, y, n, sp);
+    } else {
+        sp.prow = m;
+    }
+    mx_workgroup<TYPE, MX_WAVES, MR, PAIR>(W, row_bytes, n, nb, act, m, y, sp, W2, bid);
 }
 
 // A grouped call's weights (same type and k) in one launch: segment s owns the
@@ -327,15 +366,24 @@ struct MxSegs {
     int count;
 };
 
-template <int TYPE, int MX_WAVES, int MR>
+template <int TYPE, int MX_WAVES, int MR, bool HALVES = false>
 __global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx_seg(int64_t row_bytes, int nb, ActView act, int m, MxSegs g) {
-    const int bid = (int)blockIdx.x;
+    int bid = (int)blockIdx.x, half = 0;
+    if constexpr (HALVES) {
+        half = mx_half_bid(bid, g.wg_end[g.count - 1]);
+        if (half < 0) return;
+    }
     int s = 0;
     while (s + 1 < g.count && bid >= g.wg_end[s]) s++;
-    const MxSplit sp{g.splits[s], nullptr, nullptr, g.splits[s] == 2};
-    mx_workgroup<TYPE, MX_WAVES, MR, false>(g.w[s], row_bytes, g.n[s], nb, act, m, g.y[s], sp, nullptr,
+    MxSplit sp{g.splits[s], nullptr, nullptr, g.splits[s] == 2};
+    float *__restrict__ y = g.y[s];
+    if constexpr (HALVES) mx_half_rows(half, 0, act, m, y, g.n[s], sp);
+    else sp.prow = m;
+    mx_workgroup<TYPE, MX_WAVES, MR, false>(g.w[s], row_bytes, g.n[s], nb, act, m, y, sp, nullptr,
                                             bid - (s ? g.wg_end[s - 1] : 0));
 }
+
+static int mx_splits(int64_t n, int64_t k, int m);
 
 bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // Measured against the decode kernels (x quantised by the same separate pass
@@ -352,7 +400,16 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // us: fourteen 8-byte weight loads per block and lane) and was not kept.
     if (tuning().gemv_mx_off) return false;
     if (type != TYPE_Q4_K && type != TYPE_Q5_K) return false;
-    if (k % 256 || k / 256 > 64 || m < 2 || m > 32 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    if (k % 256 || k / 256 > 64 || m < 2 || m > 64 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    // m = 33..64 as two 32-row halves (mx_half_bid) where the m <= 32 launch has
+    // at most one workgroup per CU (up to 8192 rows): against the fp16 GEMM, Q4_K m
+    // = 64 4096 x 4096 24.1 -> 16.4 us, 1024 x 4096 17.3 -> 11.1, 4096 x 14336 32.1
+    // -> 32.0, m = 40 4096 x 4096 21.3 -> 14.7; with more tiles the halves double a
+    // launch that is not HBM-bound (14336 x 4096 m = 64 31.8 -> 36.3 us, m = 33
+    // 28.5 -> 31.5) and the GEMM keeps them.
+    if (m > 32)
+        return !tuning().gemv_mx_halves_off && !tuning().gemv_mx_wide_off && n >= 1024 &&
+               (n + 31) / 32 * mx_splits(n, k, 32) <= (int64_t)num_cus();
     // m = 9..32 (the fp16 GEMM otherwise): Q4_K 14336 x 4096 m = 16 / 32 22.1 / 23.4
     // -> 18.3 / 21.8 us, Q5_K m = 12 / 24 23.9 / 24.3 -> 18.4 / 21.8, 4096 x 14336
     // m = 16 23.6 -> 20.3, 4096 x 4096 m = 32 16.1 -> 14.9; with two workgroups per
@@ -372,13 +429,12 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
 // / 25.4 us, 4096 x 4096 m = 8 / 16 / 32 12.0 / 13.0 / 15.6 -> 11.2 / 12.1 /
 // 14.9; four workgroups per tile (or four waves each) measured slower.
 static int mx_splits(int64_t n, int64_t k, int m) {
-    (void)m;
     const int64_t tiles = (n + 31) / 32;
     const int nb = (int)(k / 256);
     int s = tuning().gemv_mx_splits;
     if (s <= 0) s = tiles <= 128 ? 2 : 1;
     s = (int)std::min<int64_t>({(int64_t)s, (int64_t)nb, (int64_t)MX_MAX_SPLITS});
-    if (tiles > KS_COUNTERS) s = 1;
+    if (tiles * (m > 32 ? 2 : 1) > KS_COUNTERS) s = 1;  // a counter per tile and row half
     return std::max(s, 1);
 }
 
@@ -390,6 +446,33 @@ size_t gemv_mx_workspace_bytes(int type, int64_t n, int64_t k, int m) {
 
 bool gemv_mx_adds(int type, int64_t n, int64_t k, int m) {
     return gemv_mx_serves(type, n, k, m) && mx_splits(n, k, m) == 2;
+}
+
+// Grid of a launch of nwg workgroups: twice that, rounded up to 16, with row halves
+static unsigned mx_grid(int64_t nwg, int m) { return (unsigned)(m > 32 ? (nwg + 7) / 8 * 16 : nwg); }
+// activation rows a launch's stage holds: 8, 16 or 32 (each half's 32 with row halves)
+static int mx_rows(int m) { return m <= 8 ? 8 : m <= 16 ? 16 : 32; }
+
+template <int TYPE, int WAVES, bool PAIR>
+static void mx_launch(int m, unsigned grid, size_t lds, hipStream_t st, const uint8_t *w, int64_t row_bytes, int n,
+                      int nb, const ActView &act, float *y, const MxSplit &sp, const uint8_t *w2, int nwg) {
+    auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(w, row_bytes, n, nb, act, m, y, sp, w2, nwg); };
+    if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
+        if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
+    }
+    if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
+    else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
+    else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
+}
+
+template <int TYPE, int WAVES>
+static void mx_seg_launch(int m, unsigned grid, size_t lds, hipStream_t st, int64_t row_bytes, int nb,
+                          const ActView &act, const MxSegs &g) {
+    auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(row_bytes, nb, act, m, g); };
+    if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
+    else if (m > 16) go(k_gemv_mx_seg<TYPE, WAVES, 32>);
+    else if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
+    else go(k_gemv_mx_seg<TYPE, WAVES, 8>);
 }
 
 hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, const int64_t *n, int64_t k,
@@ -404,7 +487,8 @@ hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, co
         const int s = mx_splits(n[i], k, m);
         if (s > 2) return hipErrorNotSupported;  // only the atomic form of a split
         const int64_t tiles = (n[i] + 31) / 32;
-        const int wv = tuning().gemv_mx_waves ? tuning().gemv_mx_waves : tiles * s <= (int64_t)num_cus() ? 8 : 4;
+        const int wv = tuning().gemv_mx_waves ? tuning().gemv_mx_waves
+                       : (int64_t)mx_grid(tiles * s, m) <= (int64_t)num_cus() ? 8 : 4;
         if (i && wv != waves) return hipErrorNotSupported;  // each weight as its own launch would run it
         waves = wv;
         wg += (int)(tiles * s);
@@ -415,29 +499,14 @@ hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, co
         g.wg_end[i] = wg;
     }
     g.count = count;
-    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
-    const size_t lds = (size_t)nb * mr * sizeof(float);
-    auto go = [&](auto kern) { kern<<<(unsigned)wg, 64 * waves, lds, st>>>(row_bytes, nb, act, m, g); };
+    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
+    const unsigned grid = mx_grid(wg, m);
     if (type == TYPE_Q4_K) {
-        if (waves == 8) {
-            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q4_K, 8, 8>);
-            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q4_K, 8, 16>);
-            else go(k_gemv_mx_seg<TYPE_Q4_K, 8, 32>);
-        } else {
-            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q4_K, 4, 8>);
-            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q4_K, 4, 16>);
-            else go(k_gemv_mx_seg<TYPE_Q4_K, 4, 32>);
-        }
+        if (waves == 8) mx_seg_launch<TYPE_Q4_K, 8>(m, grid, lds, st, row_bytes, nb, act, g);
+        else mx_seg_launch<TYPE_Q4_K, 4>(m, grid, lds, st, row_bytes, nb, act, g);
     } else {
-        if (waves == 8) {
-            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q5_K, 8, 8>);
-            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q5_K, 8, 16>);
-            else go(k_gemv_mx_seg<TYPE_Q5_K, 8, 32>);
-        } else {
-            if (mr == 8) go(k_gemv_mx_seg<TYPE_Q5_K, 4, 8>);
-            else if (mr == 16) go(k_gemv_mx_seg<TYPE_Q5_K, 4, 16>);
-            else go(k_gemv_mx_seg<TYPE_Q5_K, 4, 32>);
-        }
+        if (waves == 8) mx_seg_launch<TYPE_Q5_K, 8>(m, grid, lds, st, row_bytes, nb, act, g);
+        else mx_seg_launch<TYPE_Q5_K, 4>(m, grid, lds, st, row_bytes, nb, act, g);
     }
     return hipGetLastError();
 }
@@ -455,19 +524,12 @@ hipError_t launch_gemv_mx_pair(int type, const uint8_t *w_gate, const uint8_t *w
     const int nb = (int)(k / 256);
     if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
     const MxSplit sp{1, nullptr, nullptr, 0};
-    const unsigned grid = (unsigned)((n + 15) / 16);
-    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
-    const size_t lds = (size_t)nb * mr * sizeof(float);
-    auto go = [&](auto kern) { kern<<<grid, 64 * 4, lds, st>>>(w_gate, row_bytes, (int)n, nb, act, m, out, sp, w_up); };
-    if (type == TYPE_Q4_K) {
-        if (mr == 8) go(k_gemv_mx<TYPE_Q4_K, 4, 8, true>);
-        else if (mr == 16) go(k_gemv_mx<TYPE_Q4_K, 4, 16, true>);
-        else go(k_gemv_mx<TYPE_Q4_K, 4, 32, true>);
-    } else {
-        if (mr == 8) go(k_gemv_mx<TYPE_Q5_K, 4, 8, true>);
-        else if (mr == 16) go(k_gemv_mx<TYPE_Q5_K, 4, 16, true>);
-        else go(k_gemv_mx<TYPE_Q5_K, 4, 32, true>);
-    }
+    const int nwg = (int)((n + 15) / 16);
+    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
+    if (type == TYPE_Q4_K)
+        mx_launch<TYPE_Q4_K, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
+    else
+        mx_launch<TYPE_Q5_K, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
     return hipGetLastError();
 }
 
@@ -479,23 +541,20 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
     MxSplit sp{mx_splits(n, k, m), ws, counters, 0};
     sp.add = sp.splits == 2 && y_zeroed;
     if (sp.splits > 1 && !sp.add && (!ws || !counters)) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)((n + 31) / 32 * sp.splits);
+    const int nwg = (int)((n + 31) / 32 * sp.splits);
+    const unsigned grid = mx_grid(nwg, m);
     // Up to one workgroup per CU: eight waves split a row's blocks (2 per wave at
     // k = 4096), A operands read just in time to stay within four waves per SIMD
     // (4096 x 14336 m = 4: 21.8 -> 19.5 us; 4096 x 4096 m = 8: 12.9 -> 12.4).  With
     // more workgroups, four waves (14336 x 4096 m = 8: 16.9 at four, 18.7 at eight).
     const bool w8 = tuning().gemv_mx_waves ? tuning().gemv_mx_waves == 8 : (int64_t)grid <= (int64_t)num_cus();
-    const int mr = m <= 8 ? 8 : m <= 16 ? 16 : 32;
-    const size_t lds = (size_t)nb * mr * sizeof(float);
-    auto go = [&](auto kern, int waves) { kern<<<grid, 64 * waves, lds, st>>>(w, row_bytes, (int)n, nb, act, m, y, sp, nullptr); };
+    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
     if (type == TYPE_Q4_K) {
-        if (mr == 8) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 8>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 8>, 4);
-        else if (mr == 16) w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 16>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 16>, 4);
-        else w8 ? go(k_gemv_mx<TYPE_Q4_K, 8, 32>, 8) : go(k_gemv_mx<TYPE_Q4_K, 4, 32>, 4);
+        if (w8) mx_launch<TYPE_Q4_K, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
+        else mx_launch<TYPE_Q4_K, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
     } else {
-        if (mr == 8) w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 8>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 8>, 4);
-        else if (mr == 16) w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 16>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 16>, 4);
-        else w8 ? go(k_gemv_mx<TYPE_Q5_K, 8, 32>, 8) : go(k_gemv_mx<TYPE_Q5_K, 4, 32>, 4);
+        if (w8) mx_launch<TYPE_Q5_K, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
+        else mx_launch<TYPE_Q5_K, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
     }
     return hipGetLastError();
 }

@@ -53,8 +53,7 @@ struct ActView;
 //   LBQ_GEMV_ROWS_OFF, LBQ_GEMV1_DYNAMIC            decode GEMV plan
 //   LBQ_GEMV_MX_OFF, LBQ_GEMV_MX_WIDE_OFF (m = 9..32 only),
 //   LBQ_GEMV_MX_SPLITS=<workgroups per tile>, LBQ_GEMV_MX_WAVES=4|8, LBQ_GEMV_MX_ALL,
-//   LBQ_GEMV_MX_PAIR_OFF
-//                                                   matrix-core batch decode plan
+//   LBQ_GEMV_MX_PAIR_OFF, LBQ_GEMV_MX_HALVES_OFF   matrix-core batch decode plan
 struct Tuning {
     bool gemm_ks64 = false, gemm_no_ks = false, gemm_no_tall = false;
     int gemm_ks = 0;      // k-sliced tiles: blocks per slice (0: planned)
@@ -71,6 +70,7 @@ struct Tuning {
     int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)
     bool gemv_mx_all = false;  // matrix-core batch decode wherever it can run (m = 2..32, Q4_K / Q5_K)
     bool gemv_mx_pair_off = false;  // gate/up pairs at m = 2..32 as two launches and a product launch
+    bool gemv_mx_halves_off = false;  // m = 33..64 never on the integer matrix-core kernel
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)
 };
 Tuning tuning_from_env();

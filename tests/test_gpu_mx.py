@@ -1,5 +1,6 @@
-"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..32 with
-n >= 1024, and m = 2..8 at k > 8192) against the oracle.
+"""Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..64 with
+n >= 1024 -- m = 33..64 as two 32-row halves -- and m = 2..8 at k > 8192)
+against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -71,6 +72,52 @@ def test_mx_wide_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
 
 
+# m = 33..64 (from 1024 rows, where the m <= 32 launch has at most one workgroup per
+# CU): two 32-row halves per tile (workgroups b and b + 8 of each 16), with and
+# without the two-way split (up to 128 tiles), a last tile of 4 rows, k from 5 to
+# 56 blocks
+HALF_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (8192, 1024), (4096, 14336)]
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("n,k", HALF_SHAPES)
+@pytest.mark.parametrize("m", [33, 47, 64])
+def test_mx_halves_match_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
+    rng = np.random.default_rng(n * 3 + k + 41 * m + t)
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx halves t={t} n={n} k={k} m={m}", flush=True)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
+    # switched off: the fp16 GEMM (its own bound), which must differ in some bits
+    off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_HALVES_OFF": "1"}, t, w_raw, n, k, x, dev)
+    assert_rows_close(off, ref, 2e-3)
+    assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m,n,k", [(40, 4096, 1024), (64, 2080, 2048), (64, 8192, 1024)])
+def test_mx_halves_are_two_launches(lbq, dev, t, m, n, k, monkeypatch):
+    # each half is the 32-row launch over its rows: with the wave count pinned (the
+    # plan picks it from the grid, which the halves double), rows 0..31 carry the
+    # bits of forward(x[:32]) and rows 32.. those of forward(x[32:]), with the
+    # two-way split (4096 and 2080 rows) and without (8192)
+    rng = np.random.default_rng(960 + t + m + n)
+    w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    print(f"mx halves bits t={t} m={m} n={n} k={k}", flush=True)
+    env = {"LBQ_GEMV_MX_WAVES": "4"}
+    y = forward_with_env(monkeypatch, env, t, w_raw, n, k, x, dev)
+    lo = forward_with_env(monkeypatch, env, t, w_raw, n, k, np.ascontiguousarray(x[:32]), dev)
+    hi = forward_with_env(monkeypatch, env, t, w_raw, n, k, np.ascontiguousarray(x[32:]), dev)
+    assert np.array_equal(y[:32].view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(y[32:].view(np.uint32), hi.view(np.uint32))
+
+
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
 @pytest.mark.parametrize("m,k,n", [(6, 4096, 4096), (7, 4096, 4096), (2, 14336, 160), (3, 14336, 33), (4, 9216, 160),
                                    (2, 8448, 1), (5, 8448, 70), (12, 512, 4097), (31, 768, 4127), (25, 8448, 4100)])
@@ -114,7 +161,8 @@ def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
-@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (16, 4096, 14336), (32, 4096, 2048), (6, 2080, 8192)])
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (16, 4096, 14336), (32, 4096, 2048), (6, 2080, 8192),
+                                   (64, 4096, 4096), (45, 2080, 4096)])
 def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
     # Up to 4096 rows a tile is split over two workgroups.  forward() zeroes y in the
     # quantisation launch and the halves are added into it atomically; the
@@ -290,7 +338,8 @@ def test_mx_gate_up_pair(oracle, lbq, dev, t, m, n, k, monkeypatch):
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K])
 @pytest.mark.parametrize("m,ns,k", [(6, (4096, 1024, 2080), 4096), (16, (4096, 1024, 2080), 2048),
-                                    (32, (1024, 4096), 4096), (8, (14336, 14336), 4096)])
+                                    (32, (1024, 4096), 4096), (8, (14336, 14336), 4096),
+                                    (40, (4096, 1024, 2080), 4096), (64, (1024, 4096), 2048)])
 def test_mx_group_one_launch(oracle, lbq, dev, t, m, ns, k):
     # a grouped call whose weights all run on the kernel is one launch (each weight's
     # workgroups as its own launch would run them): the bits of the separate calls
