@@ -98,7 +98,7 @@ __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, in
                                                  int *__restrict__ erow, int opmajor) {
     constexpr int BPP = T / 16, MAXP = P;  // passes of BPP blocks, 64 blocks at most
     static_assert(BPP * P <= 64 && P >= 1, "at most 64 blocks per row");
-    __shared__ float ds[64];
+    __shared__ float wmax[T / 64];
     const int64_t m = blockIdx.x;
     const int t = threadIdx.x, sub = t & 15;
     const int nbx = (int)(K / KB), np = (nbx + BPP - 1) / BPP;
@@ -116,6 +116,7 @@ __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, in
     }
     uint4 codes[MAXP];
     float dj[MAXP];
+    float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < MAXP; j++) {
         codes[j] = make_uint4(0u, 0u, 0u, 0u);
@@ -125,13 +126,17 @@ __global__ __launch_bounds__(T) void k_quant_f16(const float *__restrict__ x, in
             int sum;
             q8k_lane16(v[j], sub, packed, &sum, &dj[j]);
             codes[j] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-            const int b = BPP * j + (t >> 4);
-            if (sub == 0 && b < nbx) ds[b] = dj[j];
+            if (BPP * j + (t >> 4) < nbx) mx = fmaxf(mx, fabsf(dj[j]));
         }
     }
+    // the row's largest |d|: a wave reduction, then across the waves (fmaxf never
+    // returns a NaN operand over a number, so the order does not matter)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
     __syncthreads();
-    float mx = 0.f;
-    for (int b = 0; b < nbx; b++) mx = fmaxf(mx, fabsf(ds[b]));
+#pragma unroll
+    for (int w = 0; w < T / 64; w++) mx = fmaxf(mx, wmax[w]);
     const int e = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) - 8 : 0;  // as k_act_f16
     if (t == 0) erow[m] = e;
 #pragma unroll
