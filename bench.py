@@ -480,17 +480,31 @@ def main():
 
 
 def prefill_profile(torch, qz, dev):
-    """Q4_K gate_proj 14336x4096 forward at M = 16 (k-sliced tiles), 32 (k-sliced) and 512 (wide
-    tiles), 8 weight copies rotated, 5 graph replays each, for counter collection."""
+    """configs[3]'s batched calls: Q4_K gate_proj 14336x4096 and down_proj 4096x14336 forward at
+    M = 16 (integer matrix cores), 64 (gate: k-sliced fp16 GEMM; down: matrix cores, two row
+    halves) and 512 (wide fp16 tiles), the weights rotated over >= 512 MB of copies, 5 graph
+    replays each, for counter collection."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B4)
     stream = torch.cuda.current_stream(dev)
-    qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, 14336, 4096, gen, dev) for _ in range(8)]
     out = {}
-    for M in (16, 32, 512):
-        x = torch.randn(M, 4096, generator=gen, device=dev)
-        out[f"q4_k_gate_proj_14336x4096_m{M}"] = round(time_forwards(torch, qms, x, stream, reps=5, warm=1), 2)
+    for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
+        qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(n_copies(n * k // 256 * 144))]
+        for M in (16, 64, 512):
+            x = torch.randn(M, k, generator=gen, device=dev)
+            out[f"q4_k_{name}_{n}x{k}_m{M}"] = round(time_forwards(torch, qms, x, stream, reps=5, warm=1), 2)
+        del qms
+        torch.cuda.empty_cache()
     print(json.dumps({"prefill_profile_us": out}), flush=True)
+
+
+def load_prefill_traffic():
+    """HBM bytes per M = 512 forward (gate and down), from the committed PMC summary."""
+    f = ROOT / "profiles" / "traffic_q4k_prefill_m512.json"
+    try:
+        return json.loads(f.read_text())
+    except (OSError, ValueError):
+        return None
 
 
 ROTATE_BYTES = 512e6  # every leg rotates at least this many distinct weight bytes (MALL: 256 MB)
@@ -540,8 +554,19 @@ def gemm_bench(torch, qz, gen, dev, stream):
             "frac_bf16_peak_forward": round(fl / us_f / 1e6 / BF16_PEAK_TFLOPS, 4),
             "frac_bf16_peak_dot": round(fl / us_d / 1e6 / BF16_PEAK_TFLOPS, 4),
             "weight_GB/s_forward": round(nbytes / us_f / 1e3, 1), "working_set_MB": ws_mb(qms)}
-        log(f"gemm {name} M={M}: forward {us_f:.1f} us, dot {us_d:.1f} us ({fl / us_d / 1e6:.0f} TFLOP/s)")
-        del g_d, qms, x, y, act
+        # yardstick: the library's plain fp16 GEMM (torch.matmul -> hipBLASLt) on the same
+        # shape, operands already fp16 (no quantisation, no dequantisation)
+        a16 = x.to(torch.float16)
+        w16 = torch.randn(k, n, generator=gen, device=dev).to(torch.float16)
+        g_l = capture(torch, lambda: torch.matmul(a16, w16))
+        timed_graph(torch, g_l, 3, stream)
+        us_l = timed_graph_median(torch, g_l, 25, stream) * 1e3
+        out[f"{name}_{n}x{k}_m{M}"]["fp16_library_gemm"] = {
+            "us": round(us_l, 2), "TFLOP/s": round(fl / us_l / 1e6, 1),
+            "what": "torch.matmul of fp16 [M, K] x [K, N] (hipBLASLt), no dequantisation: a yardstick, not this path"}
+        log(f"gemm {name} M={M}: forward {us_f:.1f} us, dot {us_d:.1f} us ({fl / us_d / 1e6:.0f} TFLOP/s); "
+            f"library fp16 GEMM {us_l:.1f} us")
+        del g_d, g_l, qms, x, y, act, a16, w16
     torch.cuda.empty_cache()
     g, d = out["gate_proj_14336x4096_m512"], out["down_proj_4096x14336_m512"]
     fl = 2.0 * 512 * 14336 * 4096
@@ -552,6 +577,10 @@ def gemm_bench(torch, qz, gen, dev, stream):
         "kernel": "QMatMul::forward at M = 512 (Q8_K quantise + fp16 operand pre-pass, then k_gemm_w: eight-wave "
                   "128 x 256 tiles, v_mfma_f32_32x32x16_f16), mean of gate 14336x4096 and down 4096x14336",
         "us_per_forward": round(us, 2), "flops_per_forward": fl}
+    tr = load_prefill_traffic()
+    if tr:
+        out["roofline"]["traffic"] = tr["bytes_per_forward"]
+        out["roofline"]["traffic_source"] = "profiles/traffic_q4k_prefill_m512.json (" + tr.get("method", "") + ")"
     return out
 
 
