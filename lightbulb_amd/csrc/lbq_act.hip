@@ -395,6 +395,90 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
     for (int64_t i = t; i < k; i += 256) y[m * k + i] = xr[i] / rms * w[i];
 }
 
+// candle's RmsNorm (f32) of each row and the Q8_K quantisation of the result in
+// one launch (the call-site entry points at m > 1): one workgroup per row, 16
+// lanes per 256-value block and 16 values per lane (q8k_lane16, as every Q8_K
+// quantiser here), P passes of 16 blocks; the normalised row never reaches
+// memory.  The norm is x / sqrt(sum(x^2) / k + eps) * w in that order, the sum
+// over the lanes' own values, then DPP rows, then the four waves.  Also zeroes
+// the listed outputs (ZeroList), as k_quant_q8k does; workgroups past the rows
+// only zero (the grid may be widened for the zeroing).
+template <int P>
+__global__ __launch_bounds__(256) void k_rmsnorm_q8k(const float *__restrict__ x, const float *__restrict__ w, float eps,
+                                                     int64_t rows, int64_t k, int8_t *__restrict__ xq,
+                                                     float *__restrict__ xd, int16_t *__restrict__ xbs, ZeroList zero) {
+    __shared__ float red[4];
+    const int64_t m = blockIdx.x;
+    if (m >= rows) {  // workgroup-uniform
+        zero_fill(zero);
+        return;
+    }
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, sub = t & 15;
+    const int nbx = (int)(k / QK_K);
+    const float *xr = x + m * k;
+    float v[P][16], al[P][16];
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        const int b = min(16 * j + (t >> 4), nbx - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(xr + (int64_t)b * QK_K + 16 * sub);
+        const float4 *wsrc = reinterpret_cast<const float4 *>(w + (int64_t)b * QK_K + 16 * sub);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 f = src[i], g = wsrc[i];
+            v[j][4 * i] = f.x; v[j][4 * i + 1] = f.y; v[j][4 * i + 2] = f.z; v[j][4 * i + 3] = f.w;
+            al[j][4 * i] = g.x; al[j][4 * i + 1] = g.y; al[j][4 * i + 2] = g.z; al[j][4 * i + 3] = g.w;
+        }
+    }
+    zero_fill(zero);  // after the loads are issued
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        if (16 * j + (t >> 4) < nbx)  // clamped duplicates do not count
+#pragma unroll
+            for (int i = 0; i < 16; i++) ss += v[j][i] * v[j][i];
+    ss = row_sum_f32(ss);
+    ss = __int_as_float(rl(__float_as_uint(ss), 0)) + __int_as_float(rl(__float_as_uint(ss), 16)) +
+         __int_as_float(rl(__float_as_uint(ss), 32)) + __int_as_float(rl(__float_as_uint(ss), 48));
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    const float rms = sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)k + eps);
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        if (j > 0 && 16 * j >= nbx) continue;  // workgroup-uniform
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[j][i] = v[j][i] / rms * al[j][i];
+        uint32_t packed[4];
+        int sum;
+        float d;
+        q8k_lane16(v[j], sub, packed, &sum, &d);
+        const int b = 16 * j + (t >> 4);
+        if (b < nbx) {
+            const int64_t blk = m * nbx + b;
+            *reinterpret_cast<uint4 *>(xq + blk * QK_K + 16 * sub) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            xbs[blk * 16 + sub] = (int16_t)sum;
+            if (sub == 0) xd[blk] = d;
+        }
+    }
+}
+
+hipError_t launch_rmsnorm_q8k(const float *x, const float *w, float eps, int64_t m, int64_t k, int8_t *xq, float *xd,
+                              int16_t *xbs, hipStream_t st, const ZeroList *zero) {
+    const ZeroList zl = zero ? *zero : ZeroList{};
+    if (k % QK_K || k / QK_K > 64 || ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15u))
+        return hipErrorInvalidValue;
+    if (m <= 0) return hipSuccess;
+    const int nbx = (int)(k / QK_K);
+    int64_t zn = 0;
+    for (int z = 0; z < zl.count; z++) zn += zl.n[z];
+    // at least one workgroup per 16 K floats to zero, at most 1024 (as launch_quant_act)
+    const dim3 grid((unsigned)std::max<int64_t>(m, std::min<int64_t>((zn + 16383) / 16384, 1024)));
+    if (nbx <= 16) k_rmsnorm_q8k<1><<<grid, 256, 0, st>>>(x, w, eps, m, k, xq, xd, xbs, zl);
+    else if (nbx <= 32) k_rmsnorm_q8k<2><<<grid, 256, 0, st>>>(x, w, eps, m, k, xq, xd, xbs, zl);
+    else if (nbx <= 48) k_rmsnorm_q8k<3><<<grid, 256, 0, st>>>(x, w, eps, m, k, xq, xd, xbs, zl);
+    else k_rmsnorm_q8k<4><<<grid, 256, 0, st>>>(x, w, eps, m, k, xq, xd, xbs, zl);
+    return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int64_t m, int64_t k, float *y, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     k_rmsnorm<<<(unsigned)m, 256, 0, st>>>(x, w, eps, k, y);

@@ -217,10 +217,22 @@ lbq::ActView view_of(uint8_t *base, const ActLayout &L, int64_t k) {
                         q81 ? reinterpret_cast<const float *>(base + L.bs_off) : nullptr};
 }
 
-// the activation quantisation into the split layout of av (zeroing the ranges of
-// `zero` in the same launch)
+// An RMS norm to apply to x before its quantisation (the call-site entry points)
+struct NormArg {
+    const float *w;
+    float eps;
+};
+
+// The activation quantisation of x -- or, with nm, of candle's RmsNorm of x (Q8_K
+// activations only) -- into the split layout of av, zeroing the ranges of `zero`
+// in the same launch
 hipError_t quant_into(int act_type, const float *d_x, int64_t m, int64_t k, const lbq::ActView &av, hipStream_t st,
-                      const lbq::ZeroList *zero = nullptr) {
+                      const lbq::ZeroList *zero = nullptr, const NormArg *nm = nullptr) {
+    if (nm) {
+        if (act_type != lbq::TYPE_Q8_K) return hipErrorInvalidValue;
+        return lbq::launch_rmsnorm_q8k(d_x, nm->w, nm->eps, m, k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
+                                       const_cast<int16_t *>(av.xbs), st, zero);
+    }
     return lbq::launch_quant_act(act_type, d_x, m, k, const_cast<int8_t *>(av.xq), const_cast<float *>(av.xd),
                                  const_cast<int16_t *>(av.xbs), const_cast<float *>(av.xs), nullptr, st, zero);
 }
@@ -685,8 +697,22 @@ int lbq_qmatmul_f32_noalloc(lbq_ctx *ctx, const lbq_weight *w, const float *d_x,
     return forward(ctx, w, d_x, m, d_y, static_cast<hipStream_t>(stream), sc, nullptr);
 }
 
+namespace {
+int group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m, float *const *d_ys,
+              void *stream, const NormArg *nm);
+}  // namespace
+
 int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m,
                           float *const *d_ys, void *stream) {
+    return group_f32(ctx, ws, count, d_x, m, d_ys, stream, nullptr);
+}
+
+namespace {
+// lbq_qmatmul_group_f32; with nm, of candle's RmsNorm of x, normalised and quantised
+// in one launch (the caller has checked that every weight takes pre-quantised
+// Q8_K activations: rmsnorm_fuses)
+int group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x, int64_t m, float *const *d_ys,
+              void *stream, const NormArg *nm) {
     if (!ctx || !ws || !d_ys) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_qmatmul_group_f32");
     if (count < 1 || count > LBQ_GROUP_MAX) return fail(LBQ_ERR_LIMIT, "count = %d outside 1..%d", count, LBQ_GROUP_MAX);
     if (m < 0) return fail(LBQ_ERR_INVALID_ARG, "m = %lld is negative", (long long)m);
@@ -728,7 +754,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     }
     rm.n = rows;
     const bool one_launch = rows <= lbq::MAX_ROWS;  // else weight by weight
-    if (one_launch && m == 1 && lbq::gemv_fuses_quant(w0->type, rows, w0->k, 1, d_x)) {
+    if (!nm && one_launch && m == 1 && lbq::gemv_fuses_quant(w0->type, rows, w0->k, 1, d_x)) {
         const lbq::ActView av{nullptr, nullptr, nullptr, w0->k, L.nb};
         hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, av, d_x, st);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
@@ -737,6 +763,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     bool all_mx = true;  // every weight on the integer matrix-core kernel: x quantised once below
     for (int i = 0; i < count; i++) all_mx = all_mx && uses_mx(ws[i], m);
     if (m > 8 && !all_mx && lbq::gemm_serves(w0->type, w0->k)) {
+        if (nm) return fail(LBQ_ERR_INVALID_ARG, "internal: the fused norm needs pre-quantised activations");
         // batched: one operand pre-pass (quantising x itself when it can) shared
         // by every weight's GEMM; weights on the integer matrix-core kernel share
         // one Q8_K quantisation of x and run after the GEMMs (their split partials
@@ -800,7 +827,7 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     lbq::ZeroList zl;
     bool zeroed[LBQ_GROUP_MAX];
     for (int i = 0; i < count; i++) zeroed[i] = zero_for_mx(zl, ws[i], m, d_ys[i]);
-    hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st, &zl);
+    hipError_t e = quant_into(act_type, d_x, m, w0->k, av, st, &zl, nm);
     if (e != hipSuccess) return hip_fail(e, "activation quantisation launch");
     bool one = count >= 2;  // every weight on the matrix-core kernel: one launch for all
     for (int i = 0; i < count; i++) one = one && uses_mx(ws[i], m) && (!mx_adds(ws[i], m) || zeroed[i]);
@@ -824,8 +851,9 @@ int lbq_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, 
     return LBQ_OK;
 }
 
-int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
-                         float *d_out, void *stream) {
+// lbq_gate_up_silu_f32; with nm, of candle's RmsNorm of x (as group_f32)
+int gate_up_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
+                float *d_out, void *stream, const NormArg *nm) {
     if (!ctx || !w_gate || !w_up || !d_out) return fail(LBQ_ERR_INVALID_ARG, "null argument to lbq_gate_up_silu_f32");
     if (w_gate->type != w_up->type || w_gate->n != w_up->n || w_gate->k != w_up->k)
         return fail(LBQ_ERR_SHAPE, "gate (type %d, %lld x %lld) and up (type %d, %lld x %lld) differ", w_gate->type,
@@ -842,7 +870,7 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
     if (g.err != hipSuccess) return hip_fail(g.err, "hipSetDevice");
     lbq::TuningScope tsc(&ctx->tune);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (m == 1 && lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
+    if (!nm && m == 1 && lbq::gemv_fuses_quant(w_gate->type, 2 * w_gate->n, w_gate->k, 1, d_x)) {
         // one launch: both weights' rows interleaved, the product in the epilogue
         hipError_t e = lbq::launch_gemv_silu_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n, w_gate->k,
                                                   w_gate->row_bytes, d_x, d_out, st);
@@ -855,7 +883,7 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
         int s = ensure_scratch(ctx, L.total);
         if (s) return s;
         const lbq::ActView av = view_of(ctx->scratch, L, w_gate->k);
-        hipError_t e = quant_into(L.act_type, d_x, m, w_gate->k, av, st);
+        hipError_t e = quant_into(L.act_type, d_x, m, w_gate->k, av, st, nullptr, nm);
         if (e == hipSuccess)
             e = lbq::launch_gemv_mx_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n, w_gate->k,
                                          w_gate->row_bytes, av, (int)m, d_out, st);
@@ -872,11 +900,17 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
     float *gy = reinterpret_cast<float *>(ctx->tmp), *uy = reinterpret_cast<float *>(ctx->tmp + half);
     const lbq_weight *pair[2] = {w_gate, w_up};
     float *outs[2] = {gy, uy};
-    int s = lbq_qmatmul_group_f32(ctx, pair, 2, d_x, m, outs, stream);
+    int s = group_f32(ctx, pair, 2, d_x, m, outs, stream, nm);
     if (s) return s;
     hipError_t e = lbq::launch_silu_mul(gy, uy, m * w_gate->n, d_out, st);
     if (e != hipSuccess) return hip_fail(e, "silu-mul launch");
     return LBQ_OK;
+}
+}  // namespace
+
+int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weight *w_up, const float *d_x, int64_t m,
+                         float *d_out, void *stream) {
+    return gate_up_f32(ctx, w_gate, w_up, d_x, m, d_out, stream, nullptr);
 }
 
 int lbq_rmsnorm_f32(const float *d_x, const float *d_w, float eps, int64_t m, int64_t k, float *d_y, void *stream) {
@@ -903,6 +937,22 @@ int norm_into_tmp(lbq_ctx *ctx, const float *d_x, const float *d_w, float eps, i
     *out = reinterpret_cast<float *>(ctx->tmp + skip);
     hipError_t e = lbq::launch_rmsnorm(d_x, d_w, eps, m, k, *out, st);
     return e == hipSuccess ? LBQ_OK : hip_fail(e, "rmsnorm launch");
+}
+
+// Whether the RMS norm can run in the Q8_K quantisation launch (launch_rmsnorm_q8k)
+// instead of a launch of its own: Q8_K activations, k up to 64 blocks, 16-byte
+// aligned x and norm weight, and every weight on a path that reads pre-quantised
+// activations (m <= 8, or the integer matrix-core kernel) -- not the fp16 GEMM's
+// pre-pass or in-kernel quantisation, which read f32 x.
+bool rmsnorm_fuses(const lbq_weight *const *ws, int count, const float *d_x, const float *d_w, int64_t m) {
+    const lbq_weight *w0 = ws[0];
+    if (lbq::is_dense(w0->type) || lbq::vec_dot_type(w0->type) != lbq::TYPE_Q8_K) return false;
+    if (w0->k % 256 || w0->k / 256 > 64) return false;
+    if ((reinterpret_cast<uintptr_t>(d_x) | reinterpret_cast<uintptr_t>(d_w)) & 15u) return false;
+    if (m <= 8) return true;
+    for (int i = 0; i < count; i++)
+        if (!uses_mx(ws[i], m)) return false;
+    return true;
 }
 }  // namespace
 
@@ -945,6 +995,10 @@ int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int
         hipError_t e = lbq::launch_gemv_group(w0->type, rm, w0->k, w0->row_bytes, none, d_x, st, d_norm_w, eps);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "grouped matmul launch");
     }
+    if (rmsnorm_fuses(ws, count, d_x, d_norm_w, m)) {  // the norm in the quantisation launch
+        const NormArg nm{d_norm_w, eps};
+        return group_f32(ctx, ws, count, d_x, m, d_ys, stream, &nm);
+    }
     float *xn;
     int s = norm_into_tmp(ctx, d_x, d_norm_w, eps, m, w0->k, 0, st, &xn);
     if (s) return s;
@@ -973,6 +1027,11 @@ int lbq_rmsnorm_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const l
         hipError_t e = lbq::launch_gemv_silu_pair(w_gate->type, w_gate->d_blocks, w_up->d_blocks, w_gate->n,
                                                   w_gate->k, w_gate->row_bytes, d_x, d_out, st, d_norm_w, eps);
         if (e != hipErrorNotSupported) return e == hipSuccess ? LBQ_OK : hip_fail(e, "gate/up launch");
+    }
+    const lbq_weight *pair[2] = {w_gate, w_up};
+    if (rmsnorm_fuses(pair, 2, d_x, d_norm_w, m)) {  // the norm in the quantisation launch
+        const NormArg nm{d_norm_w, eps};
+        return gate_up_f32(ctx, w_gate, w_up, d_x, m, d_out, stream, &nm);
     }
     // the normalised x sits after the gate/up halves lbq_gate_up_silu_f32 uses
     const size_t half = ((size_t)m * (size_t)w_gate->n * sizeof(float) + 255) / 256 * 256;

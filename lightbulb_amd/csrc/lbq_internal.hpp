@@ -115,6 +115,12 @@ struct ZeroList {
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd,
                             int16_t *xbs, float *xs, uint8_t *gguf, hipStream_t st, const ZeroList *zero = nullptr);
 
+// candle's RmsNorm of x[m][k] (f32, weight w) and the Q8_K quantisation of the
+// result into the split layout, one launch; zeroes the listed buffers as
+// launch_quant_act does.  k a multiple of 256 up to 16384, x and w 16-byte aligned.
+hipError_t launch_rmsnorm_q8k(const float *x, const float *w, float eps, int64_t m, int64_t k, int8_t *xq, float *xd,
+                              int16_t *xbs, hipStream_t st, const ZeroList *zero = nullptr);
+
 // Dequantise nelem values (multiple of the block size) of `type` blocks to f32
 // (F32 / F16: any nelem, a copy / an exact widening).
 hipError_t launch_dequant(int type, const uint8_t *blocks, int64_t nelem, float *y, hipStream_t st);

@@ -360,3 +360,43 @@ def test_mx_group_one_launch(oracle, lbq, dev, t, m, ns, k):
     i = int(np.argmin(ns))
     ref = oracle.qmatmul(t, raws[i], ns[i], k, x, nthreads=8).astype(np.float64)
     assert_rows_close(ys[i].cpu().numpy(), ref, 1e-4)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("m", [2, 6, 16, 32, 48])
+def test_mx_rmsnorm_in_quantisation(oracle, lbq, dev, t, m):
+    # at m > 1 the call-site entry points run candle's RmsNorm inside the Q8_K
+    # quantisation launch when every weight reads pre-quantised activations (the
+    # normalised x never reaches memory): grouped weights at k = 2304 (9 blocks, one
+    # partial pass), 4096 and 14336 (56 blocks, four passes) and a gate/up pair above
+    # 8192 rows, against the oracle on the numpy-normalised x
+    import torch
+    from lightbulb_amd.quantized import QMatMul, QTensor, rmsnorm_gate_up_silu, rmsnorm_qmatmul_group
+    from test_gpu_parity import _rms_norm_ref, to_dev
+    rng = np.random.default_rng(990 + t + m)
+    for k, ns in ((2304, (1024, 1040)), (4096, (2048, 1024, 1056)), (14336, (1024,))):
+        raws = [bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3) for n in ns]
+        qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r, n in zip(raws, ns)]
+        w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        x = (3.0 * rng.standard_normal((m, k)) + 0.5).astype(np.float32)
+        x[rng.random(x.shape) < 0.01] *= 20
+        xn = _rms_norm_ref(x, w, 1e-5)
+        print(f"mx rmsnorm group t={t} m={m} k={k} ns={ns}", flush=True)
+        ys = rmsnorm_qmatmul_group(qms, to_dev(x, dev), to_dev(w, dev), 1e-5)
+        torch.cuda.synchronize()
+        for y, r, n in zip(ys, raws, ns):
+            assert_rows_close(y.cpu().numpy(), oracle.qmatmul(t, r, n, k, xn, nthreads=8).astype(np.float64), 2e-3)
+    k, n = 4096, 8256
+    g_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    u_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
+    qg = QMatMul.from_qtensor(QTensor(to_dev(g_raw, dev), t, (n, k)))
+    qu = QMatMul.from_qtensor(QTensor(to_dev(u_raw, dev), t, (n, k)))
+    w = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    x = (3.0 * rng.standard_normal((m, k)) + 0.5).astype(np.float32)
+    xn = _rms_norm_ref(x, w, 1e-5)
+    print(f"mx rmsnorm pair t={t} m={m} n={n}", flush=True)
+    out = rmsnorm_gate_up_silu(qg, qu, to_dev(x, dev), to_dev(w, dev), 1e-5)
+    torch.cuda.synchronize()
+    gr = oracle.qmatmul(t, g_raw, n, k, xn, nthreads=8).astype(np.float64)
+    ur = oracle.qmatmul(t, u_raw, n, k, xn, nthreads=8).astype(np.float64)
+    assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, 2e-3)
