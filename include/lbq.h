@@ -139,9 +139,10 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * activation is quantised to Q8_K (k-quant weights), Q8_1 (Q4_1/Q5_1) or Q8_0
  * (the other 32-value types) exactly as the reference CPU path does.
  * Arithmetic by (type, m):
- *   - m <= 8, and Q4_K/Q5_K weights of 1024 rows or more up to m = 32: each
- *     output from integer sub-block dot products as in the reference (f32
- *     combine; only the summation order differs, ~1e-7 relative);
+ *   - m <= 8, and Q4_K/Q5_K weights of 1024 rows or more up to m = 32 (and
+ *     m = 33..64 up to 8192 rows, as two 32-row halves): each output from
+ *     integer sub-block dot products as in the reference (f32 combine; only the
+ *     summation order differs, ~1e-7 relative);
  *   - m > 8 otherwise, for every quantised type when k % 256 == 0 (Q4_0, Q4_1,
  *     Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K): MFMA on fp16 roundings of
  *     the same activation and weight values (about 4e-4 relative on a row);
@@ -204,8 +205,12 @@ int lbq_gate_up_silu_f32(lbq_ctx *ctx, const lbq_weight *w_gate, const lbq_weigh
  * x_norm = x / sqrt(sum(x^2) / k + eps) * norm_w), then the grouped projections or
  * the gate/up product of x_norm.  At m = 1 (k-quants, k <= 8192, x and norm_w
  * 16-byte aligned) the norm and the Q8_K quantisation run in the GEMV prologue
- * -- one launch, x_norm never written; otherwise x_norm goes to context memory
- * first.  lbq_rmsnorm_f32 is the norm alone. */
+ * -- one launch, x_norm never written.  At m > 1, where every weight reads
+ * pre-quantised Q8_K activations (k-quants, k % 256 == 0 up to 16384, x and
+ * norm_w 16-byte aligned; m <= 8, or Q4_K/Q5_K weights on the matrix-core batch
+ * decode), the norm runs inside the one Q8_K quantisation launch, x_norm again
+ * never written; otherwise x_norm goes to context memory first.
+ * lbq_rmsnorm_f32 is the norm alone. */
 int lbq_rmsnorm_f32(const float *d_x, const float *d_w, float eps, int64_t m, int64_t k, float *d_y, void *stream);
 int lbq_rmsnorm_qmatmul_group_f32(lbq_ctx *ctx, const lbq_weight *const *ws, int count, const float *d_x,
                                   const float *d_norm_w, float eps, int64_t m, float *const *d_ys, void *stream);
