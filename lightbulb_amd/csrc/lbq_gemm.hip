@@ -420,6 +420,10 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
         // (1, 2 or 4 blocks: a slice stays inside one exponent group of KS_BLOCKS)
         int bps = smax;
         if (bps == 4 && (int64_t)p.tiles_n * ((nb + 3) / 4) < (int64_t)num_cus()) bps = 2;
+        // one-block slices where two-block ones leave half the CUs idle (Q6_K
+        // 1024 x 4096, 8 column tiles: m = 16 / 32 11.0 / 13.9 -> 9.2 / 10.6 us;
+        // on 4096 x 14336 one-block slices measured 5 us slower at m = 32)
+        if (bps == 2 && p.rt == 1 && 2 * (int64_t)p.tiles_n * ((nb + 1) / 2) <= (int64_t)num_cus()) bps = 1;
         if (tu.gemm_ks) bps = std::max(1, std::min(tu.gemm_ks == 3 ? 2 : tu.gemm_ks, smax));  // tuning
         p.bps = bps;
         p.splits = (nb + bps - 1) / bps;
