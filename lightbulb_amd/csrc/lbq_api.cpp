@@ -81,6 +81,7 @@ Tuning tuning_from_env() {
     t.gemm_ks = std::max(0, env_int("LBQ_GEMM_KS"));
     if (const char *e = getenv("LBQ_GEMM_BIG")) t.gemm_big = e[0] == 't' ? 2 : 1;
     t.gemm_splits = std::max(0, env_int("LBQ_GEMM_SPLITS"));
+    if (const char *e = getenv("LBQ_GEMM_WIDE7")) t.gemm_wide7 = e[0] == '0' ? -1 : 1;
     t.gemm_split_launch = getenv("LBQ_GEMM_SPLIT_LAUNCH") != nullptr;
     t.gemm_prepass = getenv("LBQ_GEMM_PREPASS") != nullptr;
     t.gemv1_nofuse = getenv("LBQ_GEMV1_NOFUSE") != nullptr;

@@ -435,7 +435,10 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     // wide tiles (two waves per SIMD, dequantisation per 128 rows) below 256 rows,
     // and for Q4_K (the cheapest dequantisation) up to 512; tall tiles (one wave
     // per SIMD, dequantisation per 256 rows) where the dequantisation VALU per
-    // MFMA decides (measured per type and m: 128, 256, 512, 2048)
+    // MFMA decides (measured per type and m: 128, 256, 512, 2048; Q4_K at 2048
+    // with the seven-wave wide tiles below is a wash, 14336 x 4096 318 -> 308 us
+    // but 4096 x 14336 280 -> 290).  The choice must not depend on n: a grouped
+    // call's pre-pass lays out whole tiles of rows for every weight of the group.
     bool wide = m < 256 || (type == TYPE_Q4_K && m <= 512);
     if (tu.gemm_big) wide = tu.gemm_big == 1 || m < 256;  // tuning override: wide or tall
     // (Q6_K from 65 rows: its 64-row tiles took 66 us at m = 100 where the wide
@@ -446,13 +449,28 @@ Plan plan_for(int type, int64_t n, int64_t k, int64_t m) {
     p.tiles_m = (int)((m + rows - 1) / rows);
     p.tiles_n = (int)((n + cols - 1) / cols);
     const int nb = (int)(k / KB);
-    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     // split k until the grid has about one workgroup per CU (also where two fit:
     // measured at m = 64, more splits only add partial-sum traffic)
     const int64_t slots = (int64_t)num_cus();
-    int s = 1;
-    if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
-    if (tu.gemm_splits) s = std::max(1, std::min(tu.gemm_splits, nb));  // tuning override
+    auto splits_for = [&](int64_t tiles) {
+        int s = 1;
+        if (tiles * 2 <= slots) s = (int)std::min<int64_t>(slots / tiles, nb);
+        if (tu.gemm_splits) s = std::max(1, std::min(tu.gemm_splits, nb));  // tuning override
+        return s;
+    };
+    int s = splits_for((int64_t)p.tiles_m * p.tiles_n);
+    if (p.mt == MT_WIDE && n % (7 * 32) == 0 && tu.gemm_wide7 >= 0) {
+        // seven-wave tiles (224 columns) where they take fewer wave-rounds of the
+        // chip: rounds of workgroups over the CUs x waves x blocks per workgroup
+        const int tn7 = (int)(n / (7 * 32));
+        const int s7 = splits_for((int64_t)p.tiles_m * tn7);
+        auto cost = [&](int64_t wgs, int waves, int sp) { return (wgs + slots - 1) / slots * waves * ((nb + sp - 1) / sp); };
+        if (tu.gemm_wide7 > 0 || cost((int64_t)p.tiles_m * tn7 * s7, 7, s7) < cost((int64_t)p.tiles_m * p.tiles_n * s, 8, s)) {
+            p.mt = MT_WIDE7;
+            p.tiles_n = tn7;
+            s = s7;
+        }
+    }
     p.bps = (nb + s - 1) / s;
     p.splits = (nb + p.bps - 1) / p.bps;
     return p;

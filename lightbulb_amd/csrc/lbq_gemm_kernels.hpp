@@ -959,12 +959,18 @@ __global__ __launch_bounds__(256, 1) void k_gemm_t(const uint8_t *__restrict__ W
 //   k-steps 6-7 : in stage 0, the next block's weight loads;
 //   k-step 7    : in stage 1, the next block's scales and first B operand.
 // ---------------------------------------------------------------------------
+//
+// NW = 7 (224-column tiles, the staging's 32 load instructions spread over the
+// seven waves) where 256-column tiles leave part of the chip idle: 14336 columns
+// at 128 rows are 224 workgroups of eight waves but 256 of seven.
 constexpr int WBM = 128, WBN = 256;
 
-template <int TYPE>
-__global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
-                                                   const _Float16 *__restrict__ A, const int *__restrict__ erow,
-                                                   int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
+template <int TYPE, int NW = 8>
+__global__ __launch_bounds__(64 * NW, 1) void k_gemm_w(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes,
+                                                       const _Float16 *__restrict__ A, const int *__restrict__ erow,
+                                                       int64_t K, int64_t M, float *__restrict__ out, GemmGrid g) {
+    static_assert(NW == 7 || NW == 8, "wide tiles: seven or eight waves");
+    constexpr int CN = 32 * NW;  // columns per workgroup
     using B = GB<TYPE>;
     __shared__ __align__(1024) uint8_t As0[WBM * TROW];
     __shared__ __align__(1024) uint8_t As1[WBM * TROW];
@@ -975,7 +981,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
     const int tm = T % g.tiles_m, tn = (T / g.tiles_m) % g.tiles_n, z = T / (g.tiles_m * g.tiles_n);
     const int nb = (int)(K / KB);
     const int b0 = z * g.bps, b1 = min(nb, b0 + g.bps);
-    const int64_t m0 = (int64_t)tm * WBM, n0 = (int64_t)tn * WBN;
+    const int64_t m0 = (int64_t)tm * WBM, n0 = (int64_t)tn * CN;
     float *y = out + (int64_t)z * g.split_stride;
 
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6), h = lane >> 5,
@@ -986,9 +992,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
     const float wsc = __builtin_amdgcn_ldexpf(1.f, -en);
     if (t < WBM) Es[t] = erow[min(m0 + t, M - 1)];
 
-    // staging: instruction j (0..3) of wave w fills stage rows 16w + 4j + [0, 4);
-    // lane l writes row 16w + 4j + l/16, slot l%16, holding logical chunk
-    // (l%16) ^ (row & 15) = (l%16) ^ ((4j + l/16) & 15)
+    // staging: 32 load instructions per stage, instruction q filling stage rows
+    // 4q + [0, 4); wave w issues q = w + NW i (i = 0.., q < 32): i = 0..3 at the
+    // four MFMA regions of k-step 0, and with seven waves waves 0..3 a fifth at
+    // region 0 of k-step 1.  Lane l writes row 4q + l/16, slot l%16, holding
+    // logical chunk (l%16) ^ (row & 15) = (l%16) ^ ((4q + l/16) & 15).
     const uint64_t abase = reinterpret_cast<uint64_t>(A + m0 * K);
     const uint64_t abase_s = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)abase) |
                              ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(abase >> 32)) << 32);
@@ -1000,12 +1008,15 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
         const int c = (lane & 15) ^ ((4 * q + (lane >> 4)) & 15);
         voff[q] = (uint32_t)(((lane >> 4) * (int)K + 128 * (c >> 3) + 8 * (c & 7)) * 2);
     }
-    auto a_dma = [&](int u, int buf, int j) {
-        const int soff = ((16 * wave + 4 * j) * (int)K + (u >> 1) * KB + 64 * (u & 1)) * 2;
-        uint8_t *dst = (buf ? As1 : As0) + (16 * wave + 4 * j) * TROW;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)dst, 16, voff[j],
+    auto a_dma = [&](int u, int buf, int i) {  // this wave's instruction i (q = wave + NW i), if q < 32
+        const int q = wave + NW * i;
+        if (q >= 32) return;  // (wave-uniform)
+        const int soff = (4 * q * (int)K + (u >> 1) * KB + 64 * (u & 1)) * 2;
+        uint8_t *dst = (buf ? As1 : As0) + 4 * q * TROW;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void *)dst, 16, voff[q & 3],
                                                  soff, 0, 0);
     };
+    constexpr int NI = (32 + NW - 1) / NW;  // staging instructions per wave and stage (at most)
     // A operand of MFMA tile i at k-step j: row lr + 32i, chunk 8h + j in slot
     // (8h + j) ^ (lr & 15)
     const uint8_t *rb[2][8];
@@ -1034,7 +1045,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
         for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
 
 #pragma unroll
-    for (int j = 0; j < 4; j++) a_dma(2 * b0, 0, j);
+    for (int j = 0; j < NI; j++) a_dma(2 * b0, 0, j);
 #pragma unroll
     for (int q = 0; q < B::NL; q++) w_load(b0, q);
     __builtin_amdgcn_s_waitcnt(0);
@@ -1084,6 +1095,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_w(const uint8_t *__restrict__ W
                     else if (i == 1 || i == 3) { bnxt[i - 1] = B::dw(p, 0, i - 1); bnxt[i] = B::dw(p, 0, i); }
                 }
                 if (ks == 0) a_dma(un, buf ^ 1, i);
+                if (NI > 4 && ks == 1 && i == 0) a_dma(un, buf ^ 1, 4);
                 if (ts == 0 && (ks == 6 || ks == 7)) {
 #pragma unroll
                     for (int q = 4 * (ks - 6) + i; q < B::NL; q += 8) w_load(bn, q);
@@ -1451,9 +1463,12 @@ struct Plan {
     int rt = 1;                             // k-sliced kernel: 32-row tiles per workgroup
 };
 
-// mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256)
-constexpr int MT_WIDE = 16, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 64)
-inline int tile_rows(const Plan &p) { return p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TBM : p.mt == MT_WIDE ? WBM : 32 * p.mt; }
+// mt = 8 selects the tall kernel (256 x 128 tiles), MT_WIDE the wide one (128 x 256),
+// MT_WIDE7 the wide one with seven waves (128 x 224)
+constexpr int MT_WIDE = 16, MT_WIDE7 = 17, MT_KS = 32;  // MT_KS: the k-sliced kernel (m <= 64)
+inline int tile_rows(const Plan &p) {
+    return p.mt == MT_KS ? 32 * p.rt : p.mt == 8 ? TBM : (p.mt == MT_WIDE || p.mt == MT_WIDE7) ? WBM : 32 * p.mt;
+}
 // the pre-pass layout: 32-row tiles of operand-major rows, or 0 (row-major)
 inline int operand_major(const Plan &p) { return p.mt == MT_KS ? p.rt : 0; }
 template <int TYPE>
@@ -1496,6 +1511,7 @@ hipError_t launch_typed(const Plan &p, const uint8_t *w, const int8_t *rexp, int
     switch (p.mt) {
     case 8: k_gemm_t<TYPE><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case MT_WIDE: k_gemm_w<TYPE><<<grid, 512, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
+    case MT_WIDE7: k_gemm_w<TYPE, 7><<<grid, 448, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 1: k_gemm<TYPE, 1><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     case 2: k_gemm<TYPE, 2><<<grid, 256, 0, st>>>(w, n, row_bytes, a, erow, k, m, out, g); break;
     default:

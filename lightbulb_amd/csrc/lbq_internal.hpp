@@ -47,7 +47,8 @@ struct ActView;
 // the same result; only the kernel shape changes.  Zero / false: the measured
 // default plan.
 //   LBQ_GEMM_KS64, LBQ_GEMM_NO_KS, LBQ_GEMM_KS=<blocks>, LBQ_GEMM_NO_TALL,
-//   LBQ_GEMM_BIG=wide|tall, LBQ_GEMM_SPLITS=<n>     batched GEMM plan
+//   LBQ_GEMM_BIG=wide|tall, LBQ_GEMM_SPLITS=<n>,
+//   LBQ_GEMM_WIDE7=0|1                              batched GEMM plan
 //   LBQ_GEMV1_NOFUSE, LBQ_GEMV1_CFG=<ppb>,<rpw>, LBQ_GEMV1_WPC=<waves per CU>,
 //   LBQ_GEMV1_WPG=<waves per workgroup>, LBQ_GEMV="rpw,it,wpc,fused",
 //   LBQ_GEMV_ROWS_OFF, LBQ_GEMV1_DYNAMIC            decode GEMV plan
@@ -59,6 +60,7 @@ struct Tuning {
     int gemm_ks = 0;      // k-sliced tiles: blocks per slice (0: planned)
     int gemm_big = 0;     // 1: wide tiles, 2: tall tiles (0: planned)
     int gemm_splits = 0;  // split-k count (0: planned)
+    int gemm_wide7 = 0;   // seven-wave wide tiles: 1 always where n allows, -1 never (0: planned)
     bool gemm_split_launch = false;  // k-sliced slices added by the separate launch, never in the kernel
     bool gemm_prepass = false;       // k-sliced operands always from the separate pre-pass
     bool gemv1_nofuse = false, gemv_rows_off = false;

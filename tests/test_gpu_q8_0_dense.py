@@ -423,3 +423,25 @@ def test_eight_wave_workgroups_6144_rows(oracle, lbq, dev, t, k):
     ys = rmsnorm_qmatmul_group(qms[1:], xd, to_dev(w, dev), 1e-5)
     for yy, r, n in zip(ys, raws[1:], (4096, 1024, 1024)):
         assert_rows_close(yy.cpu().numpy(), oracle.qmatmul(t, r, n, k, xn, nthreads=8).astype(np.float64), 2e-3)
+
+
+@pytest.mark.parametrize("t,m,n,k", [(Q4_K, 512, 14336, 1024), (Q4_K, 256, 14336, 2048), (Q5_K, 200, 7168, 1024),
+                                     (Q6_K, 130, 448, 2048), (Q8_0, 160, 672, 512)])
+def test_wide_tiles_seven_waves(oracle, lbq, dev, t, m, n, k, monkeypatch):
+    # where n is a multiple of 224 and seven-wave (128 x 224) wide tiles take fewer
+    # rounds of the chip, the wide kernel runs with seven waves: the same columns
+    # in the same k order per wave, so the bits of the eight-wave tiles
+    # (LBQ_GEMM_WIDE7=0), and forced seven-wave tiles (=1) on shapes the plan
+    # leaves at eight; rows against the oracle
+    rng = np.random.default_rng(1400 + t + m + n)
+    w_raw = bp.random_blocks(rng, t, n * k // oracle.block_size(t), d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    print(f"wide7 t={t} m={m} n={n} k={k}", flush=True)
+    y = forward_with_env(monkeypatch, {}, t, w_raw, n, k, x, dev)
+    y8 = forward_with_env(monkeypatch, {"LBQ_GEMM_WIDE7": "0"}, t, w_raw, n, k, x, dev)
+    y7 = forward_with_env(monkeypatch, {"LBQ_GEMM_WIDE7": "1"}, t, w_raw, n, k, x, dev)
+    assert np.array_equal(y.view(np.uint32), y8.view(np.uint32))
+    assert np.array_equal(y7.view(np.uint32), y8.view(np.uint32))
+    rows = np.r_[0:2, m // 2, m - 2:m]
+    ref = oracle.qmatmul(t, w_raw, n, k, x[rows], nthreads=8).astype(np.float64)
+    assert_rows_close(y[rows], ref, tight_bound(Q4_K, m))
