@@ -1,9 +1,10 @@
-// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 2 <= m <= 32
+// Batch decode on the matrix cores: y[m][n] = x[m][k] . W[n][k]^T for 2 <= m <= 64
 // (the shapes gemv_mx_serves admits),
-// Q8_K activation rows against Q4_K / Q5_K weights, in the reference's integer
-// arithmetic (candle-core 0.10.2 k_quants.rs, BlockQ4K / BlockQ5K vec_dot with
-// BlockQ8K: integer sub-block sums scaled by the 6-bit scales, mins against the
-// Q8_K bsums, combined with d, dmin and the activation's d in f32).
+// Q8_K activation rows against Q4_K / Q5_K / Q6_K weights, in the reference's
+// integer arithmetic (candle-core 0.10.2 k_quants.rs, BlockQ4K / BlockQ5K vec_dot
+// with BlockQ8K: integer sub-block sums scaled by the 6-bit scales, mins against
+// the Q8_K bsums, combined with d, dmin and the activation's d in f32; BlockQ6K:
+// mx_block6).
 //
 // Per 32-value sub-block s of a block, the integer dot of every (activation row,
 // weight row) pair is one v_mfma_i32_32x32x32_i8: A = the Q8_K codes of the
@@ -39,6 +40,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "lbq_device.hpp"
 #include "lbq_internal.hpp"
@@ -54,13 +56,30 @@ template <int TYPE>
 struct MxW {
     uint4 hd, qh, qs[4];  // block header (d, dmin, scales), the lane half's qh, its four 16-byte qs quarters
 };
+// Q6_K (210-byte blocks, 2-byte aligned): lane half h holds bytes 16h..16h+15 of
+// each 32-byte region of ql (four) and qh (two) as loaded; mx_block6 trades
+// halves between the lane pairs so that each lane ends with its own 8-byte
+// pieces.  sc: the 16 int8 group scales; d: the f16 bits of d.
+template <>
+struct MxW<TYPE_Q6_K> {
+    uint32_t ql[4][4], qh[2][4], sc[4], d;
+};
 template <int TYPE>
 __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &r) {
-    constexpr int QS = TYPE == TYPE_Q4_K ? 16 : 48;
-    r.hd = ld_u4(blk);
-    if constexpr (TYPE == TYPE_Q5_K) r.qh = ld_u4(blk + 16 + 16 * h);
+    if constexpr (TYPE == TYPE_Q6_K) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) r.qs[c] = ld_u4(blk + QS + 32 * c + 16 * h);
+        for (int c = 0; c < 4; c++) ld16_u2(blk + 32 * c + 16 * h, r.ql[c]);
+#pragma unroll
+        for (int c = 0; c < 2; c++) ld16_u2(blk + 128 + 32 * c + 16 * h, r.qh[c]);
+        ld16_u2(blk + 192, r.sc);
+        r.d = ld2_a2(blk + 208);
+    } else {
+        constexpr int QS = TYPE == TYPE_Q4_K ? 16 : 48;
+        r.hd = ld_u4(blk);
+        if constexpr (TYPE == TYPE_Q5_K) r.qh = ld_u4(blk + 16 + 16 * h);
+#pragma unroll
+        for (int c = 0; c < 4; c++) r.qs[c] = ld_u4(blk + QS + 32 * c + 16 * h);
+    }
 }
 
 // C row (activation row) of accumulator e in lane half h
@@ -129,6 +148,106 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, 
         const float dx = sdx[mx_row(e, h)];
         acc[e] = fmaf(d * dx, (float)isum[e], acc[e]);
         acc[e] = fmaf(-(dmin * dx), ms[e], acc[e]);
+    }
+}
+
+// lanes 32..63 of a and lanes 0..31 of b trade values (v_permlane32_swap)
+__device__ __forceinline__ void swap_halves(uint32_t &a, uint32_t &b) {
+    const auto v = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = v[0];
+    b = v[1];
+}
+
+// One Q6_K block (candle-core 0.10.2 k_quants.rs, BlockQ6K vec_dot with BlockQ8K:
+// per 16-value group g, the integer dot of the 6-bit codes minus 32 with the
+// activation codes, times the group's int8 scale, summed over the block in int32,
+// then d * dx in f32).  Value v = 128n + 32u + l (l < 32) of a block is nibble
+// u >> 1 of ql byte 64n + 32(u & 1) + l with bits 2u, 2u + 1 of qh byte 32n + l
+// above it (ggml's layout), so group g = 8n + 2u + (l >= 16) takes bytes
+// 16(g & 1)..+15 of ql region 2n + (u & 1) and of qh region n.
+// Per group, one v_mfma_i32_32x32x16_i8 of the activation codes against the codes
+// q (0..63), lane half h supplying values 16g + 8h .. 16g + 8h + 7, and isum +=
+// sc_g * dot_g.  The -32 of every code is sum_g sc_g * 32 * bsum_g (bsum_g: the
+// Q8_K 16-value sums), with bsum_g = 16 hi + lo (hi in -128..127, lo in 0..15) as
+// two more v_mfma_i32_32x32x16_i8 against the int8 scales (K = the 16 groups).
+// Every sum is exact in int32.  xo: the lane's A-read offset in the stage with
+// the chunk bits of group 0 (row ra, byte 8h); sbo: its 16-value sums.
+template <int E>
+__device__ __forceinline__ void mx_block6(MxW<TYPE_Q6_K> &r, const uint8_t *st, uint32_t xo, int sbo, int h,
+                                          const float *sdx, float *acc) {
+    // half 0 keeps bytes 0..7 of a region and takes 16..23 from its partner lane;
+    // half 1 keeps 24..31 and takes 8..15: dwords 0, 1 then hold the lane's
+    // piece of the region's first 16 values, dwords 2, 3 of its second 16
+    uint32_t(&ql)[4][4] = r.ql;
+    uint32_t(&qh)[2][4] = r.qh;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        swap_halves(ql[c][0], ql[c][2]);
+        swap_halves(ql[c][1], ql[c][3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        swap_halves(qh[c][0], qh[c][2]);
+        swap_halves(qh[c][1], qh[c][3]);
+    }
+    int isum[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) isum[e] = 0;
+    const i32x16v zero = {};
+    auto dot = [&](int g) {
+        const int n = g >> 3, u = (g >> 1) & 3, p = g & 1, c = 2 * n + (u & 1);
+        uint32_t bw[2];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const uint32_t lo = (ql[c][2 * p + w] >> (4 * (u >> 1))) & 0x0f0f0f0fu;
+            const uint32_t hi = ((qh[n][2 * p + w] >> (2 * u)) & 0x03030303u) << 4;
+            bw[w] = lo | hi;
+        }
+        const long b = (long)((uint64_t)bw[0] | (uint64_t)bw[1] << 32);
+        const long a = *reinterpret_cast<const long *>(st + (xo ^ (16u * g)));
+        return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, zero, 0, 0, 0);
+    };
+    // one group's MFMA in flight while the previous one's sums are scaled: the
+    // empty asm pins each group's adds in place (otherwise the sums are
+    // reassociated after all 16 MFMAs, which then hold 16 result tiles)
+    // (at E = 16 each group waits for its own MFMA: the second result tile would
+    // take the wave past 256 registers)
+    constexpr bool PIPE = E < 16;
+    i32x16v o;
+    if constexpr (PIPE) o = dot(0);
+#pragma unroll
+    for (int g = 0; g < 16; g++) {
+        i32x16v on;
+        if constexpr (!PIPE) o = dot(g);
+        else if (g < 15) on = dot(g + 1);
+        const int sc = (int)(int8_t)(uint8_t)(r.sc[g >> 2] >> (8 * (g & 3)));
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            isum[e] += __mul24(sc, o[e]);
+            asm volatile("" : "+v"(isum[e]));
+        }
+        if (PIPE && g < 15) o = on;
+    }
+    // the offset: A = hi / lo of the row's sums of groups 8h..8h+7, B = those
+    // groups' scales
+    const i32x4v xbv = *reinterpret_cast<const i32x4v *>(st + sbo);
+    uint32_t ah[2], al[2];
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        const uint32_t w0 = (uint32_t)xbv[2 * w], w1 = (uint32_t)xbv[2 * w + 1];
+        // bytes 0 and 2 of each: bits 4..11 of both int16 sums, and their low nibbles
+        ah[w] = __builtin_amdgcn_perm(w1 >> 4, w0 >> 4, 0x06040200u);
+        al[w] = __builtin_amdgcn_perm(w1 & 0x000f000fu, w0 & 0x000f000fu, 0x06040200u);
+    }
+    const uint32_t s0 = h ? r.sc[2] : r.sc[0], s1 = h ? r.sc[3] : r.sc[1];
+    const long bs = (long)((uint64_t)s0 | (uint64_t)s1 << 32);
+    const i32x16v oh = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)((uint64_t)ah[0] | (uint64_t)ah[1] << 32), bs, zero, 0, 0, 0);
+    const i32x16v ol = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)((uint64_t)al[0] | (uint64_t)al[1] << 32), bs, zero, 0, 0, 0);
+    const float d = h2f(r.d);
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int tot = isum[e] - 32 * (16 * oh[e] + ol[e]);
+        acc[e] = fmaf(d * sdx[mx_row(e, h)], (float)tot, acc[e]);
     }
 }
 
@@ -214,7 +333,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     const uint8_t *wr = PAIR ? (j < 16 ? W : W2) + (int64_t)min(row0 + (j & 15), n - 1) * row_bytes
                              : W + (int64_t)min(row0 + j, n - 1) * row_bytes;
     const int p0 = part * nb / sp.splits, np = (part + 1) * nb / sp.splits - p0;  // this workgroup's blocks
-    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : 176;
+    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : 210;
     uint8_t *st = xs[wave];
     // this lane's share of a block's activations: MR / 4 code chunks (row 4q +
     // lane / 16, chunk lane % 16) and a sums chunk (row lane / 2, half lane % 2);
@@ -248,6 +367,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
 #pragma unroll
     for (int s = 0; s < 8; s++) ro[s] = ra * 256 + 16 * ((2 * s + h) ^ (ra & 15));
     ro[8] = MR * 256 + ra * 32 + 16 * h;
+    const uint32_t xo6 = (uint32_t)(ra * 256 + 16 * (ra & 15) + 8 * h);  // Q6_K: 8-byte A reads, group 0
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; e++) acc[e] = 0.f;
@@ -286,7 +406,8 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
                 // xr[1 - q] holds slot i + q + 1 (loaded a block ago); xr[q] takes i + q + 2
                 load_x(blk(i + q + 2), xr[q]);
                 load_w(blk(i + q + 1), rw[1 - q]);
-                mx_block<TYPE, (MX_WAVES > 4), E>(rw[q], st, ro, h, sdx + MR * blk(i + q), acc);
+                if constexpr (TYPE == TYPE_Q6_K) mx_block6<E>(rw[q], st, xo6, ro[8], h, sdx + MR * blk(i + q), acc);
+                else mx_block<TYPE, (MX_WAVES > 4), E>(rw[q], st, ro, h, sdx + MR * blk(i + q), acc);
                 if (i + q == il) break;
                 write_x(xr[1 - q]);  // after this block's stage reads (the MFMAs consumed them)
             }
@@ -348,8 +469,13 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     if (t == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Q6_K's 32-row stage kernels: two waves per SIMD (at most 256 registers), which
+// the register allocator would otherwise give up for a few registers more
+#define MX_MIN_WAVES(TYPE) ((TYPE) == TYPE_Q6_K ? 2 : 1)
+
 template <int TYPE, int MX_WAVES, int MR, bool PAIR = false, bool HALVES = false>
-__global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
+__global__ __launch_bounds__(64 * MX_WAVES) __attribute__((amdgpu_waves_per_eu(MX_MIN_WAVES(TYPE))))
+void k_gemv_mx(const uint8_t *__restrict__ W, int64_t row_bytes, int n,
                                                          int nb, ActView act, int m, float *__restrict__ y, MxSplit sp,
                                                          const uint8_t *__restrict__ W2, int nwg) {
     int bid = (int)blockIdx.x;
@@ -375,7 +501,8 @@ struct MxSegs {
 };
 
 template <int TYPE, int MX_WAVES, int MR, bool HALVES = false>
-__global__ __launch_bounds__(64 * MX_WAVES) void k_gemv_mx_seg(int64_t row_bytes, int nb, ActView act, int m, MxSegs g) {
+__global__ __launch_bounds__(64 * MX_WAVES) __attribute__((amdgpu_waves_per_eu(MX_MIN_WAVES(TYPE))))
+void k_gemv_mx_seg(int64_t row_bytes, int nb, ActView act, int m, MxSegs g) {
     int bid = (int)blockIdx.x, half = 0;
     if constexpr (HALVES) {
         half = mx_half_bid(bid, g.wg_end[g.count - 1]);
@@ -402,13 +529,17 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // that kernel quantises x in its own prologue and stays ahead (m = 2: 12.8 vs
     // 17.9 us) -- except at k > 8192, where it cannot hold the activation rows and
     // the general GEMV runs: Q4_K 4096 x 14336 m = 2 / 3 / 4 / 8 22.2 / 26.3 /
-    // 30.2 / 52.8 -> 21.0 / 20.9 / 20.8 / 21.0 us.  A Q6_K version (sixteen
-    // 16-value groups per block, one v_mfma_i32_32x32x16_i8 each, the -32 offset
-    // through the bsums) was correct but slower (14336 x 4096 m = 8 24.4 -> 30.1
-    // us: fourteen 8-byte weight loads per block and lane) and was not kept.
+    // 30.2 / 52.8 -> 21.0 / 20.9 / 20.8 / 21.0 us.
+    // Q6_K only at k > 8192 and m >= 3, where it is ahead of both the decode
+    // kernels and the fp16 GEMM (4096 x 14336 m = 4 / 8 / 16 / 32 / 64: 29.3 / 43.6
+    // / 28.5 / 29.7 / 42.8 -> 23.6 / 24.0 / 25.6 / 29.2 / 42.6 us; m = 2: 22.1 ->
+    // 23.2); at k = 4096 it is not (1024 x 4096 m = 16 9.2 -> 13.1 us, 14336 x 4096
+    // m = 32 29.4 -> 31.1, the 128256-row head m = 8 / 16 128.7 / 159.9 -> 151.5 /
+    // 167.6): sixteen MFMAs per block and a scaled sum per group and output.
     if (tuning().gemv_mx_off) return false;
-    if (type != TYPE_Q4_K && type != TYPE_Q5_K) return false;
+    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K) return false;
     if (k % 256 || k / 256 > 64 || m < 2 || m > 64 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+    if (type == TYPE_Q6_K && (k / 256 <= 32 || m == 2) && !tuning().gemv_mx_all) return false;
     // m = 33..64 as two 32-row halves (mx_half_bid) where the m <= 32 launch has
     // at most one workgroup per CU (up to 8192 rows): against the fp16 GEMM, Q4_K m
     // = 64 4096 x 4096 24.1 -> 16.4 us, 1024 x 4096 17.3 -> 11.1, 4096 x 14336 32.1
@@ -461,6 +592,14 @@ static unsigned mx_grid(int64_t nwg, int m) { return (unsigned)(m > 32 ? (nwg + 
 // activation rows a launch's stage holds: 8, 16 or 32 (each half's 32 with row halves)
 static int mx_rows(int m) { return m <= 8 ? 8 : m <= 16 ? 16 : 32; }
 
+// f(std::integral_constant<int, type>) for the types this kernel serves
+template <typename F>
+static void mx_typed(int type, F &&f) {
+    if (type == TYPE_Q4_K) f(std::integral_constant<int, TYPE_Q4_K>{});
+    else if (type == TYPE_Q5_K) f(std::integral_constant<int, TYPE_Q5_K>{});
+    else f(std::integral_constant<int, TYPE_Q6_K>{});
+}
+
 template <int TYPE, int WAVES, bool PAIR>
 static void mx_launch(int m, unsigned grid, size_t lds, hipStream_t st, const uint8_t *w, int64_t row_bytes, int n,
                       int nb, const ActView &act, float *y, const MxSplit &sp, const uint8_t *w2, int nwg) {
@@ -509,13 +648,10 @@ hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, co
     g.count = count;
     const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
     const unsigned grid = mx_grid(wg, m);
-    if (type == TYPE_Q4_K) {
-        if (waves == 8) mx_seg_launch<TYPE_Q4_K, 8>(m, grid, lds, st, row_bytes, nb, act, g);
-        else mx_seg_launch<TYPE_Q4_K, 4>(m, grid, lds, st, row_bytes, nb, act, g);
-    } else {
-        if (waves == 8) mx_seg_launch<TYPE_Q5_K, 8>(m, grid, lds, st, row_bytes, nb, act, g);
-        else mx_seg_launch<TYPE_Q5_K, 4>(m, grid, lds, st, row_bytes, nb, act, g);
-    }
+    mx_typed(type, [&](auto T) {
+        if (waves == 8) mx_seg_launch<T.value, 8>(m, grid, lds, st, row_bytes, nb, act, g);
+        else mx_seg_launch<T.value, 4>(m, grid, lds, st, row_bytes, nb, act, g);
+    });
     return hipGetLastError();
 }
 
@@ -534,10 +670,9 @@ hipError_t launch_gemv_mx_pair(int type, const uint8_t *w_gate, const uint8_t *w
     const MxSplit sp{1, nullptr, nullptr, 0};
     const int nwg = (int)((n + 15) / 16);
     const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
-    if (type == TYPE_Q4_K)
-        mx_launch<TYPE_Q4_K, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
-    else
-        mx_launch<TYPE_Q5_K, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
+    mx_typed(type, [&](auto T) {
+        mx_launch<T.value, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
+    });
     return hipGetLastError();
 }
 
@@ -557,13 +692,10 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
     // more workgroups, four waves (14336 x 4096 m = 8: 16.9 at four, 18.7 at eight).
     const bool w8 = tuning().gemv_mx_waves ? tuning().gemv_mx_waves == 8 : (int64_t)grid <= (int64_t)num_cus();
     const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
-    if (type == TYPE_Q4_K) {
-        if (w8) mx_launch<TYPE_Q4_K, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
-        else mx_launch<TYPE_Q4_K, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
-    } else {
-        if (w8) mx_launch<TYPE_Q5_K, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
-        else mx_launch<TYPE_Q5_K, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
-    }
+    mx_typed(type, [&](auto T) {
+        if (w8) mx_launch<T.value, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
+        else mx_launch<T.value, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
+    });
     return hipGetLastError();
 }
 

@@ -70,7 +70,7 @@ struct Tuning {
     bool gemv_mx_off = false;  // batch decode never on the matrix cores
     bool gemv_mx_wide_off = false;  // m = 9..32 never on the integer matrix-core kernel
     int gemv_mx_splits = 0, gemv_mx_waves = 0;  // matrix-core batch decode: workgroups per tile, waves (0: planned)
-    bool gemv_mx_all = false;  // matrix-core batch decode wherever it can run (m = 2..32, Q4_K / Q5_K)
+    bool gemv_mx_all = false;  // matrix-core batch decode wherever it can run (m = 2..32, Q4_K / Q5_K / Q6_K)
     bool gemv_mx_pair_off = false;  // gate/up pairs at m = 2..32 as two launches and a product launch
     bool gemv_mx_halves_off = false;  // m = 33..64 never on the integer matrix-core kernel
     int gemv_cfg[4] = {0, 0, 0, 0};  // general GEMV "rpw,it,wpc,fused" (gemv_cfg[0] == 0: planned)

@@ -1,6 +1,7 @@
 """Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..64 with
-n >= 1024 -- m = 33..64 as two 32-row halves -- and m = 2..8 at k > 8192)
-against the oracle.
+n >= 1024 -- m = 33..64 as two 32-row halves -- and m = 2..8 at k > 8192; Q6_K on
+the same shapes at k > 8192 only, and through LBQ_GEMV_MX_ALL at any k) against
+the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -20,6 +21,17 @@ from test_gpu_parity import Q4_K, Q5_K, Q6_K, assert_rows_close, gpu_qmatmul
 from test_gpu_q8_0_dense import forward_with_env
 
 pytestmark = pytest.mark.gpu
+
+
+def mx_env(t, k):
+    """Plan overrides that put a call on the kernel: Q6_K takes it only at k > 8192
+    by default, LBQ_GEMV_MX_ALL everywhere it can run."""
+    return {"LBQ_GEMV_MX_ALL": "1"} if t == Q6_K and k <= 8192 else {}
+
+
+def mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev):
+    env = mx_env(t, k)
+    return forward_with_env(monkeypatch, env, t, w_raw, n, k, x, dev) if env else gpu_qmatmul(t, w_raw, n, k, x, dev)
 
 # (8224 rows: 257 workgroups, the four-wave kernel; fewer rows: one workgroup per CU at
 # most, the eight-wave kernel)
@@ -45,12 +57,48 @@ def test_mx_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
 
 
+@pytest.mark.parametrize("n,k", [(4096, 4096), (2050, 2048), (64, 14336), (96, 16384)])
+@pytest.mark.parametrize("m", [2, 5, 8])
+def test_mx_q6k_small_m_forced(oracle, lbq, dev, n, k, m, monkeypatch):
+    # Q6_K at m <= 8 and k <= 8192 stays on the decode kernels; LBQ_GEMV_MX_ALL runs
+    # the kernel's 8-row form there (uneven and empty waves), k > 8192 takes it anyway
+    rng = np.random.default_rng(n + k + 53 * m)
+    w_raw = bp.random_blocks(rng, Q6_K, n * k // 256, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx q6k forced n={n} k={k} m={m}", flush=True)
+    y = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_ALL": "1"}, Q6_K, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(Q6_K, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    # (k > 8192 and m > 2: the kernel is Q6_K's default there too)
+    same = np.array_equal(gpu_qmatmul(Q6_K, w_raw, n, k, x, dev).view(np.uint32), y.view(np.uint32))
+    assert same == (k > 8192 and m > 2)
+
+
+@pytest.mark.parametrize("m", [16, 32])
+def test_mx_q6k_extreme_codes(oracle, lbq, dev, m, monkeypatch):
+    # Q6_K blocks at the ends of every integer range: scales -128 / 127, 6-bit codes
+    # 0 / 63 (values -32 / 31), activations of one magnitude (codes +-127, sums
+    # +-2032 per group): the int32 block sums and the offset term stay exact
+    rng = np.random.default_rng(970 + m)
+    n, k = 1024, 4096
+    blocks = np.zeros((n * k // 256, 210), dtype=np.uint8)
+    blocks[:, :192] = rng.choice(np.array([0x00, 0xff], dtype=np.uint8), size=(blocks.shape[0], 192))
+    blocks[:, 192:208] = rng.choice(np.array([0x80, 0x7f], dtype=np.uint8), size=(blocks.shape[0], 16))
+    blocks[:, 208:210] = (rng.standard_normal(blocks.shape[0]) * 1e-3).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    w_raw = blocks.reshape(-1)
+    x = (np.where(rng.random((m, k)) < 0.5, -100.0, 100.0)).astype(np.float32)
+    y = forward_with_env(monkeypatch, mx_env(Q6_K, k), Q6_K, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(Q6_K, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+
+
 # m = 9..32 runs on the kernel from 1024 rows: 32-128 tiles (two workgroups each),
 # 129-130 tiles (one, eight waves), 257 (one, four waves); k from 2 to 64 blocks
 WIDE_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (4096, 512), (8224, 1024), (4096, 14336), (4160, 16384)]
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("n,k", WIDE_SHAPES)
 @pytest.mark.parametrize("m", [9, 16, 17, 32])
 def test_mx_wide_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
@@ -61,10 +109,10 @@ def test_mx_wide_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[rng.random(x.shape) < 0.01] *= 20
     print(f"mx wide t={t} n={n} k={k} m={m}", flush=True)
-    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    y = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, ref, 1e-4)
-    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    again = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
     # switched off: the fp16 GEMM (its own bound), which must differ in some bits
     off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_WIDE_OFF": "1"}, t, w_raw, n, k, x, dev)
@@ -79,7 +127,7 @@ def test_mx_wide_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
 HALF_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (8192, 1024), (4096, 14336)]
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("n,k", HALF_SHAPES)
 @pytest.mark.parametrize("m", [33, 47, 64])
 def test_mx_halves_match_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
@@ -88,10 +136,10 @@ def test_mx_halves_match_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[rng.random(x.shape) < 0.01] *= 20
     print(f"mx halves t={t} n={n} k={k} m={m}", flush=True)
-    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    y = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, ref, 1e-4)
-    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    again = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
     # switched off: the fp16 GEMM (its own bound), which must differ in some bits
     off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_HALVES_OFF": "1"}, t, w_raw, n, k, x, dev)
@@ -99,7 +147,7 @@ def test_mx_halves_match_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m,n,k", [(40, 4096, 1024), (64, 2080, 2048), (64, 8192, 1024)])
 def test_mx_halves_are_two_launches(lbq, dev, t, m, n, k, monkeypatch):
     # each half is the 32-row launch over its rows: with the wave count pinned (the
@@ -110,7 +158,9 @@ def test_mx_halves_are_two_launches(lbq, dev, t, m, n, k, monkeypatch):
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = rng.standard_normal((m, k)).astype(np.float32)
     print(f"mx halves bits t={t} m={m} n={n} k={k}", flush=True)
-    env = {"LBQ_GEMV_MX_WAVES": "4"}
+    env = {"LBQ_GEMV_MX_WAVES": "4", **mx_env(t, k)}
+    if t == Q6_K:
+        env["LBQ_GEMV_MX_ALL"] = "1"  # (Q6_K at m <= 8 runs the decode kernels otherwise)
     y = forward_with_env(monkeypatch, env, t, w_raw, n, k, x, dev)
     lo = forward_with_env(monkeypatch, env, t, w_raw, n, k, np.ascontiguousarray(x[:32]), dev)
     hi = forward_with_env(monkeypatch, env, t, w_raw, n, k, np.ascontiguousarray(x[32:]), dev)
@@ -118,41 +168,41 @@ def test_mx_halves_are_two_launches(lbq, dev, t, m, n, k, monkeypatch):
     assert np.array_equal(y[32:].view(np.uint32), hi.view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m,k,n", [(6, 4096, 4096), (7, 4096, 4096), (2, 14336, 160), (3, 14336, 33), (4, 9216, 160),
                                    (2, 8448, 1), (5, 8448, 70), (12, 512, 4097), (31, 768, 4127), (25, 8448, 4100)])
-def test_mx_row_counts(oracle, lbq, dev, t, m, k, n):
+def test_mx_row_counts(oracle, lbq, dev, t, m, k, n, monkeypatch):
     # k = 8448: 33 blocks, the smallest k the kernel takes at m <= 4; n = 1 and 33:
     # a workgroup of one row, a last workgroup of one row
     rng = np.random.default_rng(900 + 10 * m + t + k + n)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    y = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, ref, 1e-4)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m,n,k", [(8, 96, 14336), (32, 4096, 4096)])
-def test_mx_nan_activations(oracle, lbq, dev, t, m, n, k):
+def test_mx_nan_activations(oracle, lbq, dev, t, m, n, k, monkeypatch):
     rng = np.random.default_rng(910 + t + m)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     x = _nan_rows(rng, m, k)
-    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    y = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
     assert np.all(np.isfinite(ref))
     assert_rows_close(y, ref, 1e-4)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m,n,k", [(8, 200, 14336), (32, 4128, 4096)])
-def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k):
+def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k, monkeypatch):
     rng = np.random.default_rng(920 + t + m)
     w_raw = bp.random_blocks(rng, t, n * k // 256, d_scale=1e-3)
     bad, nan_rows = _poison(w_raw, t, n, k // 256, rng)
     good = np.setdiff1d(np.arange(n), bad)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    y = mx_qmatmul(monkeypatch, t, w_raw, n, k, x, dev)
     ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
     assert not np.isfinite(ref[:, bad]).any() and np.isfinite(ref[:, good]).all()
     assert np.array_equal(np.isfinite(y), np.isfinite(ref))
@@ -160,9 +210,13 @@ def test_mx_nonfinite_scales(oracle, lbq, dev, t, m, n, k):
     assert_rows_close(y[:, good], ref[:, good], 1e-4)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
-@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (16, 4096, 14336), (32, 4096, 2048), (6, 2080, 8192),
-                                   (64, 4096, 4096), (45, 2080, 4096)])
+SPLIT_CASES = [(8, 4096, 4096), (16, 4096, 14336), (32, 4096, 2048), (6, 2080, 8192), (64, 4096, 4096), (45, 2080, 4096)]
+# (Q6_K: the kernel's own shapes, k > 8192)
+SPLIT_CASES_Q6 = [(6, 4096, 9216), (16, 4096, 14336), (32, 2048, 9216), (64, 4096, 9216), (45, 2080, 9216)]
+
+
+@pytest.mark.parametrize("t,m,n,k", [(t, *c) for t in (Q4_K, Q5_K) for c in SPLIT_CASES] +
+                         [(Q6_K, *c) for c in SPLIT_CASES_Q6])
 def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
     # Up to 4096 rows a tile is split over two workgroups.  forward() zeroes y in the
     # quantisation launch and the halves are added into it atomically; the
@@ -192,8 +246,8 @@ def test_mx_split_halves_same_bits(oracle, lbq, dev, t, m, n, k):
     assert np.array_equal(bits(y1b), bits(yg[1]))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
-def test_mx_split_halves_subnormal_and_host_output(oracle, lbq, dev, t):
+@pytest.mark.parametrize("t,m,k", [(Q4_K, 8, 4096), (Q5_K, 8, 4096), (Q6_K, 8, 9216)])
+def test_mx_split_halves_subnormal_and_host_output(oracle, lbq, dev, t, m, k):
     # Two-way split tiles at m = 8: with tiny weight scales (f16 d ~1e-7) and a tiny
     # x (~1e-36, Q8_K scales ~1e-38) the halves are subnormal f32.  forward() adds them with f32 atomics into y (plain device
     # memory); the pre-quantised handle, and forward() into host-pinned memory
@@ -206,7 +260,7 @@ def test_mx_split_halves_subnormal_and_host_output(oracle, lbq, dev, t):
     from lightbulb_amd.quantized import QActivation, QMatMul, QTensor
     from test_gpu_parity import to_dev
     rng = np.random.default_rng(960 + t)
-    m, n, k = 8, 2048, 4096
+    n = 2048
     L = _lib.lib()
     bits = lambda a: np.asarray(a).view(np.uint32)
     for scale, d_scale in ((1.0, 1e-3), (1e-36, 1e-7)):
@@ -316,7 +370,7 @@ def _gate_up_env(monkeypatch, env, t, g_raw, u_raw, n, k, x, dev):
         L.lbq_ctx_destroy(ctx)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m,n,k", [(2, 8224, 9216), (5, 8224, 2048), (16, 8240, 1024), (32, 8256, 4096)])
 def test_mx_gate_up_pair(oracle, lbq, dev, t, m, n, k, monkeypatch):
     # above 8192 rows a gate/up pair at m = 2..32 is one launch (16 gate and 16 up
@@ -328,18 +382,24 @@ def test_mx_gate_up_pair(oracle, lbq, dev, t, m, n, k, monkeypatch):
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[rng.random(x.shape) < 0.01] *= 20
     print(f"mx pair t={t} m={m} n={n} k={k}", flush=True)
-    y = _gate_up_env(monkeypatch, {}, t, g_raw, u_raw, n, k, x, dev)
-    off = _gate_up_env(monkeypatch, {"LBQ_GEMV_MX_PAIR_OFF": "1"}, t, g_raw, u_raw, n, k, x, dev)
+    y = _gate_up_env(monkeypatch, mx_env(t, k), t, g_raw, u_raw, n, k, x, dev)
+    off = _gate_up_env(monkeypatch, {"LBQ_GEMV_MX_PAIR_OFF": "1", **mx_env(t, k)}, t, g_raw, u_raw, n, k, x, dev)
     assert np.array_equal(y.view(np.uint32), off.view(np.uint32))
     gr = oracle.qmatmul(t, g_raw, n, k, x, nthreads=8).astype(np.float64)
     ur = oracle.qmatmul(t, u_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, gr / (1.0 + np.exp(-gr)) * ur, 1e-4)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
-@pytest.mark.parametrize("m,ns,k", [(6, (4096, 1024, 2080), 4096), (16, (4096, 1024, 2080), 2048),
-                                    (32, (1024, 4096), 4096), (8, (14336, 14336), 4096),
-                                    (40, (4096, 1024, 2080), 4096), (64, (1024, 4096), 2048)])
+GROUP_CASES = [(6, (4096, 1024, 2080), 4096), (16, (4096, 1024, 2080), 2048), (32, (1024, 4096), 4096),
+               (8, (14336, 14336), 4096), (40, (4096, 1024, 2080), 4096), (64, (1024, 4096), 2048)]
+
+
+GROUP_CASES_Q6 = [(6, (4096, 1024, 2080), 9216), (16, (4096, 1024, 2080), 9216), (32, (1024, 4096), 9216),
+                  (40, (4096, 1024, 2080), 9216), (64, (1024, 4096), 9216)]
+
+
+@pytest.mark.parametrize("t,m,ns,k", [(t, *c) for t in (Q4_K, Q5_K) for c in GROUP_CASES] +
+                         [(Q6_K, *c) for c in GROUP_CASES_Q6])
 def test_mx_group_one_launch(oracle, lbq, dev, t, m, ns, k):
     # a grouped call whose weights all run on the kernel is one launch (each weight's
     # workgroups as its own launch would run them): the bits of the separate calls
@@ -362,7 +422,7 @@ def test_mx_group_one_launch(oracle, lbq, dev, t, m, ns, k):
     assert_rows_close(ys[i].cpu().numpy(), ref, 1e-4)
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q5_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("m", [2, 6, 16, 32, 48])
 def test_mx_rmsnorm_in_quantisation(oracle, lbq, dev, t, m):
     # at m > 1 the call-site entry points run candle's RmsNorm inside the Q8_K
