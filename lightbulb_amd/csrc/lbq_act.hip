@@ -88,13 +88,14 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float *__restrict__ x, 
 template <bool GGUF_OUT, bool VEC_IN, bool S>
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float *__restrict__ x, int64_t nblocks,
                                                     int8_t *__restrict__ xq, float *__restrict__ xd,
-                                                    float *__restrict__ xs, uint8_t *__restrict__ gguf) {
+                                                    float *__restrict__ xs, uint8_t *__restrict__ gguf, ZeroList zero) {
     const int tid = blockIdx.x * 256 + threadIdx.x;
     const int64_t blk = (int64_t)tid >> 3;
     const int sub = threadIdx.x & 7;
     const bool ok = blk < nblocks;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (ok) load4f(x + blk * QK8_0 + sub * 4, VEC_IN, v);
+    zero_fill(zero);  // after the x loads are issued
     __half dh;
     const uint32_t packed = q8_0_block8(v, &dh);
     __half sh = __float2half_rn(0.f);
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd, int16_t *xbs,
                             float *xs, uint8_t *gguf, hipStream_t st, const ZeroList *zero) {
     const ZeroList zl = zero ? *zero : ZeroList{};
-    if (zl.count && act_type != TYPE_Q8_K) return hipErrorInvalidValue;
+    if (zl.count && act_type != TYPE_Q8_K && act_type != TYPE_Q8_0) return hipErrorInvalidValue;
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);
@@ -320,10 +321,13 @@ hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, 
         }
     } else if (act_type == TYPE_Q8_0 || act_type == TYPE_Q8_1) {
         const int64_t nb = m * (k / QK8_0);
-        const dim3 grid((unsigned)((nb * 8 + 255) / 256));
-#define LBQ_Q8(G, V)                                                                                   \
-    if (act_type == TYPE_Q8_1) k_quant_q8_0<G, V, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf); \
-    else k_quant_q8_0<G, V, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf);
+        int64_t zn = 0;
+        for (int z = 0; z < zl.count; z++) zn += zl.n[z];
+        // (workgroups past the blocks only zero, as for Q8_K)
+        const dim3 grid((unsigned)std::max<int64_t>((nb * 8 + 255) / 256, std::min<int64_t>((zn + 16383) / 16384, 1024)));
+#define LBQ_Q8(G, V)                                                                                       \
+    if (act_type == TYPE_Q8_1) k_quant_q8_0<G, V, true><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf, zl); \
+    else k_quant_q8_0<G, V, false><<<grid, 256, 0, st>>>(x, nb, xq, xd, xs, gguf, zl);
         if (gguf) {
             if (vec) { LBQ_Q8(true, true) } else { LBQ_Q8(true, false) }
         } else {

@@ -60,13 +60,50 @@ struct MxW {
 // each 32-byte region of ql (four) and qh (two) as loaded; mx_block6 trades
 // halves between the lane pairs so that each lane ends with its own 8-byte
 // pieces.  sc: the 16 int8 group scales; d: the f16 bits of d.
+// With AL (mx_load_w), every field is read as aligned dwords -- the 16 bytes at
+// or before it and the dword after (xl, xh, xs) -- and funnel-shifted by sh (0 or
+// 16 bits, the block's offset past 4-byte alignment) in mx_block6.
 template <>
 struct MxW<TYPE_Q6_K> {
     uint32_t ql[4][4], qh[2][4], sc[4], d;
+    uint32_t xl[4], xh[2], xs, sh;
 };
-template <int TYPE>
+// Q8_0 (34-byte blocks), eight blocks (256 values) per step.  Rows are a multiple
+// of 64 values, so a step starts 4-byte aligned and block s at 34 s: the lane
+// half's 16 codes (bytes 34 s + 2 + 16 h ..) are 4-byte aligned in odd blocks
+// and 2 bytes past alignment in even ones, which are read as the aligned 16 bytes
+// before them plus the dword after (x), funnel-shifted in mx_block8.  The first
+// raw dword of an even block holds its d in lane half 0; x of an even block holds
+// the next (odd) block's d in lane half 1.
+template <>
+struct MxW<TYPE_Q8_0> {
+    uint32_t c[8][4], x[4];
+};
+template <int TYPE, bool AL = false>
 __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &r) {
-    if constexpr (TYPE == TYPE_Q6_K) {
+    if constexpr (TYPE == TYPE_Q8_0) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(blk);
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const gbytes_c p = (gbytes_c)(a + 34 * s + 16 * h + (s & 1 ? 2 : 0));
+            const u32x4a4 v = gld16(p);
+            r.c[s][0] = v.x; r.c[s][1] = v.y; r.c[s][2] = v.z; r.c[s][3] = v.w;
+            if (!(s & 1)) r.x[s >> 1] = gld4(p + 16);
+        }
+    } else if constexpr (TYPE == TYPE_Q6_K && AL) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(blk), a4 = a & ~(uintptr_t)3;
+        r.sh = (uint32_t)(a & 2u) * 8u;
+        auto ld = [&](uintptr_t off, uint32_t *v, uint32_t &x) {
+            const u32x4a4 q = gld16((gbytes_c)(a4 + off));
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            x = gld4((gbytes_c)(a4 + off + 16));
+        };
+#pragma unroll
+        for (int c = 0; c < 4; c++) ld(32 * c + 16 * h, r.ql[c], r.xl[c]);
+#pragma unroll
+        for (int c = 0; c < 2; c++) ld(128 + 32 * c + 16 * h, r.qh[c], r.xh[c]);
+        ld(192, r.sc, r.xs);  // xs: bytes 208..209 (d) in its low (aligned block) or high half
+    } else if constexpr (TYPE == TYPE_Q6_K) {
 #pragma unroll
         for (int c = 0; c < 4; c++) ld16_u2(blk + 32 * c + 16 * h, r.ql[c]);
 #pragma unroll
@@ -172,9 +209,24 @@ __device__ __forceinline__ void swap_halves(uint32_t &a, uint32_t &b) {
 // two more v_mfma_i32_32x32x16_i8 against the int8 scales (K = the 16 groups).
 // Every sum is exact in int32.  xo: the lane's A-read offset in the stage with
 // the chunk bits of group 0 (row ra, byte 8h); sbo: its 16-value sums.
-template <int E>
+template <int E, bool AL = false>
 __device__ __forceinline__ void mx_block6(MxW<TYPE_Q6_K> &r, const uint8_t *st, uint32_t xo, int sbo, int h,
                                           const float *sdx, float *acc) {
+    if constexpr (AL) {
+        auto funnel = [&](uint32_t *v, uint32_t x) {
+            const uint32_t v0 = v[0], v1 = v[1], v2 = v[2], v3 = v[3];
+            v[0] = __builtin_amdgcn_alignbit(v1, v0, r.sh);
+            v[1] = __builtin_amdgcn_alignbit(v2, v1, r.sh);
+            v[2] = __builtin_amdgcn_alignbit(v3, v2, r.sh);
+            v[3] = __builtin_amdgcn_alignbit(x, v3, r.sh);
+        };
+#pragma unroll
+        for (int c = 0; c < 4; c++) funnel(r.ql[c], r.xl[c]);
+#pragma unroll
+        for (int c = 0; c < 2; c++) funnel(r.qh[c], r.xh[c]);
+        funnel(r.sc, r.xs);
+        r.d = (r.xs >> r.sh) & 0xffffu;
+    }
     // half 0 keeps bytes 0..7 of a region and takes 16..23 from its partner lane;
     // half 1 keeps 24..31 and takes 8..15: dwords 0, 1 then hold the lane's
     // piece of the region's first 16 values, dwords 2, 3 of its second 16
@@ -251,6 +303,63 @@ __device__ __forceinline__ void mx_block6(MxW<TYPE_Q6_K> &r, const uint8_t *st, 
     }
 }
 
+// Eight Q8_0 blocks (candle-core 0.10.2 k_quants.rs, BlockQ8_0 vec_dot with
+// BlockQ8_0: per 32-value block the integer dot of the codes, then
+// (sum as f32) * d_w * d_x added in f32).  Block s is one v_mfma_i32_32x32x32_i8
+// (its A operand is the stage chunk pair of the Q4_K sub-block s); sdx: [8][MR],
+// the activation d of block s and row i.  One block's MFMA is in flight while the
+// previous one is scaled.
+template <int MR>
+__device__ __forceinline__ void mx_block8(const MxW<TYPE_Q8_0> &r, const uint8_t *st, const int *ro, int h,
+                                          const float *sdx, float *acc) {
+    constexpr int E = MR / 2;
+    const i32x16v zero = {};
+    // the blocks' d: lane half 0 holds the even blocks' (d0 | d2 << 16, d4 | d6 <<
+    // 16), half 1 the odd ones'; one exchange gives every lane both
+    uint32_t ev[2], od[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const uint32_t own = h ? ((r.x[2 * q] >> 16) | (r.x[2 * q + 1] & 0xffff0000u))
+                               : ((r.c[4 * q][0] & 0xffffu) | (r.c[4 * q + 2][0] << 16));
+        ev[q] = own;
+        od[q] = own;
+        swap_halves(ev[q], od[q]);  // ev: half 0's (even), od: half 1's (odd), in both halves
+    }
+    auto dot = [&](int s) {
+        i32x4v bw;
+        if (s & 1) {
+            bw = i32x4v{(int)r.c[s][0], (int)r.c[s][1], (int)r.c[s][2], (int)r.c[s][3]};
+        } else {
+            const uint32_t *v = r.c[s];
+            bw[0] = (int)__builtin_amdgcn_alignbit(v[1], v[0], 16);
+            bw[1] = (int)__builtin_amdgcn_alignbit(v[2], v[1], 16);
+            bw[2] = (int)__builtin_amdgcn_alignbit(v[3], v[2], 16);
+            bw[3] = (int)__builtin_amdgcn_alignbit(r.x[s >> 1], v[3], 16);
+        }
+        const i32x4v xa = *reinterpret_cast<const i32x4v *>(st + ro[s]);
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, bw, zero, 0, 0, 0);
+    };
+    i32x16v o = dot(0);
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        i32x16v on;
+        if (s < 7) on = dot(s + 1);
+        const float dw = h2f(((s & 1 ? od : ev)[s >> 2] >> (16 * ((s >> 1) & 1))) & 0xffffu);
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            // C rows 8q + 4h .. 8q + 4h + 3 of accumulators 4q .. 4q + 3
+            const float4 dx = *reinterpret_cast<const float4 *>(sdx + s * MR + 8 * q + 4 * h);
+            const float dv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                acc[4 * q + c] = fmaf((float)o[4 * q + c] * dw, dv[c], acc[4 * q + c]);
+                asm volatile("" : "+v"(acc[4 * q + c]));
+            }
+        }
+        if (s < 7) o = on;
+    }
+}
+
 template <int MR>
 struct MxX {
     i32x4v c[MR / 4], s;  // codes (rows 4q + lane/16, chunk lane%16), sums (row lane/2, half lane%2)
@@ -323,7 +432,8 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
                                              const uint8_t *__restrict__ W2, int bid) {
     constexpr int E = MR / 2, STAGE = MR * 256 + MR * 32;  // codes of MR rows, then their 16-value sums
     static_assert(E * 64 * 4 <= STAGE, "the partial tile overlays the wave's stage");
-    extern __shared__ __align__(16) float sdx[];  // [nb][MR]: dx of block b, activation row i (0 past m)
+    // [nb][MR] (Q8_0: [8 nb][MR]): dx of activation block b, row i (0 past m)
+    extern __shared__ __align__(16) float sdx[];
     __shared__ __align__(16) uint8_t xs[MX_WAVES][STAGE];
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int j = lane & 31, h = lane >> 5;
@@ -333,7 +443,8 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     const uint8_t *wr = PAIR ? (j < 16 ? W : W2) + (int64_t)min(row0 + (j & 15), n - 1) * row_bytes
                              : W + (int64_t)min(row0 + j, n - 1) * row_bytes;
     const int p0 = part * nb / sp.splits, np = (part + 1) * nb / sp.splits - p0;  // this workgroup's blocks
-    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : 210;
+    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 8 * 34;
+    constexpr bool Q80 = TYPE == TYPE_Q8_0;  // Q8_0 activations: no 16-value sums, a d per 32 values
     uint8_t *st = xs[wave];
     // this lane's share of a block's activations: MR / 4 code chunks (row 4q +
     // lane / 16, chunk lane % 16) and a sums chunk (row lane / 2, half lane % 2);
@@ -354,12 +465,13 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
         for (int q = 0; q < MR / 4; q++)
             if (q == 0 || 4 * q + (lane >> 4) < m)
                 x.c[q] = *reinterpret_cast<const i32x4v *>(xc + (int64_t)(4 * q) * k + 256 * b);
-        x.s = *reinterpret_cast<const i32x4v *>(xsum + 16 * b);
+        if constexpr (!Q80) x.s = *reinterpret_cast<const i32x4v *>(xsum + 16 * b);
     };
     auto write_x = [&](const MxX<MR> &x) {
 #pragma unroll
         for (int q = 0; q < MR / 4; q++) *reinterpret_cast<i32x4v *>(st + wo[q]) = x.c[q];
-        if (sl) *reinterpret_cast<i32x4v *>(st + so) = x.s;
+        if constexpr (!Q80)
+            if (sl) *reinterpret_cast<i32x4v *>(st + so) = x.s;
     };
     // A-operand reads: row ra (A rows past m read row m - 1), chunk 2s + h
     const int ra = min(j, m - 1);
@@ -387,16 +499,20 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     const bool any = cnt > 0;
     MxW<TYPE> rw[2];
     MxX<MR> xr[2];
-    auto load_w = [&](int b, MxW<TYPE> &dst) { mx_load_w<TYPE>(wr + (int64_t)b * BYTES, h, dst); };
+    // Q6_K blocks are 2-byte aligned: aligned reads and funnel shifts where the
+    // registers allow (up to 16 activation rows)
+    constexpr bool AL6 = TYPE == TYPE_Q6_K && MR <= 16;
+    auto load_w = [&](int b, MxW<TYPE> &dst) { mx_load_w<TYPE, AL6>(wr + (int64_t)b * BYTES, h, dst); };
     if (any) {
         load_x(blk(0), xr[0]);
         load_x(blk(1), xr[1]);
         load_w(blk(0), rw[0]);
         write_x(xr[0]);
     }
-    for (int q = p0 * MR + t; q < (p0 + np) * MR; q += 64 * MX_WAVES) {
+    constexpr int DB = Q80 ? 8 : 1;  // activation d values per 256-value block and row
+    for (int q = DB * p0 * MR + t; q < DB * (p0 + np) * MR; q += 64 * MX_WAVES) {
         const int b = q / MR, i = q % MR;
-        sdx[q] = i < m ? act.xd[(int64_t)i * nb + b] : 0.f;
+        sdx[q] = i < m ? act.xd[(int64_t)i * (DB * nb) + b] : 0.f;
     }
     __syncthreads();  // sdx (each wave's first stage is its own)
     if (any) {
@@ -406,7 +522,8 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
                 // xr[1 - q] holds slot i + q + 1 (loaded a block ago); xr[q] takes i + q + 2
                 load_x(blk(i + q + 2), xr[q]);
                 load_w(blk(i + q + 1), rw[1 - q]);
-                if constexpr (TYPE == TYPE_Q6_K) mx_block6<E>(rw[q], st, xo6, ro[8], h, sdx + MR * blk(i + q), acc);
+                if constexpr (Q80) mx_block8<MR>(rw[q], st, ro, h, sdx + DB * MR * blk(i + q), acc);
+                else if constexpr (TYPE == TYPE_Q6_K) mx_block6<E, AL6>(rw[q], st, xo6, ro[8], h, sdx + MR * blk(i + q), acc);
                 else mx_block<TYPE, (MX_WAVES > 4), E>(rw[q], st, ro, h, sdx + MR * blk(i + q), acc);
                 if (i + q == il) break;
                 write_x(xr[1 - q]);  // after this block's stage reads (the MFMAs consumed them)
@@ -537,6 +654,16 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // m = 32 29.4 -> 31.1, the 128256-row head m = 8 / 16 128.7 / 159.9 -> 151.5 /
     // 167.6): sixteen MFMAs per block and a scaled sum per group and output.
     if (tuning().gemv_mx_off) return false;
+    if (type == TYPE_Q8_0) {
+        // m = 5..16 from 1024 rows, k % 256 == 0 (eight blocks per step), against
+        // the multi-row decode kernel and the fp16 GEMM (4096 x 4096 m = 5 / 8 / 16
+        // 13.8 / 15.7 / 19.0 -> 13.0 / 13.1 / 14.2 us, 14336 x 4096 m = 8 / 16 31.8 /
+        // 40.7 -> 26.3 / 29.5, 4096 x 14336 m = 16 42.3 -> 28.6); past 16 rows the
+        // 32-row stage would take the kernel past 256 registers
+        if (k % 256 || k / 256 > 64 || m < 2 || m > 16 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+        if (tuning().gemv_mx_all) return true;
+        return m >= 5 && n >= 1024 && (m <= 8 || !tuning().gemv_mx_wide_off);
+    }
     if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K) return false;
     if (k % 256 || k / 256 > 64 || m < 2 || m > 64 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
     if (type == TYPE_Q6_K && (k / 256 <= 32 || m == 2) && !tuning().gemv_mx_all) return false;
@@ -597,26 +724,46 @@ template <typename F>
 static void mx_typed(int type, F &&f) {
     if (type == TYPE_Q4_K) f(std::integral_constant<int, TYPE_Q4_K>{});
     else if (type == TYPE_Q5_K) f(std::integral_constant<int, TYPE_Q5_K>{});
-    else f(std::integral_constant<int, TYPE_Q6_K>{});
+    else if (type == TYPE_Q6_K) f(std::integral_constant<int, TYPE_Q6_K>{});
+    else f(std::integral_constant<int, TYPE_Q8_0>{});
+}
+
+// The activation view a launch of `type` reads: Q8_K codes, d per 256 values and
+// 16-value sums; Q8_0 codes and d per 32 values.
+static bool mx_act_ok(int type, const ActView &act, int64_t k) {
+    const int64_t nb = type == TYPE_Q8_0 ? k / 32 : k / 256;
+    return act.k == k && act.nb == nb && act.xq && act.xd && (type == TYPE_Q8_0 || act.xbs);
+}
+// LDS for the activation scales of a launch (see mx_workgroup)
+static size_t mx_lds(int type, int64_t k, int m) {
+    return (size_t)(k / 256) * (type == TYPE_Q8_0 ? 8 : 1) * mx_rows(m) * sizeof(float);
 }
 
 template <int TYPE, int WAVES, bool PAIR>
 static void mx_launch(int m, unsigned grid, size_t lds, hipStream_t st, const uint8_t *w, int64_t row_bytes, int n,
                       int nb, const ActView &act, float *y, const MxSplit &sp, const uint8_t *w2, int nwg) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(w, row_bytes, n, nb, act, m, y, sp, w2, nwg); };
-    if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
-        if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
+    if constexpr (TYPE == TYPE_Q8_0) {  // (m <= 16: gemv_mx_serves)
+        if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
+        else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
+    } else {
+        if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
+            if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
+        }
+        if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
+        else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
+        else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
     }
-    if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
-    else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
-    else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
 }
 
 template <int TYPE, int WAVES>
 static void mx_seg_launch(int m, unsigned grid, size_t lds, hipStream_t st, int64_t row_bytes, int nb,
                           const ActView &act, const MxSegs &g) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(row_bytes, nb, act, m, g); };
-    if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
+    if constexpr (TYPE == TYPE_Q8_0) {  // (m <= 16: gemv_mx_serves)
+        if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
+        else go(k_gemv_mx_seg<TYPE, WAVES, 8>);
+    } else if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
     else if (m > 16) go(k_gemv_mx_seg<TYPE, WAVES, 32>);
     else if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
     else go(k_gemv_mx_seg<TYPE, WAVES, 8>);
@@ -626,7 +773,7 @@ hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, co
                                 int64_t row_bytes, const ActView &act, int m, float *const *y, hipStream_t st) {
     if (count < 2 || count > 4) return hipErrorNotSupported;
     const int nb = (int)(k / 256);
-    if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
+    if (!mx_act_ok(type, act, k)) return hipErrorInvalidValue;
     MxSegs g{};
     int waves = 0, wg = 0;
     for (int i = 0; i < count; i++) {
@@ -646,7 +793,7 @@ hipError_t launch_gemv_mx_group(int type, int count, const uint8_t *const *w, co
         g.wg_end[i] = wg;
     }
     g.count = count;
-    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
+    const size_t lds = mx_lds(type, k, m);
     const unsigned grid = mx_grid(wg, m);
     mx_typed(type, [&](auto T) {
         if (waves == 8) mx_seg_launch<T.value, 8>(m, grid, lds, st, row_bytes, nb, act, g);
@@ -666,10 +813,10 @@ hipError_t launch_gemv_mx_pair(int type, const uint8_t *w_gate, const uint8_t *w
                                int64_t row_bytes, const ActView &act, int m, float *out, hipStream_t st) {
     if (!gemv_mx_pair_serves(type, n, k, m)) return hipErrorNotSupported;
     const int nb = (int)(k / 256);
-    if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
+    if (!mx_act_ok(type, act, k)) return hipErrorInvalidValue;
     const MxSplit sp{1, nullptr, nullptr, 0};
     const int nwg = (int)((n + 15) / 16);
-    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
+    const size_t lds = mx_lds(type, k, m);
     mx_typed(type, [&](auto T) {
         mx_launch<T.value, 4, true>(m, mx_grid(nwg, m), lds, st, w_gate, row_bytes, (int)n, nb, act, out, sp, w_up, nwg);
     });
@@ -680,7 +827,7 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
                           float *y, float *ws, uint32_t *counters, hipStream_t st, bool y_zeroed) {
     if (!gemv_mx_serves(type, n, k, m)) return hipErrorNotSupported;
     const int nb = (int)(k / 256);
-    if (act.k != k || act.nb != nb || !act.xq || !act.xd || !act.xbs) return hipErrorInvalidValue;
+    if (!mx_act_ok(type, act, k)) return hipErrorInvalidValue;
     MxSplit sp{mx_splits(n, k, m), ws, counters, 0};
     sp.add = sp.splits == 2 && y_zeroed;
     if (sp.splits > 1 && !sp.add && (!ws || !counters)) return hipErrorInvalidValue;
@@ -691,7 +838,7 @@ hipError_t launch_gemv_mx(int type, const uint8_t *w, int64_t n, int64_t k, int6
     // (4096 x 14336 m = 4: 21.8 -> 19.5 us; 4096 x 4096 m = 8: 12.9 -> 12.4).  With
     // more workgroups, four waves (14336 x 4096 m = 8: 16.9 at four, 18.7 at eight).
     const bool w8 = tuning().gemv_mx_waves ? tuning().gemv_mx_waves == 8 : (int64_t)grid <= (int64_t)num_cus();
-    const size_t lds = (size_t)nb * mx_rows(m) * sizeof(float);
+    const size_t lds = mx_lds(type, k, m);
     mx_typed(type, [&](auto T) {
         if (w8) mx_launch<T.value, 8, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);
         else mx_launch<T.value, 4, false>(m, grid, lds, st, w, row_bytes, (int)n, nb, act, y, sp, nullptr, nwg);

@@ -1,7 +1,7 @@
 """Batch decode on the matrix cores (k_gemv_mx: Q4_K / Q5_K at m = 5..64 with
 n >= 1024 -- m = 33..64 as two 32-row halves -- and m = 2..8 at k > 8192; Q6_K on
-the same shapes at k > 8192 only, and through LBQ_GEMV_MX_ALL at any k) against
-the oracle.
+the same shapes at k > 8192 only; Q8_0 at m = 9..16 from 1024 rows; and through
+LBQ_GEMV_MX_ALL wherever the kernel can run) against the oracle.
 
 The kernel forms the reference's integer sub-block sums exactly (i8 MFMA) and
 the mins term exactly (f16 MFMA of integers below 2^24), so it is held to the
@@ -17,7 +17,7 @@ import pytest
 
 import blockpack as bp
 from test_gpu_nonfinite import _nan_rows, _poison
-from test_gpu_parity import Q4_K, Q5_K, Q6_K, assert_rows_close, gpu_qmatmul
+from test_gpu_parity import Q4_K, Q5_K, Q6_K, Q8_0, assert_rows_close, gpu_qmatmul
 from test_gpu_q8_0_dense import forward_with_env
 
 pytestmark = pytest.mark.gpu
@@ -460,3 +460,114 @@ def test_mx_rmsnorm_in_quantisation(oracle, lbq, dev, t, m):
     gr = oracle.qmatmul(t, g_raw, n, k, xn, nthreads=8).astype(np.float64)
     ur = oracle.qmatmul(t, u_raw, n, k, xn, nthreads=8).astype(np.float64)
     assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, 2e-3)
+
+
+# Q8_0 (m = 9..16 from 1024 rows, k % 256 == 0): eight 34-byte blocks per step, one
+# v_mfma_i32_32x32x32_i8 per block, (sum * d_w) * d_x in f32 -- the decode bound
+Q80_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (8224, 1024), (4096, 14336), (1024, 16384)]
+
+
+@pytest.mark.parametrize("n,k", Q80_SHAPES)
+@pytest.mark.parametrize("m", [9, 12, 16])
+def test_mx_q8_0_matches_oracle(oracle, lbq, dev, n, k, m, monkeypatch):
+    rng = np.random.default_rng(n * 11 + k + 43 * m)
+    w_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx q8_0 n={n} k={k} m={m}", flush=True)
+    y = gpu_qmatmul(Q8_0, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(Q8_0, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    again = gpu_qmatmul(Q8_0, w_raw, n, k, x, dev)
+    assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
+    off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_WIDE_OFF": "1"}, Q8_0, w_raw, n, k, x, dev)
+    assert_rows_close(off, ref, 2e-3)
+    assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (2050, 2048), (64, 14336), (96, 16384)])
+@pytest.mark.parametrize("m", [2, 5, 8])
+def test_mx_q8_0_small_m_forced(oracle, lbq, dev, n, k, m, monkeypatch):
+    # Q8_0 at m <= 4 or below 1024 rows stays on the decode kernels;
+    # LBQ_GEMV_MX_ALL runs the 8-row form there
+    rng = np.random.default_rng(n + k + 59 * m)
+    w_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    print(f"mx q8_0 forced n={n} k={k} m={m}", flush=True)
+    y = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_ALL": "1"}, Q8_0, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(Q8_0, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    same = np.array_equal(gpu_qmatmul(Q8_0, w_raw, n, k, x, dev).view(np.uint32), y.view(np.uint32))
+    assert same == (m >= 5 and n >= 1024)  # (the kernel is Q8_0's default there)
+
+
+@pytest.mark.parametrize("m", [9, 16])
+def test_mx_q8_0_extremes_and_nonfinite(oracle, lbq, dev, m):
+    # codes at -128 / 127 against activations of one magnitude (codes +-127): the
+    # int32 block sums stay exact; then NaN / +-Inf block scales in a few rows
+    rng = np.random.default_rng(1010 + m)
+    n, k = 1024, 4096
+    blocks = np.zeros((n * k // 32, 34), dtype=np.uint8)
+    blocks[:, 2:] = rng.choice(np.array([0x80, 0x7f], dtype=np.uint8), size=(blocks.shape[0], 32))
+    blocks[:, :2] = (rng.standard_normal(blocks.shape[0]) * 1e-3).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    w_raw = blocks.reshape(-1)
+    x = (np.where(rng.random((m, k)) < 0.5, -100.0, 100.0)).astype(np.float32)
+    y = gpu_qmatmul(Q8_0, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(Q8_0, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    w2 = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    bad, nan_rows = _poison(w2, Q8_0, n, k // 32, rng)
+    good = np.setdiff1d(np.arange(n), bad)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = gpu_qmatmul(Q8_0, w2, n, k, x, dev)
+    ref = oracle.qmatmul(Q8_0, w2, n, k, x, nthreads=8).astype(np.float64)
+    assert np.array_equal(np.isfinite(y), np.isfinite(ref))
+    assert np.isnan(y[:, nan_rows]).all()
+    assert_rows_close(y[:, good], ref[:, good], 1e-4)
+    xn = _nan_rows(rng, m, k)
+    y = gpu_qmatmul(Q8_0, w_raw, n, k, xn, dev)
+    ref = oracle.qmatmul(Q8_0, w_raw, n, k, xn, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (12, 2080, 2048), (9, 1024, 14336)])
+def test_mx_q8_0_split_and_group_bits(oracle, lbq, dev, m, n, k):
+    # two-way split tiles: forward() (y zeroed by the Q8_0 quantisation launch, halves
+    # added atomically), the pre-quantised handle (partials and a tile counter) and a
+    # grouped call (one quantisation, one launch) give the same bits
+    import torch
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor, qmatmul_group
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(1020 + m + n + k)
+    raws = [bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3) for _ in range(2)]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), Q8_0, (n, k))) for r in raws]
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xd = to_dev(x, dev)
+    y = qms[0].forward(xd)
+    y2 = qms[0].forward_quantized(QActivation.for_weight(qms[0], m).quantize(xd))
+    yg = qmatmul_group(qms, xd)
+    y1b = qms[1].forward(xd)
+    torch.cuda.synchronize()
+    ref = oracle.qmatmul(Q8_0, raws[0], n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y.cpu().numpy(), ref, 1e-4)
+    bits = lambda a: a.cpu().numpy().view(np.uint32)
+    assert np.array_equal(bits(y), bits(y2))
+    assert np.array_equal(bits(y), bits(yg[0]))
+    assert np.array_equal(bits(y1b), bits(yg[1]))
+
+
+@pytest.mark.parametrize("m", [9, 16])
+def test_mx_q8_0_gate_up_pair(oracle, lbq, dev, m, monkeypatch):
+    # a Q8_0 gate/up pair above 8192 rows in one launch: the bits of the separate
+    # launches and the product launch, and the oracle's value
+    rng = np.random.default_rng(1030 + m)
+    n, k = 8240, 1024
+    g_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    u_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = _gate_up_env(monkeypatch, {}, Q8_0, g_raw, u_raw, n, k, x, dev)
+    off = _gate_up_env(monkeypatch, {"LBQ_GEMV_MX_PAIR_OFF": "1"}, Q8_0, g_raw, u_raw, n, k, x, dev)
+    assert np.array_equal(y.view(np.uint32), off.view(np.uint32))
+    gr = oracle.qmatmul(Q8_0, g_raw, n, k, x, nthreads=8).astype(np.float64)
+    ur = oracle.qmatmul(Q8_0, u_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, gr / (1.0 + np.exp(-gr)) * ur, 1e-4)
