@@ -630,8 +630,9 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
                                            "path": "f32 GEMV (m <= 8) / v_mfma_f32_32x32x2_f32 GEMM (fp32 peak 157.3 TFLOP/s)"}
         log(f"dense F16 M={M}: {us:.1f} us")
     del f16
-    # Q8_0 batched (prefill of the same weight): M = 16 on the integer matrix cores
-    # (Q8_0 activations, v_mfma_i32_32x32x32_i8), 64 and 512 on the fp16 MFMA GEMM
+    # Q8_0 batched (prefill of the same weight): M = 16 and 64 on the integer matrix
+    # cores (Q8_0 activations, v_mfma_i32_32x32x32_i8; 64 as two 32-row halves), 512 on
+    # the fp16 MFMA GEMM
     for M in (16, 64, 512):
         x = torch.randn(M, 4096, generator=gen, device=dev)
         us = timed_rot(q8, x, 20)
@@ -642,7 +643,7 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
                                        "weight_GB/s": round(wb / us / 1e3, 1),
                                        "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
                                        "path": ("Q8_0 quantisation, then the integer matrix-core kernel (v_mfma_i32_32x32x32_i8, "
-                                                "the reference's integer block sums)" if M <= 16 else
+                                                "the reference's integer block sums)" if M <= 64 else
                                                 "MFMA (fp16 operands of the Q8_0 activation and d*q weight values)")}
         log(f"configs[0] Q8_0 M={M}: {us:.1f} us")
     del q8

@@ -142,7 +142,8 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  *   - m <= 8, Q4_K/Q5_K weights of 1024 rows or more up to m = 32 (and
  *     m = 33..64 up to 8192 rows, as two 32-row halves), Q6_K weights with
  *     k > 8192 on the same shapes, and Q8_0 weights of 1024 rows or more
- *     (k % 256 == 0) up to m = 16: each output from integer sub-block dot
+ *     (k % 256 == 0) up to m = 32 (m = 33..64 as halves at k <= 8192 up to 8192
+ *     rows): each output from integer sub-block dot
  *     products as in the reference (f32 combine; only the summation order
  *     differs, ~1e-7 relative);
  *   - m > 8 otherwise, for every quantised type when k % 256 == 0 (Q4_0, Q4_1,

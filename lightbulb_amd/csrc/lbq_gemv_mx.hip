@@ -586,9 +586,10 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     if (t == 0) __hip_atomic_store(sp.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Q6_K's 32-row stage kernels: two waves per SIMD (at most 256 registers), which
-// the register allocator would otherwise give up for a few registers more
-#define MX_MIN_WAVES(TYPE) ((TYPE) == TYPE_Q6_K ? 2 : 1)
+// Q6_K's and Q8_0's 32-row stage kernels: two waves per SIMD (at most 256
+// registers), which the register allocator would otherwise give up for a few
+// registers more
+#define MX_MIN_WAVES(TYPE) ((TYPE) == TYPE_Q6_K || (TYPE) == TYPE_Q8_0 ? 2 : 1)
 
 template <int TYPE, int MX_WAVES, int MR, bool PAIR = false, bool HALVES = false>
 __global__ __launch_bounds__(64 * MX_WAVES) __attribute__((amdgpu_waves_per_eu(MX_MIN_WAVES(TYPE))))
@@ -655,12 +656,18 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // 167.6): sixteen MFMAs per block and a scaled sum per group and output.
     if (tuning().gemv_mx_off) return false;
     if (type == TYPE_Q8_0) {
-        // m = 5..16 from 1024 rows, k % 256 == 0 (eight blocks per step), against
-        // the multi-row decode kernel and the fp16 GEMM (4096 x 4096 m = 5 / 8 / 16
-        // 13.8 / 15.7 / 19.0 -> 13.0 / 13.1 / 14.2 us, 14336 x 4096 m = 8 / 16 31.8 /
-        // 40.7 -> 26.3 / 29.5, 4096 x 14336 m = 16 42.3 -> 28.6); past 16 rows the
-        // 32-row stage would take the kernel past 256 registers
-        if (k % 256 || k / 256 > 64 || m < 2 || m > 16 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+        // m = 5..32 from 1024 rows, k % 256 == 0 (eight blocks per step), against
+        // the multi-row decode kernel and the fp16 GEMM (4096 x 4096 m = 5 / 8 / 16 /
+        // 32 13.8 / 15.7 / 19.0 / 20.7 -> 13.0 / 13.1 / 14.2 / 16.8 us, 14336 x 4096
+        // m = 8 / 16 / 32 31.8 / 40.7 / 42.8 -> 26.3 / 29.5 / 34.4, 4096 x 14336 m =
+        // 16 / 32 42.3 / 44.4 -> 28.6 / 33.5; m = 3 / 4: 9.8 / 10.0 -> 12.6 / 12.9),
+        // and m = 33..64 as row halves at k <= 8192 (4096 x 4096 m = 48 / 64 23.4 /
+        // 25.1 -> 21.2 / 22.5, 1024 x 4096 m = 64 20.6 -> 15.6; 4096 x 14336 m = 64
+        // 53.2 -> 56.0)
+        if (k % 256 || k / 256 > 64 || m < 2 || m > 64 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+        if (m > 32)
+            return (k <= 8192 || tuning().gemv_mx_all) && !tuning().gemv_mx_halves_off &&
+                   !tuning().gemv_mx_wide_off && n >= 1024 && (n + 31) / 32 * mx_splits(n, k, 32) <= (int64_t)num_cus();
         if (tuning().gemv_mx_all) return true;
         return m >= 5 && n >= 1024 && (m <= 8 || !tuning().gemv_mx_wide_off);
     }
@@ -743,27 +750,19 @@ template <int TYPE, int WAVES, bool PAIR>
 static void mx_launch(int m, unsigned grid, size_t lds, hipStream_t st, const uint8_t *w, int64_t row_bytes, int n,
                       int nb, const ActView &act, float *y, const MxSplit &sp, const uint8_t *w2, int nwg) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(w, row_bytes, n, nb, act, m, y, sp, w2, nwg); };
-    if constexpr (TYPE == TYPE_Q8_0) {  // (m <= 16: gemv_mx_serves)
-        if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
-        else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
-    } else {
-        if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
-            if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
-        }
-        if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
-        else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
-        else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
+    if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
+        if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
     }
+    if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
+    else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
+    else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
 }
 
 template <int TYPE, int WAVES>
 static void mx_seg_launch(int m, unsigned grid, size_t lds, hipStream_t st, int64_t row_bytes, int nb,
                           const ActView &act, const MxSegs &g) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(row_bytes, nb, act, m, g); };
-    if constexpr (TYPE == TYPE_Q8_0) {  // (m <= 16: gemv_mx_serves)
-        if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
-        else go(k_gemv_mx_seg<TYPE, WAVES, 8>);
-    } else if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
+    if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
     else if (m > 16) go(k_gemv_mx_seg<TYPE, WAVES, 32>);
     else if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
     else go(k_gemv_mx_seg<TYPE, WAVES, 8>);

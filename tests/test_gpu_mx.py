@@ -462,13 +462,14 @@ def test_mx_rmsnorm_in_quantisation(oracle, lbq, dev, t, m):
     assert_rows_close(out.cpu().numpy(), gr / (1.0 + np.exp(-gr)) * ur, 2e-3)
 
 
-# Q8_0 (m = 9..16 from 1024 rows, k % 256 == 0): eight 34-byte blocks per step, one
-# v_mfma_i32_32x32x32_i8 per block, (sum * d_w) * d_x in f32 -- the decode bound
+# Q8_0 (m = 5..32 from 1024 rows, m = 33..64 as row halves at k <= 8192; k % 256 ==
+# 0): eight 34-byte blocks per step, one v_mfma_i32_32x32x32_i8 per block,
+# (sum * d_w) * d_x in f32 -- the decode bound
 Q80_SHAPES = [(4096, 4096), (1056, 4096), (4100, 1280), (8224, 1024), (4096, 14336), (1024, 16384)]
 
 
-@pytest.mark.parametrize("n,k", Q80_SHAPES)
-@pytest.mark.parametrize("m", [9, 12, 16])
+@pytest.mark.parametrize("n,k,m", [(n, k, m) for (n, k) in Q80_SHAPES for m in (9, 12, 16, 17, 32, 40, 64)
+                                   if m <= 32 or (k <= 8192 and n <= 8192)])
 def test_mx_q8_0_matches_oracle(oracle, lbq, dev, n, k, m, monkeypatch):
     rng = np.random.default_rng(n * 11 + k + 43 * m)
     w_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
@@ -483,6 +484,21 @@ def test_mx_q8_0_matches_oracle(oracle, lbq, dev, n, k, m, monkeypatch):
     off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_WIDE_OFF": "1"}, Q8_0, w_raw, n, k, x, dev)
     assert_rows_close(off, ref, 2e-3)
     assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [40, 64])
+def test_mx_q8_0_halves_are_two_launches(lbq, dev, m, monkeypatch):
+    # each 32-row half is the m <= 32 launch over its rows (the wave count pinned)
+    rng = np.random.default_rng(1040 + m)
+    n, k = 4096, 2048
+    w_raw = bp.random_blocks(rng, Q8_0, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    env = {"LBQ_GEMV_MX_WAVES": "4", "LBQ_GEMV_MX_ALL": "1"}
+    y = forward_with_env(monkeypatch, env, Q8_0, w_raw, n, k, x, dev)
+    lo = forward_with_env(monkeypatch, env, Q8_0, w_raw, n, k, np.ascontiguousarray(x[:32]), dev)
+    hi = forward_with_env(monkeypatch, env, Q8_0, w_raw, n, k, np.ascontiguousarray(x[32:]), dev)
+    assert np.array_equal(y[:32].view(np.uint32), lo.view(np.uint32))
+    assert np.array_equal(y[32:].view(np.uint32), hi.view(np.uint32))
 
 
 @pytest.mark.parametrize("n,k", [(4096, 4096), (2050, 2048), (64, 14336), (96, 16384)])
@@ -501,7 +517,7 @@ def test_mx_q8_0_small_m_forced(oracle, lbq, dev, n, k, m, monkeypatch):
     assert same == (m >= 5 and n >= 1024)  # (the kernel is Q8_0's default there)
 
 
-@pytest.mark.parametrize("m", [9, 16])
+@pytest.mark.parametrize("m", [9, 16, 32])
 def test_mx_q8_0_extremes_and_nonfinite(oracle, lbq, dev, m):
     # codes at -128 / 127 against activations of one magnitude (codes +-127): the
     # int32 block sums stay exact; then NaN / +-Inf block scales in a few rows
@@ -530,7 +546,8 @@ def test_mx_q8_0_extremes_and_nonfinite(oracle, lbq, dev, m):
     assert_rows_close(y, ref, 1e-4)
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (12, 2080, 2048), (9, 1024, 14336)])
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (12, 2080, 2048), (9, 1024, 14336), (32, 2048, 4096),
+                                   (64, 4096, 2048)])
 def test_mx_q8_0_split_and_group_bits(oracle, lbq, dev, m, n, k):
     # two-way split tiles: forward() (y zeroed by the Q8_0 quantisation launch, halves
     # added atomically), the pre-quantised handle (partials and a tile counter) and a
@@ -556,7 +573,7 @@ def test_mx_q8_0_split_and_group_bits(oracle, lbq, dev, m, n, k):
     assert np.array_equal(bits(y1b), bits(yg[1]))
 
 
-@pytest.mark.parametrize("m", [9, 16])
+@pytest.mark.parametrize("m", [9, 16, 32])
 def test_mx_q8_0_gate_up_pair(oracle, lbq, dev, m, monkeypatch):
     # a Q8_0 gate/up pair above 8192 rows in one launch: the bits of the separate
     # launches and the product launch, and the oracle's value
