@@ -16,7 +16,7 @@
 // the Q8_K 16-value sums) is one v_mfma_f32_32x32x16_f16 per block with each
 // bsum split as 64*hi + lo (|hi| <= 64, 0 <= lo < 64) against (64*m_s, m_s):
 // every operand and partial sum is an integer below 2^24, so it is exact too.
-// The block then adds d*dx*isum - dmin*dx*msum in f32, as the decode GEMV does.
+// The block then adds dx * (d*isum - dmin*msum) in f32.
 // Where the multi-row decode kernel re-does its 16 sdot4 per 64 weights for every
 // activation row, the matrix core does all rows at once: its MFMA work per weight
 // does not grow with m (up to the tile's 32 rows), only the per-row scaling does.
@@ -161,7 +161,12 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, 
         const i32x16v o = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[s], bw, zero, 0, 0, 0);
         const int sc = (int)(((s < 4 ? sc03 : sc47) >> (8 * (s & 3))) & 0xffu);
 #pragma unroll
-        for (int e = 0; e < E; e++) isum[e] += __mul24(sc, o[e]);
+        for (int e = 0; e < E; e++) {
+            // one v_mad_i32_i24 per sum (the empty asm keeps the compiler from
+            // pairing products into mul + add3: 264 -> 232 VALU per block at E = 8)
+            isum[e] += __mul24(sc, o[e]);
+            asm volatile("" : "+v"(isum[e]));
+        }
     }
     // mins: sub-blocks 4h + t of the lane half (k slots 8h + 2t, 8h + 2t + 1)
     const uint32_t mm = h ? m47 : m03;
@@ -183,8 +188,7 @@ __device__ __forceinline__ void mx_block(const MxW<TYPE> &r, const uint8_t *st, 
 #pragma unroll
     for (int e = 0; e < E; e++) {
         const float dx = sdx[mx_row(e, h)];
-        acc[e] = fmaf(d * dx, (float)isum[e], acc[e]);
-        acc[e] = fmaf(-(dmin * dx), ms[e], acc[e]);
+        acc[e] = fmaf(dx, fmaf(d, (float)isum[e], -(dmin * ms[e])), acc[e]);
     }
 }
 
