@@ -648,8 +648,9 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
         log(f"configs[0] Q8_0 M={M}: {us:.1f} us")
     del q8
     torch.cuda.empty_cache()
-    # the 32-value legacy types on the same MFMA path (not BASELINE configs: the GGUF
-    # files the reference's own tests serve, e.g. a Q4_0 TinyLlama, prefill this way)
+    # the 32-value legacy types (not BASELINE configs: the GGUF files the reference's own
+    # tests serve, e.g. a Q4_0 TinyLlama): M = 16 on the integer matrix cores, 512 on the
+    # fp16 MFMA GEMM
     for t, tname in ((qz.GgmlDType.Q4_0, "q4_0"), (qz.GgmlDType.Q4_1, "q4_1"), (qz.GgmlDType.Q5_0, "q5_0"),
                      (qz.GgmlDType.Q5_1, "q5_1")):
         bpb = {qz.GgmlDType.Q4_0: 18, qz.GgmlDType.Q4_1: 20, qz.GgmlDType.Q5_0: 22, qz.GgmlDType.Q5_1: 24}[t]
@@ -663,7 +664,10 @@ def configs_bench(torch, qz, gen, dev, stream, prefill=None):
                                               "working_set_MB": ws_mb(qms),
                                               "frac_bf16_peak": round(fl / us / 1e6 / BF16_PEAK_TFLOPS, 4),
                                               "weight_GB/s": round(lb / us / 1e3, 1),
-                                              "frac_hbm": round(lb / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                              "frac_hbm": round(lb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                              "path": ("activation quantisation, then the integer matrix-core kernel "
+                                                       "(v_mfma_i32_32x32x32_i8, the reference's integer block sums)"
+                                                       if M <= 16 else "MFMA (fp16 operands)")}
         log(f"{tname}: M=16 {out[f'{tname}_4096x4096_m16']['us']} us, M=512 {out[f'{tname}_4096x4096_m512']['us']} us")
         del qms
     torch.cuda.empty_cache()

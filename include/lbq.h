@@ -141,16 +141,17 @@ int lbq_weight_info(const lbq_weight *w, uint32_t *ggml_type, int64_t *n, int64_
  * Arithmetic by (type, m):
  *   - m <= 8, Q4_K/Q5_K weights of 1024 rows or more up to m = 32 (and
  *     m = 33..64 up to 8192 rows, as two 32-row halves), Q6_K weights with
- *     k > 8192 on the same shapes, and Q8_0 weights of 1024 rows or more
+ *     k > 8192 on the same shapes, Q8_0 weights of 1024 rows or more
  *     (k % 256 == 0) up to m = 32 (m = 33..64 as halves at k <= 8192 up to 8192
- *     rows): each output from integer sub-block dot
+ *     rows), and Q4_0/Q4_1/Q5_0/Q5_1 weights of 1024 rows or more (k % 256 == 0)
+ *     up to m = 16: each output from integer sub-block dot
  *     products as in the reference (f32 combine; only the summation order
  *     differs, ~1e-7 relative);
  *   - m > 8 otherwise, for every quantised type when k % 256 == 0 (Q4_0, Q4_1,
  *     Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K): MFMA on fp16 roundings of
  *     the same activation and weight values (about 4e-4 relative on a row);
  *   - m > 8 with k % 256 != 0: the integer GEMV over chunks of 8 rows.
- * Where the matrix-core decode kernel (Q4_K/Q5_K/Q6_K/Q8_0, m = 2..64) splits a 32-row
+ * Where the matrix-core decode kernel (m = 2..64) splits a 32-row
  * tile between two workgroups, their halves are added into y with f32 atomic
  * adds when y is plain device memory (hipMalloc; checked once per allocation),
  * else through partial sums in the workspace; either way y = a + b for the two

@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256) void k_embed_dense(const uint8_t *__restrict__
 hipError_t launch_quant_act(int act_type, const float *x, int64_t m, int64_t k, int8_t *xq, float *xd, int16_t *xbs,
                             float *xs, uint8_t *gguf, hipStream_t st, const ZeroList *zero) {
     const ZeroList zl = zero ? *zero : ZeroList{};
-    if (zl.count && act_type != TYPE_Q8_K && act_type != TYPE_Q8_0) return hipErrorInvalidValue;
+    if (zl.count && act_type != TYPE_Q8_K && act_type != TYPE_Q8_0 && act_type != TYPE_Q8_1) return hipErrorInvalidValue;
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (act_type == TYPE_Q8_K) {
         const int64_t nb = m * (k / QK_K);

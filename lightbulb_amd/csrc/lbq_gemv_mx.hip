@@ -79,9 +79,50 @@ template <>
 struct MxW<TYPE_Q8_0> {
     uint32_t c[8][4], x[4];
 };
+// The legacy 32-value types (ggml block_q4_0 / q4_1 / q5_0 / q5_1), eight blocks
+// per step: a step starts 16-byte aligned (8 x 18 / 20 / 22 / 24 bytes), and both
+// lane halves of a row read each block's 16 code bytes (half h takes nibble h:
+// values 16h .. 16h + 15).  Raw aligned dwords per block (mx_block_leg decodes):
+//   Q4_0 (18 B at 18 s): even s: the 16 bytes at 18 s and the dword after (d,
+//     codes 2..17 bytes in, the next block's d); odd s: the 16 codes at 18 s + 2
+//   Q4_1 (20 B): the codes at 20 s + 4, and d | m << 16 (w[4])
+//   Q5_0 (22 B): six dwords from 22 s (even s; codes and qh 2 bytes past
+//     alignment) or from 22 s - 2 (odd s; d in the high half of the first)
+//   Q5_1 (24 B): six dwords d | m << 16, qh, codes
+struct MxWL {
+    uint32_t w[8][6];
+};
+template <> struct MxW<TYPE_Q4_0> : MxWL {};
+template <> struct MxW<TYPE_Q4_1> : MxWL {};
+template <> struct MxW<TYPE_Q5_0> : MxWL {};
+template <> struct MxW<TYPE_Q5_1> : MxWL {};
+constexpr bool mx_legacy(int t) { return t == TYPE_Q4_0 || t == TYPE_Q4_1 || t == TYPE_Q5_0 || t == TYPE_Q5_1; }
 template <int TYPE, bool AL = false>
 __device__ __forceinline__ void mx_load_w(const uint8_t *blk, int h, MxW<TYPE> &r) {
-    if constexpr (TYPE == TYPE_Q8_0) {
+    if constexpr (mx_legacy(TYPE)) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(blk);
+        auto ld4 = [&](uintptr_t p, uint32_t *v) {
+            const u32x4a4 q = gld16((gbytes_c)p);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        };
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            uint32_t *w = r.w[s];
+            if constexpr (TYPE == TYPE_Q4_0) {
+                ld4(a + 18 * s + (s & 1 ? 2 : 0), w);
+                if (!(s & 1)) w[4] = gld4((gbytes_c)(a + 18 * s + 16));
+            } else if constexpr (TYPE == TYPE_Q4_1) {
+                w[4] = gld4((gbytes_c)(a + 20 * s));
+                ld4(a + 20 * s + 4, w);
+            } else {
+                constexpr int BS = TYPE == TYPE_Q5_0 ? 22 : 24;
+                const uintptr_t p = a + BS * s - (TYPE == TYPE_Q5_0 && (s & 1) ? 2 : 0);
+                ld4(p, w);
+                w[4] = gld4((gbytes_c)(p + 16));
+                w[5] = gld4((gbytes_c)(p + 20));
+            }
+        }
+    } else if constexpr (TYPE == TYPE_Q8_0) {
         const uintptr_t a = reinterpret_cast<uintptr_t>(blk);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
@@ -364,6 +405,97 @@ __device__ __forceinline__ void mx_block8(const MxW<TYPE_Q8_0> &r, const uint8_t
     }
 }
 
+// Eight legacy blocks (candle-core 0.10.2 k_quants.rs vec_dot: BlockQ4_0 / BlockQ5_0
+// with BlockQ8_0, per block (sum of (q - 8 or 16) * y) as f32 * d_w * d_y;
+// BlockQ4_1 / BlockQ5_1 with BlockQ8_1, + m_w * s_y).  The codes enter the
+// v_mfma_i32_32x32x32_i8 as int8 (q - 8 / q - 16 formed bytewise: adding 0x78 /
+// 0x70 to a byte below 32 never carries, then flipping bit 7); the Q5 fifth bits
+// spread from qh to bit 4 of each byte by one multiply.  sdx / ssx: [8][MR] of
+// this step: the activation d and (Q8_1) s of block s and row i.
+template <int TYPE, int MR>
+__device__ __forceinline__ void mx_block_leg(const MxW<TYPE> &r, const uint8_t *st, const int *ro, int h,
+                                             const float *sdx, const float *ssx, float *acc) {
+    constexpr int E = MR / 2;
+    constexpr bool Q5 = TYPE == TYPE_Q5_0 || TYPE == TYPE_Q5_1, MIN = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
+    constexpr uint32_t OFS = TYPE == TYPE_Q4_0 ? 0x78787878u : TYPE == TYPE_Q5_0 ? 0x70707070u : 0u;
+    const i32x16v zero = {};
+    auto dot = [&](int s) {
+        const uint32_t *w = r.w[s];
+        uint32_t q[4], qh = 0;
+        if constexpr (TYPE == TYPE_Q4_0) {
+            if (s & 1) {
+                q[0] = w[0]; q[1] = w[1]; q[2] = w[2]; q[3] = w[3];
+            } else {
+                q[0] = __builtin_amdgcn_alignbit(w[1], w[0], 16);
+                q[1] = __builtin_amdgcn_alignbit(w[2], w[1], 16);
+                q[2] = __builtin_amdgcn_alignbit(w[3], w[2], 16);
+                q[3] = __builtin_amdgcn_alignbit(w[4], w[3], 16);
+            }
+        } else if constexpr (TYPE == TYPE_Q5_0) {
+            if (s & 1) {
+                qh = w[1];
+                q[0] = w[2]; q[1] = w[3]; q[2] = w[4]; q[3] = w[5];
+            } else {
+                qh = __builtin_amdgcn_alignbit(w[1], w[0], 16);
+                q[0] = __builtin_amdgcn_alignbit(w[2], w[1], 16);
+                q[1] = __builtin_amdgcn_alignbit(w[3], w[2], 16);
+                q[2] = __builtin_amdgcn_alignbit(w[4], w[3], 16);
+                q[3] = __builtin_amdgcn_alignbit(w[5], w[4], 16);
+            }
+        } else if constexpr (TYPE == TYPE_Q5_1) {
+            qh = w[1];
+            q[0] = w[2]; q[1] = w[3]; q[2] = w[4]; q[3] = w[5];
+        } else {
+            q[0] = w[0]; q[1] = w[1]; q[2] = w[2]; q[3] = w[3];
+        }
+        i32x4v bw;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            uint32_t b = (q[v] >> (4 * h)) & 0x0f0f0f0fu;
+            if constexpr (Q5) {
+                const uint32_t hb = (qh >> (16 * h + 4 * v)) & 0xfu;  // fifth bits of values 16h + 4v ..
+                b |= ((hb * 0x00204081u) & 0x01010101u) << 4;
+            }
+            if constexpr (OFS != 0u) b = (b + OFS) ^ 0x80808080u;
+            bw[v] = (int)b;
+        }
+        const i32x4v xa = *reinterpret_cast<const i32x4v *>(st + ro[s]);
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(xa, bw, zero, 0, 0, 0);
+    };
+    auto dm = [&](int s) -> uint32_t {  // d | m << 16 of block s (Q4_0, Q5_0: d only)
+        if constexpr (TYPE == TYPE_Q4_0) return s & 1 ? r.w[s - 1][4] >> 16 : r.w[s][0] & 0xffffu;
+        else if constexpr (TYPE == TYPE_Q5_0) return s & 1 ? r.w[s][0] >> 16 : r.w[s][0] & 0xffffu;
+        else if constexpr (TYPE == TYPE_Q4_1) return r.w[s][4];
+        else return r.w[s][0];
+    };
+    i32x16v o = dot(0);
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        i32x16v on;
+        if (s < 7) on = dot(s + 1);
+        const uint32_t dmv = dm(s);
+        const float dw = h2f(dmv & 0xffffu);
+#pragma unroll
+        for (int q = 0; q < E / 4; q++) {
+            const float4 dx = *reinterpret_cast<const float4 *>(sdx + s * MR + 8 * q + 4 * h);
+            const float dv[4] = {dx.x, dx.y, dx.z, dx.w};
+            float sv[4] = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (MIN) {
+                const float4 sx = *reinterpret_cast<const float4 *>(ssx + s * MR + 8 * q + 4 * h);
+                sv[0] = sx.x; sv[1] = sx.y; sv[2] = sx.z; sv[3] = sx.w;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                float a = fmaf((float)o[4 * q + c] * dw, dv[c], acc[4 * q + c]);
+                if constexpr (MIN) a = fmaf(h2f(dmv >> 16), sv[c], a);
+                acc[4 * q + c] = a;
+                asm volatile("" : "+v"(acc[4 * q + c]));
+            }
+        }
+        if (s < 7) o = on;
+    }
+}
+
 template <int MR>
 struct MxX {
     i32x4v c[MR / 4], s;  // codes (rows 4q + lane/16, chunk lane%16), sums (row lane/2, half lane%2)
@@ -437,6 +569,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     constexpr int E = MR / 2, STAGE = MR * 256 + MR * 32;  // codes of MR rows, then their 16-value sums
     static_assert(E * 64 * 4 <= STAGE, "the partial tile overlays the wave's stage");
     // [nb][MR] (Q8_0: [8 nb][MR]): dx of activation block b, row i (0 past m)
+    // (Q8_1: then the s values, the same way)
     extern __shared__ __align__(16) float sdx[];
     __shared__ __align__(16) uint8_t xs[MX_WAVES][STAGE];
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -447,8 +580,17 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     const uint8_t *wr = PAIR ? (j < 16 ? W : W2) + (int64_t)min(row0 + (j & 15), n - 1) * row_bytes
                              : W + (int64_t)min(row0 + j, n - 1) * row_bytes;
     const int p0 = part * nb / sp.splits, np = (part + 1) * nb / sp.splits - p0;  // this workgroup's blocks
-    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 8 * 34;
-    constexpr bool Q80 = TYPE == TYPE_Q8_0;  // Q8_0 activations: no 16-value sums, a d per 32 values
+    constexpr int BYTES = TYPE == TYPE_Q4_K   ? 144
+                          : TYPE == TYPE_Q5_K ? 176
+                          : TYPE == TYPE_Q6_K ? 210
+                          : TYPE == TYPE_Q8_0 ? 8 * 34
+                          : TYPE == TYPE_Q4_0 ? 8 * 18
+                          : TYPE == TYPE_Q4_1 ? 8 * 20
+                          : TYPE == TYPE_Q5_0 ? 8 * 22
+                                              : 8 * 24;
+    // Q8_0 / Q8_1 activations: no 16-value sums, a d (and for Q8_1 an s) per 32 values
+    constexpr bool Q80 = TYPE == TYPE_Q8_0 || mx_legacy(TYPE);
+    constexpr bool XS = TYPE == TYPE_Q4_1 || TYPE == TYPE_Q5_1;
     uint8_t *st = xs[wave];
     // this lane's share of a block's activations: MR / 4 code chunks (row 4q +
     // lane / 16, chunk lane % 16) and a sums chunk (row lane / 2, half lane % 2);
@@ -517,6 +659,7 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
     for (int q = DB * p0 * MR + t; q < DB * (p0 + np) * MR; q += 64 * MX_WAVES) {
         const int b = q / MR, i = q % MR;
         sdx[q] = i < m ? act.xd[(int64_t)i * (DB * nb) + b] : 0.f;
+        if constexpr (XS) sdx[DB * nb * MR + q] = i < m ? act.xs[(int64_t)i * (DB * nb) + b] : 0.f;
     }
     __syncthreads();  // sdx (each wave's first stage is its own)
     if (any) {
@@ -526,7 +669,10 @@ __device__ __forceinline__ void mx_workgroup(const uint8_t *__restrict__ W, int6
                 // xr[1 - q] holds slot i + q + 1 (loaded a block ago); xr[q] takes i + q + 2
                 load_x(blk(i + q + 2), xr[q]);
                 load_w(blk(i + q + 1), rw[1 - q]);
-                if constexpr (Q80) mx_block8<MR>(rw[q], st, ro, h, sdx + DB * MR * blk(i + q), acc);
+                if constexpr (mx_legacy(TYPE))
+                    mx_block_leg<TYPE, MR>(rw[q], st, ro, h, sdx + DB * MR * blk(i + q),
+                                           sdx + DB * nb * MR + DB * MR * blk(i + q), acc);
+                else if constexpr (Q80) mx_block8<MR>(rw[q], st, ro, h, sdx + DB * MR * blk(i + q), acc);
                 else if constexpr (TYPE == TYPE_Q6_K) mx_block6<E, AL6>(rw[q], st, xo6, ro[8], h, sdx + MR * blk(i + q), acc);
                 else mx_block<TYPE, (MX_WAVES > 4), E>(rw[q], st, ro, h, sdx + MR * blk(i + q), acc);
                 if (i + q == il) break;
@@ -659,6 +805,13 @@ bool gemv_mx_serves(int type, int64_t n, int64_t k, int m) {
     // m = 32 29.4 -> 31.1, the 128256-row head m = 8 / 16 128.7 / 159.9 -> 151.5 /
     // 167.6): sixteen MFMAs per block and a scaled sum per group and output.
     if (tuning().gemv_mx_off) return false;
+    if (mx_legacy(type)) {
+        // Q4_0 / Q4_1 / Q5_0 / Q5_1 at m = 5..16 from 1024 rows, k % 256 == 0
+        // (eight blocks per step; the 16-row stage at most: six raw dwords per block)
+        if (k % 256 || k / 256 > 64 || m < 2 || m > 16 || n <= 0 || n > (int64_t)MAX_ROWS) return false;
+        if (tuning().gemv_mx_all) return true;
+        return m >= 5 && n >= 1024 && (m <= 8 || !tuning().gemv_mx_wide_off);
+    }
     if (type == TYPE_Q8_0) {
         // m = 5..32 from 1024 rows, k % 256 == 0 (eight blocks per step), against
         // the multi-row decode kernel and the fp16 GEMM (4096 x 4096 m = 5 / 8 / 16 /
@@ -736,37 +889,51 @@ static void mx_typed(int type, F &&f) {
     if (type == TYPE_Q4_K) f(std::integral_constant<int, TYPE_Q4_K>{});
     else if (type == TYPE_Q5_K) f(std::integral_constant<int, TYPE_Q5_K>{});
     else if (type == TYPE_Q6_K) f(std::integral_constant<int, TYPE_Q6_K>{});
-    else f(std::integral_constant<int, TYPE_Q8_0>{});
+    else if (type == TYPE_Q8_0) f(std::integral_constant<int, TYPE_Q8_0>{});
+    else if (type == TYPE_Q4_0) f(std::integral_constant<int, TYPE_Q4_0>{});
+    else if (type == TYPE_Q4_1) f(std::integral_constant<int, TYPE_Q4_1>{});
+    else if (type == TYPE_Q5_0) f(std::integral_constant<int, TYPE_Q5_0>{});
+    else f(std::integral_constant<int, TYPE_Q5_1>{});
 }
 
 // The activation view a launch of `type` reads: Q8_K codes, d per 256 values and
 // 16-value sums; Q8_0 codes and d per 32 values.
 static bool mx_act_ok(int type, const ActView &act, int64_t k) {
-    const int64_t nb = type == TYPE_Q8_0 ? k / 32 : k / 256;
-    return act.k == k && act.nb == nb && act.xq && act.xd && (type == TYPE_Q8_0 || act.xbs);
+    const bool x32 = type == TYPE_Q8_0 || mx_legacy(type), xs = type == TYPE_Q4_1 || type == TYPE_Q5_1;
+    return act.k == k && act.nb == (x32 ? k / 32 : k / 256) && act.xq && act.xd && (x32 || act.xbs) && (!xs || act.xs);
 }
 // LDS for the activation scales of a launch (see mx_workgroup)
 static size_t mx_lds(int type, int64_t k, int m) {
-    return (size_t)(k / 256) * (type == TYPE_Q8_0 ? 8 : 1) * mx_rows(m) * sizeof(float);
+    const bool x32 = type == TYPE_Q8_0 || mx_legacy(type), xs = type == TYPE_Q4_1 || type == TYPE_Q5_1;
+    return (size_t)(k / 256) * (x32 ? 8 : 1) * (xs ? 2 : 1) * mx_rows(m) * sizeof(float);
 }
 
 template <int TYPE, int WAVES, bool PAIR>
 static void mx_launch(int m, unsigned grid, size_t lds, hipStream_t st, const uint8_t *w, int64_t row_bytes, int n,
                       int nb, const ActView &act, float *y, const MxSplit &sp, const uint8_t *w2, int nwg) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(w, row_bytes, n, nb, act, m, y, sp, w2, nwg); };
+    if constexpr (mx_legacy(TYPE)) {  // (m <= 16: gemv_mx_serves)
+        if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
+        else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
+        return;
+    } else {
     if constexpr (!PAIR) {  // (a pair has more tiles than CUs: never row halves)
         if (m > 32) return go(k_gemv_mx<TYPE, WAVES, 32, false, true>);
     }
     if (m > 16) go(k_gemv_mx<TYPE, WAVES, 32, PAIR>);
     else if (m > 8) go(k_gemv_mx<TYPE, WAVES, 16, PAIR>);
     else go(k_gemv_mx<TYPE, WAVES, 8, PAIR>);
+    }
 }
 
 template <int TYPE, int WAVES>
 static void mx_seg_launch(int m, unsigned grid, size_t lds, hipStream_t st, int64_t row_bytes, int nb,
                           const ActView &act, const MxSegs &g) {
     auto go = [&](auto kern) { kern<<<grid, 64 * WAVES, lds, st>>>(row_bytes, nb, act, m, g); };
-    if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
+    if constexpr (mx_legacy(TYPE)) {  // (m <= 16: gemv_mx_serves)
+        if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
+        else go(k_gemv_mx_seg<TYPE, WAVES, 8>);
+    } else if (m > 32) go(k_gemv_mx_seg<TYPE, WAVES, 32, true>);
     else if (m > 16) go(k_gemv_mx_seg<TYPE, WAVES, 32>);
     else if (m > 8) go(k_gemv_mx_seg<TYPE, WAVES, 16>);
     else go(k_gemv_mx_seg<TYPE, WAVES, 8>);

@@ -588,3 +588,85 @@ def test_mx_q8_0_gate_up_pair(oracle, lbq, dev, m, monkeypatch):
     gr = oracle.qmatmul(Q8_0, g_raw, n, k, x, nthreads=8).astype(np.float64)
     ur = oracle.qmatmul(Q8_0, u_raw, n, k, x, nthreads=8).astype(np.float64)
     assert_rows_close(y, gr / (1.0 + np.exp(-gr)) * ur, 1e-4)
+
+
+# The legacy 32-value types (m = 5..16 from 1024 rows, k % 256 == 0): eight blocks per
+# step, q - 8 / q - 16 formed bytewise (Q4_0 / Q5_0), + m * s (Q4_1 / Q5_1 against
+# Q8_1 activations) -- the decode bound; byte sizes 18 / 20 / 22 / 24
+LEG = [2, 3, 6, 7]
+LEG_BYTES = {2: 18, 3: 20, 6: 22, 7: 24}
+
+
+@pytest.mark.parametrize("t", LEG)
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1056, 4096), (4100, 1280), (4096, 14336), (1024, 16384)])
+@pytest.mark.parametrize("m", [5, 9, 16])
+def test_mx_legacy_matches_oracle(oracle, lbq, dev, t, n, k, m, monkeypatch):
+    rng = np.random.default_rng(n * 13 + k + 47 * m + t)
+    w_raw = bp.random_blocks(rng, t, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    print(f"mx legacy t={t} n={n} k={k} m={m}", flush=True)
+    y = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    again = gpu_qmatmul(t, w_raw, n, k, x, dev)
+    assert np.array_equal(again.view(np.uint32), y.view(np.uint32))  # deterministic
+    off = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_OFF": "1"}, t, w_raw, n, k, x, dev)
+    assert_rows_close(off, ref, 2e-3)
+    assert not np.array_equal(off.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", LEG)
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 2), (2050, 2048, 8), (64, 14336, 4), (96, 16384, 8)])
+def test_mx_legacy_forced_and_extremes(oracle, lbq, dev, t, n, k, m, monkeypatch):
+    # LBQ_GEMV_MX_ALL runs the kernel at m <= 4 and below 1024 rows; then blocks at the
+    # ends of every field (codes 0 / 15 or 31, every fifth bit set or clear, d and m of
+    # both signs) against activations of one magnitude
+    rng = np.random.default_rng(1050 + t + m + n)
+    w_raw = bp.random_blocks(rng, t, n * k // 32, d_scale=1e-3)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_ALL": "1"}, t, w_raw, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_raw, n, k, x, nthreads=8).astype(np.float64)
+    assert_rows_close(y, ref, 1e-4)
+    blocks = w_raw.reshape(-1, LEG_BYTES[t]).copy()
+    hdr = 4 if t in (3, 7) else 2
+    body = rng.choice(np.array([0x00, 0xff], dtype=np.uint8), size=(blocks.shape[0], LEG_BYTES[t] - hdr))
+    blocks[:, hdr:] = body
+    w2 = blocks.reshape(-1)
+    x2 = (np.where(rng.random((m, k)) < 0.5, -100.0, 100.0)).astype(np.float32)
+    y2 = forward_with_env(monkeypatch, {"LBQ_GEMV_MX_ALL": "1"}, t, w2, n, k, x2, dev)
+    ref2 = oracle.qmatmul(t, w2, n, k, x2, nthreads=8).astype(np.float64)
+    assert_rows_close(y2, ref2, 1e-4)
+
+
+@pytest.mark.parametrize("t", LEG)
+def test_mx_legacy_nonfinite_and_bits(oracle, lbq, dev, t):
+    # NaN / Inf block scales in a few rows; then forward(), the pre-quantised handle and
+    # a grouped call give the same bits (two-way split tiles at 4096 rows)
+    import torch
+    from lightbulb_amd.quantized import QActivation, QMatMul, QTensor, qmatmul_group
+    from test_gpu_parity import to_dev
+    rng = np.random.default_rng(1060 + t)
+    n, k, m = 4096, 2048, 12
+    w_raw = bp.random_blocks(rng, t, n * k // 32, d_scale=1e-3)
+    w_bad = w_raw.copy()
+    bad, nan_rows = _poison(w_bad, t, n, k // 32, rng)
+    good = np.setdiff1d(np.arange(n), bad)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = gpu_qmatmul(t, w_bad, n, k, x, dev)
+    ref = oracle.qmatmul(t, w_bad, n, k, x, nthreads=8).astype(np.float64)
+    assert np.array_equal(np.isfinite(y), np.isfinite(ref))
+    assert np.isnan(y[:, nan_rows]).all()
+    assert_rows_close(y[:, good], ref[:, good], 1e-4)
+    raws = [w_raw, bp.random_blocks(rng, t, n * k // 32, d_scale=1e-3)]
+    qms = [QMatMul.from_qtensor(QTensor(to_dev(r, dev), t, (n, k))) for r in raws]
+    xd = to_dev(x, dev)
+    y0 = qms[0].forward(xd)
+    y0q = qms[0].forward_quantized(QActivation.for_weight(qms[0], m).quantize(xd))
+    yg = qmatmul_group(qms, xd)
+    y1 = qms[1].forward(xd)
+    torch.cuda.synchronize()
+    bits = lambda a: a.cpu().numpy().view(np.uint32)
+    assert np.array_equal(bits(y0), bits(y0q))
+    assert np.array_equal(bits(y0), bits(yg[0]))
+    assert np.array_equal(bits(y1), bits(yg[1]))
