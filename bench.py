@@ -59,8 +59,11 @@ def parse():
     p.add_argument("--no-configs", action="store_true",
                    help="skip configs 1, 3 and 4 (Q8_0 GEMV, Q6_K head / Q5_K batch 1-8, M crossover)")
     p.add_argument("--prefill-profile", action="store_true",
-                   help="only run QMatMul::forward for Q4_K gate_proj 14336x4096 at M = 16, 32 and 512 "
-                        "(a short, fixed workload for rocprofv3 counter runs of the batched kernels)")
+                   help="only run QMatMul::forward for Q4_K gate_proj 14336x4096 and down_proj 4096x14336 at "
+                        "the --prefill-ms batch sizes (a short, fixed workload for rocprofv3 counter runs of "
+                        "the batched kernels)")
+    p.add_argument("--prefill-ms", default="16,64,512",
+                   help="batch sizes M of --prefill-profile, comma-separated (configs[3]: 16,64,512,2048)")
     p.add_argument("--copy-probe", action="store_true",
                    help="first run a 256 MiB device copy 4 times (reference kernel of known size for "
                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -283,7 +286,7 @@ def main():
     if args.copy_probe:
         copy_probe(torch, dev)
     if args.prefill_profile:
-        prefill_profile(torch, qz, dev)
+        prefill_profile(torch, qz, dev, [int(v) for v in args.prefill_ms.split(",")])
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B1)
@@ -487,18 +490,18 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def prefill_profile(torch, qz, dev):
+def prefill_profile(torch, qz, dev, ms):
     """configs[3]'s batched calls: Q4_K gate_proj 14336x4096 and down_proj 4096x14336 forward at
-    M = 16 (integer matrix cores), 64 (gate: k-sliced fp16 GEMM; down: matrix cores, two row
-    halves) and 512 (wide fp16 tiles), the weights rotated over >= 512 MB of copies, 5 graph
-    replays each, for counter collection."""
+    each M of ms -- by default 16 (integer matrix cores), 64 (gate: k-sliced fp16 GEMM; down:
+    matrix cores, two row halves) and 512 (wide fp16 tiles); 2048 takes the tall fp16 tiles --
+    the weights rotated over >= 512 MB of copies, 5 graph replays each, for counter collection."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B4)
     stream = torch.cuda.current_stream(dev)
     out = {}
     for name, n, k in (("gate_proj", 14336, 4096), ("down_proj", 4096, 14336)):
         qms = [make_weights(torch, qz, qz.GgmlDType.Q4K, n, k, gen, dev) for _ in range(n_copies(n * k // 256 * 144))]
-        for M in (16, 64, 512):
+        for M in ms:
             x = torch.randn(M, k, generator=gen, device=dev)
             out[f"q4_k_{name}_{n}x{k}_m{M}"] = round(time_forwards(torch, qms, x, stream, reps=5, warm=1), 2)
         del qms
