@@ -238,15 +238,6 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 __device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
 __device__ __forceinline__ uint4 ld_u4(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
-// the same loads with the nontemporal (streaming) hint
-typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_u4_nt(const uint8_t *p) {
-    const u32x4v_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4v_t *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t ld_u32_nt(const uint8_t *p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
-}
 
 // Weight blocks live in global memory.  Aligned dwords around a 2-byte aligned
 // field are addressed through an explicit global pointer built from the integer

@@ -99,19 +99,16 @@ struct FastK45 {  // Q4_K and Q5_K
     static constexpr int NBUF = 3;  // three-buffer ring allowed (see k_gemv1)
     static constexpr int RAW = TYPE == TYPE_Q4_K ? 9 : 17;  // registers a loaded piece occupies
     struct Raw { uint32_t hw; uint4 qh0, qh1, qs0, qs1; };
-    // NT: nontemporal loads (see k_gemv1)
-    template <bool NT = false>
     __device__ static Raw load(const uint8_t *blk, int p) {
-        auto u4 = [](const uint8_t *a) { return NT ? ld_u4_nt(a) : ld_u4(a); };
         Raw r;
-        r.hw = NT ? ld_u32_nt(blk + 4 * p) : *reinterpret_cast<const uint32_t *>(blk + 4 * p);
+        r.hw = *reinterpret_cast<const uint32_t *>(blk + 4 * p);
         if (TYPE == TYPE_Q5_K) {
-            r.qh0 = u4(blk + 16);
-            r.qh1 = u4(blk + 32);
+            r.qh0 = ld_u4(blk + 16);
+            r.qh1 = ld_u4(blk + 32);
         }
         const uint8_t *qs = blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 32 * p;
-        r.qs0 = u4(qs);
-        r.qs1 = u4(qs + 16);
+        r.qs0 = ld_u4(qs);
+        r.qs1 = ld_u4(qs + 16);
         return r;
     }
     // activation registers for piece p: codes 64p .. 64p + 63 (xr[0..15]), the
@@ -196,13 +193,11 @@ struct FastK45T {  // Q4_K and Q5_K, eight lanes per block
     static constexpr int NBUF = 3;
     static constexpr int RAW = TYPE == TYPE_Q4_K ? 5 : 9;
     struct Raw { uint32_t hw; uint4 qh, qs; };
-    template <bool NT = false>
     __device__ static Raw load(const uint8_t *blk, int p) {
-        auto u4 = [](const uint8_t *a) { return NT ? ld_u4_nt(a) : ld_u4(a); };
         Raw r;
-        r.hw = NT ? ld_u32_nt(blk + 4 * (p & 3)) : *reinterpret_cast<const uint32_t *>(blk + 4 * (p & 3));
-        if (TYPE == TYPE_Q5_K) r.qh = u4(blk + 16 + 16 * (p & 1));
-        r.qs = u4(blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 16 * p);
+        r.hw = *reinterpret_cast<const uint32_t *>(blk + 4 * (p & 3));
+        if (TYPE == TYPE_Q5_K) r.qh = ld_u4(blk + 16 + 16 * (p & 1));
+        r.qs = ld_u4(blk + (TYPE == TYPE_Q4_K ? 16 : 48) + 16 * p);
         return r;
     }
     // activation registers for piece p of a block, from the LDS layout
@@ -747,12 +742,6 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
     const uint64_t wdiff = rs.w1 - rs.w0;
     using F = Fast<TYPE, PPB>;
     using Raw = typename F::Raw;
-    // Nontemporal weight loads where each wave streams one single-sweep row group
-    // (static schedule, RMAX = 1, one activation row): Q4_K 1024 x 4096 3.13 ->
-    // 2.68 us, 512 x 4096 3.03 -> 2.60, Q5_K 1024 x 4096 3.22 -> 3.05.  Longer
-    // streams lose with them (4096 x 4096 4.39 -> 4.70, 14336 x 4096 9.0 -> 11.6,
-    // 1024 x 14336 6.1 -> 7.0, Q5_K 2048 x 4096 3.94 -> 4.15).
-    constexpr bool NTL = (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) && RMAX == 1 && IT == 1 && MR == 1;
     constexpr int LPR = 64 / RPW;
     constexpr int BPI = LPR / F::PPB;
     static_assert(BPI >= 1, "a row needs at least one whole block per sweep");
@@ -806,13 +795,9 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv1(RowMap rm, int64_t row_bytes
         // blocks of sweeps before the last are in range (the host launches the
         // smallest IT with nb <= BPI * IT); only the last sweep's block is clamped
         const uint8_t *lb = wr + bs0 * F::BYTES;
-        if constexpr (NTL) {
-            buf[0] = F::template load<true>(wr + (int64_t)min(bs0, nb - 1) * F::BYTES, p);
-        } else {
 #pragma unroll
-            for (int i = 0; i < IT - 1; i++) buf[i] = F::load(lb + i * BPI * F::BYTES, p);
-            buf[IT - 1] = F::load(wr + (int64_t)min(bs0 + BPI * (IT - 1), nb - 1) * F::BYTES, p);
-        }
+        for (int i = 0; i < IT - 1; i++) buf[i] = F::load(lb + i * BPI * F::BYTES, p);
+        buf[IT - 1] = F::load(wr + (int64_t)min(bs0 + BPI * (IT - 1), nb - 1) * F::BYTES, p);
     };
 
     // group indices are clamped into the wave's range (a wave without groups
