@@ -62,6 +62,9 @@ def parse():
                    help="only run QMatMul::forward for Q4_K gate_proj 14336x4096 and down_proj 4096x14336 at "
                         "the --prefill-ms batch sizes (a short, fixed workload for rocprofv3 counter runs of "
                         "the batched kernels)")
+    p.add_argument("--prefill-library", action="store_true",
+                   help="with --prefill-profile: also run the library fp16 GEMM (torch.matmul, hipBLASLt) "
+                        "on the same shapes and batch sizes, operands already fp16, for counter runs of it")
     p.add_argument("--prefill-ms", default="16,64,512",
                    help="batch sizes M of --prefill-profile, comma-separated (configs[3]: 16,64,512,2048)")
     p.add_argument("--copy-probe", action="store_true",
@@ -286,7 +289,7 @@ def main():
     if args.copy_probe:
         copy_probe(torch, dev)
     if args.prefill_profile:
-        prefill_profile(torch, qz, dev, [int(v) for v in args.prefill_ms.split(",")])
+        prefill_profile(torch, qz, dev, [int(v) for v in args.prefill_ms.split(",")], args.prefill_library)
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x1B1)
@@ -490,7 +493,7 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def prefill_profile(torch, qz, dev, ms):
+def prefill_profile(torch, qz, dev, ms, library=False):
     """configs[3]'s batched calls: Q4_K gate_proj 14336x4096 and down_proj 4096x14336 forward at
     each M of ms -- by default 16 (integer matrix cores), 64 (gate: k-sliced fp16 GEMM; down:
     matrix cores, two row halves) and 512 (wide fp16 tiles); 2048 takes the tall fp16 tiles --
@@ -506,6 +509,20 @@ def prefill_profile(torch, qz, dev, ms):
             out[f"q4_k_{name}_{n}x{k}_m{M}"] = round(time_forwards(torch, qms, x, stream, reps=5, warm=1), 2)
         del qms
         torch.cuda.empty_cache()
+        if library:
+            # the library's fp16 GEMM on the same shape (LDS-staged operand tiles, no
+            # dequantisation): fp16 weight copies rotated over the same >= 512 MB
+            w16s = [torch.randn(k, n, generator=gen, device=dev).to(torch.float16)
+                    for _ in range(n_copies(n * k * 2))]
+            for M in ms:
+                a16 = torch.randn(M, k, generator=gen, device=dev).to(torch.float16)
+                g = capture(torch, lambda: [torch.matmul(a16, w) for w in w16s])
+                timed_graph(torch, g, 1, stream)
+                us = timed_graph_median(torch, g, 5, stream) / len(w16s) * 1e3
+                out[f"fp16_library_{name}_{n}x{k}_m{M}"] = round(us, 2)
+                del g, a16
+            del w16s
+            torch.cuda.empty_cache()
     print(json.dumps({"prefill_profile_us": out}), flush=True)
 
 
