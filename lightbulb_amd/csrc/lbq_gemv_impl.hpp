@@ -719,9 +719,14 @@ static hipError_t launch_fast(const RowMap &rm, int64_t row_bytes, int nb, const
     // CU does better, and so it does for k = 14336 and for Q6_K throughout.
     // Measured (fused / pre-quantised x): Q4_K 4096 x 4096 5.0 / 4.5 us at 4 vs
     // 5.7 / 4.6 at 8; 14336 x 4096 9.3 / 8.8 at 4 vs 9.1 / 8.4 at 8; 4096 x 14336
-    // 10.1 / 8.2 at 4 vs 11.2 / 9.0 at 8; Q6_K 14336 x 4096 14.4 at 4 vs 16.1 at 8.
-    // Q8_0 takes eight everywhere (4096 x 4096 fused: 6.2 us at 4, 5.7 at 8).
-    int wpc = (TYPE == TYPE_Q6_K || (TYPE != TYPE_Q8_0 && n < 8192 && (x || nb > 32))) ? 4 : 8;
+    // 10.1 / 8.2 at 4 vs 11.2 / 9.0 at 8.  Q6_K takes four except from 8192 to 32768
+    // rows at k <= 4096 (14336 x 4096 14.0 -> 13.4 us, 28672 x 4096 25.1 -> 24.1 at
+    // eight; 4096 / 8192 rows 5.5 / 8.4 -> 5.7 / 8.7 and the 128256-row head 94.1 ->
+    // 97.3 us, so those keep four).  Q8_0 takes eight everywhere (4096 x 4096 fused:
+    // 6.2 us at 4, 5.7 at 8).
+    const bool q6_8 = TYPE == TYPE_Q6_K && n > 8192 && n <= 32768 && nb <= 16;
+    int wpc = ((TYPE == TYPE_Q6_K && !q6_8) ||
+               (TYPE != TYPE_Q6_K && TYPE != TYPE_Q8_0 && n < 8192 && (x || nb > 32))) ? 4 : 8;
     if (tuning().gemv1_wpc > 0) wpc = tuning().gemv1_wpc;
     int64_t waves = (int64_t)num_cus() * wpc;
     if (waves > ng) waves = ng;
