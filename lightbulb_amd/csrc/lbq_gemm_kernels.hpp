@@ -725,7 +725,9 @@ __global__ __launch_bounds__(256, (gemm_occupancy<TYPE, MT>())) void k_gemm(cons
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int64_t n = n0 + 64 * wave + 32 * j + lr;
-                if (m < M && n < N) y[m * N + n] = __builtin_amdgcn_ldexpf(acc[i][j][v], e + en[j]);
+                // nontemporal, as in the wide and tall tiles (Q4_K 14336x4096 M = 48 / 64
+                // 30.1 / 32.1 -> 29.5 / 31.2 us, split partials included)
+                if (m < M && n < N) __builtin_nontemporal_store(__builtin_amdgcn_ldexpf(acc[i][j][v], e + en[j]), y + m * N + n);
             }
         }
     }
