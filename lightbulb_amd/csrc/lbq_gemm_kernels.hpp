@@ -1312,7 +1312,9 @@ __device__ __forceinline__ void ks_slice_sum(const float *out, int64_t split_str
                 const int r = (t >> 5) + RS * (r0 + j);
                 if (r >= rows) continue;
                 float *yo = g.y + (int64_t)r * N + col;
-                yo[0] = sum[j].x; yo[1] = sum[j].y; yo[2] = sum[j].z; yo[3] = sum[j].w;
+                // the output: nontemporal, as every tile's final stores
+                __builtin_nontemporal_store(sum[j].x, yo); __builtin_nontemporal_store(sum[j].y, yo + 1);
+                __builtin_nontemporal_store(sum[j].z, yo + 2); __builtin_nontemporal_store(sum[j].w, yo + 3);
             }
         }
     }
@@ -1459,6 +1461,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ks(const uint8_t *W, int64_t N,
             acc[u][v] = __builtin_amdgcn_ldexpf(acc[u][v], ex[u][v] + en);
             if (r < M && n < N) {
                 if (g.cnt) __hip_atomic_store(y + (int64_t)r * N + n, acc[u][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // y itself (no split): nontemporal (Q6_K 128256x4096 m = 32 184.3 -> 182.9 us);
+                // split partials, which the split-sum launch reads right back, stay cached
+                // (nontemporal: 1024x4096 m = 32 10.7 -> 11.1 us)
+                else if (g.split_stride == 0) __builtin_nontemporal_store(acc[u][v], y + (int64_t)r * N + n);
                 else y[(int64_t)r * N + n] = acc[u][v];
             }
         }
